@@ -1,0 +1,92 @@
+// Shared device helpers for the DASH HIP kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+namespace dash {
+
+typedef __bf16 bf16;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4;
+
+// Sentinels of the reference router (dash_attention.py:600-604,
+// modeling_deepseekv2.py:56).
+constexpr float kScoreNeg = -1.0e9f;
+constexpr float kEntmaxNeg = -1.0e4f;
+constexpr float kActClamp = 1.0e4f;
+
+constexpr int kWave = 64;
+
+// Status codes returned by every C entry point.
+enum Status : int {
+  kOk = 0,
+  kErrUnsupported = -2,   // a shape or parameter this build does not implement
+  kErrInvalid = -3,       // inconsistent arguments (null pointer, negative size...)
+  kErrWorkspace = -4,     // caller-provided workspace too small
+};
+
+__device__ __forceinline__ float bf2f(bf16 x) { return (float)x; }
+
+__device__ __forceinline__ int wave_lane() { return threadIdx.x & (kWave - 1); }
+
+template <typename T>
+__device__ __forceinline__ T shfl_xor(T v, int mask) {
+  return __shfl_xor(v, mask, kWave);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+// Where token t of sequence b lives, for the three layouts the path uses:
+//   contiguous  row = b*stride_b + t*stride_t
+//   varlen      row = (cu[b] + t)*stride_t          (packed documents)
+//   paged       row = table[b][t / page]*stride_page + (t % page)*stride_t
+struct SeqLayout {
+  const int32_t* cu;          // [B+1] or null
+  const int32_t* table;       // [B, table_stride] or null
+  int64_t table_stride;
+  int64_t stride_b;           // contiguous layout
+  int64_t stride_page;        // paged layout
+  int64_t stride_t;
+  int page;                   // tokens per page (paged layout)
+
+  __device__ __forceinline__ int64_t row(int b, int t) const {
+    if (table) {
+      const int p = table[(int64_t)b * table_stride + t / page];
+      return (int64_t)p * stride_page + (int64_t)(t % page) * stride_t;
+    }
+    if (cu) return (int64_t)(cu[b] + t) * stride_t;
+    return (int64_t)b * stride_b + (int64_t)t * stride_t;
+  }
+};
+
+// Length of sequence b: cu_seqlens, explicit lengths, or the common length.
+__device__ __forceinline__ int seq_length(const int32_t* cu, const int32_t* lens, int b, int S) {
+  if (cu) return cu[b + 1] - cu[b];
+  if (lens) return lens[b];
+  return S;
+}
+
+// Flat row index of (sequence b, token t) for per-token outputs such as the
+// block scores or the routed indices: varlen rows are packed, the others are b*S+t.
+__device__ __forceinline__ int64_t token_row(const int32_t* cu, int b, int t, int S) {
+  if (cu) return (int64_t)cu[b] + t;
+  return (int64_t)b * S + t;
+}
+
+}  // namespace dash

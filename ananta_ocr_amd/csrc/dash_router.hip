@@ -1,0 +1,483 @@
+// DASH router kernels: stage-0 block summaries, block scores and 1.5-entmax
+// routing.  Written for gfx950 (wave64).
+//
+//   kbar_kernel        k_bar = softmax(k.head_cls/sqrt(d)) pooling per key block
+//                      (dash_attention.py:851-888, modeling_deepseekv2.py:362-377)
+//   scores_kernel      z = clamp(q.k_bar/sqrt(d)), remote-block mask
+//                      (modeling_deepseekv2.py:378-386)
+//   blockmax_kernel    indexer stage-0: per-block max of q.k over non-local keys
+//                      (modeling_deepseekv2.py:387-400, sparse_gather_triton.py:395-428)
+//   route_kernel       top-M selection + 1.5-entmax + top-K + centred log-prior bias
+//                      (modeling_deepseekv2.py:309-333, dash_attention.py:615-662)
+
+#include "dash_common.h"
+
+namespace dash {
+
+// ---------------------------------------------------------------------------
+// k_bar: one work-group (256 threads) per (key block, sequence).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void kbar_kernel(
+    const float* __restrict__ idx_k, SeqLayout lay, const int32_t* __restrict__ cu,
+    const int32_t* __restrict__ lens, const float* __restrict__ head_cls, int S, int d,
+    int bs, int tail_only, float inv_sqrt_d, float* __restrict__ kbar, int64_t kb_sb) {
+  __shared__ float s_aw[256];
+  __shared__ float s_red[2];
+  const int b = blockIdx.y;
+  const int len = seq_length(cu, lens, b, S);
+  if (len <= 0) return;
+  const int c = tail_only ? (len - 1) / bs : (int)blockIdx.x;
+  const int t0 = c * bs;
+  if (t0 >= len) return;
+  const int n = min(bs, len - t0);
+  const int lane = wave_lane();
+  const int wv = threadIdx.x / kWave;
+
+  // per-token logits aw_j = clamp((k_j . head_cls) / sqrt(d), +-1e4)
+  for (int j = wv; j < n; j += 4) {
+    const float* kr = idx_k + lay.row(b, t0 + j);
+    float acc = 0.f;
+    for (int i = lane; i < d; i += kWave) acc += kr[i] * head_cls[i];
+    acc = wave_sum(acc);
+    if (lane == 0) s_aw[j] = fminf(fmaxf(acc * inv_sqrt_d, -kActClamp), kActClamp);
+  }
+  __syncthreads();
+  if (threadIdx.x < kWave) {
+    float m = -INFINITY;
+    for (int j = lane; j < n; j += kWave) m = fmaxf(m, s_aw[j]);
+    m = wave_max(m);
+    float sum = 0.f;
+    for (int j = lane; j < n; j += kWave) sum += expf(s_aw[j] - m);
+    sum = wave_sum(sum);
+    if (lane == 0) { s_red[0] = m; s_red[1] = fmaxf(sum, 1e-6f); }
+  }
+  __syncthreads();
+  const float m = s_red[0], den = s_red[1];
+  for (int j = threadIdx.x; j < n; j += blockDim.x) s_aw[j] = expf(s_aw[j] - m) / den;
+  __syncthreads();
+  for (int i = threadIdx.x; i < d; i += blockDim.x) {
+    float acc = 0.f;
+    for (int j = 0; j < n; ++j) acc += s_aw[j] * idx_k[lay.row(b, t0 + j) + i];
+    if (!(fabsf(acc) <= 3.402823466e38f)) acc = 0.f;   // nan_to_num(nan/inf -> 0)
+    kbar[(int64_t)b * kb_sb + (int64_t)c * d + i] = acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// head_cls block scores: 64 query rows x 64 key blocks per work-group, fp32 FMA.
+// ---------------------------------------------------------------------------
+constexpr int kScTile = 64;
+constexpr int kScK = 16;
+
+__global__ __launch_bounds__(256) void scores_kernel(
+    const float* __restrict__ idx_q, SeqLayout lay_q, const int32_t* __restrict__ cu_q,
+    int Lq, const int32_t* __restrict__ q_pos, const float* __restrict__ kbar, int64_t kb_sb,
+    const int32_t* __restrict__ cu_k, const int32_t* __restrict__ lens_k, int S, int d,
+    int bs, int local_blocks, int nblk_cap, float inv_sqrt_d, float* __restrict__ z,
+    int64_t z_stride) {
+  __shared__ float sq[kScK][kScTile + 1];
+  __shared__ float sk[kScK][kScTile + 1];
+  const int b = blockIdx.z;
+  const int nq = cu_q ? (cu_q[b + 1] - cu_q[b]) : Lq;
+  const int r0 = blockIdx.x * kScTile;
+  const int c0 = blockIdx.y * kScTile;
+  if (r0 >= nq) return;
+  const int klen = seq_length(cu_k, lens_k, b, S);
+  const int nblk_b = (klen + bs - 1) / bs;
+  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+
+  for (int k0 = 0; k0 < d; k0 += kScK) {
+    // stage 64 rows x 16 dims of q and of k_bar
+    for (int e = threadIdx.x; e < kScTile * kScK; e += 256) {
+      const int rr = e / kScK, kk = e % kScK;
+      const int r = r0 + rr, c = c0 + rr, dd = k0 + kk;
+      float qv = 0.f, kv = 0.f;
+      if (r < nq && dd < d) qv = idx_q[lay_q.row(b, r) + dd];
+      if (c < nblk_cap && dd < d) kv = kbar[(int64_t)b * kb_sb + (int64_t)c * d + dd];
+      sq[kk][rr] = qv;
+      sk[kk][rr] = kv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < kScK; ++kk) {
+      float a[4], bb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = sq[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bb[j] = sk[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], bb[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = r0 + ty * 4 + i;
+    if (r >= nq) continue;
+    const int64_t row = token_row(cu_q, b, r, Lq);
+    const int pos = q_pos ? q_pos[row] : r;
+    const int lim = (pos >= 0 ? pos / bs : -((-pos + bs - 1) / bs)) - local_blocks;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = c0 + tx * 4 + j;
+      if (c >= nblk_cap) continue;
+      float v = kScoreNeg;
+      if (c <= lim && c < nblk_b) {
+        v = acc[i][j] * inv_sqrt_d;
+        v = fminf(fmaxf(v, -kActClamp), kActClamp);
+      }
+      z[row * z_stride + c] = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Indexer stage-0 block scores: per-block max of q.k_j over keys j < ls(t)
+// (ls = pos - LW + 1), optionally j >= seg[t].  mode 0: torch form (clamp to
+// +-1e4, SCORE_NEG for empty blocks); mode 1: fused-kernel form (no clamp,
+// -inf for empty blocks).  One work-group per (64 query rows, key block).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void blockmax_kernel(
+    const float* __restrict__ q, SeqLayout lay_q, int C, const int32_t* __restrict__ pos,
+    const int32_t* __restrict__ seg, int64_t ps_sb, const float* __restrict__ k,
+    SeqLayout lay_k, int Sk, int d, int bs, int lw, int nblk, int mode,
+    float* __restrict__ out, int64_t o_sb, int64_t o_sc) {
+  __shared__ float sq[kScK][kScTile + 1];
+  __shared__ float sk[kScK][kScTile + 1];
+  __shared__ float smax[kScTile][17];
+  const int b = blockIdx.z;
+  const int r0 = blockIdx.x * kScTile;
+  const int c = blockIdx.y;
+  if (r0 >= C) return;
+  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  const float empty = mode == 0 ? kScoreNeg : -INFINITY;
+  float best[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) best[i] = -INFINITY;
+  int lsr[4], sgr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = min(r0 + ty * 4 + i, C - 1);
+    const int p = pos[(int64_t)b * ps_sb + r];
+    lsr[i] = max(p - lw + 1, 0);
+    sgr[i] = seg ? seg[(int64_t)b * ps_sb + r] : 0;
+  }
+  for (int j0 = c * bs; j0 < min((c + 1) * bs, Sk); j0 += kScTile) {
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+    const int jend = min(min((c + 1) * bs, Sk), j0 + kScTile);
+    for (int k0 = 0; k0 < d; k0 += kScK) {
+      for (int e = threadIdx.x; e < kScTile * kScK; e += 256) {
+        const int rr = e / kScK, kk = e % kScK;
+        const int r = r0 + rr, j = j0 + rr, dd = k0 + kk;
+        sq[kk][rr] = (r < C && dd < d) ? q[lay_q.row(b, r) + dd] : 0.f;
+        sk[kk][rr] = (j < jend && dd < d) ? k[lay_k.row(b, j) + dd] : 0.f;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int kk = 0; kk < kScK; ++kk) {
+        float a[4], bb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = sq[kk][ty * 4 + i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bb[j] = sk[kk][tx * 4 + j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], bb[j], acc[i][j]);
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = j0 + tx * 4 + j;
+        if (key < jend && key < lsr[i] && key >= sgr[i]) {
+          float v = acc[i][j];
+          if (mode == 0) v = fminf(fmaxf(v, -kActClamp), kActClamp);
+          best[i] = fmaxf(best[i], v);
+        }
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) smax[ty * 4 + i][tx] = best[i];
+  __syncthreads();
+  if (threadIdx.x < kScTile) {
+    const int r = r0 + threadIdx.x;
+    if (r < C) {
+      float m = -INFINITY;
+      for (int j = 0; j < 16; ++j) m = fmaxf(m, smax[threadIdx.x][j]);
+      out[(int64_t)b * o_sb + (int64_t)r * o_sc + c] = (m == -INFINITY) ? empty : m;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Routing: one wavefront per query row.
+// ---------------------------------------------------------------------------
+constexpr int kMaxM = 16;
+
+// (value desc, block id asc) order; id carries the candidacy flag in bit 30.
+__device__ __forceinline__ bool route_better(float va, int ka, float vb, int kb) {
+  const int ia = ka & 0x3fffffff, ib = kb & 0x3fffffff;
+  return va > vb || (va == vb && ia < ib);
+}
+
+// 1.5-entmax over M values sorted in descending order, bit-for-bit the fp32
+// sequence of dash_attention.py:623-647 on the CPU: X = (x - max)/2, cumsums
+// accumulated in double and rounded to fp32, every other operation a single
+// correctly rounded fp32 operation (no contraction).
+__device__ __forceinline__ void entmax15_sorted(const float (&x)[kMaxM], int M,
+                                                float (&p)[kMaxM]) {
+#pragma clang fp contract(off)
+  float X[kMaxM], tau[kMaxM];
+  double cs = 0.0, cs2 = 0.0;
+  int support = 0;
+#pragma unroll
+  for (int m = 0; m < kMaxM; ++m) {
+    X[m] = __fdiv_rn(__fsub_rn(x[m], x[0]), 2.0f);
+    tau[m] = 0.f;
+    if (m < M) {
+      const float rho = (float)(m + 1);
+      cs += (double)X[m];
+      cs2 += (double)__fmul_rn(X[m], X[m]);
+      const float mean = __fdiv_rn((float)cs, rho);
+      const float mean_sq = __fdiv_rn((float)cs2, rho);
+      const float ss = __fmul_rn(rho, __fsub_rn(mean_sq, __fmul_rn(mean, mean)));
+      const float delta = __fdiv_rn(__fsub_rn(1.0f, ss), rho);
+      const float delta_nz = delta > 0.f ? delta : 0.f;
+      tau[m] = __fsub_rn(mean, __fsqrt_rn(delta_nz));
+      if (tau[m] <= X[m]) ++support;
+    }
+  }
+  support = max(support, 1);
+  float tau_star = tau[0];
+#pragma unroll
+  for (int m = 1; m < kMaxM; ++m)
+    if (m == support - 1) tau_star = tau[m];
+#pragma unroll
+  for (int m = 0; m < kMaxM; ++m) {
+    const float t = __fsub_rn(X[m], tau_star);
+    const float c = t > 0.f ? t : 0.f;
+    p[m] = (m < M) ? __fmul_rn(c, c) : 0.f;
+  }
+}
+
+template <int NPL>
+__global__ __launch_bounds__(256) void route_kernel(
+    const float* __restrict__ z, int64_t z_stride, int rows, int nblk_cols,
+    const int32_t* __restrict__ row_nblk, const uint8_t* __restrict__ cand_in,
+    int64_t cand_stride, float idx_scale, float floor_p, float inv_sigma, int K, int topm,
+    int Kout, int32_t* __restrict__ idx_out, float* __restrict__ bias_out,
+    uint8_t* __restrict__ valid_out) {
+  const int lane = wave_lane();
+  const int row = blockIdx.x * 4 + threadIdx.x / kWave;
+  if (row >= rows) return;
+  const int nblk = row_nblk ? min(row_nblk[row], nblk_cols) : nblk_cols;
+  const float* zr = z + (int64_t)row * z_stride;
+
+  bool remote[NPL], cand[NPL];
+  float zv[NPL];
+  bool any_cand = false;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int c = lane + kWave * i;
+    zv[i] = (c < nblk) ? zr[c] : kScoreNeg;
+    remote[i] = (c < nblk) && (zv[i] > kScoreNeg * 0.5f);
+    bool cd = remote[i];
+    if (cand_in && c < nblk) cd = cd && cand_in[(int64_t)row * cand_stride + c] != 0;
+    cand[i] = cd;
+    any_cand |= cd;
+  }
+  // rows without any candidate fall back to every remote block
+  any_cand = __any(any_cand);
+  float v[NPL];
+  int key[NPL];
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int c = lane + kWave * i;
+    const bool cd = any_cand ? cand[i] : remote[i];
+    float x = cd ? zv[i] * idx_scale : kEntmaxNeg;
+    if (!(fabsf(x) <= 3.402823466e38f)) x = kEntmaxNeg;
+    v[i] = (c < nblk) ? x : -INFINITY;
+    key[i] = (c < nblk) ? (c | (cd ? (1 << 30) : 0)) : 0x3fffffff;
+  }
+  const int M = topm > 0 ? max(1, min(topm, nblk)) : nblk;
+  const int Kp = max(1, min(K, M));
+
+  float bv = -INFINITY;
+  int bk = 0x3fffffff;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i)
+    if (route_better(v[i], key[i], bv, bk)) { bv = v[i]; bk = key[i]; }
+
+  float sel_v[kMaxM];
+  int sel_k[kMaxM];
+#pragma unroll
+  for (int m = 0; m < kMaxM; ++m) {
+    sel_v[m] = 0.f;
+    sel_k[m] = 0x3fffffff;
+    if (m < M) {
+      float wv = bv;
+      int wk = bk;
+#pragma unroll
+      for (int s = 32; s >= 1; s >>= 1) {
+        const float ov = __shfl_xor(wv, s, kWave);
+        const int ok = __shfl_xor(wk, s, kWave);
+        if (route_better(ov, ok, wv, wk)) { wv = ov; wk = ok; }
+      }
+      sel_v[m] = wv;
+      sel_k[m] = wk;
+      const int wc = wk & 0x3fffffff;
+      if ((wc & (kWave - 1)) == lane) {
+        const int wi = wc / kWave;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i)
+          if (i == wi) { v[i] = -INFINITY; key[i] = 0x3fffffff; }
+        bv = -INFINITY;
+        bk = 0x3fffffff;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i)
+          if (route_better(v[i], key[i], bv, bk)) { bv = v[i]; bk = key[i]; }
+      }
+    }
+  }
+  float prior[kMaxM];
+  entmax15_sorted(sel_v, M, prior);
+
+  float logp[kMaxM];
+  float musum = 0.f;
+  int cnt = 0;
+#pragma unroll
+  for (int m = 0; m < kMaxM; ++m) {
+    logp[m] = logf(fmaxf(prior[m], floor_p));
+    const bool va = m < Kp && (sel_k[m] & (1 << 30));
+    if (va) { musum += logp[m]; ++cnt; }
+  }
+  const float mu = musum / (float)max(cnt, 1);
+  for (int m = lane; m < Kout; m += kWave) {
+    int oi = -1;
+    float ob = 0.f;
+    uint8_t ov = 0;
+#pragma unroll
+    for (int s = 0; s < kMaxM; ++s) {
+      if (s == m && s < Kp) {
+        oi = sel_k[s] & 0x3fffffff;
+        const bool va = (sel_k[s] & (1 << 30)) != 0;
+        ov = va ? 1 : 0;
+        ob = va ? (logp[s] - mu) * inv_sigma : 0.f;
+      }
+    }
+    idx_out[(int64_t)row * Kout + m] = oi;
+    bias_out[(int64_t)row * Kout + m] = ob;
+    if (valid_out) valid_out[(int64_t)row * Kout + m] = ov;
+  }
+}
+
+}  // namespace dash
+
+// ---------------------------------------------------------------------------
+// C entry points
+// ---------------------------------------------------------------------------
+namespace {
+inline int launch_status() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? dash::kOk : (int)e;
+}
+}  // namespace
+
+extern "C" int dash_kbar(const float* idx_k, int64_t ik_sb, int64_t ik_st, int64_t ik_sp,
+                         const int32_t* cu_seqlens, const int32_t* seq_lens,
+                         const int32_t* block_table, int64_t table_stride, int page_size,
+                         const float* head_cls, int B, int S, int d, int block_size,
+                         int tail_only, float* kbar, int64_t kb_sb, int nblk_cap,
+                         void* stream) {
+  using namespace dash;
+  if (!idx_k || !head_cls || !kbar || B < 0 || S < 0 || d <= 0) return kErrInvalid;
+  if (block_size <= 0 || block_size > 256) return kErrUnsupported;
+  if (block_table && page_size <= 0) return kErrInvalid;
+  if (B == 0 || nblk_cap == 0) return kOk;
+  SeqLayout lay{cu_seqlens, block_table, table_stride, ik_sb, ik_sp, ik_st, page_size};
+  dim3 grid(tail_only ? 1 : nblk_cap, B);
+  hipLaunchKernelGGL(kbar_kernel, grid, dim3(256), 0, (hipStream_t)stream, idx_k, lay,
+                     cu_seqlens, seq_lens, head_cls, S, d, block_size, tail_only,
+                     (float)(1.0 / sqrt((double)d)), kbar, kb_sb);
+  return launch_status();
+}
+
+extern "C" int dash_block_scores(const float* idx_q, int64_t iq_sb, int64_t iq_st,
+                                 const int32_t* cu_q, int Lq, const int32_t* q_pos,
+                                 const float* kbar, int64_t kb_sb, int nblk_cap,
+                                 const int32_t* cu_k, const int32_t* lens_k, int S, int B,
+                                 int d, int block_size, int local_blocks, float* z,
+                                 int64_t z_stride, void* stream) {
+  using namespace dash;
+  if (!idx_q || !kbar || !z || B < 0 || Lq < 0 || d <= 0 || nblk_cap < 0) return kErrInvalid;
+  if (block_size <= 0) return kErrInvalid;
+  if (B == 0 || Lq == 0 || nblk_cap == 0) return kOk;
+  SeqLayout lay{cu_q, nullptr, 0, iq_sb, 0, iq_st, 1};
+  dim3 grid((Lq + kScTile - 1) / kScTile, (nblk_cap + kScTile - 1) / kScTile, B);
+  hipLaunchKernelGGL(scores_kernel, grid, dim3(256), 0, (hipStream_t)stream, idx_q, lay, cu_q,
+                     Lq, q_pos, kbar, kb_sb, cu_k, lens_k, S, d, block_size, local_blocks,
+                     nblk_cap, (float)(1.0 / sqrt((double)d)), z, z_stride);
+  return launch_status();
+}
+
+extern "C" int dash_block_max_score(const float* q, int64_t q_sb, int64_t q_st, int C,
+                                    const int32_t* pos, const int32_t* seg, int64_t ps_sb,
+                                    const float* k, int64_t k_sb, int64_t k_st, int Sk, int B,
+                                    int d, int block_size, int local_window, int nblk, int mode,
+                                    float* out, int64_t o_sb, int64_t o_sc, void* stream) {
+  using namespace dash;
+  if (!q || !pos || !k || !out || B < 0 || C < 0 || d <= 0 || nblk < 0) return kErrInvalid;
+  if (block_size <= 0 || (mode != 0 && mode != 1)) return kErrInvalid;
+  if (B == 0 || C == 0 || nblk == 0) return kOk;
+  SeqLayout lq{nullptr, nullptr, 0, q_sb, 0, q_st, 1};
+  SeqLayout lk{nullptr, nullptr, 0, k_sb, 0, k_st, 1};
+  dim3 grid((C + kScTile - 1) / kScTile, nblk, B);
+  hipLaunchKernelGGL(blockmax_kernel, grid, dim3(256), 0, (hipStream_t)stream, q, lq, C, pos,
+                     seg, ps_sb, k, lk, Sk, d, block_size, max(1, local_window), nblk, mode,
+                     out, o_sb, o_sc);
+  return launch_status();
+}
+
+extern "C" int dash_route(const float* z, int64_t z_stride, int rows, int nblk_cols,
+                          const int32_t* row_nblk, const uint8_t* cand, int64_t cand_stride,
+                          float idx_scale, float floor_p, float sigma, int K, int topm,
+                          int Kout, int32_t* idx, float* bias, uint8_t* valid,
+                          void* stream) {
+  using namespace dash;
+  if (!z || !idx || !bias || rows < 0 || nblk_cols < 0) return kErrInvalid;
+  if (topm < 1 || topm > kMaxM) return kErrUnsupported;
+  if (K < 1 || Kout < 1) return kErrInvalid;
+  if (Kout < std::min(K, std::min(topm, std::max(nblk_cols, 1)))) return kErrInvalid;
+  if (nblk_cols > 64 * 32) return kErrUnsupported;
+  if (rows == 0) return kOk;
+  const float inv_sigma = (float)(1.0 / (double)sigma);
+  dim3 grid((rows + 3) / 4);
+  hipStream_t st = (hipStream_t)stream;
+  const int npl = (nblk_cols + 63) / 64;
+#define DASH_ROUTE(N)                                                                       \
+  hipLaunchKernelGGL(route_kernel<N>, grid, dim3(256), 0, st, z, z_stride, rows, nblk_cols, \
+                     row_nblk, cand, cand_stride, idx_scale, floor_p, inv_sigma, K, topm,   \
+                     Kout, idx, bias, valid)
+  if (npl <= 1) DASH_ROUTE(1);
+  else if (npl <= 2) DASH_ROUTE(2);
+  else if (npl <= 4) DASH_ROUTE(4);
+  else if (npl <= 8) DASH_ROUTE(8);
+  else if (npl <= 16) DASH_ROUTE(16);
+  else DASH_ROUTE(32);
+#undef DASH_ROUTE
+  return launch_status();
+}

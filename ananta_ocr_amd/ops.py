@@ -1,0 +1,280 @@
+"""Torch-facing wrappers of the DASH HIP kernels.
+
+Each function takes device tensors, checks shapes on the host, allocates its
+outputs with torch (the library allocates nothing) and calls one C entry point
+on the current HIP stream.  CPU tensors are rejected: the product has no CPU path.
+"""
+
+import math
+
+import torch
+
+from . import _lib
+
+_NULL = None
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _need_gpu(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("DASH HIP ops take GPU tensors (no CPU path)")
+
+
+def _i32(t):
+    return None if t is None else t.to(torch.int32).contiguous()
+
+
+def _u8(t):
+    return None if t is None else t.to(torch.uint8).contiguous()
+
+
+def _rows(x):
+    """bf16 [.., D] tensor whose feature axis is contiguous with 16-byte rows."""
+    if x.stride(-1) != 1 or any(s % 8 for s in x.stride()[:-1]) or x.data_ptr() % 16:
+        x = x.contiguous()
+    return x
+
+
+def kbar(idx_k, head_cls, block_size, cu_seqlens=None, seq_lens=None, nblk_cap=None,
+         tail_only=False, out=None, block_table=None, page_size=None):
+    """Stage-0 block summaries.  idx_k fp32 [B,S,d] (or [1,T,d] with cu_seqlens, or
+    paged [pages, page_size, d] with block_table).  Returns [B, nblk_cap, d] fp32."""
+    _need_gpu(idx_k, head_cls)
+    lib = _lib.load()
+    idx_k = idx_k.float()
+    if idx_k.stride(-1) != 1:
+        idx_k = idx_k.contiguous()
+    d = idx_k.shape[-1]
+    if cu_seqlens is not None:
+        cu = _i32(cu_seqlens)
+        B = cu.numel() - 1
+        S = int((cu[1:] - cu[:-1]).max().item()) if B > 0 else 0
+        sb, st, sp = 0, idx_k.stride(-2), 0
+    elif block_table is not None:
+        cu = None
+        B = block_table.shape[0]
+        S = block_table.shape[1] * page_size
+        sb, st, sp = 0, idx_k.stride(1), idx_k.stride(0)
+    else:
+        cu = None
+        B, S = idx_k.shape[0], idx_k.shape[1]
+        sb, st, sp = idx_k.stride(0), idx_k.stride(1), 0
+    if seq_lens is not None:
+        seq_lens = _i32(seq_lens)
+    if nblk_cap is None:
+        nblk_cap = (S + block_size - 1) // block_size
+    if out is None:
+        out = torch.zeros(B, nblk_cap, d, dtype=torch.float32, device=idx_k.device)
+    hc = head_cls.float().contiguous()
+    bt = _i32(block_table)
+    st_ = lib.dash_kbar(_ptr(idx_k), sb, st, sp, _ptr(cu), _ptr(seq_lens), _ptr(bt),
+                        0 if bt is None else bt.stride(0), page_size or 0, _ptr(hc), B, S, d,
+                        block_size, int(bool(tail_only)), _ptr(out), out.stride(0), nblk_cap,
+                        _stream())
+    _lib.check(st_, "dash_kbar")
+    return out
+
+
+def block_scores(idx_q, kb, block_size, local_blocks, q_pos=None, cu_seqlens=None,
+                 seq_lens=None, S=None):
+    """Block scores z for query rows idx_q fp32 [B,Lq,d] (or [1,T,d] + cu_seqlens)
+    against k_bar [B,nblk,d].  Returns [B,Lq,nblk] (or [T,nblk]) fp32."""
+    _need_gpu(idx_q, kb)
+    lib = _lib.load()
+    idx_q = idx_q.float()
+    if idx_q.stride(-1) != 1:
+        idx_q = idx_q.contiguous()
+    kb = kb.contiguous()
+    B, nblk, d = kb.shape
+    if cu_seqlens is not None:
+        cu = _i32(cu_seqlens)
+        T = idx_q.shape[-2]
+        Lq = int((cu[1:] - cu[:-1]).max().item()) if B > 0 else 0
+        z = torch.empty(T, nblk, dtype=torch.float32, device=idx_q.device)
+        sb, st = 0, idx_q.stride(-2)
+        Sk = Lq if S is None else S
+    else:
+        cu = None
+        Lq = idx_q.shape[1]
+        z = torch.empty(B, Lq, nblk, dtype=torch.float32, device=idx_q.device)
+        sb, st = idx_q.stride(0), idx_q.stride(1)
+        Sk = Lq if S is None else S
+    qp = _i32(q_pos)
+    lens = _i32(seq_lens)
+    st_ = lib.dash_block_scores(_ptr(idx_q), sb, st, _ptr(cu), Lq, _ptr(qp), _ptr(kb),
+                                kb.stride(0), nblk, _ptr(cu), _ptr(lens), Sk, B, d, block_size,
+                                local_blocks, _ptr(z), nblk, _stream())
+    _lib.check(st_, "dash_block_scores")
+    return z
+
+
+def block_max_score(q, k, pos, seg, block_size, num_key_blocks, local_window, mode=1):
+    """Indexer block-max scores (mode 1: triton_block_max_score semantics, mode 0:
+    the torch indexer form).  q [B,C,d], k [B,Sk,d] fp32; pos/seg [B,C]."""
+    _need_gpu(q, k, pos)
+    lib = _lib.load()
+    q = q.float().contiguous()
+    k = k.float().contiguous()
+    B, C, d = q.shape
+    Sk = k.shape[1]
+    pos = _i32(pos)
+    seg = _i32(seg)
+    out = torch.empty(B, C, num_key_blocks, dtype=torch.float32, device=q.device)
+    lw = block_size if local_window is None else max(1, int(local_window))
+    st_ = lib.dash_block_max_score(_ptr(q), q.stride(0), q.stride(1), C, _ptr(pos), _ptr(seg),
+                                   pos.stride(0), _ptr(k), k.stride(0), k.stride(1), Sk, B, d,
+                                   block_size, lw, num_key_blocks, mode, _ptr(out),
+                                   out.stride(0), out.stride(1), _stream())
+    _lib.check(st_, "dash_block_max_score")
+    return out
+
+
+def route(z, cand, idx_scale, floor, sigma, K, topm, row_nblk=None, width=None):
+    """Inference routing of every row of z [..., nblk] fp32.
+    Returns (idx int32 [..., K'], bias fp32, valid bool) with K' = max(1, min(K, M'))."""
+    _need_gpu(z)
+    lib = _lib.load()
+    lead = z.shape[:-1]
+    nblk = z.shape[-1]
+    z2 = z.reshape(-1, nblk).float()
+    if z2.stride(-1) != 1:
+        z2 = z2.contiguous()
+    rows = z2.shape[0]
+    M = max(1, min(int(topm), nblk)) if int(topm) > 0 else nblk
+    Kp = max(1, min(int(K), M)) if width is None else int(width)
+    idx = torch.empty(rows, Kp, dtype=torch.int32, device=z.device)
+    bias = torch.empty(rows, Kp, dtype=torch.float32, device=z.device)
+    valid = torch.empty(rows, Kp, dtype=torch.uint8, device=z.device)
+    c2 = None
+    if cand is not None:
+        c2 = _u8(cand.reshape(-1, nblk))
+    rn = _i32(row_nblk)
+    st_ = lib.dash_route(_ptr(z2), z2.stride(0), rows, nblk, _ptr(rn), _ptr(c2),
+                         0 if c2 is None else c2.stride(0), float(idx_scale), float(floor),
+                         float(sigma), int(K), int(topm), Kp, _ptr(idx), _ptr(bias),
+                         _ptr(valid), _stream())
+    _lib.check(st_, "dash_route")
+    return idx.view(*lead, Kp), bias.view(*lead, Kp), valid.view(*lead, Kp).bool()
+
+
+def attn_prefill(q, k, v, idx, bias, valid, block_size, local_window, scale,
+                 cu_seqlens=None, kmin=None, return_lse=False):
+    """Block-sparse prefill attention.  q/k/v bf16 [B,H,S,D] (any strides with a
+    contiguous head dim) or [1,H,T,D] with cu_seqlens; idx/bias/valid [B,S,K] (or
+    [T,K]).  Returns o [B,H,S,D] bf16 (and lse [B,S,H] fp32)."""
+    _need_gpu(q, k, v)
+    lib = _lib.load()
+    if q.dtype != torch.bfloat16:
+        raise NotImplementedError("dash_attn_prefill computes in bf16")
+    q, k, v = _rows(q), _rows(k.to(q.dtype)), _rows(v.to(q.dtype))
+    B, H, S, D = q.shape
+    if k.shape != q.shape or v.shape != q.shape:
+        raise NotImplementedError("q_len == k_len and equal head counts are required")
+    o = torch.empty(B, H, S, D, dtype=q.dtype, device=q.device)
+    lse = torch.empty(B, S, H, dtype=torch.float32, device=q.device) if return_lse else None
+    K = 0 if idx is None else idx.shape[-1]
+    idx_c = None if idx is None else _i32(idx)
+    bias_c = None if bias is None else bias.float().contiguous()
+    valid_c = _u8(valid)
+    cu = _i32(cu_seqlens)
+    nb = B
+    if cu is not None:
+        if B != 1:
+            raise ValueError("varlen prefill takes q of shape [1, H, T, D]")
+        nb = cu.numel() - 1
+        Smax = int((cu[1:] - cu[:-1]).max().item()) if nb > 0 else 0
+    else:
+        Smax = S
+    km = _i32(kmin)
+    st_ = lib.dash_attn_prefill(
+        _ptr(q), q.stride(0), q.stride(1), q.stride(2),
+        _ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        _ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        _ptr(o), o.stride(0), o.stride(1), o.stride(2),
+        _ptr(lse), H, 1,
+        _ptr(idx_c), _ptr(valid_c), _ptr(bias_c), K, _ptr(cu), _ptr(km),
+        nb, H, Smax, D, int(block_size), int(local_window), float(scale), _stream())
+    _lib.check(st_, "dash_attn_prefill")
+    return (o, lse) if return_lse else o
+
+
+def default_nsplit(B, H, nunits):
+    """Split count so that B*H*nsplit fills the 256 CUs several times over."""
+    want = max(1, (1024 + B * H - 1) // max(1, B * H))
+    return int(max(1, min(want, nunits)))
+
+
+def attn_decode(q, k, v, idx, bias, valid, block_size, local_window, scale, seq_lens=None,
+                q_pos=None, block_table=None, page_size=None, out_dtype=torch.float32,
+                nsplit=None, return_lse=False):
+    """Decode attention for one query per sequence.  q [B,H,D] (or [B,H,1,D]) bf16;
+    k/v contiguous [B,H,S,D] or paged [pages, page_size, H, D] with block_table [B,P];
+    idx/bias/valid [B,K] (or [B,1,K]).  Returns out [B,H,D] (out_dtype)."""
+    _need_gpu(q, k, v)
+    lib = _lib.load()
+    squeeze = q.dim() == 4
+    if squeeze:
+        q = q[:, :, 0]
+    q = _rows(q.to(torch.bfloat16))
+    k = _rows(k.to(torch.bfloat16))
+    v = _rows(v.to(torch.bfloat16))
+    B, H, D = q.shape
+    if block_table is not None:
+        bt = _i32(block_table)
+        S = bt.shape[1] * page_size
+        k_sb, k_sh, k_st, k_sp = 0, k.stride(2), k.stride(1), k.stride(0)
+        v_sb, v_sh, v_st, v_sp = 0, v.stride(2), v.stride(1), v.stride(0)
+        bt_stride = bt.stride(0)
+    else:
+        bt = None
+        S = k.shape[2]
+        k_sb, k_sh, k_st, k_sp = k.stride(0), k.stride(1), k.stride(2), 0
+        v_sb, v_sh, v_st, v_sp = v.stride(0), v.stride(1), v.stride(2), 0
+        bt_stride = 0
+    if idx is not None and idx.dim() == 3:
+        idx, bias = idx[:, 0], bias[:, 0]
+        valid = None if valid is None else valid[:, 0]
+    K = 0 if idx is None else idx.shape[-1]
+    idx_c = None if idx is None else _i32(idx)
+    bias_c = None if bias is None else bias.float().contiguous()
+    valid_c = _u8(valid)
+    if nsplit is None:
+        nunits = (local_window + block_size - 1) // block_size + 1 + K
+        nsplit = default_nsplit(B, H, nunits)
+    ws_bytes = ctypes_int64()
+    _lib.check(lib.dash_attn_decode_workspace_size(B, H, D, nsplit, ws_bytes), "workspace")
+    ws = torch.empty(max(1, ws_bytes.value // 4), dtype=torch.float32, device=q.device)
+    out = torch.empty(B, H, D, dtype=out_dtype, device=q.device)
+    lse = torch.empty(B, H, dtype=torch.float32, device=q.device) if return_lse else None
+    lens = _i32(seq_lens)
+    qp = _i32(q_pos)
+    st_ = lib.dash_attn_decode(
+        _ptr(q), q.stride(0), q.stride(1),
+        _ptr(k), k_sb, k_sh, k_st, k_sp, _ptr(v), v_sb, v_sh, v_st, v_sp,
+        _ptr(bt), bt_stride, int(page_size or 0), _ptr(lens), _ptr(qp),
+        _ptr(idx_c), _ptr(valid_c), _ptr(bias_c), K,
+        _ptr(out), int(out_dtype == torch.bfloat16), out.stride(0), out.stride(1),
+        _ptr(lse), 0 if lse is None else lse.stride(0), 1,
+        B, H, S, D, int(block_size), int(local_window), float(scale), int(nsplit),
+        _ptr(ws), ws.numel() * 4, _stream())
+    _lib.check(st_, "dash_attn_decode")
+    if squeeze:
+        out = out[:, :, None]
+    return (out, lse) if return_lse else out
+
+
+def ctypes_int64():
+    import ctypes
+    return ctypes.c_int64(0)
+
+
+def inv_sqrt(d):
+    return 1.0 / math.sqrt(d)

@@ -1,0 +1,152 @@
+/*
+ * dash_hip.h -- C ABI of the MI355X (gfx950) DASH attention library
+ * (libdash_hip.so).  Plain pointers, sizes and strides; no framework types.
+ *
+ * Conventions shared by every entry point
+ *   - Every pointer argument is a device pointer unless stated otherwise; the
+ *     caller owns every buffer (outputs and workspace included).  The library
+ *     allocates nothing and keeps no state between calls.
+ *   - Strides are in elements, not bytes.  The innermost (feature) axis must be
+ *     contiguous; bf16 tensors need 16-byte aligned rows.
+ *   - `stream` is a hipStream_t; all work is enqueued on it, nothing synchronises.
+ *   - Return value: 0 ok, -2 unsupported shape/parameter (the Python layer raises
+ *     NotImplementedError), -3 invalid argument, -4 workspace too small, >0 a
+ *     hipError_t from the launch.
+ *   - Sequence layouts: contiguous ([B, S, ...] with a batch stride), varlen
+ *     (`cu_seqlens` [B+1] prefix sums over a packed token axis; every sequence has
+ *     its own block grid starting at its first token) or paged (`block_table`
+ *     [B, table_stride] of physical page ids; token t of sequence b lives in page
+ *     block_table[b][t / page_size] at row t % page_size).
+ *
+ * Reference interfaces replaced (paths are in the ANANTA_OCR repository).
+ */
+#ifndef DASH_HIP_H
+#define DASH_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI version of this header (1). */
+int dash_abi_version(void);
+
+/* Human-readable text for a status code. Host pointer, static storage. */
+const char* dash_status_string(int status);
+
+/*
+ * Stage-0 block summaries k_bar[b, c, :] = sum_j softmax_j(k_j.head_cls/sqrt(d)) k_j over
+ * the real tokens of key block c (mean pooling when head_cls == 0).
+ * Replaces the head_cls summary of DashAttention._block_scores_headcls
+ * (dash_attention.py:851-888) and _block_scores_infer (modeling_deepseekv2.py:362-377).
+ *   idx_k      fp32 index keys; token rows addressed by (ik_sb, ik_st) contiguous,
+ *              cu_seqlens (varlen) or block_table/ik_sp/page_size (paged)
+ *   seq_lens   [B] key lengths (contiguous/paged) or NULL for S
+ *   tail_only  1: recompute only the last block of every sequence (decode refresh)
+ *   kbar       [B, nblk_cap, d] fp32, batch stride kb_sb
+ */
+int dash_kbar(const float* idx_k, int64_t ik_sb, int64_t ik_st, int64_t ik_sp,
+              const int32_t* cu_seqlens, const int32_t* seq_lens,
+              const int32_t* block_table, int64_t table_stride, int page_size,
+              const float* head_cls, int B, int S, int d, int block_size, int tail_only,
+              float* kbar, int64_t kb_sb, int nblk_cap, void* stream);
+
+/*
+ * Block scores z[row, c] = clamp(idx_q.k_bar_c/sqrt(d), +-1e4) for remote blocks
+ * (c <= q_pos//block_size - local_blocks, c < nblk of the sequence), -1e9 otherwise.
+ * Replaces the scoring loop of _block_scores_infer (modeling_deepseekv2.py:378-386) /
+ * DashAttention._block_scores_headcls (dash_attention.py:890-904).
+ *   idx_q   fp32 [B, Lq, d] (iq_sb, iq_st) or varlen via cu_q
+ *   q_pos   per query row position (NULL: the row index within the sequence)
+ *   cu_k/lens_k  key lengths per sequence (NULL/NULL: S)
+ *   z       fp32 rows (b*Lq + t, or cu_q[b] + t) with row stride z_stride
+ */
+int dash_block_scores(const float* idx_q, int64_t iq_sb, int64_t iq_st,
+                      const int32_t* cu_q, int Lq, const int32_t* q_pos,
+                      const float* kbar, int64_t kb_sb, int nblk_cap,
+                      const int32_t* cu_k, const int32_t* lens_k, int S, int B,
+                      int d, int block_size, int local_blocks, float* z,
+                      int64_t z_stride, void* stream);
+
+/*
+ * Indexer stage-0 scores: per key block, max over keys seg[t] <= j < max(pos[t]-LW+1,0),
+ * j < Sk of q_t.k_j.  mode 0 = the torch form of modeling_deepseekv2.py:387-400 /
+ * dash_attention.py:815-835 (clamp +-1e4, -1e9 for empty blocks, seg ignored when NULL);
+ * mode 1 = triton_block_max_score (sparse_gather_triton.py:395-467; no clamp, -inf).
+ *   q [B, C, d], k [B, Sk, d] fp32; pos/seg [B, C] int32 with batch stride ps_sb;
+ *   out[b*o_sb + t*o_sc + c], nblk blocks.
+ */
+int dash_block_max_score(const float* q, int64_t q_sb, int64_t q_st, int C,
+                         const int32_t* pos, const int32_t* seg, int64_t ps_sb,
+                         const float* k, int64_t k_sb, int64_t k_st, int Sk, int B,
+                         int d, int block_size, int local_window, int nblk, int mode,
+                         float* out, int64_t o_sb, int64_t o_sc, void* stream);
+
+/*
+ * Inference routing of every score row: candidates (remote, optionally AND cand,
+ * falling back to remote), x = z*idx_scale, top-M by (value desc, block id asc),
+ * 1.5-entmax prior over the M values, first K' = max(1,min(K,M)) slots, bias =
+ * valid ? (log(max(prior,floor)) - mean_valid)/sigma : 0.
+ * Replaces _infer_route_select (modeling_deepseekv2.py:309-333) with entmax15
+ * (dash_attention.py:615-662).  1 <= topm <= 16, nblk_cols <= 2048.
+ *   z         fp32 [rows, z_stride]; row_nblk optional per-row block count
+ *   cand      optional uint8 [rows, cand_stride]
+ *   idx/bias/valid  [rows, Kout]; slots >= K' get idx -1, bias 0, valid 0.
+ *   idx holds the selected block id also where valid == 0 (as topk does).
+ */
+int dash_route(const float* z, int64_t z_stride, int rows, int nblk_cols,
+               const int32_t* row_nblk, const uint8_t* cand, int64_t cand_stride,
+               float idx_scale, float floor_p, float sigma, int K, int topm, int Kout,
+               int32_t* idx, float* bias, uint8_t* valid, void* stream);
+
+/*
+ * Prefill block-sparse attention (q_len == k_len), bf16 in/out, fp32 accumulation:
+ * window keys [max(t-LW+1, kmin[t]), t] with bias 0 and the keys kmin[t] <= j < t-LW+1
+ * of the routed blocks idx[t, :] (skipped where idx < 0 or valid == 0) with bias[t, slot].
+ * Replaces triton_gather_attention_e2e / _e2e_attn_fwd_kernel
+ * (sparse_gather_e2e_triton.py:34-115, :342-391) and, with bias = 0 and kmin = the
+ * packing segment start, triton_gather_attention (sparse_gather_triton.py:29-104,
+ * :343-392).  q/k/v/o [B, H, S, D] by strides (or varlen via cu_seqlens);
+ * lse (optional) fp32 at lse[token_row*lse_row + h*lse_sh].  D == 128,
+ * block_size in {32, 64, ..., 256}, K <= 16.
+ */
+int dash_attn_prefill(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                      const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                      const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                      void* o, int64_t o_sb, int64_t o_sh, int64_t o_st,
+                      float* lse, int64_t lse_row, int64_t lse_sh,
+                      const int32_t* idx, const uint8_t* valid, const float* bias, int K,
+                      const int32_t* cu_seqlens, const int32_t* kmin,
+                      int B, int H, int S, int D, int block_size, int local_window,
+                      float scale, void* stream);
+
+/* Workspace bytes dash_attn_decode needs for (B, H, D, nsplit). */
+int dash_attn_decode_workspace_size(int B, int H, int D, int nsplit, int64_t* bytes);
+
+/*
+ * Decode attention, one query per sequence at q_pos[b] (default seq_lens[b]-1):
+ * window (q-LW, q] plus the keys < q-LW+1 of the routed blocks idx[b, :] with their bias.
+ * Replaces _decode_attend (modeling_deepseekv2.py:424-451) as called by
+ * _dash_decode_forward (:454-500).  Cache: contiguous [B, H, S, D] (k_sb, k_sh, k_st) or
+ * paged [pages, page_size, H, D] (k_sp, k_st, k_sh + block_table).  Split-K over nsplit
+ * work-groups per (b, h) then a log-sum-exp merge.  out [B, H, D] fp32 (out_bf16 = 0)
+ * or bf16, lse optional.  D == 128, block_size 32 or a multiple of 64, K <= 16.
+ */
+int dash_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
+                     const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t k_sp,
+                     const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t v_sp,
+                     const int32_t* block_table, int64_t table_stride, int page_size,
+                     const int32_t* seq_lens, const int32_t* q_pos,
+                     const int32_t* idx, const uint8_t* valid, const float* bias, int K,
+                     void* out, int out_bf16, int64_t o_sb, int64_t o_sh,
+                     float* lse, int64_t lse_sb, int64_t lse_sh,
+                     int B, int H, int S, int D, int block_size, int local_window,
+                     float scale, int nsplit, void* workspace, int64_t workspace_bytes,
+                     void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DASH_HIP_H */

@@ -1,0 +1,396 @@
+"""CPU oracle for the DASH attention hot path.  TEST INFRASTRUCTURE ONLY.
+
+This module is the checker, never the product: only ``tests/``, the entry
+point's ``smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may import it.
+The shipped package (``ananta_ocr_amd``) never imports it and has no CPU path.
+
+It restates, op for op in fp32 on the CPU, the reference's PyTorch algorithm
+for the path (citations are ``file:line`` in the reference repository):
+
+* stage-0 block summaries ``k_bar`` (head_cls softmax pooling; mean pooling when
+  ``head_cls == 0``)          -- dash_attention.py:851-888, modeling_deepseekv2.py:362-377
+* head_cls block scores       -- dash_attention.py:890-904, modeling_deepseekv2.py:378-386
+* indexer (block-max) scores  -- modeling_deepseekv2.py:387-400, dash_attention.py:815-835
+* fused block-max scorer      -- sparse_gather_triton.py:395-467 (``-inf`` sentinel, seg)
+* 1.5-entmax                  -- dash_attention.py:615-662
+* inference routing           -- modeling_deepseekv2.py:309-333
+* training routing            -- dash_attention.py:906-960
+* prefill attention           -- dash_attention.py:980-1006 (mask algebra + SDPA), with the
+                                 fused-kernel set semantics of sparse_gather_e2e_triton.py:34-115
+                                 and the segment start of sparse_gather_triton.py:42,63,73
+* decode attention            -- modeling_deepseekv2.py:424-451
+* packed varlen (cu_seqlens)  -- block-diagonal: each document is run on its own
+                                 block grid (the per-request semantics of the serving path)
+
+Deliberate, documented deviation: ``torch.topk`` leaves the order of tied values
+unspecified (the CPU kernel returns ties in an arbitrary order).  The oracle
+selects with a *stable* descending sort, so ties go to the lower block id.  Tests
+compare the oracle with ``torch.topk`` as sets wherever ties straddle the cut.
+
+Parity pinning (what each function is checked against, in tests/):
+  kbar/scores      -> brute-force float64 loops, closed form (mean pooling)
+  entmax15         -> closed forms, invariants, independent float64 bisection
+  route            -> brute-force stable ranking, torch.topk as sets
+  dense_attend     -> brute-force float64 enumeration of the explicit key sets,
+                      sliding-window / causal SDPA special cases
+  decode_attend    -> the same enumeration at one query; equality with prefill rows
+"""
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+SCORE_NEG = -1.0e9     # dash_attention.py:602
+MASK_NEG = -1.0e9      # dash_attention.py:601
+ACT_CLAMP = 1.0e4      # dash_attention.py:604
+ENTMAX_NEG = -1.0e4    # modeling_deepseekv2.py:56
+
+
+# ----------------------------------------------------------------------------
+# stage 0: block summaries and block scores
+# ----------------------------------------------------------------------------
+
+def kbar_headcls(idx_k, head_cls, block_size):
+    """k_bar [B,nblk,d] fp32 and chunk_valid [B,nblk] bool.
+
+    Follows modeling_deepseekv2.py:362-377 (== dash_attention.py:851-888):
+    zero-pad the key axis to nblk*bs, per-token logit ``k_j.head_cls/sqrt(d)``
+    clamped to +-1e4, masked softmax over each block's real tokens (max over
+    valid tokens, denominator >= 1e-6), weighted sum, NaN/inf -> 0.
+    """
+    idx_k = idx_k.float()
+    B, S, d = idx_k.shape
+    bs = int(block_size)
+    nblk = (S + bs - 1) // bs
+    Sp = nblk * bs
+    inv_sqrt_d = 1.0 / math.sqrt(d)
+    if Sp > S:
+        kk = F.pad(idx_k, (0, 0, 0, Sp - S))
+        real = F.pad(idx_k.new_ones(B, S, dtype=torch.bool), (0, Sp - S), value=False)
+    else:
+        kk = idx_k[:, :Sp]
+        real = idx_k.new_ones(B, Sp, dtype=torch.bool)
+    kk = kk.view(B, nblk, bs, d)
+    vmask = real.view(B, nblk, bs)
+    hc = head_cls.float().view(1, 1, 1, d)
+    aw = ((kk * hc).sum(-1) * inv_sqrt_d).clamp(-ACT_CLAMP, ACT_CLAMP)
+    neg = torch.finfo(aw.dtype).min
+    row_max = torch.where(vmask, aw, aw.new_full((), neg)).amax(dim=-1, keepdim=True)
+    row_max = torch.where(vmask.any(dim=-1, keepdim=True), row_max, torch.zeros_like(row_max))
+    e = torch.exp(aw - row_max) * vmask.to(aw.dtype)
+    w = e / e.sum(dim=-1, keepdim=True).clamp_min(1e-6)
+    k_bar = torch.nan_to_num((w.unsqueeze(-1) * kk).sum(dim=2), nan=0.0, posinf=0.0, neginf=0.0)
+    chunk_valid = vmask.any(dim=-1)
+    return k_bar, chunk_valid
+
+
+def block_scores_headcls(idx_q, k_bar, chunk_valid, q_pos, block_size, local_blocks,
+                         q_chunk=2048):
+    """z [B,Lq,nblk] fp32: ``clamp(q.k_bar/sqrt(d), +-1e4)`` where the block is a
+    causal remote block (``c <= q_pos//bs - local_blocks``) with a real token,
+    else ``SCORE_NEG``.  modeling_deepseekv2.py:378-386."""
+    idx_q = idx_q.float()
+    B, Lq, d = idx_q.shape
+    nblk = k_bar.shape[1]
+    inv_sqrt_d = 1.0 / math.sqrt(d)
+    blk_ids = torch.arange(nblk)
+    out = []
+    for c0 in range(0, Lq, q_chunk):
+        c1 = min(c0 + q_chunk, Lq)
+        z = torch.matmul(idx_q[:, c0:c1], k_bar.transpose(-1, -2)) * inv_sqrt_d
+        z = z.clamp(-ACT_CLAMP, ACT_CLAMP)
+        qblk = q_pos[:, c0:c1].long() // block_size
+        keep = (blk_ids[None, None, :] <= (qblk[:, :, None] - local_blocks)) \
+            & chunk_valid[:, None, :]
+        out.append(z.masked_fill(~keep, SCORE_NEG))
+    return torch.cat(out, dim=1)
+
+
+def block_scores_indexer(idx_q, idx_k, q_pos, nblk, block_size, local_window, q_chunk=2048):
+    """Indexer stage-0: ``max_j clamp(q.k_j, +-1e4)`` over keys with
+    ``j <= pos - local_window`` (causal, outside the window); SCORE_NEG where a
+    block has no such key.  modeling_deepseekv2.py:387-400."""
+    idx_q = idx_q.float()
+    idx_k = idx_k.float()
+    B, S, d = idx_k.shape
+    Sp = nblk * block_size
+    kpos = torch.arange(S)
+    out = []
+    for c0 in range(0, idx_q.shape[1], q_chunk):
+        c1 = min(c0 + q_chunk, idx_q.shape[1])
+        sc = torch.matmul(idx_q[:, c0:c1], idx_k.transpose(-1, -2)).clamp(-ACT_CLAMP, ACT_CLAMP)
+        pos = q_pos[:, c0:c1].long()
+        future = kpos[None, None, :] > pos[:, :, None]
+        local = (kpos[None, None, :] > (pos[:, :, None] - local_window)) & ~future
+        sc = sc.masked_fill(future | local, SCORE_NEG)
+        if Sp > S:
+            sc = F.pad(sc, (0, Sp - S), value=SCORE_NEG)
+        out.append(sc.view(B, c1 - c0, nblk, block_size).amax(dim=-1))
+    return torch.cat(out, dim=1)
+
+
+def block_max_score(q, k, pos, seg, block_size, num_key_blocks, local_window):
+    """Fused block-max scorer semantics: ``max_j q.k_j`` over keys
+    ``seg <= j < max(pos - LW + 1, 0)``, ``j < Sk``; ``-inf`` where the block has
+    no such key; no clamp.  sparse_gather_triton.py:395-428 (kernel), :431-467."""
+    q = q.float()
+    k = k.float()
+    B, C, D = q.shape
+    Sk = k.shape[1]
+    bs = int(block_size)
+    lw = bs if local_window is None else max(1, int(local_window))
+    s = torch.matmul(q, k.transpose(-1, -2))
+    j = torch.arange(Sk)
+    ls = (pos.long() - (lw - 1)).clamp(min=0)
+    ok = (j[None, None, :] < ls[:, :, None]) & (j[None, None, :] >= seg.long()[:, :, None])
+    s = s.masked_fill(~ok, float("-inf"))
+    Sp = num_key_blocks * bs
+    if Sp > Sk:
+        s = F.pad(s, (0, Sp - Sk), value=float("-inf"))
+    else:
+        s = s[..., :Sp]
+    return s.view(B, C, num_key_blocks, bs).amax(dim=-1)
+
+
+# ----------------------------------------------------------------------------
+# 1.5-entmax and routing
+# ----------------------------------------------------------------------------
+
+def _entmax_threshold_and_support(X, dim=-1):
+    """Sort-based threshold (dash_attention.py:623-635)."""
+    Xsrt, _ = torch.sort(X, descending=True, dim=dim)
+    d = X.size(dim)
+    rho = torch.arange(1, d + 1, dtype=X.dtype)
+    view = [1] * X.dim()
+    view[0] = -1
+    rho = rho.view(view).transpose(0, dim)
+    mean = Xsrt.cumsum(dim) / rho
+    mean_sq = (Xsrt ** 2).cumsum(dim) / rho
+    ss = rho * (mean_sq - mean ** 2)
+    delta = (1 - ss) / rho
+    delta_nz = torch.clamp(delta, 0)
+    tau = mean - torch.sqrt(delta_nz)
+    support_size = (tau <= Xsrt).sum(dim).unsqueeze(dim)
+    support_size = support_size.clamp(min=1)
+    tau_star = tau.gather(dim, support_size - 1)
+    return tau_star, support_size
+
+
+def entmax15(X, dim=-1):
+    """1.5-entmax forward (dash_attention.py:638-662): ``X=(X-max)/2``,
+    ``p = clamp(X - tau*, 0)^2``."""
+    max_val, _ = X.max(dim=dim, keepdim=True)
+    X = X - max_val
+    X = X / 2
+    tau_star, _ = _entmax_threshold_and_support(X, dim)
+    return torch.clamp(X - tau_star, min=0) ** 2
+
+
+def stable_topk(x, k):
+    """Top-k along the last axis ordered by (value desc, index asc).
+
+    Stands in for ``torch.topk`` (whose tie order is unspecified) in
+    modeling_deepseekv2.py:322."""
+    vals, idx = torch.sort(x, dim=-1, descending=True, stable=True)
+    return vals[..., :k], idx[..., :k]
+
+
+def route_inputs(block_scores, block_cand, idx_scale):
+    """``(x, cand)`` exactly as modeling_deepseekv2.py:316-320 builds them."""
+    remote = block_scores > (SCORE_NEG * 0.5)
+    cand = remote if block_cand is None else (remote & block_cand)
+    cand = torch.where(~cand.any(dim=-1, keepdim=True), remote, cand)
+    x = torch.where(cand, block_scores * idx_scale, block_scores.new_full((), ENTMAX_NEG))
+    x = torch.nan_to_num(x, nan=ENTMAX_NEG, posinf=ENTMAX_NEG, neginf=ENTMAX_NEG)
+    return x, cand
+
+
+def infer_route_select(block_scores, block_cand, idx_scale, floor, sigma, K, topm):
+    """Inference routing, modeling_deepseekv2.py:309-333.
+
+    Returns ``(topi [.., K'] int64, bias [.., K'] fp32, valid [.., K'] bool)``
+    with ``K' = max(1, min(K, M'))`` and ``M' = max(1, min(topm, nblk))``
+    (``nblk`` when ``topm <= 0``).
+    """
+    block_scores = block_scores.float()
+    x, cand = route_inputs(block_scores, block_cand, idx_scale)
+    nblk = x.shape[-1]
+    M = max(1, min(int(topm), nblk)) if int(topm) > 0 else nblk
+    xv, xi = stable_topk(x, M)
+    prior = entmax15(xv, dim=-1)
+    is_cand = cand.gather(-1, xi)
+    Kp = max(1, min(int(K), M))
+    xi, prior, valid = xi[..., :Kp], prior[..., :Kp], is_cand[..., :Kp]
+    logp = torch.log(prior.clamp_min(floor))
+    cnt = valid.sum(dim=-1, keepdim=True).clamp(min=1)
+    mu = torch.where(valid, logp, torch.zeros_like(logp)).sum(dim=-1, keepdim=True) / cnt
+    bias = torch.where(valid, (logp - mu) * (1.0 / sigma), torch.zeros_like(logp))
+    return xi, bias.float(), valid
+
+
+def train_route_select(block_scores, block_cand, idx_scale, floor, sigma, K):
+    """Training-mode routing: full-width entmax prior (dash_attention.py:906-930)
+    then top-K of the masked prior with the centred log-prior bias
+    (dash_attention.py:932-960).  Ties in the prior are broken by lower block id."""
+    block_scores = block_scores.float()
+    x, cand = route_inputs(block_scores, block_cand, idx_scale)
+    prior = entmax15(x, dim=-1)
+    nblk = x.shape[-1]
+    Kp = max(1, min(int(K), nblk))
+    sel_prior = prior.masked_fill(~cand, -1.0)
+    topv, topi = stable_topk(sel_prior, Kp)
+    valid = topv >= 0.0
+    logp = torch.log(topv.clamp_min(floor))
+    cnt = valid.sum(dim=-1, keepdim=True).clamp(min=1)
+    mu = torch.where(valid, logp, torch.zeros_like(logp)).sum(dim=-1, keepdim=True) / cnt
+    bias = (logp - mu) * (1.0 / sigma)
+    bias = torch.where(valid, bias, torch.zeros_like(bias)).clamp(-ACT_CLAMP, ACT_CLAMP)
+    return topi, bias, valid
+
+
+# ----------------------------------------------------------------------------
+# attention
+# ----------------------------------------------------------------------------
+
+def dense_block_bias(topi, bias, valid, nblk):
+    """[..., nblk] fp32 per-block bias, ``MASK_NEG`` for unrouted blocks.
+
+    Slots with ``valid == False`` or a negative index are dropped; a duplicated
+    block keeps its first slot (the dedup of sparse_gather_e2e_triton.py:374-384,
+    made deterministic).  For the distinct in-range indices routing produces,
+    this equals the scatter of dash_attention.py:984-986."""
+    topi = topi.long()
+    keep = valid & (topi >= 0) & (topi < nblk)
+    K = topi.shape[-1]
+    if K > 1:
+        same = topi[..., :, None] == topi[..., None, :]
+        earlier = torch.tril(torch.ones(K, K, dtype=torch.bool), diagonal=-1)
+        dup = (same & keep[..., None, :] & earlier).any(-1)
+        keep = keep & ~dup
+    idx = torch.where(keep, topi, torch.full_like(topi, nblk))
+    src = torch.where(keep, bias.float(), torch.full_like(bias.float(), MASK_NEG))
+    out = torch.full(topi.shape[:-1] + (nblk + 1,), MASK_NEG, dtype=torch.float32)
+    out = out.scatter(-1, idx, src)
+    return out[..., :nblk]
+
+
+def dense_attend(q, k, v, topi, bias, valid, block_size, local_window, scale,
+                 q_chunk=2048, kmin=None):
+    """Prefill DASH attention, fp32: dash_attention.py:980-1006.
+
+    Key j is kept for query t when it is causal and either in the token-level
+    window ``(t - LW, t]`` (bias 0) or in a routed block (bias of that block);
+    the window wins on overlap.  ``kmin`` [B,S] (optional) adds ``j >= kmin[t]``
+    (the packing segment start of sparse_gather_triton.py:42,63,73).
+    q, k, v: [B,H,S,D]; topi/bias/valid: [B,S,K].  Returns [B,H,S,D] fp32.
+    """
+    q = q.float(); k = k.float(); v = v.float()
+    B, H, S, D = q.shape
+    nblk = (S + block_size - 1) // block_size
+    kidx = torch.arange(S)
+    key_block = kidx // block_size
+    logp = dense_block_bias(topi, bias, valid, nblk)
+    out_chunks = []
+    for qs in range(0, S, q_chunk):
+        qe = min(qs + q_chunk, S)
+        qidx = torch.arange(qs, qe)
+        base = logp[:, qs:qe].index_select(-1, key_block)[:, None]
+        causal = (kidx[None, :] <= qidx[:, None])[None, None]
+        local = ((kidx[None, :] <= qidx[:, None]) &
+                 (kidx[None, :] > (qidx[:, None] - local_window)))[None, None]
+        sel = base > (MASK_NEG * 0.5)
+        keep = causal & (local | sel)
+        if kmin is not None:
+            keep = keep & (kidx[None, None, None, :] >= kmin[:, None, qs:qe, None].long())
+        mask = torch.where(local, torch.zeros_like(base), base)
+        mask = mask.masked_fill(~keep, MASK_NEG)
+        mask = mask.clamp_min(MASK_NEG)
+        out_chunks.append(F.scaled_dot_product_attention(
+            q[:, :, qs:qe], k, v, attn_mask=mask, is_causal=False, scale=scale))
+    return torch.cat(out_chunks, dim=2)
+
+
+def decode_attend(q, k_all, v_all, topi, bias, valid, q_pos, block_size, local_window, scale):
+    """Decode DASH attention, fp32: modeling_deepseekv2.py:424-451.
+
+    q [B,H,Lq,D], k_all/v_all [B,Hkv,S,D], topi/bias/valid [B,Lq,K], q_pos [B,Lq].
+    Returns [B,H,Lq,D] fp32."""
+    B, H, Lq, D = q.shape
+    S = k_all.shape[2]
+    nblk = (S + block_size - 1) // block_size
+    kpos = torch.arange(S)
+    blk = dense_block_bias(topi, bias, valid, nblk)
+    base = blk.index_select(-1, kpos // block_size)
+    qp = q_pos.long()[:, :, None]
+    causal = kpos[None, None, :] <= qp
+    local = causal & (kpos[None, None, :] > (qp - local_window))
+    keep = causal & (local | (base > MASK_NEG * 0.5))
+    m = torch.where(local, torch.zeros_like(base), base).masked_fill(~keep, float("-inf"))
+    kk = k_all.float()
+    vv = v_all.float()
+    if kk.shape[1] != H:
+        rep = H // kk.shape[1]
+        kk = kk.repeat_interleave(rep, dim=1)
+        vv = vv.repeat_interleave(rep, dim=1)
+    s = torch.matmul(q.float(), kk.transpose(-1, -2)) * scale + m[:, None]
+    return torch.matmul(torch.softmax(s, dim=-1), vv)
+
+
+# ----------------------------------------------------------------------------
+# whole-path pipelines (the CPU baseline and the end-to-end checks)
+# ----------------------------------------------------------------------------
+
+def prefill_route(idx_q, idx_k, head_cls, block_size, local_blocks, idx_scale, floor,
+                  sigma, K, topm, q_pos=None, block_cand=None):
+    """Inference prefill routing: k_bar -> scores -> route
+    (modeling_deepseekv2.py:403-416).  Returns (z, topi, bias, valid)."""
+    B, S, d = idx_q.shape
+    if q_pos is None:
+        q_pos = torch.arange(S)[None].expand(B, -1)
+    k_bar, cv = kbar_headcls(idx_k, head_cls, block_size)
+    z = block_scores_headcls(idx_q, k_bar, cv, q_pos, block_size, local_blocks)
+    topi, bias, valid = infer_route_select(z, block_cand, idx_scale, floor, sigma, K, topm)
+    return z, topi, bias, valid
+
+
+def prefill_pipeline(q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks, idx_scale,
+                     floor, sigma, K, topm, scale):
+    """Full inference prefill (route + dense attend), fp32.  Returns (out, topi, bias, valid)."""
+    _, topi, bias, valid = prefill_route(idx_q, idx_k, head_cls, block_size, local_blocks,
+                                         idx_scale, floor, sigma, K, topm)
+    out = dense_attend(q, k, v, topi, bias, valid, block_size, local_blocks * block_size, scale)
+    return out, topi, bias, valid
+
+
+def prefill_varlen(q, k, v, idx_q, idx_k, cu_seqlens, head_cls, block_size, local_blocks,
+                   idx_scale, floor, sigma, K, topm, scale):
+    """Packed varlen prefill with block-diagonal semantics: every document is an
+    independent DASH prefill on its own block grid.  q/k/v [1,H,T,D];
+    idx_q/idx_k [1,T,d]; cu_seqlens [ndoc+1].  Returns (out [1,H,T,D], topi list,
+    bias list, valid list)."""
+    outs, tis, bis, vas = [], [], [], []
+    cu = [int(c) for c in cu_seqlens]
+    for d0, d1 in zip(cu[:-1], cu[1:]):
+        o, ti, bi, va = prefill_pipeline(q[:, :, d0:d1], k[:, :, d0:d1], v[:, :, d0:d1],
+                                         idx_q[:, d0:d1], idx_k[:, d0:d1], head_cls,
+                                         block_size, local_blocks, idx_scale, floor, sigma,
+                                         K, topm, scale)
+        outs.append(o); tis.append(ti); bis.append(bi); vas.append(va)
+    return torch.cat(outs, dim=2), tis, bis, vas
+
+
+def decode_pipeline(q, k_all, v_all, idx_q, idx_k, head_cls, block_size, local_blocks,
+                    idx_scale, floor, sigma, K, topm, scale, q_pos=None):
+    """One inference decode step for queries at ``q_pos`` (default: the last
+    cached token) -- modeling_deepseekv2.py:481-498.  q [B,H,1,D], idx_q [B,1,d],
+    idx_k [B,S,d].  Returns (out [B,H,1,D], topi, bias, valid)."""
+    B, S, d = idx_k.shape
+    if q_pos is None:
+        q_pos = torch.full((B, 1), S - 1, dtype=torch.long)
+    k_bar, cv = kbar_headcls(idx_k, head_cls, block_size)
+    z = block_scores_headcls(idx_q, k_bar, cv, q_pos, block_size, local_blocks)
+    topi, bias, valid = infer_route_select(z, None, idx_scale, floor, sigma, K, topm)
+    out = decode_attend(q, k_all, v_all, topi, bias, valid, q_pos, block_size,
+                        local_blocks * block_size, scale)
+    return out, topi, bias, valid

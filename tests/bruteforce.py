@@ -1,0 +1,114 @@
+"""Independent float64 brute-force formulations used to pin the oracle.
+
+These are written from the mathematical definition of each quantity (explicit
+key-set enumeration, bisection for the entmax threshold, plain ranking), not by
+retyping the oracle's tensor algebra, so a dropped term, a wrong sign or an
+off-by-one in the oracle fails a comparison against them.
+"""
+
+import math
+
+import numpy as np
+
+
+def entmax15_bisect(x, iters=200):
+    """1.5-entmax by bisection on tau: p_i = max(x_i/2 - tau, 0)^2 with sum 1
+    (Peters, Niculae & Martins 2019, eq. for alpha = 1.5).  float64."""
+    x = np.asarray(x, dtype=np.float64)
+    X = (x - x.max()) / 2.0
+    lo, hi = X.max() - 1.0, X.max()          # f(lo) >= 1, f(hi) = 0
+    for _ in range(iters):
+        mid = 0.5 * (lo + hi)
+        f = np.sum(np.maximum(X - mid, 0.0) ** 2)
+        if f >= 1.0:
+            lo = mid
+        else:
+            hi = mid
+    tau = 0.5 * (lo + hi)
+    return np.maximum(X - tau, 0.0) ** 2
+
+
+def rank_desc(values):
+    """Indices ordered by (value desc, index asc), by plain Python sorting."""
+    return sorted(range(len(values)), key=lambda i: (-values[i], i))
+
+
+def route_row(z_row, cand_row, idx_scale, floor, sigma, K, topm):
+    """Inference routing of one query row from the definition.
+    z_row: float32 numpy [nblk]; cand_row: bool numpy [nblk] or None.
+    Returns (idx list, valid list, bias list [float64])."""
+    nblk = len(z_row)
+    remote = [float(z) > -5.0e8 for z in z_row]
+    cand = list(remote) if cand_row is None else [r and bool(c) for r, c in zip(remote, cand_row)]
+    if not any(cand):
+        cand = list(remote)
+    x = []
+    for i in range(nblk):
+        if cand[i]:
+            v = np.float32(z_row[i]) * np.float32(idx_scale)
+            if not np.isfinite(v):
+                v = np.float32(-1.0e4)
+        else:
+            v = np.float32(-1.0e4)
+        x.append(float(v))
+    M = max(1, min(topm, nblk)) if topm > 0 else nblk
+    order = rank_desc(x)[:M]
+    prior = entmax15_bisect([x[i] for i in order])
+    Kp = max(1, min(K, M))
+    idx = order[:Kp]
+    valid = [cand[i] for i in idx]
+    logp = [math.log(max(p, floor)) for p in prior[:Kp]]
+    cnt = max(1, sum(valid))
+    mu = sum(lp for lp, va in zip(logp, valid) if va) / cnt
+    bias = [((lp - mu) / sigma) if va else 0.0 for lp, va in zip(logp, valid)]
+    return idx, valid, bias
+
+
+def key_sets(t, S, topi_row, bias_row, valid_row, block_size, local_window, kmin=0):
+    """Explicit key set of query t: dict key -> additive bias.
+
+    Window keys: max(t - LW + 1, kmin) <= j <= t, bias 0.
+    Routed keys: j in a valid routed block, j <= t, kmin <= j < t - LW + 1,
+    bias of the block (first slot wins on a duplicated block)."""
+    ls = t - local_window + 1
+    keys = {}
+    for j in range(max(ls, kmin, 0), t + 1):
+        keys[j] = 0.0
+    seen = set()
+    for c, b, va in zip(topi_row, bias_row, valid_row):
+        c = int(c)
+        if not va or c < 0 or c in seen:
+            continue
+        seen.add(c)
+        for j in range(c * block_size, min((c + 1) * block_size, S)):
+            if j <= t and j < ls and j >= kmin:
+                keys[j] = float(b)
+    return keys
+
+
+def attend_row(qv, K, V, keys, scale):
+    """softmax over an explicit key set, float64.  qv [D], K/V [S,D]."""
+    js = sorted(keys)
+    if not js:
+        return np.zeros(V.shape[1])
+    s = np.array([scale * float(np.dot(qv, K[j])) + keys[j] for j in js])
+    s -= s.max()
+    p = np.exp(s)
+    p /= p.sum()
+    return p @ V[js]
+
+
+def attend_brute(q, k, v, topi, bias, valid, block_size, local_window, scale, rows=None,
+                 kmin=None):
+    """q,k,v float64 numpy [B,H,S,D]; topi/bias/valid [B,S,K].
+    Returns {(b,h,t): out[D]} for the requested rows (default all)."""
+    B, H, S, D = q.shape
+    out = {}
+    for b in range(B):
+        for t in (range(S) if rows is None else rows):
+            km = 0 if kmin is None else int(kmin[b, t])
+            keys = key_sets(t, S, topi[b, t], bias[b, t], valid[b, t], block_size,
+                            local_window, km)
+            for h in range(H):
+                out[(b, h, t)] = attend_row(q[b, h, t], k[b, h], v[b, h], keys, scale)
+    return out

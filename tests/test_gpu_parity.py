@@ -1,0 +1,362 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle on the
+same seeded inputs.  Integer outputs (routed block ids, validity) must be
+bit-exact on identical fp32 scores; floating outputs meet the stated tolerances.
+"""
+
+import math
+
+import pytest
+import torch
+
+from ananta_ocr_amd import ops
+from ananta_ocr_amd import workloads as W
+from oracle import dash_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+# north-star output tolerance (bf16 output, fp32 accumulation)
+ATOL, RTOL = 2e-2, 1e-2
+
+
+def _gen(seed):
+    return torch.Generator("cpu").manual_seed(seed)
+
+
+def _close(out, ref, what, tight=1.5e-2):
+    """north-star allclose plus a scale-aware bound: the max error must also be
+    below `tight` x max|ref| (bf16 rounding of P and of the output)."""
+    out = out.float().cpu()
+    ref = ref.float().cpu()
+    err = (out - ref).abs()
+    assert torch.all(err <= ATOL + RTOL * ref.abs()), f"{what}: max err {err.max().item()}"
+    scale = ref.abs().max().item()
+    assert err.max().item() <= tight * scale + 1e-6, \
+        f"{what}: max err {err.max().item():.3e} vs scale {scale:.3e}"
+
+
+# ------------------------------------------------------------------ stage 0
+
+@pytest.mark.parametrize("S,d,bs,hc", [(2730, 128, 64, 0.0), (1000, 128, 32, 0.7), (77, 64, 64, 2.0)])
+def test_kbar_matches_oracle(S, d, bs, hc):
+    g = _gen(100 + S)
+    ik = torch.randn(2, S, d, generator=g) * 0.1
+    head_cls = torch.randn(d, generator=g) * hc
+    kb_ref, _ = O.kbar_headcls(ik, head_cls, bs)
+    kb = ops.kbar(ik.to(DEV), head_cls.to(DEV), bs)
+    torch.testing.assert_close(kb.cpu(), kb_ref, atol=1e-6, rtol=1e-5)
+
+
+def test_kbar_varlen_and_tail_refresh():
+    g = _gen(101)
+    cu = [0, 300, 301, 301 + 640]
+    ik = torch.randn(1, cu[-1], 128, generator=g)
+    hc = torch.randn(128, generator=g)
+    kb = ops.kbar(ik.to(DEV), hc.to(DEV), 64, cu_seqlens=torch.tensor(cu).to(DEV))
+    for b in range(3):
+        ref, _ = O.kbar_headcls(ik[:, cu[b]:cu[b + 1]], hc, 64)
+        torch.testing.assert_close(kb[b, :ref.shape[1]].cpu(), ref[0], atol=1e-5, rtol=1e-5)
+    # tail refresh on a contiguous cache with per-sequence lengths
+    ik2 = torch.randn(3, 500, 128, generator=g)
+    lens = torch.tensor([500, 130, 64], dtype=torch.int32)
+    kb2 = torch.zeros(3, 8, 128, device=DEV)
+    ops.kbar(ik2.to(DEV), hc.to(DEV), 64, seq_lens=lens.to(DEV), nblk_cap=8, tail_only=True,
+             out=kb2)
+    for b in range(3):
+        L = int(lens[b])
+        ref, _ = O.kbar_headcls(ik2[b:b + 1, :L], hc, 64)
+        c = (L - 1) // 64
+        torch.testing.assert_close(kb2[b, c].cpu(), ref[0, c], atol=1e-5, rtol=1e-5)
+        assert kb2[b, :c].abs().sum().item() == 0  # only the tail block was written
+
+
+@pytest.mark.parametrize("S,bs,lb", [(2730, 64, 8), (1000, 32, 4), (5000, 64, 16)])
+def test_block_scores_match_oracle(S, bs, lb):
+    g = _gen(102 + S)
+    q = torch.randn(1, 10, S, 128, generator=g) * 128 ** -0.5
+    k = torch.randn(1, 10, S, 128, generator=g) * 128 ** -0.5
+    iq, ik = W.router_inputs(q.bfloat16(), k.bfloat16())
+    kb_ref, cv = O.kbar_headcls(ik, torch.zeros(128), bs)
+    z_ref = O.block_scores_headcls(iq, kb_ref, cv, torch.arange(S)[None], bs, lb)
+    kb = ops.kbar(ik.to(DEV), torch.zeros(128, device=DEV), bs)
+    z = ops.block_scores(iq.to(DEV), kb, bs, lb).cpu()
+    sent = z_ref == O.SCORE_NEG
+    assert torch.equal(z == O.SCORE_NEG, sent)
+    torch.testing.assert_close(z[~sent], z_ref[~sent], atol=1e-7, rtol=1e-5)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_block_max_score_matches_oracle(mode):
+    g = _gen(103)
+    B, C, Sk, d, bs, lw = 2, 300, 300, 128, 64, 100
+    q = torch.randn(B, C, d, generator=g)
+    k = torch.randn(B, Sk, d, generator=g)
+    pos = torch.arange(C)[None].expand(B, -1).contiguous()
+    seg = torch.zeros(B, C, dtype=torch.long)
+    seg[1, 150:] = 150
+    nblk = (Sk + bs - 1) // bs
+    out = ops.block_max_score(q.to(DEV), k.to(DEV), pos.to(DEV), seg.to(DEV), bs, nblk, lw,
+                              mode=mode).cpu()
+    if mode == 1:
+        ref = O.block_max_score(q, k, pos, seg, bs, nblk, lw)
+    else:
+        ref = O.block_scores_indexer(q[:1], k[:1], pos[:1], nblk, bs, lw)
+        out = out[:1]
+    fin = torch.isfinite(ref) & (ref > -5e8)
+    assert torch.equal(fin, torch.isfinite(out) & (out > -5e8))
+    torch.testing.assert_close(out[fin], ref[fin], atol=2e-5, rtol=1e-5)
+    assert torch.equal(out[~fin], ref[~fin])
+
+
+# ------------------------------------------------------------------ routing
+
+def _route_check(z, cand, idx_scale, K, topm):
+    ti_r, bi_r, va_r = O.infer_route_select(z, cand, idx_scale, W.FLOOR, W.SIGMA, K, topm)
+    ti, bi, va = ops.route(z.to(DEV), None if cand is None else cand.to(DEV), idx_scale,
+                           W.FLOOR, W.SIGMA, K, topm)
+    ti, bi, va = ti.cpu().long(), bi.cpu(), va.cpu()
+    assert ti.shape == ti_r.shape
+    assert torch.equal(va, va_r), "valid mismatch"
+    mism = (ti != ti_r).nonzero()
+    assert mism.numel() == 0, f"routed ids differ at {mism[:5].tolist()}"
+    torch.testing.assert_close(bi, bi_r, atol=2e-5, rtol=1e-5)
+
+
+def _scores(S, nblk, bs, lb, seed, scale, quant=None, nan_frac=0.0):
+    g = _gen(seed)
+    z = torch.randn(1, S, nblk, generator=g) * scale
+    if quant:
+        z = torch.round(z * quant) / quant           # many exact ties
+    t = torch.arange(S)[None, :, None]
+    keep = torch.arange(nblk)[None, None, :] <= (t // bs - lb)
+    if nan_frac:
+        z = z.masked_fill((torch.rand(z.shape, generator=g) < nan_frac) & keep, float("nan"))
+    return z.masked_fill(~keep, O.SCORE_NEG)
+
+
+@pytest.mark.parametrize("nblk,scale,K,topm", [
+    (43, 1e-4, 8, 8),          # prefill at 2,730 tokens: full support
+    (427, 1e-3, 16, 16),       # 27,300 tokens
+    (427, 0.5, 16, 16),        # partial entmax support
+    (100, 3.0, 5, 12),         # K < M, narrow support
+    (2048, 0.2, 16, 16),       # widest row the kernel takes
+    (7, 1.0, 16, 16),          # M' = nblk < topm
+])
+def test_route_bit_exact_on_identical_scores(nblk, scale, K, topm):
+    bs, lb = 64, 8
+    S = min((nblk + lb + 1) * bs, 6000)
+    z = _scores(S, nblk, bs, lb, 200 + nblk, scale)
+    _route_check(z, None, W.IDX_SCALE, K, topm)
+
+
+def test_route_ties_nans_and_candidates():
+    bs, lb, nblk, S = 16, 2, 150, 2600
+    z = _scores(S, nblk, bs, lb, 210, 1.0, quant=4.0, nan_frac=0.01)
+    g = _gen(211)
+    cand = torch.rand(1, S, nblk, generator=g) < 0.3
+    cand[:, ::5] = False                      # rows that fall back to `remote`
+    _route_check(z, cand, W.IDX_SCALE, 8, 16)
+    _route_check(z, None, 40.0, 16, 16)
+
+
+def test_route_on_gpu_scores_end_to_end():
+    """scores -> route on the GPU, the oracle routing the GPU's own scores."""
+    d = W.make_prefill(W.PREFILL_2730)
+    kb = ops.kbar(d["idx_k"].to(DEV), torch.zeros(128, device=DEV), 64)
+    z = ops.block_scores(d["idx_q"].to(DEV), kb, 64, 8)
+    _route_check(z.cpu(), None, W.IDX_SCALE, 8, 8)
+
+
+# ------------------------------------------------------------------ prefill attention
+
+def _attn_inputs(seed, B, H, S, bs, lw, K, qscale=1.0, dup=False):
+    g = _gen(seed)
+    q = (torch.randn(B, H, S, 128, generator=g) * qscale * 0.3).bfloat16()
+    k = (torch.randn(B, H, S, 128, generator=g) * 0.3).bfloat16()
+    v = torch.randn(B, H, S, 128, generator=g).bfloat16()
+    nblk = (S + bs - 1) // bs
+    lb = (lw + bs - 1) // bs
+    qblk = torch.arange(S)[None, :, None] // bs
+    # random remote blocks (as routing returns), some invalid / -1 slots
+    hi = (qblk - lb).clamp(min=0).float()
+    idx = (torch.rand(B, S, K, generator=g) * (hi + 1)).floor().long()
+    valid = (torch.rand(B, S, K, generator=g) < 0.85) & (qblk - lb >= 0)
+    if dup:
+        idx[..., 1] = idx[..., 0]
+    else:
+        # distinct ids per row like topk
+        for j in range(1, K):
+            same = (idx[..., j:j + 1] == idx[..., :j]).any(-1)
+            valid[..., j] &= ~same
+    idx = torch.where(torch.rand(B, S, K, generator=g) < 0.05, torch.full_like(idx, -1), idx)
+    bias = torch.randn(B, S, K, generator=g) * 2
+    return q, k, v, idx.clamp(max=nblk - 1), bias, valid
+
+
+@pytest.mark.parametrize("B,H,S,bs,lw,K,qs", [
+    (1, 2, 300, 64, 128, 4, 3.0),
+    (2, 3, 700, 64, 512, 8, 1.0),
+    (1, 2, 513, 32, 100, 6, 3.0),     # window not a block multiple, bs 32
+    (1, 1, 1100, 128, 256, 3, 2.0),   # bs 128
+    (1, 2, 64, 64, 512, 4, 1.0),      # window covers everything
+])
+def test_prefill_attention_matches_oracle(B, H, S, bs, lw, K, qs):
+    q, k, v, idx, bias, valid = _attn_inputs(300 + S, B, H, S, bs, lw, K, qscale=qs)
+    scale = 1 / math.sqrt(128)
+    ref = O.dense_attend(q, k, v, idx, bias, valid, bs, lw, scale)
+    out, lse = ops.attn_prefill(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), bias.to(DEV),
+                                valid.to(DEV), bs, lw, scale, return_lse=True)
+    _close(out, ref, "prefill")
+    assert torch.isfinite(lse).all()
+
+
+def test_prefill_duplicates_and_strided_inputs():
+    B, H, S, bs, lw, K = 1, 2, 400, 64, 128, 4
+    q, k, v, idx, bias, valid = _attn_inputs(310, B, H, S, bs, lw, K, qscale=2.0, dup=True)
+    scale = 1 / math.sqrt(128)
+    ref = O.dense_attend(q, k, v, idx, bias, valid, bs, lw, scale)
+    # [B,S,H,D] storage viewed as [B,H,S,D]
+    qs_, ks_, vs_ = (t.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for t in (q, k, v))
+    out = ops.attn_prefill(qs_, ks_, vs_, idx.to(DEV), bias.to(DEV), valid.to(DEV), bs, lw, scale)
+    _close(out, ref, "prefill strided")
+
+
+def test_prefill_segment_start():
+    B, H, S, bs, lw, K = 1, 2, 600, 64, 128, 5
+    q, k, v, idx, bias, valid = _attn_inputs(320, B, H, S, bs, lw, K, qscale=2.0)
+    kmin = torch.zeros(1, S, dtype=torch.long)
+    kmin[0, 250:] = 250
+    scale = 1 / math.sqrt(128)
+    ref = O.dense_attend(q, k, v, idx, bias, valid, bs, lw, scale, kmin=kmin)
+    out = ops.attn_prefill(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), bias.to(DEV),
+                           valid.to(DEV), bs, lw, scale, kmin=kmin.to(DEV))
+    _close(out, ref, "prefill kmin")
+
+
+def test_prefill_varlen_block_diagonal():
+    g = _gen(330)
+    cu = [0, 273, 273 + 819, 273 + 819 + 64, 273 + 819 + 64 + 1000]
+    T, H, bs, lw, K = cu[-1], 2, 64, 256, 4
+    q, k, v, idx, bias, valid = _attn_inputs(331, 1, H, T, bs, lw, K, qscale=2.0)
+    scale = 1 / math.sqrt(128)
+    # per-document routing on each document's own grid
+    for b in range(len(cu) - 1):
+        L = cu[b + 1] - cu[b]
+        t = torch.arange(L)
+        lb = lw // bs
+        hi = (t // bs - lb).clamp(min=0)
+        i2 = (torch.rand(L, K, generator=g) * (hi[:, None] + 1)).floor().long()
+        idx[0, cu[b]:cu[b + 1]] = i2
+        valid[0, cu[b]:cu[b + 1]] &= (t // bs - lb >= 0)[:, None]
+    out = ops.attn_prefill(q.to(DEV), k.to(DEV), v.to(DEV), idx[0].to(DEV), bias[0].to(DEV),
+                           valid[0].to(DEV), bs, lw, scale,
+                           cu_seqlens=torch.tensor(cu, dtype=torch.int32).to(DEV))
+    for b in range(len(cu) - 1):
+        s0, s1 = cu[b], cu[b + 1]
+        ref = O.dense_attend(q[:, :, s0:s1], k[:, :, s0:s1], v[:, :, s0:s1], idx[:, s0:s1],
+                             bias[:, s0:s1], valid[:, s0:s1], bs, lw, scale)
+        _close(out[:, :, s0:s1], ref, f"varlen doc {b}")
+
+
+def test_prefill_pipeline_2730_tokens():
+    """Prefill at 2,730 tokens (10 pages): GPU k_bar -> scores -> route -> attention.
+    Routing is bit-exact against the oracle on the GPU's scores; the attention is
+    compared with the oracle on the same routing."""
+    cfg = W.PREFILL_2730
+    d = W.make_prefill(cfg)
+    kb = ops.kbar(d["idx_k"].to(DEV), torch.zeros(128, device=DEV), cfg.bs)
+    z = ops.block_scores(d["idx_q"].to(DEV), kb, cfg.bs, cfg.lw // cfg.bs)
+    ti, bi, va = ops.route(z, None, W.IDX_SCALE, W.FLOOR, W.SIGMA, cfg.cap, cfg.cap)
+    ti_r, bi_r, va_r = O.infer_route_select(z.cpu(), None, W.IDX_SCALE, W.FLOOR, W.SIGMA,
+                                            cfg.cap, cfg.cap)
+    assert torch.equal(ti.cpu().long(), ti_r) and torch.equal(va.cpu(), va_r)
+    scale = 1 / math.sqrt(128)
+    out = ops.attn_prefill(d["q"].to(DEV), d["k"].to(DEV), d["v"].to(DEV), ti, bi, va,
+                           cfg.bs, cfg.lw, scale)
+    ref = O.dense_attend(d["q"], d["k"], d["v"], ti_r, bi_r, va_r, cfg.bs, cfg.lw, scale)
+    _close(out, ref, "prefill 2730")
+
+
+# ------------------------------------------------------------------ decode attention
+
+def _decode_inputs(seed, B, H, S, bs, lw, K, lens=None):
+    g = _gen(seed)
+    q = (torch.randn(B, H, 128, generator=g) * 0.6).bfloat16()
+    k = (torch.randn(B, H, S, 128, generator=g) * 0.3).bfloat16()
+    v = torch.randn(B, H, S, 128, generator=g).bfloat16()
+    if lens is None:
+        lens = torch.full((B,), S, dtype=torch.int32)
+    idx = torch.zeros(B, K, dtype=torch.long)
+    valid = torch.zeros(B, K, dtype=torch.bool)
+    for b in range(B):
+        L = int(lens[b])
+        hi = (L - 1) // bs - (lw + bs - 1) // bs
+        if hi >= 0:
+            perm = torch.randperm(hi + 1, generator=g)[:K]
+            idx[b, :perm.numel()] = perm
+            valid[b, :perm.numel()] = True
+    bias = torch.randn(B, K, generator=g)
+    return q, k, v, idx, bias, valid, lens
+
+
+def _decode_ref(q, k, v, idx, bias, valid, lens, bs, lw, scale):
+    outs = []
+    for b in range(q.shape[0]):
+        L = int(lens[b])
+        o = O.decode_attend(q[b:b + 1, :, None], k[b:b + 1, :, :L], v[b:b + 1, :, :L],
+                            idx[b:b + 1, None], bias[b:b + 1, None], valid[b:b + 1, None],
+                            torch.tensor([[L - 1]]), bs, lw, scale)
+        outs.append(o[:, :, 0])
+    return torch.cat(outs)
+
+
+@pytest.mark.parametrize("nsplit", [None, 1, 3])
+def test_decode_contiguous_matches_oracle(nsplit):
+    B, H, S, bs, lw, K = 3, 2, 3000, 64, 1024, 16
+    lens = torch.tensor([3000, 1500, 1100], dtype=torch.int32)
+    q, k, v, idx, bias, valid, lens = _decode_inputs(400, B, H, S, bs, lw, K, lens)
+    scale = 1 / math.sqrt(128)
+    ref = _decode_ref(q, k, v, idx, bias, valid, lens, bs, lw, scale)
+    out = ops.attn_decode(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), bias.to(DEV),
+                          valid.to(DEV), bs, lw, scale, seq_lens=lens.to(DEV), nsplit=nsplit)
+    _close(out, ref, "decode")
+
+
+def test_decode_paged_matches_contiguous_oracle():
+    B, H, bs, lw, K = 4, 2, 64, 512, 8
+    lens = torch.tensor([2000, 700, 1300, 65], dtype=torch.int32)
+    S = int(lens.max())
+    q, k, v, idx, bias, valid, lens = _decode_inputs(410, B, H, S, bs, lw, K, lens)
+    g = _gen(411)
+    npg = [(int(L) + bs - 1) // bs for L in lens]
+    perm = torch.randperm(sum(npg), generator=g)
+    table = torch.zeros(B, max(npg), dtype=torch.int32)
+    kp = torch.zeros(sum(npg), bs, H, 128, dtype=torch.bfloat16)
+    vp = torch.zeros_like(kp)
+    o = 0
+    for b in range(B):
+        for p in range(npg[b]):
+            phys = int(perm[o + p])
+            table[b, p] = phys
+            seg = slice(p * bs, min((p + 1) * bs, int(lens[b])))
+            n = seg.stop - seg.start
+            kp[phys, :n] = k[b, :, seg].transpose(0, 1)
+            vp[phys, :n] = v[b, :, seg].transpose(0, 1)
+        o += npg[b]
+    scale = 1 / math.sqrt(128)
+    ref = _decode_ref(q, k, v, idx, bias, valid, lens, bs, lw, scale)
+    out = ops.attn_decode(q.to(DEV), kp.to(DEV), vp.to(DEV), idx.to(DEV), bias.to(DEV),
+                          valid.to(DEV), bs, lw, scale, seq_lens=lens.to(DEV),
+                          block_table=table.to(DEV), page_size=bs)
+    _close(out, ref, "decode paged")
+
+
+def test_decode_equals_prefill_last_row():
+    B, H, S, bs, lw, K = 1, 2, 900, 64, 256, 4
+    q, k, v, idx, bias, valid = _attn_inputs(420, B, H, S, bs, lw, K, qscale=2.0)
+    scale = 1 / math.sqrt(128)
+    pre = ops.attn_prefill(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), bias.to(DEV),
+                           valid.to(DEV), bs, lw, scale).float().cpu()
+    dec = ops.attn_decode(q[:, :, -1].to(DEV), k.to(DEV), v.to(DEV), idx[:, -1].to(DEV),
+                          bias[:, -1].to(DEV), valid[:, -1].to(DEV), bs, lw, scale).cpu()
+    _close(dec, pre[:, :, -1], "decode vs prefill", tight=2e-2)

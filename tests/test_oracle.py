@@ -1,0 +1,328 @@
+"""Pins the CPU oracle (oracle/dash_oracle.py) to independent formulations:
+closed forms, invariants, float64 brute force and bisection.  CPU only."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import bruteforce as bf
+from oracle import dash_oracle as O
+
+
+def _rng(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ---------------------------------------------------------------- entmax15
+
+def test_entmax_two_point_closed_form():
+    # x = [a, 0]: support 1 (p = [1, 0]) iff a >= 2; otherwise tau solves
+    # 2 tau^2 + a tau + a^2/4 - 1 = 0 with X = [0, -a/2].
+    for a in [0.0, 0.3, 1.0, 1.7, 1.999, 2.0, 2.5, 10.0]:
+        p = O.entmax15(torch.tensor([[a, 0.0]], dtype=torch.float64))[0].numpy()
+        if a >= 2.0:
+            exp = np.array([1.0, 0.0])
+        else:
+            tau = (-a - math.sqrt(8.0 - a * a)) / 4.0
+            exp = np.array([tau * tau, (a / 2.0 + tau) ** 2])
+        np.testing.assert_allclose(p, exp, atol=1e-12)
+
+
+def test_entmax_uniform_and_invariants():
+    for n in [1, 2, 5, 16]:
+        p = O.entmax15(torch.full((1, n), 3.25))[0]
+        torch.testing.assert_close(p, torch.full((n,), 1.0 / n), atol=1e-6, rtol=0)
+    x = torch.randn(64, 16, generator=_rng(0)) * 3
+    p = O.entmax15(x)
+    assert (p >= 0).all()
+    torch.testing.assert_close(p.sum(-1), torch.ones(64), atol=1e-5, rtol=0)
+    torch.testing.assert_close(O.entmax15(x + 7.5), p, atol=1e-5, rtol=0)
+    # order-equivariance: permuting the input permutes the output
+    perm = torch.randperm(16, generator=_rng(1))
+    torch.testing.assert_close(O.entmax15(x[:, perm]), p[:, perm], atol=1e-6, rtol=0)
+
+
+@pytest.mark.parametrize("scale", [0.1, 1.0, 4.0, 30.0])
+def test_entmax_matches_bisection(scale):
+    x = torch.randn(200, 16, generator=_rng(2)) * scale
+    p = O.entmax15(x.double()).numpy()
+    for r in range(x.shape[0]):
+        np.testing.assert_allclose(p[r], bf.entmax15_bisect(x[r].double().numpy()), atol=1e-9)
+    # fp32 path stays within fp32 tolerance of the exact threshold
+    p32 = O.entmax15(x).numpy()
+    for r in range(x.shape[0]):
+        np.testing.assert_allclose(p32[r], bf.entmax15_bisect(x[r].double().numpy()), atol=2e-5)
+
+
+def test_entmax_sentinel_entries_get_zero():
+    x = torch.tensor([[0.5, 0.2, -1.0e4, -1.0e4]])
+    p = O.entmax15(x)[0]
+    assert p[2] == 0 and p[3] == 0
+    torch.testing.assert_close(p[:2].sum(), torch.tensor(1.0))
+
+
+# ---------------------------------------------------------------- routing
+
+def test_stable_topk_is_plain_ranking():
+    x = torch.randint(-3, 4, (50, 40), generator=_rng(3)).float()  # many ties
+    v, i = O.stable_topk(x, 12)
+    for r in range(50):
+        exp = bf.rank_desc(x[r].tolist())[:12]
+        assert i[r].tolist() == exp
+
+
+def test_idx_scale_multiply_is_single_fp32_rounding():
+    z = torch.randn(10000, generator=_rng(4)) * 1e-3
+    s = 128.0 / math.sqrt(128.0)
+    a = (z * s).numpy()
+    b = z.numpy() * np.float32(s)
+    assert np.array_equal(a, b)
+
+
+def _route_case(seed, B, S, nblk, scale_z, with_cand, nan_frac=0.0):
+    g = _rng(seed)
+    z = torch.randn(B, S, nblk, generator=g) * scale_z
+    # remote mask pattern like the real scores: block c remote iff c <= t//bs - LB
+    bs, lb = 4, 2
+    t = torch.arange(S)[None, :, None]
+    keep = torch.arange(nblk)[None, None, :] <= (t // bs - lb)
+    z = z.masked_fill(~keep, O.SCORE_NEG)
+    if nan_frac:
+        m = torch.rand(B, S, nblk, generator=g) < nan_frac
+        z = z.masked_fill(m & keep, float("nan"))
+    cand = None
+    if with_cand:
+        cand = torch.rand(B, S, nblk, generator=g) < 0.4
+        cand[:, ::7] = False          # rows that fall back to `remote`
+    return z, cand
+
+
+@pytest.mark.parametrize("with_cand", [False, True])
+@pytest.mark.parametrize("scale_z,K,topm", [(1e-3, 8, 8), (1.0, 4, 16), (0.3, 16, 16), (5.0, 3, 0)])
+def test_infer_route_matches_definition(with_cand, scale_z, K, topm):
+    z, cand = _route_case(11, 2, 60, 15, scale_z, with_cand, nan_frac=0.02)
+    idx_scale, floor, sigma = 128 / math.sqrt(128), 1e-4, 1.0
+    ti, bi, va = O.infer_route_select(z, cand, idx_scale, floor, sigma, K, topm)
+    for b in range(2):
+        for t in range(60):
+            e_idx, e_val, e_bias = bf.route_row(
+                z[b, t].numpy(), None if cand is None else cand[b, t].numpy(),
+                idx_scale, floor, sigma, K, topm)
+            assert ti[b, t].tolist() == e_idx, (b, t)
+            assert va[b, t].tolist() == e_val, (b, t)
+            np.testing.assert_allclose(bi[b, t].numpy(), e_bias, atol=2e-4)
+
+
+def test_infer_route_sets_match_torch_topk_without_ties():
+    z, _ = _route_case(12, 2, 80, 19, 0.5, False)
+    idx_scale = 128 / math.sqrt(128)
+    ti, _, va = O.infer_route_select(z, None, idx_scale, 1e-4, 1.0, 6, 8)
+    x, cand = O.route_inputs(z, None, idx_scale)
+    xv, xi = x.topk(8, dim=-1)
+    for b in range(2):
+        for t in range(80):
+            vals = xv[b, t]
+            cut_tie = (vals[5] == vals[6]).item() or (vals[7] == x[b, t].sort(descending=True)[0][8]).item()
+            if not cut_tie:
+                assert set(ti[b, t].tolist()) == set(xi[b, t, :6].tolist())
+
+
+def test_route_no_remote_rows_are_invalid():
+    z = torch.full((1, 3, 5), O.SCORE_NEG)
+    ti, bi, va = O.infer_route_select(z, None, 2.0, 1e-4, 1.0, 4, 4)
+    assert not va.any()
+    assert (bi == 0).all()
+
+
+def test_train_route_selects_top_prior():
+    z, cand = _route_case(13, 1, 50, 13, 0.5, True)
+    ti, bi, va = O.train_route_select(z, cand, 11.3, 1e-4, 1.0, 5)
+    x, c = O.route_inputs(z, cand, 11.3)
+    prior = O.entmax15(x)
+    for t in range(50):
+        pr = prior[0, t].masked_fill(~c[0, t], -1.0).tolist()
+        assert ti[0, t].tolist() == bf.rank_desc(pr)[:5]
+
+
+# ---------------------------------------------------------------- stage 0
+
+def test_kbar_zero_headcls_is_block_mean():
+    idx_k = torch.randn(2, 37, 8, generator=_rng(5))
+    kb, cv = O.kbar_headcls(idx_k, torch.zeros(8), 8)
+    assert kb.shape == (2, 5, 8) and cv.all()
+    k64 = idx_k.double()
+    for c in range(5):
+        exp = k64[:, c * 8:min((c + 1) * 8, 37)].mean(1)
+        torch.testing.assert_close(kb[:, c].double(), exp, atol=1e-6, rtol=0)
+
+
+def test_kbar_headcls_softmax_pooling():
+    idx_k = torch.randn(1, 21, 6, generator=_rng(6))
+    hc = torch.randn(6, generator=_rng(7)) * 3
+    kb, _ = O.kbar_headcls(idx_k, hc, 4)
+    k = idx_k[0].double().numpy()
+    h = hc.double().numpy()
+    for c in range(6):
+        rows = k[c * 4:min(c * 4 + 4, 21)]
+        aw = rows @ h / math.sqrt(6)
+        w = np.exp(aw - aw.max())
+        w /= w.sum()
+        np.testing.assert_allclose(kb[0, c].numpy(), w @ rows, atol=1e-5)
+
+
+def test_block_scores_headcls_definition():
+    B, S, d, bs, lb = 2, 45, 8, 4, 3
+    iq = torch.randn(B, S, d, generator=_rng(8))
+    ik = torch.randn(B, S, d, generator=_rng(9))
+    kb, cv = O.kbar_headcls(ik, torch.zeros(d), bs)
+    pos = torch.arange(S)[None].expand(B, -1)
+    z = O.block_scores_headcls(iq, kb, cv, pos, bs, lb, q_chunk=7)
+    nblk = kb.shape[1]
+    for b in range(B):
+        for t in range(S):
+            for c in range(nblk):
+                if c <= t // bs - lb:
+                    e = float(np.dot(iq[b, t].double().numpy(), kb[b, c].double().numpy())) / math.sqrt(d)
+                    assert abs(z[b, t, c].item() - e) < 1e-5
+                else:
+                    assert z[b, t, c].item() == O.SCORE_NEG
+
+
+def test_block_scores_indexer_definition():
+    B, S, d, bs, lw = 1, 30, 4, 4, 6
+    iq = torch.randn(B, S, d, generator=_rng(10))
+    ik = torch.randn(B, S, d, generator=_rng(11))
+    nblk = 8
+    pos = torch.arange(S)[None]
+    z = O.block_scores_indexer(iq, ik, pos, nblk, bs, lw, q_chunk=9)
+    for t in range(S):
+        for c in range(nblk):
+            js = [j for j in range(c * bs, min(c * bs + bs, S)) if j <= t - lw]
+            if js:
+                e = max(float(np.dot(iq[0, t].double().numpy(), ik[0, j].double().numpy())) for j in js)
+                assert abs(z[0, t, c].item() - e) < 1e-5
+            else:
+                assert z[0, t, c].item() == O.SCORE_NEG
+
+
+def test_block_max_score_definition():
+    B, C, D, Sk, bs, lw = 1, 20, 4, 24, 4, 5
+    q = torch.randn(B, C, D, generator=_rng(12))
+    k = torch.randn(B, Sk, D, generator=_rng(13))
+    pos = torch.arange(C)[None] + 3
+    seg = torch.tensor([[0] * 10 + [9] * 10])
+    out = O.block_max_score(q, k, pos, seg, bs, 6, lw)
+    for t in range(C):
+        ls = max(int(pos[0, t]) - lw + 1, 0)
+        for c in range(6):
+            js = [j for j in range(c * bs, c * bs + bs) if j < ls and j >= seg[0, t] and j < Sk]
+            if js:
+                e = max(float(np.dot(q[0, t].double().numpy(), k[0, j].double().numpy())) for j in js)
+                assert abs(out[0, t, c].item() - e) < 1e-5
+            else:
+                assert out[0, t, c].item() == float("-inf")
+
+
+# ---------------------------------------------------------------- attention
+
+def _attn_case(seed, B=1, H=2, S=70, D=16, bs=8, lb=2, K=3, qscale=2.0):
+    g = _rng(seed)
+    q = torch.randn(B, H, S, D, generator=g) * qscale
+    k = torch.randn(B, H, S, D, generator=g)
+    v = torch.randn(B, H, S, D, generator=g)
+    nblk = (S + bs - 1) // bs
+    topi = torch.randint(0, nblk, (B, S, K), generator=g)
+    bias = torch.randn(B, S, K, generator=g)
+    valid = torch.rand(B, S, K, generator=g) < 0.8
+    # routed blocks are remote, as the router guarantees; a few -1 slots
+    qblk = torch.arange(S)[None, :, None] // bs
+    valid &= topi <= qblk - lb
+    topi = torch.where(torch.rand(B, S, K, generator=g) < 0.1, torch.full_like(topi, -1), topi)
+    return q, k, v, topi, bias, valid, bs, lb * bs
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_dense_attend_matches_key_set_enumeration(seed):
+    q, k, v, topi, bias, valid, bs, lw = _attn_case(20 + seed)
+    scale = 1.0 / math.sqrt(q.shape[-1])
+    out = O.dense_attend(q, k, v, topi, bias, valid, bs, lw, scale, q_chunk=17)
+    ref = bf.attend_brute(q.double().numpy(), k.double().numpy(), v.double().numpy(),
+                          topi.numpy(), bias.numpy(), valid.numpy(), bs, lw, scale)
+    for (b, h, t), o in ref.items():
+        np.testing.assert_allclose(out[b, h, t].double().numpy(), o, atol=2e-5)
+
+
+def test_dense_attend_with_segment_start():
+    q, k, v, topi, bias, valid, bs, lw = _attn_case(30, S=50)
+    kmin = torch.tensor([[0] * 20 + [20] * 30])
+    scale = 0.25
+    out = O.dense_attend(q, k, v, topi, bias, valid, bs, lw, scale, kmin=kmin)
+    ref = bf.attend_brute(q.double().numpy(), k.double().numpy(), v.double().numpy(),
+                          topi.numpy(), bias.numpy(), valid.numpy(), bs, lw, scale,
+                          kmin=kmin.numpy())
+    for (b, h, t), o in ref.items():
+        np.testing.assert_allclose(out[b, h, t].double().numpy(), o, atol=2e-5)
+
+
+def test_dense_attend_reduces_to_sliding_window_and_causal():
+    q, k, v, topi, bias, valid, bs, lw = _attn_case(31, S=64)
+    scale = 0.25
+    S = 64
+    none = torch.zeros_like(valid)
+    out = O.dense_attend(q, k, v, topi, bias, none, bs, lw, scale)
+    i = torch.arange(S)
+    win = (i[None, :] <= i[:, None]) & (i[None, :] > i[:, None] - lw)
+    exp = F.scaled_dot_product_attention(q, k, v, attn_mask=win, scale=scale)
+    torch.testing.assert_close(out, exp, atol=1e-5, rtol=1e-5)
+    out2 = O.dense_attend(q, k, v, topi, bias, none, bs, 10 * S, scale)
+    exp2 = F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=scale)
+    torch.testing.assert_close(out2, exp2, atol=1e-5, rtol=1e-5)
+    # every remote block routed with zero bias -> plain causal attention
+    nblk = S // bs
+    allb = torch.arange(nblk)[None, None, :].expand(1, S, nblk)
+    qblk = torch.arange(S)[None, :, None] // bs
+    out3 = O.dense_attend(q, k, v, allb, torch.zeros(1, S, nblk), allb <= qblk - lw // bs,
+                          bs, lw, scale)
+    torch.testing.assert_close(out3, exp2, atol=1e-5, rtol=1e-5)
+    # row 0 attends only key 0
+    torch.testing.assert_close(out[:, :, 0], v[:, :, 0], atol=1e-6, rtol=0)
+
+
+def test_decode_attend_equals_prefill_last_row_and_brute_force():
+    q, k, v, topi, bias, valid, bs, lw = _attn_case(32, S=77, K=4)
+    scale = 0.3
+    S = 77
+    full = O.dense_attend(q, k, v, topi, bias, valid, bs, lw, scale)
+    for t in [S - 1, 40, 17]:
+        dec = O.decode_attend(q[:, :, t:t + 1], k[:, :, :t + 1], v[:, :, :t + 1],
+                              topi[:, t:t + 1], bias[:, t:t + 1], valid[:, t:t + 1],
+                              torch.tensor([[t]]), bs, lw, scale)
+        torch.testing.assert_close(dec[:, :, 0], full[:, :, t], atol=1e-5, rtol=1e-5)
+
+
+def test_varlen_documents_are_isolated():
+    g = _rng(40)
+    H, D, d = 2, 16, 8
+    cu = [0, 37, 37 + 61, 37 + 61 + 20]
+    T = cu[-1]
+    q = torch.randn(1, H, T, D, generator=g)
+    k = torch.randn(1, H, T, D, generator=g)
+    v = torch.randn(1, H, T, D, generator=g)
+    iq = torch.randn(1, T, d, generator=g)
+    ik = torch.randn(1, T, d, generator=g)
+    args = (torch.zeros(d), 4, 2, 3.0, 1e-4, 1.0, 3, 3, 0.25)
+    out, *_ = O.prefill_varlen(q, k, v, iq, ik, cu, *args)
+    k2, v2, ik2 = k.clone(), v.clone(), ik.clone()
+    k2[:, :, cu[1]:cu[2]] += 5
+    v2[:, :, cu[1]:cu[2]] -= 3
+    ik2[:, cu[1]:cu[2]] *= -2
+    out2, *_ = O.prefill_varlen(q, k2, v2, iq, ik2, cu, *args)
+    torch.testing.assert_close(out[:, :, :cu[1]], out2[:, :, :cu[1]])
+    torch.testing.assert_close(out[:, :, cu[2]:], out2[:, :, cu[2]:])
+    # the middle document alone equals a standalone run on its own grid
+    alone, *_ = O.prefill_pipeline(q[:, :, cu[1]:cu[2]], k[:, :, cu[1]:cu[2]], v[:, :, cu[1]:cu[2]],
+                                   iq[:, cu[1]:cu[2]], ik[:, cu[1]:cu[2]], *args)
+    torch.testing.assert_close(out[:, :, cu[1]:cu[2]], alone)
