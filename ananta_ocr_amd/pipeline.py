@@ -1,0 +1,91 @@
+"""DASH prefill and decode passes built from the HIP ops.
+
+``prefill`` is the inference prefill of modeling_deepseekv2.py:403-421 (k_bar ->
+block scores -> route -> fused attention) and ``decode_step`` the decode step of
+modeling_deepseekv2.py:481-498, except that the k_bar cache is refreshed only at
+the tail block instead of being rebuilt from the whole index-key cache every step
+(the summaries of complete blocks never change).
+"""
+
+import math
+
+import torch
+
+from . import ops
+
+
+def prefill(q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks, idx_scale, floor,
+            sigma, K, topm, scale=None, cu_seqlens=None, max_seqlen=None, block_cand=None,
+            return_routing=False):
+    """q/k/v bf16 [B,H,S,D] (or [1,H,T,D] + cu_seqlens), idx_q/idx_k fp32 [B,S,d]."""
+    D = q.shape[-1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    kb = ops.kbar(idx_k, head_cls, block_size, cu_seqlens=cu_seqlens)
+    z = ops.block_scores(idx_q, kb, block_size, local_blocks, cu_seqlens=cu_seqlens)
+    if cu_seqlens is not None:
+        lens = (cu_seqlens[1:] - cu_seqlens[:-1]).to(torch.int32)
+        nblk_doc = (lens + block_size - 1) // block_size
+        row_nblk = torch.repeat_interleave(nblk_doc, lens.long(), output_size=z.shape[0])
+        width = max(1, min(int(K), int(topm)))
+        idx, bias, valid = ops.route(z, block_cand, idx_scale, floor, sigma, K, topm,
+                                     row_nblk=row_nblk, width=width)
+    else:
+        idx, bias, valid = ops.route(z, block_cand, idx_scale, floor, sigma, K, topm)
+    out = ops.attn_prefill(q, k, v, idx, bias, valid, block_size, local_blocks * block_size,
+                           scale, cu_seqlens=cu_seqlens)
+    if return_routing:
+        return out, (idx, bias, valid)
+    return out
+
+
+class DecodeState:
+    """Per-layer decode state: the k_bar cache [B, nblk_cap, d] of the index keys."""
+
+    def __init__(self, kbar):
+        self.kbar = kbar
+
+
+def init_decode_state(idx_k, head_cls, block_size, nblk_cap, seq_lens=None, block_table=None,
+                      page_size=None):
+    kb = ops.kbar(idx_k, head_cls, block_size, seq_lens=seq_lens, nblk_cap=nblk_cap,
+                  block_table=block_table, page_size=page_size)
+    return DecodeState(kb)
+
+
+def decode_step(state, q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks, idx_scale,
+                floor, sigma, K, topm, scale=None, seq_lens=None, block_table=None,
+                page_size=None, out_dtype=torch.float32, nsplit=None, block_cand=None,
+                return_routing=False):
+    """One decode step for the query at the last cached token of each sequence.
+    The newest token is already in k/v and idx_k; its block's summary is refreshed."""
+    D = q.shape[-1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    B = q.shape[0]
+    nblk = state.kbar.shape[1]
+    ops.kbar(idx_k, head_cls, block_size, seq_lens=seq_lens, nblk_cap=nblk, tail_only=True,
+             out=state.kbar, block_table=block_table, page_size=page_size)
+    S = k.shape[2] if block_table is None else block_table.shape[1] * page_size
+    if seq_lens is None:
+        q_pos = None
+        z = ops.block_scores(idx_q, state.kbar, block_size, local_blocks,
+                             q_pos=torch.full((B,), S - 1, dtype=torch.int32,
+                                              device=q.device), S=S)
+    else:
+        q_pos = (seq_lens - 1).to(torch.int32)
+        z = ops.block_scores(idx_q, state.kbar, block_size, local_blocks, q_pos=q_pos,
+                             seq_lens=seq_lens, S=S)
+    row_nblk = None
+    if seq_lens is not None:
+        row_nblk = ((seq_lens + block_size - 1) // block_size).to(torch.int32)
+    width = max(1, min(int(K), int(topm)))
+    idx, bias, valid = ops.route(z, block_cand, idx_scale, floor, sigma, K, topm,
+                                 row_nblk=row_nblk, width=width)
+    out = ops.attn_decode(q, k, v, idx[:, 0], bias[:, 0], valid[:, 0], block_size,
+                          local_blocks * block_size, scale, seq_lens=seq_lens, q_pos=q_pos,
+                          block_table=block_table, page_size=page_size, out_dtype=out_dtype,
+                          nsplit=nsplit)
+    if return_routing:
+        return out, (idx, bias, valid)
+    return out

@@ -276,7 +276,7 @@ def dense_block_bias(topi, bias, valid, nblk):
 
 
 def dense_attend(q, k, v, topi, bias, valid, block_size, local_window, scale,
-                 q_chunk=2048, kmin=None):
+                 q_chunk=2048, kmin=None, rows=None):
     """Prefill DASH attention, fp32: dash_attention.py:980-1006.
 
     Key j is kept for query t when it is causal and either in the token-level
@@ -292,8 +292,9 @@ def dense_attend(q, k, v, topi, bias, valid, block_size, local_window, scale,
     key_block = kidx // block_size
     logp = dense_block_bias(topi, bias, valid, nblk)
     out_chunks = []
-    for qs in range(0, S, q_chunk):
-        qe = min(qs + q_chunk, S)
+    r0, r1 = (0, S) if rows is None else rows
+    for qs in range(r0, r1, q_chunk):
+        qe = min(qs + q_chunk, r1)
         qidx = torch.arange(qs, qe)
         base = logp[:, qs:qe].index_select(-1, key_block)[:, None]
         causal = (kidx[None, :] <= qidx[:, None])[None, None]
