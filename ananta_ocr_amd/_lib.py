@@ -27,7 +27,11 @@ SIGNATURES = {
     "dash_route": (_i, [_p, _l, _i, _i, _p, _p, _l, _f, _f, _f, _i, _i, _i, _p, _p, _p, _p]),
     "dash_attn_prefill": (_i, [_p, _l, _l, _l, _p, _l, _l, _l, _p, _l, _l, _l, _p, _l, _l, _l,
                                _p, _l, _l, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _f,
-                               _p]),
+                               _i, _l, _p, _l, _p]),
+    "dash_attn_prefill_workspace_size": (_i, [_i, _i, _i, _l, _i, _i, _i, ctypes.POINTER(_l)]),
+    "dash_decode_route": (_i, [_p, _l, _p, _l, _l, _l, _p, _l, _i, _p, _i, _p, _i, _p, _l, _i,
+                               _p, _l, _i, _i, _i, _i, _f, _f, _f, _i, _i, _i, _p, _p, _p, _p,
+                               _l, _p]),
     "dash_attn_decode_workspace_size": (_i, [_i, _i, _i, _i, ctypes.POINTER(_l)]),
     "dash_attn_decode": (_i, [_p, _l, _l, _p, _l, _l, _l, _l, _p, _l, _l, _l, _l, _p, _l, _i,
                               _p, _p, _p, _p, _p, _i, _p, _i, _l, _l, _p, _l, _l, _i, _i, _i,

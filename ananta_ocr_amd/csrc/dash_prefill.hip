@@ -8,23 +8,31 @@
 //   routed keys  j in routed block c, kmin(t) <= j < t-LW+1  bias b(t,c)
 // (duplicated routed blocks count once, first slot wins; rows with no key give 0).
 //
-// Work decomposition: one work-group of 4 wavefronts per (128-query tile, head,
-// sequence); each wavefront owns 32 queries.  Keys are staged in LDS 32 at a
-// time.  For every key tile the wavefront computes S^T = K Q^T (32 keys x 32
-// queries) with v_mfma_f32_32x32x16_bf16, applies masks/bias and the online
-// softmax, and accumulates O^T = V^T P^T (128 dims x 32 queries), so each lane
-// owns one query's softmax state and no cross-lane rescale is needed.
-// The routed blocks of a tile are processed as the union over its queries,
-// each query masking the blocks it did not select.
+// Work decomposition (hybrid):
+//   * tile kernel: one work-group of 4 wavefronts per (128-query tile, head,
+//     sequence), 32 queries per wavefront.  Keys are staged in LDS 32 at a time;
+//     S^T = K Q^T (32 keys x 32 queries, v_mfma_f32_32x32x16_bf16), masks, bias,
+//     online softmax (base 2), O^T += V^T P^T, so each lane owns one query's
+//     softmax state.  It covers the window band and the routed blocks that many
+//     queries of the tile share ("dense" blocks: every query masks the blocks it
+//     did not select), then merges the partials of the other routed blocks.
+//   * sparse kernel: routed (query, block) pairs whose block few queries of the
+//     tile selected are grouped by block (plan -> scan -> scatter kernels); one
+//     work-group stages the block's K/V in LDS once and runs up to 128 gathered
+//     queries through the same MFMA tiles, writing a normalised bf16 partial and
+//     its base-2 log-sum-exp per (pair, head).
+// With no plan (dense_threshold <= 0) the tile kernel processes every routed
+// block of the tile as a dense block.
 
 #include "dash_common.h"
 
 namespace dash {
 
-constexpr int kPfTQ = 128;        // queries per work-group
-constexpr int kPfKT = 32;         // keys per LDS tile
+constexpr int kPfTQ = 128;        // queries per tile work-group
+constexpr int kPfKT = 32;         // keys per LDS tile in the tile kernel
 constexpr int kPfMaxK = 16;       // routed slots per query
 constexpr int kPfMaxBlocks = 2048;
+constexpr int kPfCH = 128;        // pairs per sparse chunk
 
 struct PrefillArgs {
   const bf16* q; const bf16* k; const bf16* v;
@@ -32,22 +40,309 @@ struct PrefillArgs {
   int64_t k_sb, k_sh, k_st;
   int64_t v_sb, v_sh, v_st;
   bf16* o; int64_t o_sb, o_sh, o_st;
-  float* lse; int64_t lse_sh;          // lse[token_row * lse_row + h * lse_sh]
-  int64_t lse_row;
+  float* lse; int64_t lse_row, lse_sh;  // lse[token_row * lse_row + h * lse_sh]
   const int32_t* idx; const uint8_t* valid; const float* bias; int K;   // [rows, K]
   const int32_t* cu;                   // varlen: [B+1]
   const int32_t* kmin;                 // per token row, or null
-  int S, H, bs, lw;
+  int S, H, bs, lw, nblk_cap;
   float scale_log2e;
+  // hybrid plan (null kind: every routed block is processed by the tile kernel)
+  uint8_t* kind;                       // [rows, K]: 0 skip, 1 tile (dense), 2 sparse
+  int dense_threshold;
+  int32_t* blk_count;                  // [B, nblk_cap]  zero between calls
+  int32_t* blk_fill;                   // [B, nblk_cap]
+  int32_t* blk_off;                    // [B, nblk_cap]
+  int32_t* num_chunks;                 // [B]
+  int4* chunk_tab;                     // [B, chunk_cap]: block, start, count
+  int chunk_cap;
+  int32_t* pairs;                      // [rows * K] grouped by block per sequence
+  float* part_lse;                     // [rows * K, H]  base-2 log-sum-exp
+  bf16* part_o;                        // [rows * K, H, D]  normalised partial output
 };
 
+__device__ __forceinline__ int seq_len(const PrefillArgs& a, int b) {
+  return a.cu ? a.cu[b + 1] - a.cu[b] : a.S;
+}
+__device__ __forceinline__ int64_t row0(const PrefillArgs& a, int b) {
+  return a.cu ? (int64_t)a.cu[b] : (int64_t)b * a.S;
+}
 __device__ __forceinline__ const bf16* seq_ptr(const bf16* base, const int32_t* cu, int b,
                                                int64_t sb, int64_t st) {
   return cu ? base + (int64_t)cu[b] * st : base + (int64_t)b * sb;
 }
 
+// Keep a routed slot?  The block must exist, be valid, and have keys below the
+// window start and at or above the segment start.
+__device__ __forceinline__ bool slot_usable(const PrefillArgs& a, int c, int64_t p, int t, int nblk,
+                                            int km) {
+  if (c < 0 || c >= nblk) return false;
+  if (a.valid && !a.valid[p]) return false;
+  const int ls = t - a.lw + 1;
+  return c * a.bs < ls && (c + 1) * a.bs > km;
+}
+
+// ---------------------------------------------------------------------------
+// MFMA building blocks (32 queries per wavefront, lane = query n, half hl)
+// ---------------------------------------------------------------------------
+template <int D, int LDK>
+__device__ __forceinline__ floatx16 qk_tile(const bf16 (*sK)[LDK], int krow0, const bf16x8 (&qop)[D / 16],
+                                            int n, int hl) {
+  floatx16 s;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s[r] = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) {
+    const bf16x8 kop = *(const bf16x8*)&sK[krow0 + n][kk * 16 + hl * 8];
+    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qop[kk], s, 0, 0, 0);
+  }
+  return s;
+}
+
+// acc_o[dt] += V^T (keys key0 .. key0+15 of the LDS tile) * P^T (pop)
+template <int D, int LDV>
+__device__ __forceinline__ void pv_slice(const bf16 (*sVt)[LDV], int key0, const bf16x8& pop,
+                                         floatx16 (&acc_o)[D / 32], int n, int hl) {
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) {
+    const bf16* vrow = &sVt[dt * 32 + n][key0 + 4 * hl];
+    const bf16x4 lo = *(const bf16x4*)vrow;
+    const bf16x4 hi = *(const bf16x4*)(vrow + 8);
+    bf16x8 vop;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { vop[e] = lo[e]; vop[e + 4] = hi[e]; }
+    acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pop, acc_o[dt], 0, 0, 0);
+  }
+}
+
+// Stage rows j0 .. j0+nrows-1 of K (row-major) and V (transposed) into LDS;
+// rows at or beyond len are zero.  nrows * D / 8 chunks over 256 threads.
+template <int D, int LDK, int LDV>
+__device__ __forceinline__ void stage_kv(bf16 (*sK)[LDK], bf16 (*sVt)[LDV], const bf16* kb,
+                                         const bf16* vb, int64_t k_st, int64_t v_st, int j0,
+                                         int nrows, int len, int tid) {
+  const int nchunks = nrows * (D / 8);
+  for (int chunk = tid; chunk < nchunks; chunk += 256) {
+    const int kr = chunk / (D / 8), c8 = (chunk % (D / 8)) * 8;
+    const int j = j0 + kr;
+    bf16x8 kv8, vv8;
+    if (j < len) {
+      kv8 = *(const bf16x8*)(kb + (int64_t)j * k_st + c8);
+      vv8 = *(const bf16x8*)(vb + (int64_t)j * v_st + c8);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { kv8[e] = (bf16)0.f; vv8[e] = (bf16)0.f; }
+    }
+    *(bf16x8*)&sK[kr][c8] = kv8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sVt[c8 + e][kr] = vv8[e];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Plan: classify every routed (query, slot) of a 128-query tile as skipped,
+// dense (block selected by >= dense_threshold queries of the tile) or sparse,
+// and count the sparse pairs per block.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kPfTQ) void prefill_plan_kernel(PrefillArgs a) {
+  __shared__ int32_t sCnt[kPfMaxBlocks];
+  __shared__ int32_t sKept[kPfTQ][kPfMaxK];
+  const int b = blockIdx.y, tid = threadIdx.x;
+  const int len = seq_len(a, b);
+  const int t0 = blockIdx.x * kPfTQ;
+  if (t0 >= len) return;
+  const int nblk = (len + a.bs - 1) / a.bs;
+  for (int i = tid; i < nblk; i += kPfTQ) sCnt[i] = 0;
+  __syncthreads();
+  const int t = t0 + tid;
+  const int64_t row = row0(a, b) + t;
+  int32_t* kept = sKept[tid];
+  uint32_t keep_mask = 0;
+  if (t < len) {
+    const int km = a.kmin ? a.kmin[row] : 0;
+    for (int s = 0; s < a.K; ++s) {
+      const int64_t p = row * a.K + s;
+      const int c = a.idx[p];
+      kept[s] = c;
+      if (!slot_usable(a, c, p, t, nblk, km)) continue;
+      bool dup = false;
+      for (int u = 0; u < s; ++u) dup |= ((keep_mask >> u) & 1u) && kept[u] == c;
+      if (dup) continue;
+      keep_mask |= 1u << s;
+      atomicAdd(&sCnt[c], 1);
+    }
+  }
+  __syncthreads();
+  if (t < len) {
+    for (int s = 0; s < a.K; ++s) {
+      uint8_t kd = 0;
+      if ((keep_mask >> s) & 1u) {
+        const int c = kept[s];
+        kd = sCnt[c] >= a.dense_threshold ? 1 : 2;
+        if (kd == 2) atomicAdd(&a.blk_count[(int64_t)b * a.nblk_cap + c], 1);
+      }
+      a.kind[row * a.K + s] = kd;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Scan: per sequence, block offsets of the sparse pairs and the chunk table.
+// Resets the block counters (they are zero between calls) and the fill cursors.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
+  __shared__ int32_t sC[kPfMaxBlocks];
+  __shared__ int32_t sOff[kPfMaxBlocks];
+  __shared__ int32_t sCh[kPfMaxBlocks];
+  __shared__ int32_t sWave[2][16];
+  const int b = blockIdx.x, tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
+  const int len = seq_len(a, b);
+  const int nblk = len > 0 ? (len + a.bs - 1) / a.bs : 0;
+  int32_t* cnt = a.blk_count + (int64_t)b * a.nblk_cap;
+  int32_t* fill = a.blk_fill + (int64_t)b * a.nblk_cap;
+  // two entries per thread
+  int v0 = 0, v1 = 0;
+  const int e0 = tid * 2, e1 = tid * 2 + 1;
+  if (e0 < a.nblk_cap) { v0 = e0 < nblk ? cnt[e0] : 0; cnt[e0] = 0; fill[e0] = 0; }
+  if (e1 < a.nblk_cap) { v1 = e1 < nblk ? cnt[e1] : 0; cnt[e1] = 0; fill[e1] = 0; }
+  const int c0 = (v0 + kPfCH - 1) / kPfCH, c1 = (v1 + kPfCH - 1) / kPfCH;
+  int sp = v0 + v1, sc = c0 + c1;
+  int ip = sp, ic = sc;
+#pragma unroll
+  for (int s = 1; s < kWave; s <<= 1) {
+    const int op = __shfl_up(ip, s, kWave), oc = __shfl_up(ic, s, kWave);
+    if (lane >= s) { ip += op; ic += oc; }
+  }
+  if (lane == kWave - 1) { sWave[0][wv] = ip; sWave[1][wv] = ic; }
+  __syncthreads();
+  int bp = 0, bc = 0;
+  for (int w = 0; w < wv; ++w) { bp += sWave[0][w]; bc += sWave[1][w]; }
+  const int xp = bp + ip - sp, xc = bc + ic - sc;   // exclusive prefix of this thread
+  if (e0 < kPfMaxBlocks) { sC[e0] = v0; sOff[e0] = xp; sCh[e0] = xc; }
+  if (e1 < kPfMaxBlocks) { sC[e1] = v1; sOff[e1] = xp + v0; sCh[e1] = xc + c0; }
+  if (tid == 1023) a.num_chunks[b] = bc + ic;
+  __syncthreads();
+  int4* tab = a.chunk_tab + (int64_t)b * a.chunk_cap;
+  for (int c = tid; c < nblk; c += 1024) {
+    a.blk_off[(int64_t)b * a.nblk_cap + c] = sOff[c];
+    const int n = sC[c];
+    for (int i = 0; i * kPfCH < n; ++i)
+      tab[sCh[c] + i] = make_int4(c, sOff[c] + i * kPfCH, min(kPfCH, n - i * kPfCH), 0);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Scatter: sparse pairs into per-block lists (order within a block is free).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kPfTQ) void prefill_scatter_kernel(PrefillArgs a) {
+  const int b = blockIdx.y, tid = threadIdx.x;
+  const int len = seq_len(a, b);
+  const int t = blockIdx.x * kPfTQ + tid;
+  if (t >= len) return;
+  const int64_t row = row0(a, b) + t;
+  const int64_t base = row0(a, b) * a.K;
+  for (int s = 0; s < a.K; ++s) {
+    const int64_t p = row * a.K + s;
+    if (a.kind[p] != 2) continue;
+    const int c = a.idx[p];
+    const int pos = atomicAdd(&a.blk_fill[(int64_t)b * a.nblk_cap + c], 1);
+    a.pairs[base + a.blk_off[(int64_t)b * a.nblk_cap + c] + pos] = (int32_t)(p - base);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Sparse kernel: one chunk of <= 128 pairs of one routed block, one head.
+// ---------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(256) void prefill_union_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256) void prefill_sparse_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) bf16 sK[64][D + 8];
+  __shared__ __attribute__((aligned(16))) bf16 sVt[D][64 + 8];
+  const int b = blockIdx.z, h = blockIdx.y, ch = blockIdx.x;
+  if (ch >= a.num_chunks[b]) return;
+  const int4 e = a.chunk_tab[(int64_t)b * a.chunk_cap + ch];
+  const int c = e.x, start = e.y, npairs = e.z;
+  const int len = seq_len(a, b);
+  const int tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
+  const int hl = lane >> 5, n = lane & 31;
+  const int64_t r0 = row0(a, b);
+  const bf16* kb = seq_ptr(a.k, a.cu, b, a.k_sb, a.k_st) + (int64_t)h * a.k_sh;
+  const bf16* vb = seq_ptr(a.v, a.cu, b, a.v_sb, a.v_st) + (int64_t)h * a.v_sh;
+  stage_kv<D, D + 8, 64 + 8>(sK, sVt, kb, vb, a.k_st, a.v_st, c * a.bs, a.bs, len, tid);
+
+  const int pi = wv * 32 + n;
+  const bool active = pi < npairs;
+  const int32_t pl = a.pairs[r0 * a.K + start + min(pi, npairs - 1)];   // pair index in sequence
+  const int64_t p = r0 * a.K + pl;
+  const int t = pl / a.K;
+  const int ls = t - a.lw + 1;
+  const int km = a.kmin ? a.kmin[r0 + t] : 0;
+  const float bias2 = a.bias[p] * 1.4426950408889634f;
+  const bf16* qb = seq_ptr(a.q, a.cu, b, a.q_sb, a.q_st) + (int64_t)h * a.q_sh + (int64_t)t * a.q_st;
+  bf16x8 qop[D / 16];
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) qop[kk] = *(const bf16x8*)(qb + kk * 16 + hl * 8);
+  __syncthreads();
+  if (!__any(active)) return;
+
+  const int nsub = a.bs / 32;     // 1 or 2 key sub-tiles of 32
+  floatx16 s[2];
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    if (sub < nsub) {
+      s[sub] = qk_tile<D, D + 8>(sK, sub * 32, qop, n, hl);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = c * a.bs + sub * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
+        const bool ok = active && key < ls && key >= km && key < len;
+        const float x = ok ? s[sub][r] * a.scale_log2e + bias2 : -INFINITY;
+        s[sub][r] = x;
+        mloc = fmaxf(mloc, x);
+      }
+    }
+  }
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
+  const float mu = (mloc == -INFINITY) ? 0.f : mloc;
+  floatx16 acc_o[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_o[dt][r] = 0.f;
+  float psum = 0.f;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    if (sub < nsub) {
+      bf16x8 pop[2];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pr = exp2f(s[sub][r] - mu);
+        psum += pr;
+        pop[r >> 3][r & 7] = (bf16)pr;
+      }
+      pv_slice<D, 64 + 8>(sVt, sub * 32, pop[0], acc_o, n, hl);
+      pv_slice<D, 64 + 8>(sVt, sub * 32 + 16, pop[1], acc_o, n, hl);
+    }
+  }
+  const float l_tot = psum + __shfl_xor(psum, 32, kWave);
+  if (!active) return;
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  bf16* po = a.part_o + (p * a.H + h) * D;
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      bf16x4 w;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) w[q4] = (bf16)(acc_o[dt][g * 4 + q4] * inv);
+      *(bf16x4*)(po + dt * 32 + 8 * g + 4 * hl) = w;
+    }
+  if (hl == 0) a.part_lse[p * a.H + h] = l_tot > 0.f ? mloc + log2f(l_tot) : -INFINITY;
+}
+
+// ---------------------------------------------------------------------------
+// Tile kernel: window band + dense routed blocks + merge of the sparse partials.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void prefill_tile_kernel(PrefillArgs a) {
   static_assert(D == 128, "head_dim 128");
   __shared__ __attribute__((aligned(16))) bf16 sK[kPfKT][D + 8];
   __shared__ __attribute__((aligned(16))) bf16 sVt[D][kPfKT + 4];
@@ -59,35 +354,37 @@ __global__ __launch_bounds__(256) void prefill_union_kernel(PrefillArgs a) {
   __shared__ int32_t sNU;
 
   const int b = blockIdx.z, h = blockIdx.y;
-  const int len = a.cu ? a.cu[b + 1] - a.cu[b] : a.S;
+  const int len = seq_len(a, b);
   const int t0 = blockIdx.x * kPfTQ;
   if (t0 >= len) return;
   const int nblk = (len + a.bs - 1) / a.bs;
   const int tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
   const int hl = lane >> 5;         // half of the wave: 0/1
   const int n = lane & 31;          // query column within the wave
+  const int64_t r0 = row0(a, b);
 
   for (int i = tid; i < kPfMaxBlocks / 32; i += 256) sBits[i] = 0u;
   __syncthreads();
 
-  // ---- routed blocks of every query row: filter, dedup, sort ascending ----
+  // ---- dense routed blocks of every query row: filter, dedup, sort ascending ----
   if (tid < kPfTQ) {
     const int t = t0 + tid;
     int cnt = 0;
     if (t < len) {
-      const int64_t row = token_row(a.cu, b, t, a.S);
-      const int ls = t - a.lw + 1;
+      const int64_t row = r0 + t;
       const int km = a.kmin ? a.kmin[row] : 0;
       for (int s = 0; s < a.K; ++s) {
-        const int c = a.idx[row * a.K + s];
-        if (c < 0 || c >= nblk) continue;
-        if (a.valid && !a.valid[row * a.K + s]) continue;
-        // a routed block contributes only keys below the window start
-        if (c * a.bs >= ls || (c + 1) * a.bs <= km) continue;
-        bool dup = false;
-        for (int u = 0; u < cnt; ++u) dup |= (sIdx[tid][u] == c);
-        if (dup) continue;
-        const float bv = a.bias[row * a.K + s];
+        const int64_t p = row * a.K + s;
+        const int c = a.idx[p];
+        if (a.kind) {
+          if (a.kind[p] != 1) continue;
+        } else {
+          if (!slot_usable(a, c, p, t, nblk, km)) continue;
+          bool dup = false;
+          for (int u = 0; u < cnt; ++u) dup |= (sIdx[tid][u] == c);
+          if (dup) continue;
+        }
+        const float bv = a.bias[p];
         int u = cnt;
         while (u > 0 && sIdx[tid][u - 1] > c) {
           sIdx[tid][u] = sIdx[tid][u - 1];
@@ -131,7 +428,7 @@ __global__ __launch_bounds__(256) void prefill_union_kernel(PrefillArgs a) {
   // ---- this lane's query and its Q^T operand (8 k-steps of 16 dims) ----
   const int tq = t0 + wv * 32 + n;
   const int tqc = min(tq, len - 1);
-  const int64_t qrow = token_row(a.cu, b, tqc, a.S);
+  const int64_t qrow = r0 + tqc;
   const bf16* qb = seq_ptr(a.q, a.cu, b, a.q_sb, a.q_st) + (int64_t)h * a.q_sh;
   bf16x8 qop[D / 16];
 #pragma unroll
@@ -159,7 +456,7 @@ __global__ __launch_bounds__(256) void prefill_union_kernel(PrefillArgs a) {
   const bf16* kb = seq_ptr(a.k, a.cu, b, a.k_sb, a.k_st) + (int64_t)h * a.k_sh;
   const bf16* vb = seq_ptr(a.v, a.cu, b, a.v_sb, a.v_st) + (int64_t)h * a.v_sh;
   const int myrow = wv * 32 + n;           // row within the tile
-  int ptr = 0;                             // next routed block of this query
+  int ptr = 0;                             // next dense block of this query
   bool cur_sel = false;
   float cur_bias = 0.f;
   const float log2e = 1.4426950408889634f;
@@ -175,25 +472,8 @@ __global__ __launch_bounds__(256) void prefill_union_kernel(PrefillArgs a) {
       sub = r % subs;
       j0 = c * a.bs + sub * kPfKT;
     }
-    // ---- stage K (row major) and V (transposed) for keys j0..j0+31 ----
     __syncthreads();
-#pragma unroll
-    for (int rep = 0; rep < 2; ++rep) {
-      const int chunk = tid + rep * 256;           // 32 rows x 16 chunks of 8 dims
-      const int kr = chunk >> 4, c8 = (chunk & 15) * 8;
-      const int j = j0 + kr;
-      bf16x8 kv8, vv8;
-      if (j < len) {
-        kv8 = *(const bf16x8*)(kb + (int64_t)j * a.k_st + c8);
-        vv8 = *(const bf16x8*)(vb + (int64_t)j * a.v_st + c8);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) { kv8[e] = (bf16)0.f; vv8[e] = (bf16)0.f; }
-      }
-      *(bf16x8*)&sK[kr][c8] = kv8;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sVt[c8 + e][kr] = vv8[e];
-    }
+    stage_kv<D, D + 8, kPfKT + 4>(sK, sVt, kb, vb, a.k_st, a.v_st, j0, kPfKT, len, tid);
     __syncthreads();
 
     // ---- does any query of this wavefront use this key tile? ----
@@ -215,15 +495,7 @@ __global__ __launch_bounds__(256) void prefill_union_kernel(PrefillArgs a) {
     }
     if (!__any(use)) continue;
 
-    // ---- S^T = K Q^T ----
-    floatx16 s;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) {
-      const bf16x8 kop = *(const bf16x8*)&sK[n][kk * 16 + hl * 8];
-      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qop[kk], s, 0, 0, 0);
-    }
+    floatx16 s = qk_tile<D, D + 8>(sK, 0, qop, n, hl);
     // ---- mask, bias, online softmax (base 2) ----
     float mloc = -INFINITY;
 #pragma unroll
@@ -244,9 +516,9 @@ __global__ __launch_bounds__(256) void prefill_union_kernel(PrefillArgs a) {
     bf16x8 pop[2];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float p = exp2f(s[r] - m_use);
-      psum += p;
-      pop[r >> 3][r & 7] = (bf16)p;
+      const float pr = exp2f(s[r] - m_use);
+      psum += pr;
+      pop[r >> 3][r & 7] = (bf16)pr;
     }
     l_run = l_run * alpha + psum;
     m_run = m_new;
@@ -254,19 +526,33 @@ __global__ __launch_bounds__(256) void prefill_union_kernel(PrefillArgs a) {
     for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
-    // ---- O^T += V^T P^T ----
+    pv_slice<D, kPfKT + 4>(sVt, 0, pop[0], acc_o, n, hl);
+    pv_slice<D, kPfKT + 4>(sVt, 16, pop[1], acc_o, n, hl);
+  }
+
+  // ---- merge the sparse partials of this query ----
+  if (a.kind && tq < len) {
+    const int64_t row = r0 + tq;
+    for (int s = 0; s < a.K; ++s) {
+      const int64_t p = row * a.K + s;
+      if (a.kind[p] != 2) continue;
+      const float lse2 = a.part_lse[p * a.H + h];
+      if (lse2 == -INFINITY) continue;
+      const float m_new = fmaxf(m_run, lse2);
+      const float alpha = exp2f(m_run - m_new);
+      const float w = exp2f(lse2 - m_new);
+      l_run = l_run * alpha + (hl == 0 ? w : 0.f);
+      m_run = m_new;
+      const bf16* po = a.part_o + (p * a.H + h) * D;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) {
+      for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-      for (int sl = 0; sl < 2; ++sl) {
-        const bf16* vrow = &sVt[dt * 32 + n][sl * 16 + 4 * hl];
-        const bf16x4 lo = *(const bf16x4*)vrow;
-        const bf16x4 hi = *(const bf16x4*)(vrow + 8);
-        bf16x8 vop;
+        for (int g = 0; g < 4; ++g) {
+          const bf16x4 ov = *(const bf16x4*)(po + dt * 32 + 8 * g + 4 * hl);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) { vop[e] = lo[e]; vop[e + 4] = hi[e]; }
-        acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pop[sl], acc_o[dt], 0, 0, 0);
-      }
+          for (int q4 = 0; q4 < 4; ++q4)
+            acc_o[dt][g * 4 + q4] = acc_o[dt][g * 4 + q4] * alpha + w * bf2f(ov[q4]);
+        }
     }
   }
 
@@ -287,16 +573,53 @@ __global__ __launch_bounds__(256) void prefill_union_kernel(PrefillArgs a) {
       }
     if (a.lse && hl == 0) {
       const float lse = l_tot > 0.f ? (m_run + log2f(l_tot)) * 0.6931471805599453f : -INFINITY;
-      a.lse[token_row(a.cu, b, tq, a.S) * a.lse_row + (int64_t)h * a.lse_sh] = lse;
+      a.lse[(r0 + tq) * a.lse_row + (int64_t)h * a.lse_sh] = lse;
     }
   }
+}
+
+// Workspace layout of the hybrid plan (byte offsets, 256-byte aligned pieces).
+struct PlanLayout {
+  int64_t count, fill, off, nchunks, tab, pairs, kind, plse, po, total;
+  int chunk_cap;
+};
+
+inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+inline PlanLayout plan_layout(int B, int H, int S_max, int64_t rows, int K, int D,
+                              int nblk_cap) {
+  PlanLayout L;
+  L.chunk_cap = (int)((int64_t)S_max * K / kPfCH) + nblk_cap + 1;
+  const int64_t nbc = (int64_t)B * nblk_cap;
+  int64_t o = 0;
+  L.count = o; o = align256(o + nbc * 4);
+  L.fill = o; o = align256(o + nbc * 4);
+  L.off = o; o = align256(o + nbc * 4);
+  L.nchunks = o; o = align256(o + (int64_t)B * 4);
+  L.tab = o; o = align256(o + (int64_t)B * L.chunk_cap * 16);
+  L.pairs = o; o = align256(o + rows * K * 4);
+  L.kind = o; o = align256(o + rows * K);
+  L.plse = o; o = align256(o + rows * K * H * 4);
+  L.po = o; o = align256(o + rows * K * H * D * 2);
+  L.total = o;
+  return L;
 }
 
 }  // namespace dash
 
 // ---------------------------------------------------------------------------
-// C entry point
+// C entry points
 // ---------------------------------------------------------------------------
+extern "C" int dash_attn_prefill_workspace_size(int B, int H, int S_max, int64_t total_rows,
+                                                int K, int D, int block_size, int64_t* bytes) {
+  using namespace dash;
+  if (!bytes || B < 0 || H <= 0 || S_max < 0 || total_rows < 0 || K < 0 || block_size <= 0)
+    return kErrInvalid;
+  const int nblk_cap = (S_max + block_size - 1) / block_size;
+  *bytes = plan_layout(B, H, S_max, total_rows, K, D, nblk_cap).total;
+  return kOk;
+}
+
 extern "C" int dash_attn_prefill(
     const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
     const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
@@ -306,6 +629,7 @@ extern "C" int dash_attn_prefill(
     const int32_t* idx, const uint8_t* valid, const float* bias, int K,
     const int32_t* cu_seqlens, const int32_t* kmin,
     int B, int H, int S, int D, int block_size, int local_window, float scale,
+    int dense_threshold, int64_t total_rows, void* workspace, int64_t workspace_bytes,
     void* stream) {
   using namespace dash;
   if (!q || !k || !v || !o || B < 0 || H <= 0 || S < 0) return kErrInvalid;
@@ -315,7 +639,8 @@ extern "C" int dash_attn_prefill(
   if (K < 0 || K > kPfMaxK) return kErrUnsupported;
   if (local_window < 1) return kErrInvalid;
   if (B == 0 || S == 0) return kOk;
-  if ((S + block_size - 1) / block_size > kPfMaxBlocks) return kErrUnsupported;
+  const int nblk_cap = (S + block_size - 1) / block_size;
+  if (nblk_cap > kPfMaxBlocks) return kErrUnsupported;
   // 16-byte rows for the bf16x8 loads and stores
   const int64_t strides[] = {q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st};
   for (int64_t s : strides)
@@ -323,7 +648,7 @@ extern "C" int dash_attn_prefill(
   const void* ptrs[] = {q, k, v, o};
   for (const void* p : ptrs)
     if ((uintptr_t)p % 16 != 0) return kErrUnsupported;
-  PrefillArgs a;
+  PrefillArgs a = {};
   a.q = (const bf16*)q; a.k = (const bf16*)k; a.v = (const bf16*)v;
   a.q_sb = q_sb; a.q_sh = q_sh; a.q_st = q_st;
   a.k_sb = k_sb; a.k_sh = k_sh; a.k_st = k_st;
@@ -332,10 +657,34 @@ extern "C" int dash_attn_prefill(
   a.lse = lse; a.lse_row = lse_row; a.lse_sh = lse_sh;
   a.idx = idx; a.valid = valid; a.bias = bias; a.K = K;
   a.cu = cu_seqlens; a.kmin = kmin;
-  a.S = S; a.H = H; a.bs = block_size; a.lw = local_window;
+  a.S = S; a.H = H; a.bs = block_size; a.lw = local_window; a.nblk_cap = nblk_cap;
   a.scale_log2e = scale * 1.4426950408889634f;
-  dim3 grid((S + kPfTQ - 1) / kPfTQ, H, B);
-  hipLaunchKernelGGL(prefill_union_kernel<128>, grid, dim3(256), 0, (hipStream_t)stream, a);
+  hipStream_t st = (hipStream_t)stream;
+  const int ntiles = (S + kPfTQ - 1) / kPfTQ;
+  const bool hybrid = dense_threshold > 0 && K > 0 && block_size <= 64;
+  if (hybrid) {
+    if (total_rows <= 0) return kErrInvalid;
+    const PlanLayout L = plan_layout(B, H, S, total_rows, K, D, nblk_cap);
+    if (!workspace || workspace_bytes < L.total || (uintptr_t)workspace % 256 != 0)
+      return kErrWorkspace;
+    char* w = (char*)workspace;
+    a.kind = (uint8_t*)(w + L.kind);
+    a.dense_threshold = dense_threshold;
+    a.blk_count = (int32_t*)(w + L.count);
+    a.blk_fill = (int32_t*)(w + L.fill);
+    a.blk_off = (int32_t*)(w + L.off);
+    a.num_chunks = (int32_t*)(w + L.nchunks);
+    a.chunk_tab = (int4*)(w + L.tab);
+    a.chunk_cap = L.chunk_cap;
+    a.pairs = (int32_t*)(w + L.pairs);
+    a.part_lse = (float*)(w + L.plse);
+    a.part_o = (bf16*)(w + L.po);
+    hipLaunchKernelGGL(prefill_plan_kernel, dim3(ntiles, B), dim3(kPfTQ), 0, st, a);
+    hipLaunchKernelGGL(prefill_scan_kernel, dim3(B), dim3(1024), 0, st, a);
+    hipLaunchKernelGGL(prefill_scatter_kernel, dim3(ntiles, B), dim3(kPfTQ), 0, st, a);
+    hipLaunchKernelGGL(prefill_sparse_kernel<128>, dim3(L.chunk_cap, H, B), dim3(256), 0, st, a);
+  }
+  hipLaunchKernelGGL(prefill_tile_kernel<128>, dim3(ntiles, H, B), dim3(256), 0, st, a);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? kOk : (int)e;
 }

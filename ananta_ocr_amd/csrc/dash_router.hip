@@ -481,3 +481,272 @@ extern "C" int dash_route(const float* z, int64_t z_stride, int rows, int nblk_c
 #undef DASH_ROUTE
   return launch_status();
 }
+
+// ---------------------------------------------------------------------------
+// Decode router: one query per sequence, one 1024-thread work-group per
+// sequence.  Fuses the k_bar refresh of the tail block, the block scores and
+// the routing; no cross-work-group communication.
+// ---------------------------------------------------------------------------
+namespace dash {
+
+constexpr int kDrThreads = 1024;
+constexpr int kDrMaxBlocks = 2048;
+
+struct DecodeRouteArgs {
+  const float* idx_q; int64_t iq_sb;
+  const float* idx_k; SeqLayout lay_k;
+  const int32_t* lens; int S;
+  const float* head_cls; int refresh_tail;
+  float* kbar; int64_t kb_sb; int nblk_cap;
+  const uint8_t* cand; int64_t cand_stride;
+  int d, bs, local_blocks;
+  float inv_sqrt_d, idx_scale, floor_p, inv_sigma;
+  int K, topm, Kout;
+  int32_t* idx; float* bias; uint8_t* valid;
+  float* z; int64_t z_stride;
+};
+
+__global__ __launch_bounds__(kDrThreads) void decode_route_kernel(DecodeRouteArgs a) {
+  __shared__ __attribute__((aligned(16))) float s_q[256];
+  __shared__ __attribute__((aligned(16))) float s_tail[256];
+  __shared__ float s_aw[256];
+  __shared__ float s_red[2];
+  __shared__ float s_part[8][128];
+  __shared__ float s_x[kDrMaxBlocks + 8];
+  __shared__ int s_key[kDrMaxBlocks + 8];
+  __shared__ uint8_t s_flag[kDrMaxBlocks];
+  __shared__ float s_selv[kMaxM];
+  __shared__ int s_selk[kMaxM];
+
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
+  const int len = a.lens ? a.lens[b] : a.S;
+  const int nblk = len > 0 ? (len + a.bs - 1) / a.bs : 0;
+  const int qp = len - 1;
+  const int lim = (qp >= 0 ? qp / a.bs : -1) - a.local_blocks;
+  const int ct = nblk - 1;               // tail block
+  if (nblk == 0) {
+    for (int m = tid; m < a.Kout; m += kDrThreads) {
+      a.idx[(int64_t)b * a.Kout + m] = -1;
+      a.bias[(int64_t)b * a.Kout + m] = 0.f;
+      if (a.valid) a.valid[(int64_t)b * a.Kout + m] = 0;
+    }
+    return;
+  }
+  for (int i = tid; i < a.d; i += kDrThreads) s_q[i] = a.idx_q[(int64_t)b * a.iq_sb + i];
+  if (a.refresh_tail) {
+    const int t0 = ct * a.bs, n = len - t0;
+    const float* hcp = a.head_cls;
+    // logits of the tail tokens: 4 lanes per token, a quarter of the dims each
+    for (int j0 = 0; j0 < n; j0 += kDrThreads / 4) {
+      const int j = j0 + tid / 4, part = tid % 4;
+      float acc = 0.f;
+      if (j < n) {
+        const float* kr = a.idx_k + a.lay_k.row(b, t0 + j);
+        const int q4 = a.d / 4;
+        for (int i = part * q4; i < (part + 1) * q4; i += 4) {
+          const float4 kv = *(const float4*)(kr + i);
+          const float4 hv = *(const float4*)(hcp + i);
+          acc += kv.x * hv.x + kv.y * hv.y + kv.z * hv.z + kv.w * hv.w;
+        }
+      }
+      acc += __shfl_xor(acc, 1, kWave);
+      acc += __shfl_xor(acc, 2, kWave);
+      if (j < n && part == 0) s_aw[j] = fminf(fmaxf(acc * a.inv_sqrt_d, -kActClamp), kActClamp);
+    }
+    __syncthreads();
+    if (wv == 0) {
+      float m = -INFINITY;
+      for (int j = lane; j < n; j += kWave) m = fmaxf(m, s_aw[j]);
+      m = wave_max(m);
+      float sum = 0.f;
+      for (int j = lane; j < n; j += kWave) sum += expf(s_aw[j] - m);
+      sum = wave_sum(sum);
+      if (lane == 0) { s_red[0] = m; s_red[1] = fmaxf(sum, 1e-6f); }
+    }
+    __syncthreads();
+    for (int j = tid; j < n; j += kDrThreads) s_aw[j] = expf(s_aw[j] - s_red[0]) / s_red[1];
+    __syncthreads();
+    // weighted sum: 8 token groups x 128 dims, partials reduced through LDS
+    const int jg = tid / 128, di = tid % 128;
+    for (int i0 = 0; i0 < a.d; i0 += 128) {
+      const int i = i0 + di;
+      float acc = 0.f;
+      if (i < a.d) {
+#pragma unroll 8
+        for (int j = jg; j < n; j += 8) acc += s_aw[j] * a.idx_k[a.lay_k.row(b, t0 + j) + i];
+      }
+      s_part[jg][di] = acc;
+      __syncthreads();
+      if (tid < 128 && i < a.d) {
+        float t = 0.f;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) t += s_part[g][tid];
+        if (!(fabsf(t) <= 3.402823466e38f)) t = 0.f;
+        s_tail[i] = t;
+        a.kbar[(int64_t)b * a.kb_sb + (int64_t)ct * a.d + i] = t;
+      }
+      __syncthreads();
+    }
+  }
+  __syncthreads();
+  // scores: 32 lanes per block (4 dims per lane per step), 32 blocks per pass,
+  // loads of 8 passes issued before use; the refreshed tail block from LDS
+  {
+    const int l32 = lane & 31, row0 = tid / 32;
+    for (int cb = 0; cb < nblk; cb += 8 * (kDrThreads / 32)) {
+      float acc[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) acc[r] = 0.f;
+      for (int i = l32 * 4; i < a.d; i += 128) {
+        float4 kv[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          const int c = min(cb + row0 + r * (kDrThreads / 32), nblk - 1);
+          kv[r] = *(const float4*)(a.kbar + (int64_t)b * a.kb_sb + (int64_t)c * a.d + i);
+        }
+        const float4 qv = *(const float4*)(s_q + i);
+        const float4 tv = *(const float4*)(s_tail + i);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          const int c = cb + row0 + r * (kDrThreads / 32);
+          const float4 k4 = (a.refresh_tail && c == ct) ? tv : kv[r];
+          acc[r] += qv.x * k4.x + qv.y * k4.y + qv.z * k4.z + qv.w * k4.w;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        float v = acc[r];
+#pragma unroll
+        for (int m = 16; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+        const int c = cb + row0 + r * (kDrThreads / 32);
+        if (l32 == 0 && c < nblk) {
+          float zz = kScoreNeg;
+          if (c <= lim) zz = fminf(fmaxf(v * a.inv_sqrt_d, -kActClamp), kActClamp);
+          s_x[c] = zz;
+          a.z[(int64_t)b * a.z_stride + c] = zz;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // candidates, with the fall-back to every remote block
+  bool any = false;
+  for (int c = tid; c < nblk; c += kDrThreads) {
+    const float z = s_x[c];
+    const bool remote = z > kScoreNeg * 0.5f;
+    bool cd = remote;
+    if (a.cand) cd = cd && a.cand[(int64_t)b * a.cand_stride + c] != 0;
+    s_x[c] = z;
+    s_flag[c] = (remote ? 1 : 0) | (cd ? 2 : 0);
+    any |= cd;
+  }
+  any = __syncthreads_or(any);
+  for (int c = tid; c < nblk; c += kDrThreads) {
+    const bool cd = any ? (s_flag[c] & 2) : (s_flag[c] & 1);
+    float x = cd ? s_x[c] * a.idx_scale : kEntmaxNeg;
+    if (!(fabsf(x) <= 3.402823466e38f)) x = kEntmaxNeg;
+    s_x[c] = x;
+    s_key[c] = c | (cd ? (1 << 30) : 0);
+  }
+  __syncthreads();
+  const int M = a.topm > 0 ? max(1, min(a.topm, nblk)) : nblk;
+  const int Kp = max(1, min(a.K, M));
+  // pad to a multiple of 8 with entries that lose every comparison
+  for (int c = nblk + tid; c < ((nblk + 7) & ~7); c += kDrThreads) {
+    s_x[c] = -INFINITY;
+    s_key[c] = 0x3fffffff;
+  }
+  __syncthreads();
+  // rank of every entry; an entry stops counting once it cannot be in the top M
+  for (int c = tid; c < nblk; c += kDrThreads) {
+    const float x = s_x[c];
+    const int key = s_key[c];
+    int rank = 0;
+    for (int j0 = 0; j0 < nblk && rank < M; j0 += 8) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) rank += route_better(s_x[j0 + u], s_key[j0 + u], x, key);
+    }
+    if (rank < M) { s_selv[rank] = x; s_selk[rank] = key; }
+  }
+  __syncthreads();
+  if (wv != 0) return;
+  float sel_v[kMaxM];
+  int sel_k[kMaxM];
+#pragma unroll
+  for (int m = 0; m < kMaxM; ++m) {
+    sel_v[m] = m < M ? s_selv[m] : 0.f;
+    sel_k[m] = m < M ? s_selk[m] : 0x3fffffff;
+  }
+  float prior[kMaxM];
+  entmax15_sorted(sel_v, M, prior);
+  float logp[kMaxM];
+  float musum = 0.f;
+  int cnt = 0;
+#pragma unroll
+  for (int m = 0; m < kMaxM; ++m) {
+    logp[m] = logf(fmaxf(prior[m], a.floor_p));
+    if (m < Kp && (sel_k[m] & (1 << 30))) { musum += logp[m]; ++cnt; }
+  }
+  const float mu = musum / (float)max(cnt, 1);
+  for (int m = lane; m < a.Kout; m += kWave) {
+    int oi = -1;
+    float ob = 0.f;
+    uint8_t ov = 0;
+#pragma unroll
+    for (int s = 0; s < kMaxM; ++s) {
+      if (s == m && s < Kp) {
+        oi = sel_k[s] & 0x3fffffff;
+        const bool va = (sel_k[s] & (1 << 30)) != 0;
+        ov = va ? 1 : 0;
+        ob = va ? (logp[s] - mu) * a.inv_sigma : 0.f;
+      }
+    }
+    a.idx[(int64_t)b * a.Kout + m] = oi;
+    a.bias[(int64_t)b * a.Kout + m] = ob;
+    if (a.valid) a.valid[(int64_t)b * a.Kout + m] = ov;
+  }
+}
+
+}  // namespace dash
+
+extern "C" int dash_decode_route(const float* idx_q, int64_t iq_sb, const float* idx_k,
+                                 int64_t ik_sb, int64_t ik_st, int64_t ik_sp,
+                                 const int32_t* block_table, int64_t table_stride,
+                                 int page_size, const int32_t* seq_lens, int S,
+                                 const float* head_cls, int refresh_tail, float* kbar,
+                                 int64_t kb_sb, int nblk_cap, const uint8_t* cand,
+                                 int64_t cand_stride, int B, int d, int block_size,
+                                 int local_blocks, float idx_scale, float floor_p, float sigma,
+                                 int K, int topm, int Kout, int32_t* idx, float* bias,
+                                 uint8_t* valid, float* z, int64_t z_stride, void* stream) {
+  using namespace dash;
+  if (!idx_q || !idx_k || !head_cls || !kbar || !idx || !bias || !z) return kErrInvalid;
+  if (B < 0 || d <= 0 || d > 256 || block_size <= 0 || block_size > 256) return kErrUnsupported;
+  if (topm < 1 || topm > kMaxM) return kErrUnsupported;
+  if (K < 1 || Kout < std::min(K, topm)) return kErrInvalid;
+  if (nblk_cap <= 0 || nblk_cap > kDrMaxBlocks) return kErrUnsupported;
+  if (block_table && page_size <= 0) return kErrInvalid;
+  if (d % 16 != 0 || kb_sb % 4 != 0 || (uintptr_t)kbar % 16 != 0) return kErrUnsupported;
+  if (ik_st % 4 != 0 || ik_sp % 4 != 0 || ik_sb % 4 != 0 || (uintptr_t)idx_k % 16 != 0 ||
+      (uintptr_t)head_cls % 16 != 0)
+    return kErrUnsupported;
+  if (B == 0) return kOk;
+  DecodeRouteArgs a;
+  a.idx_q = idx_q; a.iq_sb = iq_sb;
+  a.idx_k = idx_k;
+  a.lay_k = SeqLayout{nullptr, block_table, table_stride, ik_sb, ik_sp, ik_st, page_size};
+  a.lens = seq_lens; a.S = S;
+  a.head_cls = head_cls; a.refresh_tail = refresh_tail;
+  a.kbar = kbar; a.kb_sb = kb_sb; a.nblk_cap = nblk_cap;
+  a.cand = cand; a.cand_stride = cand_stride;
+  a.d = d; a.bs = block_size; a.local_blocks = local_blocks;
+  a.inv_sqrt_d = (float)(1.0 / sqrt((double)d));
+  a.idx_scale = idx_scale; a.floor_p = floor_p; a.inv_sigma = (float)(1.0 / (double)sigma);
+  a.K = K; a.topm = topm; a.Kout = Kout;
+  a.idx = idx; a.bias = bias; a.valid = valid;
+  a.z = z; a.z_stride = z_stride;
+  hipLaunchKernelGGL(decode_route_kernel, dim3(B), dim3(kDrThreads), 0, (hipStream_t)stream, a);
+  return launch_status();
+}

@@ -5,6 +5,7 @@ outputs with torch (the library allocates nothing) and calls one C entry point
 on the current HIP stream.  CPU tensors are rejected: the product has no CPU path.
 """
 
+import ctypes
 import math
 
 import torch
@@ -165,11 +166,34 @@ def route(z, cand, idx_scale, floor, sigma, K, topm, row_nblk=None, width=None):
     return idx.view(*lead, Kp), bias.view(*lead, Kp), valid.view(*lead, Kp).bool()
 
 
+DENSE_THRESHOLD = 24   # of the 128 queries of a tile; below it a routed block goes sparse
+
+_WORKSPACES = {}
+
+
+def zeroed_workspace(key, nbytes, device):
+    """A cached device buffer of at least `nbytes`, zero-filled when (re)allocated.
+    The kernels using it leave their counters at zero, so it is reused as is.
+    Calls that share it are ordered on the current stream."""
+    k = (key, str(device))
+    buf = _WORKSPACES.get(k)
+    if buf is None or buf.numel() < nbytes:
+        if buf is not None:
+            del _WORKSPACES[k]
+            del buf
+        buf = torch.zeros(int(nbytes * 1.1) + 4096, dtype=torch.uint8, device=device)
+        _WORKSPACES[k] = buf
+    return buf
+
+
 def attn_prefill(q, k, v, idx, bias, valid, block_size, local_window, scale,
-                 cu_seqlens=None, kmin=None, return_lse=False):
+                 cu_seqlens=None, kmin=None, return_lse=False, dense_threshold=None,
+                 max_seqlen=None):
     """Block-sparse prefill attention.  q/k/v bf16 [B,H,S,D] (any strides with a
     contiguous head dim) or [1,H,T,D] with cu_seqlens; idx/bias/valid [B,S,K] (or
-    [T,K]).  Returns o [B,H,S,D] bf16 (and lse [B,S,H] fp32)."""
+    [T,K]).  Returns o [B,H,S,D] bf16 (and lse [B,S,H] fp32).
+    dense_threshold: routed blocks shared by fewer queries of a 128-query tile take
+    the block-major sparse path (<= 0: all routed blocks with the tile)."""
     _need_gpu(q, k, v)
     lib = _lib.load()
     if q.dtype != torch.bfloat16:
@@ -190,9 +214,21 @@ def attn_prefill(q, k, v, idx, bias, valid, block_size, local_window, scale,
         if B != 1:
             raise ValueError("varlen prefill takes q of shape [1, H, T, D]")
         nb = cu.numel() - 1
-        Smax = int((cu[1:] - cu[:-1]).max().item()) if nb > 0 else 0
+        if max_seqlen is None:
+            max_seqlen = int((cu[1:] - cu[:-1]).max().item()) if nb > 0 else 0
+        Smax = int(max_seqlen)
+        rows = S
     else:
         Smax = S
+        rows = B * S
+    thr = DENSE_THRESHOLD if dense_threshold is None else int(dense_threshold)
+    ws, ws_n = None, 0
+    if thr > 0 and K > 0 and block_size <= 64 and rows > 0:
+        nbytes = ctypes.c_int64(0)
+        _lib.check(lib.dash_attn_prefill_workspace_size(nb, H, Smax, rows, K, D, int(block_size),
+                                                        nbytes), "workspace")
+        ws = zeroed_workspace("prefill", nbytes.value, q.device)
+        ws_n = ws.numel()
     km = _i32(kmin)
     st_ = lib.dash_attn_prefill(
         _ptr(q), q.stride(0), q.stride(1), q.stride(2),
@@ -201,15 +237,15 @@ def attn_prefill(q, k, v, idx, bias, valid, block_size, local_window, scale,
         _ptr(o), o.stride(0), o.stride(1), o.stride(2),
         _ptr(lse), H, 1,
         _ptr(idx_c), _ptr(valid_c), _ptr(bias_c), K, _ptr(cu), _ptr(km),
-        nb, H, Smax, D, int(block_size), int(local_window), float(scale), _stream())
+        nb, H, Smax, D, int(block_size), int(local_window), float(scale),
+        thr, rows, _ptr(ws), ws_n, _stream())
     _lib.check(st_, "dash_attn_prefill")
     return (o, lse) if return_lse else o
 
 
-def default_nsplit(B, H, nunits):
-    """Split count so that B*H*nsplit fills the 256 CUs several times over."""
-    want = max(1, (1024 + B * H - 1) // max(1, B * H))
-    return int(max(1, min(want, nunits)))
+def default_nsplit(nunits):
+    """One unit (key block) per wavefront, at most 64 partials per (b, h)."""
+    return int(max(1, min(64, nunits)))
 
 
 def attn_decode(q, k, v, idx, bias, valid, block_size, local_window, scale, seq_lens=None,
@@ -247,11 +283,10 @@ def attn_decode(q, k, v, idx, bias, valid, block_size, local_window, scale, seq_
     bias_c = None if bias is None else bias.float().contiguous()
     valid_c = _u8(valid)
     if nsplit is None:
-        nunits = (local_window + block_size - 1) // block_size + 1 + K
-        nsplit = default_nsplit(B, H, nunits)
-    ws_bytes = ctypes_int64()
+        nsplit = default_nsplit((local_window + block_size - 1) // block_size + 1 + K)
+    ws_bytes = ctypes.c_int64(0)
     _lib.check(lib.dash_attn_decode_workspace_size(B, H, D, nsplit, ws_bytes), "workspace")
-    ws = torch.empty(max(1, ws_bytes.value // 4), dtype=torch.float32, device=q.device)
+    ws = torch.empty((ws_bytes.value + 3) // 4, dtype=torch.float32, device=q.device)
     out = torch.empty(B, H, D, dtype=out_dtype, device=q.device)
     lse = torch.empty(B, H, dtype=torch.float32, device=q.device) if return_lse else None
     lens = _i32(seq_lens)
@@ -271,9 +306,51 @@ def attn_decode(q, k, v, idx, bias, valid, block_size, local_window, scale, seq_
     return (out, lse) if return_lse else out
 
 
-def ctypes_int64():
-    import ctypes
-    return ctypes.c_int64(0)
+def decode_route(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, idx_scale,
+                 floor, sigma, K, topm, seq_lens=None, block_table=None, page_size=None,
+                 cand=None, refresh_tail=True, width=None, return_scores=False):
+    """Decode routing for one query per sequence (the last cached token): refreshes the
+    tail block of `kbar_cache` [B, nblk_cap, d] in place, scores and routes.
+    idx_q [B,d] or [B,1,d]; idx_k contiguous [B,S,d] or paged [pages, page_size, d].
+    Returns idx int32 [B,1,K'], bias fp32, valid bool (and the scores [B,nblk_cap])."""
+    _need_gpu(idx_q, idx_k, kbar_cache)
+    lib = _lib.load()
+    if idx_q.dim() == 3:
+        idx_q = idx_q[:, 0]
+    idx_q = idx_q.float().contiguous()
+    idx_k = idx_k.float()
+    if idx_k.stride(-1) != 1:
+        idx_k = idx_k.contiguous()
+    B, d = idx_q.shape
+    nblk_cap = kbar_cache.shape[1]
+    if block_table is not None:
+        bt = _i32(block_table)
+        S = bt.shape[1] * page_size
+        sb, st, sp = 0, idx_k.stride(1), idx_k.stride(0)
+    else:
+        bt = None
+        S = idx_k.shape[1]
+        sb, st, sp = idx_k.stride(0), idx_k.stride(1), 0
+    Kw = max(1, min(int(K), int(topm))) if width is None else int(width)
+    if seq_lens is None and width is None:
+        Kw = max(1, min(int(K), max(1, min(int(topm), (S + block_size - 1) // block_size))))
+    idx = torch.empty(B, Kw, dtype=torch.int32, device=idx_q.device)
+    bias = torch.empty(B, Kw, dtype=torch.float32, device=idx_q.device)
+    valid = torch.empty(B, Kw, dtype=torch.uint8, device=idx_q.device)
+    z = torch.empty(B, nblk_cap, dtype=torch.float32, device=idx_q.device)
+    lens = _i32(seq_lens)
+    c2 = None if cand is None else _u8(cand.reshape(B, -1))
+    hc = head_cls.float().contiguous()
+    st_ = lib.dash_decode_route(
+        _ptr(idx_q), idx_q.stride(0), _ptr(idx_k), sb, st, sp, _ptr(bt),
+        0 if bt is None else bt.stride(0), int(page_size or 0), _ptr(lens), S, _ptr(hc),
+        int(bool(refresh_tail)), _ptr(kbar_cache), kbar_cache.stride(0), nblk_cap, _ptr(c2),
+        0 if c2 is None else c2.stride(0), B, d, int(block_size), int(local_blocks),
+        float(idx_scale), float(floor), float(sigma), int(K), int(topm), Kw, _ptr(idx),
+        _ptr(bias), _ptr(valid), _ptr(z), z.stride(0), _stream())
+    _lib.check(st_, "dash_decode_route")
+    res = (idx[:, None], bias[:, None], valid[:, None].bool())
+    return res + (z,) if return_scores else res
 
 
 def inv_sqrt(d):

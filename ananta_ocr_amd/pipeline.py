@@ -58,32 +58,18 @@ def decode_step(state, q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks
                 page_size=None, out_dtype=torch.float32, nsplit=None, block_cand=None,
                 return_routing=False):
     """One decode step for the query at the last cached token of each sequence.
-    The newest token is already in k/v and idx_k; its block's summary is refreshed."""
+    The newest token is already in k/v and idx_k; its block's summary is refreshed
+    inside the fused decode router."""
     D = q.shape[-1]
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    B = q.shape[0]
-    nblk = state.kbar.shape[1]
-    ops.kbar(idx_k, head_cls, block_size, seq_lens=seq_lens, nblk_cap=nblk, tail_only=True,
-             out=state.kbar, block_table=block_table, page_size=page_size)
-    S = k.shape[2] if block_table is None else block_table.shape[1] * page_size
-    if seq_lens is None:
-        q_pos = None
-        z = ops.block_scores(idx_q, state.kbar, block_size, local_blocks,
-                             q_pos=torch.full((B,), S - 1, dtype=torch.int32,
-                                              device=q.device), S=S)
-    else:
-        q_pos = (seq_lens - 1).to(torch.int32)
-        z = ops.block_scores(idx_q, state.kbar, block_size, local_blocks, q_pos=q_pos,
-                             seq_lens=seq_lens, S=S)
-    row_nblk = None
-    if seq_lens is not None:
-        row_nblk = ((seq_lens + block_size - 1) // block_size).to(torch.int32)
-    width = max(1, min(int(K), int(topm)))
-    idx, bias, valid = ops.route(z, block_cand, idx_scale, floor, sigma, K, topm,
-                                 row_nblk=row_nblk, width=width)
+    width = None if seq_lens is None else max(1, min(int(K), int(topm)))
+    idx, bias, valid = ops.decode_route(idx_q, idx_k, head_cls, state.kbar, block_size,
+                                        local_blocks, idx_scale, floor, sigma, K, topm,
+                                        seq_lens=seq_lens, block_table=block_table,
+                                        page_size=page_size, cand=block_cand, width=width)
     out = ops.attn_decode(q, k, v, idx[:, 0], bias[:, 0], valid[:, 0], block_size,
-                          local_blocks * block_size, scale, seq_lens=seq_lens, q_pos=q_pos,
+                          local_blocks * block_size, scale, seq_lens=seq_lens,
                           block_table=block_table, page_size=page_size, out_dtype=out_dtype,
                           nsplit=nsplit)
     if return_routing:

@@ -107,9 +107,16 @@ int dash_route(const float* z, int64_t z_stride, int rows, int nblk_cols,
  * Replaces triton_gather_attention_e2e / _e2e_attn_fwd_kernel
  * (sparse_gather_e2e_triton.py:34-115, :342-391) and, with bias = 0 and kmin = the
  * packing segment start, triton_gather_attention (sparse_gather_triton.py:29-104,
- * :343-392).  q/k/v/o [B, H, S, D] by strides (or varlen via cu_seqlens);
- * lse (optional) fp32 at lse[token_row*lse_row + h*lse_sh].  D == 128,
+ * :343-392).  q/k/v/o [B, H, S, D] by strides (or varlen via cu_seqlens, S = the longest
+ * sequence); lse (optional) fp32 at lse[token_row*lse_row + h*lse_sh].  D == 128,
  * block_size in {32, 64, ..., 256}, K <= 16.
+ * dense_threshold > 0 (block_size <= 64): routed blocks selected by fewer than
+ * dense_threshold of the 128 queries of a tile go through the block-major sparse path,
+ * which needs `workspace` (dash_attn_prefill_workspace_size bytes, 256-byte aligned; its
+ * leading block counters must be zero before the first call and are left zero by every
+ * call) and total_rows (B*S, or cu_seqlens[B]).  dense_threshold <= 0: no workspace,
+ * every routed block of a tile is processed with the tile.  Calls sharing a workspace
+ * must not overlap.
  */
 int dash_attn_prefill(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                       const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
@@ -119,7 +126,33 @@ int dash_attn_prefill(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                       const int32_t* idx, const uint8_t* valid, const float* bias, int K,
                       const int32_t* cu_seqlens, const int32_t* kmin,
                       int B, int H, int S, int D, int block_size, int local_window,
-                      float scale, void* stream);
+                      float scale, int dense_threshold, int64_t total_rows,
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes of the sparse path of dash_attn_prefill. */
+int dash_attn_prefill_workspace_size(int B, int H, int S_max, int64_t total_rows, int K, int D,
+                                     int block_size, int64_t* bytes);
+
+/*
+ * Decode router, one query per sequence (the last cached token, q_pos = seq_lens[b]-1):
+ * refreshes k_bar of the tail block (refresh_tail = 1), scores every block of the
+ * sequence and routes the row exactly as dash_route does.  Replaces the decode routing of
+ * _dash_decode_forward (modeling_deepseekv2.py:481-496: _block_scores_infer over the whole
+ * index-key cache + _infer_route_select), keeping the summaries of complete blocks cached.
+ *   idx_q    fp32 [B, d] rows (iq_sb); idx_k index-key cache addressed like dash_kbar
+ *   kbar     [B, nblk_cap, d] fp32 cache (updated in place at the tail block)
+ *   z        [B, z_stride] fp32 scores (written, for inspection)
+ *   One 1024-thread work-group per sequence.  nblk_cap <= 2048, d <= 256.
+ */
+int dash_decode_route(const float* idx_q, int64_t iq_sb, const float* idx_k,
+                      int64_t ik_sb, int64_t ik_st, int64_t ik_sp,
+                      const int32_t* block_table, int64_t table_stride, int page_size,
+                      const int32_t* seq_lens, int S, const float* head_cls, int refresh_tail,
+                      float* kbar, int64_t kb_sb, int nblk_cap, const uint8_t* cand,
+                      int64_t cand_stride, int B, int d, int block_size, int local_blocks,
+                      float idx_scale, float floor_p, float sigma, int K, int topm, int Kout,
+                      int32_t* idx, float* bias, uint8_t* valid, float* z, int64_t z_stride,
+                      void* stream);
 
 /* Workspace bytes dash_attn_decode needs for (B, H, D, nsplit). */
 int dash_attn_decode_workspace_size(int B, int H, int D, int nsplit, int64_t* bytes);
@@ -130,8 +163,9 @@ int dash_attn_decode_workspace_size(int B, int H, int D, int nsplit, int64_t* by
  * Replaces _decode_attend (modeling_deepseekv2.py:424-451) as called by
  * _dash_decode_forward (:454-500).  Cache: contiguous [B, H, S, D] (k_sb, k_sh, k_st) or
  * paged [pages, page_size, H, D] (k_sp, k_st, k_sh + block_table).  Split-K over nsplit
- * work-groups per (b, h) then a log-sum-exp merge.  out [B, H, D] fp32 (out_bf16 = 0)
+ * (<= 64) wavefronts per (b, h), then a merge kernel.  out [B, H, D] fp32 (out_bf16 = 0)
  * or bf16, lse optional.  D == 128, block_size 32 or a multiple of 64, K <= 16.
+ * workspace: dash_attn_decode_workspace_size bytes (the split partials), 16-byte aligned.
  */
 int dash_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
                      const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t k_sp,

@@ -193,35 +193,41 @@ def _attn_inputs(seed, B, H, S, bs, lw, K, qscale=1.0, dup=False):
     return q, k, v, idx.clamp(max=nblk - 1), bias, valid
 
 
+@pytest.mark.parametrize("thr", [0, 1, 24, 129])   # all tile / mixed / all sparse
 @pytest.mark.parametrize("B,H,S,bs,lw,K,qs", [
     (1, 2, 300, 64, 128, 4, 3.0),
     (2, 3, 700, 64, 512, 8, 1.0),
     (1, 2, 513, 32, 100, 6, 3.0),     # window not a block multiple, bs 32
-    (1, 1, 1100, 128, 256, 3, 2.0),   # bs 128
+    (1, 1, 1100, 128, 256, 3, 2.0),   # bs 128 (tile path only)
     (1, 2, 64, 64, 512, 4, 1.0),      # window covers everything
+    (1, 2, 3000, 64, 256, 16, 2.0),   # many remote blocks per tile
 ])
-def test_prefill_attention_matches_oracle(B, H, S, bs, lw, K, qs):
+def test_prefill_attention_matches_oracle(B, H, S, bs, lw, K, qs, thr):
     q, k, v, idx, bias, valid = _attn_inputs(300 + S, B, H, S, bs, lw, K, qscale=qs)
     scale = 1 / math.sqrt(128)
     ref = O.dense_attend(q, k, v, idx, bias, valid, bs, lw, scale)
     out, lse = ops.attn_prefill(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), bias.to(DEV),
-                                valid.to(DEV), bs, lw, scale, return_lse=True)
-    _close(out, ref, "prefill")
+                                valid.to(DEV), bs, lw, scale, return_lse=True,
+                                dense_threshold=thr)
+    _close(out, ref, f"prefill thr={thr}")
     assert torch.isfinite(lse).all()
 
 
-def test_prefill_duplicates_and_strided_inputs():
+@pytest.mark.parametrize("thr", [0, 1, 129])
+def test_prefill_duplicates_and_strided_inputs(thr):
     B, H, S, bs, lw, K = 1, 2, 400, 64, 128, 4
     q, k, v, idx, bias, valid = _attn_inputs(310, B, H, S, bs, lw, K, qscale=2.0, dup=True)
     scale = 1 / math.sqrt(128)
     ref = O.dense_attend(q, k, v, idx, bias, valid, bs, lw, scale)
     # [B,S,H,D] storage viewed as [B,H,S,D]
     qs_, ks_, vs_ = (t.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for t in (q, k, v))
-    out = ops.attn_prefill(qs_, ks_, vs_, idx.to(DEV), bias.to(DEV), valid.to(DEV), bs, lw, scale)
+    out = ops.attn_prefill(qs_, ks_, vs_, idx.to(DEV), bias.to(DEV), valid.to(DEV), bs, lw, scale,
+                           dense_threshold=thr)
     _close(out, ref, "prefill strided")
 
 
-def test_prefill_segment_start():
+@pytest.mark.parametrize("thr", [0, 129])
+def test_prefill_segment_start(thr):
     B, H, S, bs, lw, K = 1, 2, 600, 64, 128, 5
     q, k, v, idx, bias, valid = _attn_inputs(320, B, H, S, bs, lw, K, qscale=2.0)
     kmin = torch.zeros(1, S, dtype=torch.long)
@@ -229,11 +235,12 @@ def test_prefill_segment_start():
     scale = 1 / math.sqrt(128)
     ref = O.dense_attend(q, k, v, idx, bias, valid, bs, lw, scale, kmin=kmin)
     out = ops.attn_prefill(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), bias.to(DEV),
-                           valid.to(DEV), bs, lw, scale, kmin=kmin.to(DEV))
+                           valid.to(DEV), bs, lw, scale, kmin=kmin.to(DEV), dense_threshold=thr)
     _close(out, ref, "prefill kmin")
 
 
-def test_prefill_varlen_block_diagonal():
+@pytest.mark.parametrize("thr", [0, 24, 129])
+def test_prefill_varlen_block_diagonal(thr):
     g = _gen(330)
     cu = [0, 273, 273 + 819, 273 + 819 + 64, 273 + 819 + 64 + 1000]
     T, H, bs, lw, K = cu[-1], 2, 64, 256, 4
@@ -250,7 +257,8 @@ def test_prefill_varlen_block_diagonal():
         valid[0, cu[b]:cu[b + 1]] &= (t // bs - lb >= 0)[:, None]
     out = ops.attn_prefill(q.to(DEV), k.to(DEV), v.to(DEV), idx[0].to(DEV), bias[0].to(DEV),
                            valid[0].to(DEV), bs, lw, scale,
-                           cu_seqlens=torch.tensor(cu, dtype=torch.int32).to(DEV))
+                           cu_seqlens=torch.tensor(cu, dtype=torch.int32).to(DEV),
+                           dense_threshold=thr)
     for b in range(len(cu) - 1):
         s0, s1 = cu[b], cu[b + 1]
         ref = O.dense_attend(q[:, :, s0:s1], k[:, :, s0:s1], v[:, :, s0:s1], idx[:, s0:s1],
@@ -310,7 +318,7 @@ def _decode_ref(q, k, v, idx, bias, valid, lens, bs, lw, scale):
     return torch.cat(outs)
 
 
-@pytest.mark.parametrize("nsplit", [None, 1, 3])
+@pytest.mark.parametrize("nsplit", [None, 1, 3, 20, 64])
 def test_decode_contiguous_matches_oracle(nsplit):
     B, H, S, bs, lw, K = 3, 2, 3000, 64, 1024, 16
     lens = torch.tensor([3000, 1500, 1100], dtype=torch.int32)
@@ -360,3 +368,114 @@ def test_decode_equals_prefill_last_row():
     dec = ops.attn_decode(q[:, :, -1].to(DEV), k.to(DEV), v.to(DEV), idx[:, -1].to(DEV),
                           bias[:, -1].to(DEV), valid[:, -1].to(DEV), bs, lw, scale).cpu()
     _close(dec, pre[:, :, -1], "decode vs prefill", tight=2e-2)
+
+
+# ------------------------------------------------------------------ fused decode router
+
+def _decode_route_check(ik_seq, iq, lens, bs, lb, K, topm, hc, cand=None, paged=None):
+    """ik_seq: list of per-sequence idx_k [L_b, d] (CPU).  The k_bar cache starts from
+    the summaries of all complete blocks (the tail block is left stale on purpose)."""
+    B = len(ik_seq)
+    d = iq.shape[-1]
+    nblk_cap = max((int(L) + bs - 1) // bs for L in lens)
+    kb0 = torch.zeros(B, nblk_cap, d)
+    refs = []
+    for b in range(B):
+        kb_r, _ = O.kbar_headcls(ik_seq[b][None], hc, bs)
+        refs.append(kb_r[0])
+        n = kb_r.shape[1]
+        kb0[b, :n - 1] = kb_r[0, :n - 1]          # tail block stale (zeros)
+    if paged is None:
+        S = max(int(L) for L in lens)
+        ik = torch.zeros(B, S, d)
+        for b in range(B):
+            ik[b, :int(lens[b])] = ik_seq[b]
+        kw = {}
+        ik_dev = ik.to(DEV)
+    else:
+        pages, table = paged
+        ik_dev = pages.to(DEV)
+        kw = dict(block_table=table.to(DEV), page_size=bs)
+    kb = kb0.to(DEV)
+    ti, bi, va, z = ops.decode_route(iq.to(DEV), ik_dev, hc.to(DEV), kb, bs, lb, W.IDX_SCALE,
+                                     W.FLOOR, W.SIGMA, K, topm,
+                                     seq_lens=torch.tensor(lens, dtype=torch.int32).to(DEV),
+                                     cand=None if cand is None else cand.to(DEV),
+                                     return_scores=True, **kw)
+    ti, bi, va, z, kb = ti.cpu(), bi.cpu(), va.cpu(), z.cpu(), kb.cpu()
+    for b in range(B):
+        L = int(lens[b])
+        n = (L + bs - 1) // bs
+        torch.testing.assert_close(kb[b, n - 1], refs[b][n - 1], atol=1e-5, rtol=1e-5)
+        zr = O.block_scores_headcls(iq[b:b + 1, None], refs[b][None], torch.ones(1, n, dtype=torch.bool),
+                                    torch.tensor([[L - 1]]), bs, lb)[0, 0]
+        sent = zr == O.SCORE_NEG
+        assert torch.equal(z[b, :n] == O.SCORE_NEG, sent)
+        torch.testing.assert_close(z[b, :n][~sent], zr[~sent], atol=1e-7, rtol=1e-5)
+        # routing bit-exact on the kernel's own scores
+        cb = None if cand is None else cand[b:b + 1, None, :n]
+        t_r, b_r, v_r = O.infer_route_select(z[b:b + 1, None, :n], cb, W.IDX_SCALE, W.FLOOR,
+                                             W.SIGMA, K, topm)
+        kp = t_r.shape[-1]
+        assert torch.equal(va[b, 0, :kp], v_r[0, 0]), b
+        assert torch.equal(ti[b, 0, :kp].long(), t_r[0, 0]), b
+        torch.testing.assert_close(bi[b, 0, :kp], b_r[0, 0], atol=2e-5, rtol=1e-5)
+        assert (ti[b, 0, kp:] == -1).all() and not va[b, 0, kp:].any()
+
+
+@pytest.mark.parametrize("hc_scale,scale", [(0.0, 1.0), (1.5, 30.0)])
+def test_decode_route_contiguous(hc_scale, scale):
+    g = _gen(500)
+    lens = [27300, 5000, 1100, 640, 1]
+    d, bs, lb = 128, 64, 16
+    ik_seq = [torch.randn(L, d, generator=g) * 0.1 for L in lens]
+    iq = torch.randn(len(lens), d, generator=g) * scale
+    hc = torch.randn(d, generator=g) * hc_scale
+    _decode_route_check(ik_seq, iq, lens, bs, lb, 16, 16, hc)
+
+
+def test_decode_route_paged_with_candidates():
+    g = _gen(501)
+    lens = [3000, 2049, 700]
+    d, bs, lb = 128, 64, 4
+    ik_seq = [torch.randn(L, d, generator=g) for L in lens]
+    iq = torch.randn(len(lens), d, generator=g) * 10
+    npg = [(L + bs - 1) // bs for L in lens]
+    perm = torch.randperm(sum(npg), generator=g)
+    table = torch.zeros(len(lens), max(npg), dtype=torch.int32)
+    pages = torch.zeros(sum(npg), bs, d)
+    o = 0
+    for b, L in enumerate(lens):
+        for p in range(npg[b]):
+            ph = int(perm[o + p])
+            table[b, p] = ph
+            seg = ik_seq[b][p * bs:min((p + 1) * bs, L)]
+            pages[ph, :seg.shape[0]] = seg
+        o += npg[b]
+    cand = torch.rand(len(lens), max(npg), generator=g) < 0.3
+    cand[2] = False                             # falls back to every remote block
+    _decode_route_check(ik_seq, iq, lens, bs, lb, 8, 12, torch.zeros(d), cand=cand,
+                        paged=(pages, table))
+
+
+def test_decode_step_pipeline_matches_oracle():
+    """decode_step (fused router + split-K attention) against the oracle decode path."""
+    from ananta_ocr_amd import pipeline
+    cfg = W.Decode("small", 3, 4000, 64, 1024, 16, seed=9)
+    d = W.make_decode(cfg)
+    hc = torch.zeros(128)
+    nblk = (cfg.S + cfg.bs - 1) // cfg.bs
+    st = pipeline.init_decode_state(d["idx_k"].to(DEV), hc.to(DEV), cfg.bs, nblk)
+    scale = 1 / math.sqrt(128)
+    out, (ti, bi, va) = pipeline.decode_step(
+        st, d["q"].to(DEV), d["k"].to(DEV), d["v"].to(DEV), d["idx_q"].to(DEV),
+        d["idx_k"].to(DEV), hc.to(DEV), cfg.bs, cfg.lw // cfg.bs, W.IDX_SCALE * 50, W.FLOOR,
+        W.SIGMA, cfg.cap, cfg.cap, scale, return_routing=True)
+    ref, t_r, b_r, v_r = O.decode_pipeline(d["q"][:, :, None], d["k"], d["v"], d["idx_q"],
+                                           d["idx_k"], hc, cfg.bs, cfg.lw // cfg.bs,
+                                           W.IDX_SCALE * 50, W.FLOOR, W.SIGMA, cfg.cap, cfg.cap,
+                                           scale)
+    # the oracle routes its own scores: compare ids as sets where both are valid
+    assert torch.equal(va.cpu(), v_r)
+    assert torch.equal(ti.cpu().long(), t_r)
+    _close(out, ref[:, :, 0], "decode step")
