@@ -33,6 +33,11 @@ enum Status : int {
 
 __device__ __forceinline__ float bf2f(bf16 x) { return (float)x; }
 
+// 2^x with the bare v_exp_f32 (no denormal range fix-up): the attention softmax
+// only feeds it x <= small positive values and needs no denormal results;
+// -inf gives 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ __forceinline__ int wave_lane() { return threadIdx.x & (kWave - 1); }
 
 template <typename T>

@@ -152,13 +152,13 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeArgs a) {
       mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
       const float m_new = fmaxf(m_run, mloc);
       const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = exp2f(m_run - m_use);
+      const float alpha = fast_exp2(m_run - m_use);
       l_run *= alpha;
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] *= alpha;
 #pragma unroll
       for (int st = 0; st < 16; ++st) {
-        const float p = exp2f(s[st] - m_use);
+        const float p = fast_exp2(s[st] - m_use);
         l_run += p;
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = fmaf(p, bf2f(vr[st][e]), o[e]);
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
   if (lane < a.nsplit) { ms = pb[lane * (D + 2) + D]; lsum = pb[lane * (D + 2) + D + 1]; }
   const float M = wave_max(ms);
   const float Mu = (M == -INFINITY) ? 0.f : M;
-  const float w = lane < a.nsplit ? exp2f(ms - Mu) : 0.f;
+  const float w = lane < a.nsplit ? fast_exp2(ms - Mu) : 0.f;
   const float L = wave_sum(lsum * w);
   sW[lane] = w;
   __syncthreads();

@@ -29,7 +29,6 @@
 namespace dash {
 
 constexpr int kPfTQ = 128;        // queries per tile work-group
-constexpr int kPfKT = 32;         // keys per LDS tile in the tile kernel
 constexpr int kPfMaxK = 16;       // routed slots per query
 constexpr int kPfMaxBlocks = 2048;
 constexpr int kPfCH = 128;        // pairs per sparse chunk
@@ -50,7 +49,8 @@ struct PrefillArgs {
   uint8_t* kind;                       // [rows, K]: 0 skip, 1 tile (dense), 2 sparse
   int dense_threshold;
   int32_t* blk_count;                  // [B, nblk_cap]  zero between calls
-  int32_t* blk_fill;                   // [B, nblk_cap]
+  int32_t* tile_base;                  // [B, ntiles_cap, nblk_cap] offset of a tile's pairs
+  int ntiles_cap;
   int32_t* blk_off;                    // [B, nblk_cap]
   int32_t* num_chunks;                 // [B]
   int4* chunk_tab;                     // [B, chunk_cap]: block, start, count
@@ -98,26 +98,41 @@ __device__ __forceinline__ floatx16 qk_tile(const bf16 (*sK)[LDK], int krow0, co
   return s;
 }
 
-// acc_o[dt] += V^T (keys key0 .. key0+15 of the LDS tile) * P^T (pop)
+// acc_o[dt] += V^T P^T over keys kbase .. kbase+15 of a row-major LDS V tile.
+// ds_read_tr16_b64 (gfx950): within each 16-lane group, result lane i element j
+// is element (i % 4) of the 8 bytes read by lane 4j + i/4.  Lane l reads the 4
+// dims 32dt + 16((l/16)%2) + 4(l%4) .. +3 of key row kbase + 4hl + (l%16)/4 (and
+// +8), which gives every lane the 8 keys kbase + 8(e/4) + 4hl + e%4 of its dim
+// row m = l % 32: the same key order as the P^T operand built from S^T.
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4;
+
 template <int D, int LDV>
-__device__ __forceinline__ void pv_slice(const bf16 (*sVt)[LDV], int key0, const bf16x8& pop,
-                                         floatx16 (&acc_o)[D / 32], int n, int hl) {
+__device__ __forceinline__ void pv_slice_tr(const bf16 (*sV)[LDV], int kbase, const bf16x8& pop,
+                                            floatx16 (&acc_o)[D / 32], int lane) {
+  const int hl = lane >> 5;
+  const int row = kbase + 4 * hl + ((lane & 15) >> 2);
+  const int colq = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) {
-    const bf16* vrow = &sVt[dt * 32 + n][key0 + 4 * hl];
-    const bf16x4 lo = *(const bf16x4*)vrow;
-    const bf16x4 hi = *(const bf16x4*)(vrow + 8);
+    const int col = dt * 32 + colq;
+    const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_short4*)(__attribute__((address_space(3))) void*)&sV[row][col]);
+    const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_short4*)(__attribute__((address_space(3))) void*)&sV[row + 8][col]);
     bf16x8 vop;
+    const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo);
+    const bf16x4 h4 = __builtin_bit_cast(bf16x4, hi);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) { vop[e] = lo[e]; vop[e + 4] = hi[e]; }
+    for (int e = 0; e < 4; ++e) { vop[e] = l4[e]; vop[e + 4] = h4[e]; }
     acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pop, acc_o[dt], 0, 0, 0);
   }
 }
 
-// Stage rows j0 .. j0+nrows-1 of K (row-major) and V (transposed) into LDS;
-// rows at or beyond len are zero.  nrows * D / 8 chunks over 256 threads.
+// Stage rows j0 .. j0+nrows-1 of K and V (both row-major) into LDS; rows at or
+// beyond len are zero.  nrows * D / 8 chunks of 16 bytes over 256 threads.
 template <int D, int LDK, int LDV>
-__device__ __forceinline__ void stage_kv(bf16 (*sK)[LDK], bf16 (*sVt)[LDV], const bf16* kb,
+__device__ __forceinline__ void stage_kv(bf16 (*sK)[LDK], bf16 (*sV)[LDV], const bf16* kb,
                                          const bf16* vb, int64_t k_st, int64_t v_st, int j0,
                                          int nrows, int len, int tid) {
   const int nchunks = nrows * (D / 8);
@@ -133,19 +148,38 @@ __device__ __forceinline__ void stage_kv(bf16 (*sK)[LDK], bf16 (*sVt)[LDV], cons
       for (int e = 0; e < 8; ++e) { kv8[e] = (bf16)0.f; vv8[e] = (bf16)0.f; }
     }
     *(bf16x8*)&sK[kr][c8] = kv8;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) sVt[c8 + e][kr] = vv8[e];
+    *(bf16x8*)&sV[kr][c8] = vv8;
   }
 }
 
-// ---------------------------------------------------------------------------
-// Plan: classify every routed (query, slot) of a 128-query tile as skipped,
-// dense (block selected by >= dense_threshold queries of the tile) or sparse,
-// and count the sparse pairs per block.
-// ---------------------------------------------------------------------------
+// Load the K <= 16 routed slots of one row: ids, validity and bias, with
+// vector loads where the row is 16-byte aligned.
+__device__ __forceinline__ void load_row_slots(const PrefillArgs& a, int64_t row, int32_t (&c)[kPfMaxK],
+                                               uint32_t& vmask) {
+  const int64_t p0 = row * a.K;
+  if (a.K == kPfMaxK) {
+    const int4* ip = (const int4*)(a.idx + p0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int4 v = ip[q];
+      c[4 * q] = v.x; c[4 * q + 1] = v.y; c[4 * q + 2] = v.z; c[4 * q + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < kPfMaxK; ++s) c[s] = s < a.K ? a.idx[p0 + s] : -1;
+  }
+  vmask = 0;
+  if (a.valid) {
+#pragma unroll
+    for (int s = 0; s < kPfMaxK; ++s)
+      if (s < a.K && a.valid[p0 + s]) vmask |= 1u << s;
+  } else {
+    vmask = (a.K >= 32) ? 0xffffffffu : ((1u << a.K) - 1u);
+  }
+}
+
 __global__ __launch_bounds__(kPfTQ) void prefill_plan_kernel(PrefillArgs a) {
   __shared__ int32_t sCnt[kPfMaxBlocks];
-  __shared__ int32_t sKept[kPfTQ][kPfMaxK];
   const int b = blockIdx.y, tid = threadIdx.x;
   const int len = seq_len(a, b);
   const int t0 = blockIdx.x * kPfTQ;
@@ -155,39 +189,49 @@ __global__ __launch_bounds__(kPfTQ) void prefill_plan_kernel(PrefillArgs a) {
   __syncthreads();
   const int t = t0 + tid;
   const int64_t row = row0(a, b) + t;
-  int32_t* kept = sKept[tid];
-  uint32_t keep_mask = 0;
+  int32_t c[kPfMaxK];
+  uint32_t vmask = 0, keep_mask = 0;
   if (t < len) {
+    load_row_slots(a, row, c, vmask);
     const int km = a.kmin ? a.kmin[row] : 0;
-    for (int s = 0; s < a.K; ++s) {
-      const int64_t p = row * a.K + s;
-      const int c = a.idx[p];
-      kept[s] = c;
-      if (!slot_usable(a, c, p, t, nblk, km)) continue;
-      bool dup = false;
-      for (int u = 0; u < s; ++u) dup |= ((keep_mask >> u) & 1u) && kept[u] == c;
-      if (dup) continue;
-      keep_mask |= 1u << s;
-      atomicAdd(&sCnt[c], 1);
+    const int ls = t - a.lw + 1;
+#pragma unroll
+    for (int s = 0; s < kPfMaxK; ++s) {
+      bool ok = s < a.K && ((vmask >> s) & 1u) && c[s] >= 0 && c[s] < nblk &&
+                c[s] * a.bs < ls && (c[s] + 1) * a.bs > km;
+#pragma unroll
+      for (int u = 0; u < s; ++u) ok = ok && !(((keep_mask >> u) & 1u) && c[u] == c[s]);
+      if (ok) {
+        keep_mask |= 1u << s;
+        atomicAdd(&sCnt[c[s]], 1);
+      }
     }
   }
   __syncthreads();
+  // one global atomic per sparse block of this tile: reserves the tile's range
+  // in the block's pair list (its base is kept for the scatter kernel)
+  int32_t* tb = a.tile_base + ((int64_t)b * a.ntiles_cap + blockIdx.x) * a.nblk_cap;
+  for (int cc = tid; cc < nblk; cc += kPfTQ) {
+    const int n = sCnt[cc];
+    if (n > 0 && n < a.dense_threshold)
+      tb[cc] = atomicAdd(&a.blk_count[(int64_t)b * a.nblk_cap + cc], n);
+  }
   if (t < len) {
-    for (int s = 0; s < a.K; ++s) {
-      uint8_t kd = 0;
-      if ((keep_mask >> s) & 1u) {
-        const int c = kept[s];
-        kd = sCnt[c] >= a.dense_threshold ? 1 : 2;
-        if (kd == 2) atomicAdd(&a.blk_count[(int64_t)b * a.nblk_cap + c], 1);
-      }
-      a.kind[row * a.K + s] = kd;
+    uint8_t kd[kPfMaxK];
+#pragma unroll
+    for (int s = 0; s < kPfMaxK; ++s) {
+      kd[s] = 0;
+      if ((keep_mask >> s) & 1u) kd[s] = sCnt[c[s]] >= a.dense_threshold ? 1 : 2;
     }
+#pragma unroll
+    for (int s = 0; s < kPfMaxK; ++s)
+      if (s < a.K) a.kind[row * a.K + s] = kd[s];
   }
 }
 
 // ---------------------------------------------------------------------------
 // Scan: per sequence, block offsets of the sparse pairs and the chunk table.
-// Resets the block counters (they are zero between calls) and the fill cursors.
+// Resets the block counters (they are zero between calls).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
   __shared__ int32_t sC[kPfMaxBlocks];
@@ -198,12 +242,11 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
   const int len = seq_len(a, b);
   const int nblk = len > 0 ? (len + a.bs - 1) / a.bs : 0;
   int32_t* cnt = a.blk_count + (int64_t)b * a.nblk_cap;
-  int32_t* fill = a.blk_fill + (int64_t)b * a.nblk_cap;
   // two entries per thread
   int v0 = 0, v1 = 0;
   const int e0 = tid * 2, e1 = tid * 2 + 1;
-  if (e0 < a.nblk_cap) { v0 = e0 < nblk ? cnt[e0] : 0; cnt[e0] = 0; fill[e0] = 0; }
-  if (e1 < a.nblk_cap) { v1 = e1 < nblk ? cnt[e1] : 0; cnt[e1] = 0; fill[e1] = 0; }
+  if (e0 < a.nblk_cap) { v0 = e0 < nblk ? cnt[e0] : 0; cnt[e0] = 0; }
+  if (e1 < a.nblk_cap) { v1 = e1 < nblk ? cnt[e1] : 0; cnt[e1] = 0; }
   const int c0 = (v0 + kPfCH - 1) / kPfCH, c1 = (v1 + kPfCH - 1) / kPfCH;
   int sp = v0 + v1, sc = c0 + c1;
   int ip = sp, ic = sc;
@@ -234,19 +277,33 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
 // Scatter: sparse pairs into per-block lists (order within a block is free).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kPfTQ) void prefill_scatter_kernel(PrefillArgs a) {
+  __shared__ int32_t sFill[kPfMaxBlocks];
   const int b = blockIdx.y, tid = threadIdx.x;
   const int len = seq_len(a, b);
-  const int t = blockIdx.x * kPfTQ + tid;
+  const int t0 = blockIdx.x * kPfTQ;
+  if (t0 >= len) return;
+  const int nblk = (len + a.bs - 1) / a.bs;
+  for (int i = tid; i < nblk; i += kPfTQ) sFill[i] = 0;
+  __syncthreads();
+  const int t = t0 + tid;
   if (t >= len) return;
   const int64_t row = row0(a, b) + t;
   const int64_t base = row0(a, b) * a.K;
-  for (int s = 0; s < a.K; ++s) {
-    const int64_t p = row * a.K + s;
-    if (a.kind[p] != 2) continue;
-    const int c = a.idx[p];
-    const int pos = atomicAdd(&a.blk_fill[(int64_t)b * a.nblk_cap + c], 1);
-    a.pairs[base + a.blk_off[(int64_t)b * a.nblk_cap + c] + pos] = (int32_t)(p - base);
+  const int32_t* tb = a.tile_base + ((int64_t)b * a.ntiles_cap + blockIdx.x) * a.nblk_cap;
+  const int32_t* off = a.blk_off + (int64_t)b * a.nblk_cap;
+  int32_t c[kPfMaxK];
+  uint32_t vmask;
+  load_row_slots(a, row, c, vmask);
+  int pos[kPfMaxK];
+  bool sp[kPfMaxK];
+#pragma unroll
+  for (int s = 0; s < kPfMaxK; ++s) {
+    sp[s] = s < a.K && a.kind[row * a.K + s] == 2;
+    pos[s] = sp[s] ? atomicAdd(&sFill[c[s]], 1) : 0;
   }
+#pragma unroll
+  for (int s = 0; s < kPfMaxK; ++s)
+    if (sp[s]) a.pairs[base + off[c[s]] + tb[c[s]] + pos[s]] = (int32_t)(row * a.K + s - base);
 }
 
 // ---------------------------------------------------------------------------
@@ -255,7 +312,7 @@ __global__ __launch_bounds__(kPfTQ) void prefill_scatter_kernel(PrefillArgs a) {
 template <int D>
 __global__ __launch_bounds__(256) void prefill_sparse_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 sK[64][D + 8];
-  __shared__ __attribute__((aligned(16))) bf16 sVt[D][64 + 8];
+  __shared__ __attribute__((aligned(16))) bf16 sV[64][D + 32];
   const int b = blockIdx.z, h = blockIdx.y, ch = blockIdx.x;
   if (ch >= a.num_chunks[b]) return;
   const int4 e = a.chunk_tab[(int64_t)b * a.chunk_cap + ch];
@@ -266,7 +323,7 @@ __global__ __launch_bounds__(256) void prefill_sparse_kernel(PrefillArgs a) {
   const int64_t r0 = row0(a, b);
   const bf16* kb = seq_ptr(a.k, a.cu, b, a.k_sb, a.k_st) + (int64_t)h * a.k_sh;
   const bf16* vb = seq_ptr(a.v, a.cu, b, a.v_sb, a.v_st) + (int64_t)h * a.v_sh;
-  stage_kv<D, D + 8, 64 + 8>(sK, sVt, kb, vb, a.k_st, a.v_st, c * a.bs, a.bs, len, tid);
+  stage_kv<D, D + 8, D + 32>(sK, sV, kb, vb, a.k_st, a.v_st, c * a.bs, a.bs, len, tid);
 
   const int pi = wv * 32 + n;
   const bool active = pi < npairs;
@@ -314,12 +371,12 @@ __global__ __launch_bounds__(256) void prefill_sparse_kernel(PrefillArgs a) {
       bf16x8 pop[2];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float pr = exp2f(s[sub][r] - mu);
+        const float pr = fast_exp2(s[sub][r] - mu);
         psum += pr;
         pop[r >> 3][r & 7] = (bf16)pr;
       }
-      pv_slice<D, 64 + 8>(sVt, sub * 32, pop[0], acc_o, n, hl);
-      pv_slice<D, 64 + 8>(sVt, sub * 32 + 16, pop[1], acc_o, n, hl);
+      pv_slice_tr<D, D + 32>(sV, sub * 32, pop[0], acc_o, lane);
+      pv_slice_tr<D, D + 32>(sV, sub * 32 + 16, pop[1], acc_o, lane);
     }
   }
   const float l_tot = psum + __shfl_xor(psum, 32, kWave);
@@ -341,11 +398,56 @@ __global__ __launch_bounds__(256) void prefill_sparse_kernel(PrefillArgs a) {
 // ---------------------------------------------------------------------------
 // Tile kernel: window band + dense routed blocks + merge of the sparse partials.
 // ---------------------------------------------------------------------------
+// Register-staged K/V rows for the software pipeline of the tile kernel:
+// thread tid holds chunks tid + 256*i (i < 4) of a 64-key x 128-dim tile.
+struct KVRegs {
+  bf16x8 k[4], v[4];
+};
+
 template <int D>
-__global__ __launch_bounds__(256) void prefill_tile_kernel(PrefillArgs a) {
+__device__ __forceinline__ void kv_prefetch(KVRegs& r, const bf16* kb, const bf16* vb,
+                                            int64_t k_st, int64_t v_st, int j0, int nkeys,
+                                            int len, int tid) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int chunk = tid + 256 * i;
+    const int kr = chunk / (D / 8), c8 = (chunk % (D / 8)) * 8;
+    const int j = j0 + kr;
+    if (kr < nkeys && j < len) {
+      r.k[i] = *(const bf16x8*)(kb + (int64_t)j * k_st + c8);
+      r.v[i] = *(const bf16x8*)(vb + (int64_t)j * v_st + c8);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { r.k[i][e] = (bf16)0.f; r.v[i][e] = (bf16)0.f; }
+    }
+  }
+}
+
+template <int D, int LDK, int LDV>
+__device__ __forceinline__ void kv_commit(const KVRegs& r, bf16 (*sK)[LDK], bf16 (*sV)[LDV],
+                                          int tid) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int chunk = tid + 256 * i;
+    const int kr = chunk / (D / 8), c8 = (chunk % (D / 8)) * 8;
+    *(bf16x8*)&sK[kr][c8] = r.k[i];
+    *(bf16x8*)&sV[kr][c8] = r.v[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Tile kernel: window band + dense routed blocks + merge of the sparse partials.
+// Items of up to 64 keys: the window band in 64-key steps, then one item per
+// dense routed block (per 64 keys of it).  The next item's K/V is loaded into
+// registers while the current one computes.
+// ---------------------------------------------------------------------------
+constexpr int kPfIT = 64;         // keys per item in the tile kernel
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
   static_assert(D == 128, "head_dim 128");
-  __shared__ __attribute__((aligned(16))) bf16 sK[kPfKT][D + 8];
-  __shared__ __attribute__((aligned(16))) bf16 sVt[D][kPfKT + 4];
+  __shared__ __attribute__((aligned(16))) bf16 sK[kPfIT][D + 8];
+  __shared__ __attribute__((aligned(16))) bf16 sV[kPfIT][D + 32];
   __shared__ int32_t sIdx[kPfTQ][kPfMaxK];
   __shared__ float sBias[kPfTQ][kPfMaxK];
   __shared__ int32_t sCnt[kPfTQ];
@@ -448,41 +550,60 @@ __global__ __launch_bounds__(256) void prefill_tile_kernel(PrefillArgs a) {
   __syncthreads();
   const int nu = sNU;
   const int t_last = min(t0 + kPfTQ - 1, len - 1);
-  const int jw0 = (max(t0 - a.lw + 1, 0) / kPfKT) * kPfKT;
-  const int n_win = (t_last - jw0) / kPfKT + 1;
-  const int subs = a.bs / kPfKT;
-  const int n_items = n_win + nu * subs;
+  const int jw0 = (max(t0 - a.lw + 1, 0) / kPfIT) * kPfIT;
+  const int n_win = (t_last - jw0) / kPfIT + 1;
+  const int ipb = (a.bs + kPfIT - 1) / kPfIT;      // items per routed block
+  const int keys_rt = min(a.bs, kPfIT);            // keys per routed item
+  const int n_items = n_win + nu * ipb;
 
   const bf16* kb = seq_ptr(a.k, a.cu, b, a.k_sb, a.k_st) + (int64_t)h * a.k_sh;
   const bf16* vb = seq_ptr(a.v, a.cu, b, a.v_sb, a.v_st) + (int64_t)h * a.v_sh;
   const int myrow = wv * 32 + n;           // row within the tile
+  const int tw = t0 + wv * 32;             // first query of this wavefront
   int ptr = 0;                             // next dense block of this query
   bool cur_sel = false;
   float cur_bias = 0.f;
   const float log2e = 1.4426950408889634f;
 
+  auto item_start = [&](int it, int& nkeys) -> int {
+    if (it < n_win) { nkeys = kPfIT; return jw0 + it * kPfIT; }
+    const int r = it - n_win;
+    nkeys = keys_rt;
+    return sUnion[r / ipb] * a.bs + (r % ipb) * kPfIT;
+  };
+
+  KVRegs pre;
+  if (n_items > 0) {
+    int nk0;
+    const int j00 = item_start(0, nk0);
+    kv_prefetch<D>(pre, kb, vb, a.k_st, a.v_st, j00, nk0, len, tid);
+  }
   for (int it = 0; it < n_items; ++it) {
     const bool routed = it >= n_win;
-    int j0, c = -1, sub = 0;
-    if (!routed) {
-      j0 = jw0 + it * kPfKT;
-    } else {
+    int nkeys;
+    const int j0 = item_start(it, nkeys);
+    int c = -1, sub_item = 0;
+    if (routed) {
       const int r = it - n_win;
-      c = sUnion[r / subs];
-      sub = r % subs;
-      j0 = c * a.bs + sub * kPfKT;
+      c = sUnion[r / ipb];
+      sub_item = r % ipb;
     }
+    __syncthreads();                       // the previous item is done with LDS
+    kv_commit<D, D + 8, D + 32>(pre, sK, sV, tid);
     __syncthreads();
-    stage_kv<D, D + 8, kPfKT + 4>(sK, sVt, kb, vb, a.k_st, a.v_st, j0, kPfKT, len, tid);
-    __syncthreads();
+    if (it + 1 < n_items) {
+      int nk1;
+      const int j1 = item_start(it + 1, nk1);
+      kv_prefetch<D>(pre, kb, vb, a.k_st, a.v_st, j1, nk1, len, tid);
+    }
 
-    // ---- does any query of this wavefront use this key tile? ----
+    // ---- does any query of this wavefront use this item? ----
     bool use;
     float brow = 0.f;
     if (!routed) {
-      use = (j0 <= tq) && (j0 + kPfKT - 1 >= q_lo) && (tq < len);
+      use = (j0 <= tq) && (j0 + nkeys - 1 >= q_lo) && (tq < len);
     } else {
-      if (sub == 0) {
+      if (sub_item == 0) {
         cur_sel = false;
         if (ptr < sCnt[myrow] && sIdx[myrow][ptr] == c) {
           cur_sel = true;
@@ -495,39 +616,65 @@ __global__ __launch_bounds__(256) void prefill_tile_kernel(PrefillArgs a) {
     }
     if (!__any(use)) continue;
 
-    floatx16 s = qk_tile<D, D + 8>(sK, 0, qop, n, hl);
-    // ---- mask, bias, online softmax (base 2) ----
-    float mloc = -INFINITY;
+    // ---- per 32-key sub-tile: S^T, masks, bias, online softmax, O^T += V^T P^T ----
+    // A sub-tile is skipped when no key of it is visible to any query of the
+    // wavefront, and needs no per-element mask when every key is visible to every
+    // query (unselected routed queries carry a -inf bias instead).
+    const int nsub = nkeys / 32;
+    const float bsel = use ? brow : -INFINITY;
+    for (int sb = 0; sb < nsub; ++sb) {
+      const int k0 = j0 + sb * 32;
+      bool full;
+      if (!routed) {
+        if (k0 > tw + 31 || k0 + 31 < max(tw - a.lw + 1, 0)) continue;
+        full = !a.kmin && k0 + 31 <= tw && k0 >= tw + 31 - a.lw + 1 && tw + 31 < len;
+      } else {
+        full = !a.kmin && k0 + 31 < tw - a.lw + 1 && k0 + 31 < len;
+      }
+      floatx16 s = qk_tile<D, D + 8>(sK, sb * 32, qop, n, hl);
+      float mloc = -INFINITY;
+      if (full) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = j0 + 8 * (r >> 2) + 4 * hl + (r & 3);
-      bool ok;
-      if (!routed) ok = use && key >= q_lo && key <= tq;
-      else ok = use && key < q_ls && key >= q_km && key < len;
-      const float x = ok ? s[r] * a.scale_log2e + brow : -INFINITY;
-      s[r] = x;
-      mloc = fmaxf(mloc, x);
+        for (int r = 0; r < 16; ++r) {
+          s[r] = fmaf(s[r], a.scale_log2e, bsel);
+          mloc = fmaxf(mloc, s[r]);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + 8 * (r >> 2) + 4 * hl + (r & 3);
+          bool ok;
+          if (!routed) ok = use && key >= q_lo && key <= tq;
+          else ok = use && key < q_ls && key >= q_km && key < len;
+          const float x = ok ? fmaf(s[r], a.scale_log2e, brow) : -INFINITY;
+          s[r] = x;
+          mloc = fmaxf(mloc, x);
+        }
+      }
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
+      // Lazy rescale: the exponent reference m_run only moves when some query's
+      // maximum exceeds it by more than 8 (probabilities stay <= 2^8).
+      if (__any(mloc > m_run + 8.f)) {
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
+        m_run = m_new;
+      }
+      const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
+      bf16x8 pop[2];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pr = fast_exp2(s[r] - m_use);
+        l_run += pr;
+        pop[r >> 3][r & 7] = (bf16)pr;
+      }
+      pv_slice_tr<D, D + 32>(sV, sb * 32, pop[0], acc_o, lane);
+      pv_slice_tr<D, D + 32>(sV, sb * 32 + 16, pop[1], acc_o, lane);
     }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
-    const float m_new = fmaxf(m_run, mloc);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = exp2f(m_run - m_use);
-    float psum = 0.f;
-    bf16x8 pop[2];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float pr = exp2f(s[r] - m_use);
-      psum += pr;
-      pop[r >> 3][r & 7] = (bf16)pr;
-    }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
-    pv_slice<D, kPfKT + 4>(sVt, 0, pop[0], acc_o, n, hl);
-    pv_slice<D, kPfKT + 4>(sVt, 16, pop[1], acc_o, n, hl);
   }
 
   // ---- merge the sparse partials of this query ----
@@ -539,8 +686,8 @@ __global__ __launch_bounds__(256) void prefill_tile_kernel(PrefillArgs a) {
       const float lse2 = a.part_lse[p * a.H + h];
       if (lse2 == -INFINITY) continue;
       const float m_new = fmaxf(m_run, lse2);
-      const float alpha = exp2f(m_run - m_new);
-      const float w = exp2f(lse2 - m_new);
+      const float alpha = fast_exp2(m_run - m_new);
+      const float w = fast_exp2(lse2 - m_new);
       l_run = l_run * alpha + (hl == 0 ? w : 0.f);
       m_run = m_new;
       const bf16* po = a.part_o + (p * a.H + h) * D;
@@ -580,8 +727,8 @@ __global__ __launch_bounds__(256) void prefill_tile_kernel(PrefillArgs a) {
 
 // Workspace layout of the hybrid plan (byte offsets, 256-byte aligned pieces).
 struct PlanLayout {
-  int64_t count, fill, off, nchunks, tab, pairs, kind, plse, po, total;
-  int chunk_cap;
+  int64_t count, tbase, off, nchunks, tab, pairs, kind, plse, po, total;
+  int chunk_cap, ntiles_cap;
 };
 
 inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -590,10 +737,11 @@ inline PlanLayout plan_layout(int B, int H, int S_max, int64_t rows, int K, int 
                               int nblk_cap) {
   PlanLayout L;
   L.chunk_cap = (int)((int64_t)S_max * K / kPfCH) + nblk_cap + 1;
+  L.ntiles_cap = (S_max + kPfTQ - 1) / kPfTQ;
   const int64_t nbc = (int64_t)B * nblk_cap;
   int64_t o = 0;
   L.count = o; o = align256(o + nbc * 4);
-  L.fill = o; o = align256(o + nbc * 4);
+  L.tbase = o; o = align256(o + nbc * L.ntiles_cap * 4);
   L.off = o; o = align256(o + nbc * 4);
   L.nchunks = o; o = align256(o + (int64_t)B * 4);
   L.tab = o; o = align256(o + (int64_t)B * L.chunk_cap * 16);
@@ -635,7 +783,7 @@ extern "C" int dash_attn_prefill(
   if (!q || !k || !v || !o || B < 0 || H <= 0 || S < 0) return kErrInvalid;
   if (K > 0 && (!idx || !bias)) return kErrInvalid;
   if (D != 128) return kErrUnsupported;
-  if (block_size <= 0 || block_size % kPfKT != 0 || block_size > 256) return kErrUnsupported;
+  if (block_size <= 0 || block_size % 32 != 0 || block_size > 256) return kErrUnsupported;
   if (K < 0 || K > kPfMaxK) return kErrUnsupported;
   if (local_window < 1) return kErrInvalid;
   if (B == 0 || S == 0) return kOk;
@@ -671,7 +819,8 @@ extern "C" int dash_attn_prefill(
     a.kind = (uint8_t*)(w + L.kind);
     a.dense_threshold = dense_threshold;
     a.blk_count = (int32_t*)(w + L.count);
-    a.blk_fill = (int32_t*)(w + L.fill);
+    a.tile_base = (int32_t*)(w + L.tbase);
+    a.ntiles_cap = L.ntiles_cap;
     a.blk_off = (int32_t*)(w + L.off);
     a.num_chunks = (int32_t*)(w + L.nchunks);
     a.chunk_tab = (int4*)(w + L.tab);
