@@ -1,0 +1,151 @@
+"""The drop-in Python interfaces (DashAttention, the inference helpers and the
+fused gather-attention entry points) against the CPU oracle."""
+
+import math
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from ananta_ocr_amd import modeling_deepseekv2 as MD
+from ananta_ocr_amd import sparse_gather as SG
+from ananta_ocr_amd.dash_attention import DashAttention
+from oracle import dash_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _close(out, ref, what, tight=1.5e-2):
+    out, ref = out.float().cpu(), ref.float().cpu()
+    err = (out - ref).abs()
+    assert torch.all(err <= 2e-2 + 1e-2 * ref.abs()), f"{what}: {err.max().item()}"
+    assert err.max().item() <= tight * ref.abs().max().item() + 1e-6, f"{what}: {err.max().item()}"
+
+
+def _config(stage0, bs=64, lb=4, budget=6, scale=128.0, hidden=256, heads=2):
+    sp = dict(sparse_block_size=bs, sparse_local_block=lb, dash_scaling_factor=scale,
+              dash_prior_floor=1e-4, dash_sigma=1.0, dash_topk_blocks=budget,
+              sparse_index_dim=128, dash_stage0=stage0, dash_image_only=True)
+    return SimpleNamespace(num_attention_heads=heads, hidden_size=heads * 128,
+                           rms_norm_eps=1e-6, sparse_attention_config=sp)
+
+
+@pytest.mark.parametrize("stage0", ["head_cls", "indexer"])
+def test_dash_attention_forward_matches_oracle(stage0):
+    torch.manual_seed(0)
+    cfg = _config(stage0)
+    mod = DashAttention(cfg).eval()
+    with torch.no_grad():
+        mod.head_cls.normal_(0, 0.5)
+        mod.q_norm.weight.normal_(0, 0.1)
+    B, S, H = 1, 900, 2
+    g = torch.Generator().manual_seed(1)
+    hs = torch.randn(B, S, cfg.hidden_size, generator=g)
+    q = (torch.randn(B, H, S, 128, generator=g) * 0.5).bfloat16()
+    k = (torch.randn(B, H, S, 128, generator=g) * 0.5).bfloat16()
+    v = torch.randn(B, H, S, 128, generator=g).bfloat16()
+    mod_gpu = mod.to(DEV)
+    with torch.no_grad():
+        out = mod_gpu(hs.to(DEV), q.to(DEV), k.to(DEV), v.to(DEV))
+        iq, ik = mod_gpu.router_qk(hs.to(DEV))
+        sc = mod_gpu.block_scores(iq, ik)
+        ti, bi, va = mod_gpu.route(sc)
+    iq, ik, sc = iq.cpu(), ik.cpu(), sc.cpu()
+    nblk = (S + 63) // 64
+    pos = torch.arange(S)[None]
+    if stage0 == "head_cls":
+        kb, cv = O.kbar_headcls(ik, mod.head_cls.detach().cpu(), 64)
+        sc_r = O.block_scores_headcls(iq, kb, cv, pos, 64, 4)
+    else:
+        sc_r = O.block_scores_indexer(iq, ik, pos, nblk, 64, 256)
+    sent = sc_r < -5e8
+    assert torch.equal(sc < -5e8, sent)
+    torch.testing.assert_close(sc[~sent], sc_r[~sent], atol=2e-5, rtol=2e-5)
+    p = mod._infer_params
+    t_r, b_r, v_r = O.infer_route_select(sc, None, p["idx_scale"], p["floor"], p["sigma"],
+                                         p["K"], p["topm"])
+    assert torch.equal(ti.cpu().long(), t_r) and torch.equal(va.cpu(), v_r)
+    ref = O.dense_attend(q, k, v, t_r, b_r, v_r, 64, 256, 1 / math.sqrt(128))
+    _close(out, ref, f"DashAttention {stage0}")
+
+
+def test_dash_attention_candidate_mask_and_errors():
+    torch.manual_seed(2)
+    cfg = _config("head_cls")
+    mod = DashAttention(cfg).eval().to(DEV)
+    B, S, H = 1, 700, 2
+    hs = torch.randn(B, S, cfg.hidden_size, device=DEV)
+    q = torch.randn(B, H, S, 128, device=DEV).bfloat16()
+    k = torch.randn(B, H, S, 128, device=DEV).bfloat16()
+    v = torch.randn(B, H, S, 128, device=DEV).bfloat16()
+    nblk = (S + 63) // 64
+    cand = torch.rand(B, S, nblk, device=DEV) < 0.5
+    with torch.no_grad():
+        out = mod(hs, q, k, v, block_cand=cand)
+        iq, ik = mod.router_qk(hs)
+        sc = mod.block_scores(iq, ik)
+    p = mod._infer_params
+    t_r, b_r, v_r = O.infer_route_select(sc.cpu(), cand.cpu(), p["idx_scale"], p["floor"],
+                                         p["sigma"], p["K"], p["topm"])
+    ref = O.dense_attend(q.cpu(), k.cpu(), v.cpu(), t_r, b_r, v_r, 64, 256, 1 / math.sqrt(128))
+    _close(out, ref, "DashAttention block_cand")
+    with pytest.raises(NotImplementedError):
+        mod(hs, q, k, v, attention_mask=torch.zeros(1, 1, S, S, device=DEV))
+
+
+def test_gather_attention_e2e_matches_oracle_and_returns_none():
+    g = torch.Generator().manual_seed(3)
+    B, H, T, bs, lw, K = 2, 2, 500, 64, 128, 5
+    q = (torch.randn(B, H, T, 128, generator=g) * 0.5).bfloat16()
+    k = (torch.randn(B, H, T, 128, generator=g) * 0.5).bfloat16()
+    v = torch.randn(B, H, T, 128, generator=g).bfloat16()
+    nblk = (T + bs - 1) // bs
+    sel = torch.randint(-1, nblk, (B, 1, T, K), generator=g, dtype=torch.int32)
+    bias = torch.randn(B, T, K, generator=g)
+    pos = torch.arange(T)[None].expand(B, -1)
+    out = SG.triton_gather_attention_e2e(q.to(DEV), k.to(DEV), v.to(DEV), sel.to(DEV),
+                                         bias.to(DEV), pos.to(DEV), None, bs, 0.1, lw)
+    ref = O.dense_attend(q, k, v, sel[:, 0].long(), bias, sel[:, 0] >= 0, bs, lw, 0.1)
+    _close(out, ref, "gather e2e")
+    assert SG.triton_gather_attention_e2e(q.to(DEV), k.to(DEV), v.to(DEV), sel.to(DEV),
+                                          bias.to(DEV), pos.to(DEV), torch.zeros(1, device=DEV),
+                                          bs, 0.1, lw) is None
+    assert SG.triton_gather_attention_e2e(q.to(DEV), k.to(DEV), v.to(DEV), sel.to(DEV),
+                                          bias.to(DEV), (pos + 1).to(DEV), None, bs, 0.1,
+                                          lw) is None
+
+
+def test_gather_attention_packed_segments():
+    g = torch.Generator().manual_seed(4)
+    H, bs, lw, K = 2, 64, 128, 4
+    lens = [300, 200, 150]
+    T = sum(lens)
+    pos = torch.cat([torch.arange(L) for L in lens])[None]
+    q = (torch.randn(1, H, T, 128, generator=g) * 0.5).bfloat16()
+    k = (torch.randn(1, H, T, 128, generator=g) * 0.5).bfloat16()
+    v = torch.randn(1, H, T, 128, generator=g).bfloat16()
+    nblk = (T + bs - 1) // bs
+    sel = torch.randint(-1, nblk, (1, 1, T, K), generator=g, dtype=torch.int32)
+    out = SG.triton_gather_attention(q.to(DEV), k.to(DEV), v.to(DEV), sel.to(DEV), pos.to(DEV),
+                                     None, bs, 0.1, lw)
+    kmin = torch.arange(T)[None] - pos
+    ref = O.dense_attend(q, k, v, sel[:, 0].long(), torch.zeros(1, T, K), sel[:, 0] >= 0, bs, lw,
+                         0.1, kmin=kmin)
+    _close(out, ref, "gather packed")
+
+
+def test_decode_attend_helper_matches_oracle():
+    g = torch.Generator().manual_seed(5)
+    B, H, S, bs, lw, K = 2, 2, 2000, 64, 512, 6
+    q = (torch.randn(B, H, 1, 128, generator=g) * 0.5).bfloat16()
+    k = (torch.randn(B, H, S, 128, generator=g) * 0.5).bfloat16()
+    v = torch.randn(B, H, S, 128, generator=g).bfloat16()
+    qp = torch.tensor([[S - 1], [1500]])
+    topi = torch.stack([torch.randperm(20, generator=g)[:K] for _ in range(B)])[:, None]
+    bias = torch.randn(B, 1, K, generator=g)
+    valid = torch.rand(B, 1, K, generator=g) < 0.8
+    out = MD._decode_attend(q.to(DEV), k.to(DEV), v.to(DEV), topi.to(DEV), bias.to(DEV),
+                            valid.to(DEV), qp.to(DEV), bs, lw, 0.1)
+    ref = O.decode_attend(q, k, v, topi, bias, valid, qp, bs, lw, 0.1)
+    _close(out, ref, "decode helper")
