@@ -64,19 +64,110 @@ __global__ __launch_bounds__(256) void kbar_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// k_bar for d = 128 and blocks of at most 64 keys: the block's key rows are
+// staged once in LDS with every load in flight together, then read twice (the
+// logits, with four lanes per key, and the weighted sum, with eight key groups
+// per dimension quad).  Same results as kbar_kernel up to summation order.
+// ---------------------------------------------------------------------------
+constexpr int kKbD = 128;
+constexpr int kKbMaxBs = 64;
+
+__global__ __launch_bounds__(256) void kbar128_kernel(
+    const float* __restrict__ idx_k, SeqLayout lay, const int32_t* __restrict__ cu,
+    const int32_t* __restrict__ lens, const float* __restrict__ head_cls, int S, int bs,
+    int tail_only, float inv_sqrt_d, float* __restrict__ kbar, int64_t kb_sb) {
+  __shared__ float4 s_k[kKbMaxBs][kKbD / 4 + 1];
+  __shared__ float s_w[kKbMaxBs];
+  __shared__ float4 s_part[8][kKbD / 4];
+  const int b = blockIdx.y;
+  const int len = seq_length(cu, lens, b, S);
+  if (len <= 0) return;
+  const int c = tail_only ? (len - 1) / bs : (int)blockIdx.x;
+  const int t0 = c * bs;
+  if (t0 >= len) return;
+  const int n = min(bs, len - t0);
+  const int tid = threadIdx.x, lane = wave_lane();
+
+  // stage: 8 float4 per thread, all issued before the first LDS write
+  float4 buf[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int e = tid + 256 * u, j = e / 32, f = e % 32;
+    buf[u] = j < n ? reinterpret_cast<const float4*>(idx_k + lay.row(b, t0 + j))[f]
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int e = tid + 256 * u;
+    s_k[e / 32][e % 32] = buf[u];
+  }
+  __syncthreads();
+
+  // logits: key j = tid / 4, lanes 4j..4j+3 take float4 columns q, q+4, ..., q+28
+  {
+    const int j = tid / 4, q = tid % 4;
+    const float4* hc = reinterpret_cast<const float4*>(head_cls);
+    float acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float4 kv = s_k[j][q + 4 * u], h = hc[q + 4 * u];
+      acc += kv.x * h.x + kv.y * h.y + kv.z * h.z + kv.w * h.w;
+    }
+    acc += __shfl_xor(acc, 1, kWave);
+    acc += __shfl_xor(acc, 2, kWave);
+    if (q == 0 && j < n) s_w[j] = fminf(fmaxf(acc * inv_sqrt_d, -kActClamp), kActClamp);
+  }
+  __syncthreads();
+  // softmax over the n logits (wave 0), weights left in s_w
+  if (tid < kWave) {
+    const float x = lane < n ? s_w[lane] : -INFINITY;
+    const float m = wave_max(x);
+    const float e = lane < n ? expf(x - m) : 0.f;
+    const float den = fmaxf(wave_sum(e), 1e-6f);
+    if (lane < n) s_w[lane] = e / den;
+  }
+  __syncthreads();
+  // weighted sum: group g = tid / 32 takes keys g, g+8, ...; f = float4 column
+  {
+    const int g = tid / 32, f = tid % 32;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = g; j < n; j += 8) {
+      const float w = s_w[j];
+      const float4 kv = s_k[j][f];
+      acc.x += w * kv.x; acc.y += w * kv.y; acc.z += w * kv.z; acc.w += w * kv.w;
+    }
+    s_part[g][f] = acc;
+  }
+  __syncthreads();
+  if (tid < kKbD) {
+    const float* sp = reinterpret_cast<const float*>(&s_part[0][0]);
+    float acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) acc += sp[g * kKbD + tid];
+    if (!(fabsf(acc) <= 3.402823466e38f)) acc = 0.f;   // nan_to_num(nan/inf -> 0)
+    kbar[(int64_t)b * kb_sb + (int64_t)c * kKbD + tid] = acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // head_cls block scores: 64 query rows x 64 key blocks per work-group, fp32 FMA.
+// Tiles whose blocks are all beyond every row's causal limit only write the
+// sentinel.  VEC: d % 16 == 0 and 16-byte aligned rows, staged with float4 loads
+// one k-slice ahead.
 // ---------------------------------------------------------------------------
 constexpr int kScTile = 64;
 constexpr int kScK = 16;
+constexpr int kScPad = kScTile + 4;
 
+template <bool VEC>
 __global__ __launch_bounds__(256) void scores_kernel(
     const float* __restrict__ idx_q, SeqLayout lay_q, const int32_t* __restrict__ cu_q,
     int Lq, const int32_t* __restrict__ q_pos, const float* __restrict__ kbar, int64_t kb_sb,
     const int32_t* __restrict__ cu_k, const int32_t* __restrict__ lens_k, int S, int d,
     int bs, int local_blocks, int nblk_cap, float inv_sqrt_d, float* __restrict__ z,
     int64_t z_stride) {
-  __shared__ float sq[kScK][kScTile + 1];
-  __shared__ float sk[kScK][kScTile + 1];
+  __shared__ __align__(16) float sq[kScK][kScPad];
+  __shared__ __align__(16) float sk[kScK][kScPad];
   const int b = blockIdx.z;
   const int nq = cu_q ? (cu_q[b + 1] - cu_q[b]) : Lq;
   const int r0 = blockIdx.x * kScTile;
@@ -84,36 +175,76 @@ __global__ __launch_bounds__(256) void scores_kernel(
   if (r0 >= nq) return;
   const int klen = seq_length(cu_k, lens_k, b, S);
   const int nblk_b = (klen + bs - 1) / bs;
-  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  const int tid = threadIdx.x;
+  const int tx = tid % 16, ty = tid / 16;
+
+  int lim[4];
+  int my_max = INT_MIN;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = r0 + ty * 4 + i;
+    lim[i] = INT_MIN;
+    if (r < nq) {
+      const int pos = q_pos ? q_pos[token_row(cu_q, b, r, Lq)] : r;
+      lim[i] = (pos >= 0 ? pos / bs : -((-pos + bs - 1) / bs)) - local_blocks;
+      my_max = max(my_max, lim[i]);
+    }
+  }
+  if (!__syncthreads_or(c0 <= my_max && c0 < nblk_b)) {
+    for (int e = tid; e < kScTile * kScTile; e += 256) {
+      const int r = r0 + e / kScTile, c = c0 + e % kScTile;
+      if (r < nq && c < nblk_cap) z[token_row(cu_q, b, r, Lq) * z_stride + c] = kScoreNeg;
+    }
+    return;
+  }
+
   float acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
 
+  const int srr = tid / 4, skq = tid % 4;   // VEC staging: row srr, dims 4*skq..+3
+  const bool q_ok = r0 + srr < nq, k_ok = c0 + srr < nblk_cap;
+  const float* qrow = q_ok ? idx_q + lay_q.row(b, r0 + srr) + 4 * skq : nullptr;
+  const float* krow = k_ok ? kbar + (int64_t)b * kb_sb + (int64_t)(c0 + srr) * d + 4 * skq
+                           : nullptr;
+  float4 qn = make_float4(0.f, 0.f, 0.f, 0.f), kn = qn;
+  if (VEC) {
+    if (q_ok) qn = *reinterpret_cast<const float4*>(qrow);
+    if (k_ok) kn = *reinterpret_cast<const float4*>(krow);
+  }
   for (int k0 = 0; k0 < d; k0 += kScK) {
-    // stage 64 rows x 16 dims of q and of k_bar
-    for (int e = threadIdx.x; e < kScTile * kScK; e += 256) {
-      const int rr = e / kScK, kk = e % kScK;
-      const int r = r0 + rr, c = c0 + rr, dd = k0 + kk;
-      float qv = 0.f, kv = 0.f;
-      if (r < nq && dd < d) qv = idx_q[lay_q.row(b, r) + dd];
-      if (c < nblk_cap && dd < d) kv = kbar[(int64_t)b * kb_sb + (int64_t)c * d + dd];
-      sq[kk][rr] = qv;
-      sk[kk][rr] = kv;
+    if (VEC) {
+      sq[4 * skq + 0][srr] = qn.x; sq[4 * skq + 1][srr] = qn.y;
+      sq[4 * skq + 2][srr] = qn.z; sq[4 * skq + 3][srr] = qn.w;
+      sk[4 * skq + 0][srr] = kn.x; sk[4 * skq + 1][srr] = kn.y;
+      sk[4 * skq + 2][srr] = kn.z; sk[4 * skq + 3][srr] = kn.w;
+      if (k0 + kScK < d) {
+        if (q_ok) qn = *reinterpret_cast<const float4*>(qrow + k0 + kScK);
+        if (k_ok) kn = *reinterpret_cast<const float4*>(krow + k0 + kScK);
+      }
+    } else {
+      for (int e = tid; e < kScTile * kScK; e += 256) {
+        const int rr = e / kScK, kk = e % kScK;
+        const int r = r0 + rr, c = c0 + rr, dd = k0 + kk;
+        float qv = 0.f, kv = 0.f;
+        if (r < nq && dd < d) qv = idx_q[lay_q.row(b, r) + dd];
+        if (c < nblk_cap && dd < d) kv = kbar[(int64_t)b * kb_sb + (int64_t)c * d + dd];
+        sq[kk][rr] = qv;
+        sk[kk][rr] = kv;
+      }
     }
     __syncthreads();
 #pragma unroll
     for (int kk = 0; kk < kScK; ++kk) {
-      float a[4], bb[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = sq[kk][ty * 4 + i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bb[j] = sk[kk][tx * 4 + j];
+      const float4 a = *reinterpret_cast<const float4*>(&sq[kk][ty * 4]);
+      const float4 bb = *reinterpret_cast<const float4*>(&sk[kk][tx * 4]);
+      const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {bb.x, bb.y, bb.z, bb.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], bb[j], acc[i][j]);
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
     }
     __syncthreads();
   }
@@ -122,14 +253,12 @@ __global__ __launch_bounds__(256) void scores_kernel(
     const int r = r0 + ty * 4 + i;
     if (r >= nq) continue;
     const int64_t row = token_row(cu_q, b, r, Lq);
-    const int pos = q_pos ? q_pos[row] : r;
-    const int lim = (pos >= 0 ? pos / bs : -((-pos + bs - 1) / bs)) - local_blocks;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int c = c0 + tx * 4 + j;
       if (c >= nblk_cap) continue;
       float v = kScoreNeg;
-      if (c <= lim && c < nblk_b) {
+      if (c <= lim[i] && c < nblk_b) {
         v = acc[i][j] * inv_sqrt_d;
         v = fminf(fmaxf(v, -kActClamp), kActClamp);
       }
@@ -228,11 +357,6 @@ __global__ __launch_bounds__(256) void blockmax_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kMaxM = 16;
 
-// (value desc, block id asc) order; id carries the candidacy flag in bit 30.
-__device__ __forceinline__ bool route_better(float va, int ka, float vb, int kb) {
-  const int ia = ka & 0x3fffffff, ib = kb & 0x3fffffff;
-  return va > vb || (va == vb && ia < ib);
-}
 
 // 1.5-entmax over M values sorted in descending order, bit-for-bit the fp32
 // sequence of dash_attention.py:623-647 on the CPU: X = (x - max)/2, cumsums
@@ -274,114 +398,291 @@ __device__ __forceinline__ void entmax15_sorted(const float (&x)[kMaxM], int M,
   }
 }
 
+// Order-preserving key of a finite float: larger value -> larger key; -0 and +0
+// share a key (they compare equal).
+__device__ __forceinline__ uint32_t ord_key(float x) {
+  const uint32_t b = x == 0.f ? 0u : __float_as_uint(x);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ int lane_prefix(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
+}
+
+// DPP controls: quad_perm [1,0,3,2] and [2,3,0,1]; row_ror 4 and 8.
+#define DASH_DPP(v, c) ((uint32_t)__builtin_amdgcn_mov_dpp((int)(v), c, 0xf, 0xf, false))
+__device__ __forceinline__ uint32_t quad_max_u32(uint32_t v) {
+  v = max(v, DASH_DPP(v, 0xB1));
+  return max(v, DASH_DPP(v, 0x4E));
+}
+// For values uniform within each quad: min / max over the wavefront, uniform.
+__device__ __forceinline__ uint32_t wave_min_of_quads(uint32_t v) {
+  v = min(v, DASH_DPP(v, 0x124));
+  v = min(v, DASH_DPP(v, 0x128));
+  const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+  return min(min(a, b), min(c, d));
+}
+__device__ __forceinline__ uint32_t wave_max_of_quads(uint32_t v) {
+  v = max(v, DASH_DPP(v, 0x124));
+  v = max(v, DASH_DPP(v, 0x128));
+  const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+  return max(max(a, b), max(c, d));
+}
+#undef DASH_DPP
+
+// Largest T with #{keys >= T} >= M over the wavefront's keys (NV per lane, 0 =
+// absent), given a lower bound t_lo with #{keys >= t_lo} >= M and the maximum
+// key t_hi.  T shares the bits above the highest bit where t_lo and t_hi differ;
+// the rest is found two bits per step with ballots.
+template <int NV>
+__device__ __forceinline__ uint32_t kth_key(const uint32_t (&h)[NV], int M, uint32_t t_lo,
+                                            uint32_t t_hi) {
+  const uint32_t diff = t_lo ^ t_hi;
+  int nb = diff ? 32 - __clz(diff) : 0;
+  uint32_t T = nb >= 32 ? 0u : (t_lo & ~((1u << nb) - 1u));
+  auto count = [&](uint32_t t) {
+    int n = 0;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) n += __popcll(__ballot(h[i] >= t));
+    return n;
+  };
+  while (nb >= 2) {
+    nb -= 2;
+    const uint32_t c3 = T | (3u << nb), c2 = T | (2u << nb), c1 = T | (1u << nb);
+    const int n3 = count(c3), n2 = count(c2), n1 = count(c1);
+    T = n3 >= M ? c3 : n2 >= M ? c2 : n1 >= M ? c1 : T;
+    if (n3 == M || n2 == M || n1 == M) return T;
+  }
+  if (nb == 1) {
+    const uint32_t c1 = T | 1u;
+    if (count(c1) >= M) T = c1;
+  }
+  return T;
+}
+
+// Routing: work-groups of four wavefronts own 16 consecutive score rows, four
+// per wavefront.
+//  Phase 1, one row at a time over the whole wavefront: every entry gets the
+//  64-bit key  ord_key(x) << 32 | (0xffff - block id) << 1 | candidate  whose
+//  descending order is (value desc, block id asc).  The top-M set is found
+//  exactly without sorting:
+//   * t0 = min over the 16 residue classes (block id mod 16) of the class
+//     maximum.  At least 16 >= M entries reach t0, so the top M are among the
+//     entries >= t0; these (at most 64, one per lane) are compacted in block-id
+//     order and the M-th largest value key T among them is found by bisection
+//     over its 32 bits with ballots;
+//   * rows with more than 64 entries >= t0 (ties, e.g. fewer than 16 remote
+//     blocks) run the same bisection over all their entries.
+//  The entries above T and the lowest-id entries at T form the set, parked in
+//  LDS.
+//  Phase 2, wavefront 0 with one row per lane: bitonic sort of the M keys,
+//  1.5-entmax, first K, centred log-prior bias.
+constexpr int kRtRowsPerWave = 4;
+constexpr int kRtWaves = 4;
+constexpr int kRtRows = kRtRowsPerWave * kRtWaves;
+
+__device__ __forceinline__ float ord_key_inv(uint32_t h) {
+  return __uint_as_float((h & 0x80000000u) ? (h & 0x7fffffffu) : ~h);
+}
+
 template <int NPL>
-__global__ __launch_bounds__(256) void route_kernel(
+__global__ __launch_bounds__(kRtWaves * kWave) void route_kernel(
     const float* __restrict__ z, int64_t z_stride, int rows, int nblk_cols,
     const int32_t* __restrict__ row_nblk, const uint8_t* __restrict__ cand_in,
     int64_t cand_stride, float idx_scale, float floor_p, float inv_sigma, int K, int topm,
     int Kout, int32_t* __restrict__ idx_out, float* __restrict__ bias_out,
     uint8_t* __restrict__ valid_out) {
-  const int lane = wave_lane();
-  const int row = blockIdx.x * 4 + threadIdx.x / kWave;
-  if (row >= rows) return;
-  const int nblk = row_nblk ? min(row_nblk[row], nblk_cols) : nblk_cols;
-  const float* zr = z + (int64_t)row * z_stride;
+  __shared__ uint64_t s_cand[kRtWaves][kWave];
+  __shared__ uint64_t s_sel[kRtRows][kMaxM];
+  __shared__ int s_M[kRtRows];
+  const int lane = wave_lane(), wv = threadIdx.x / kWave;
+  const int wg_row0 = blockIdx.x * kRtRows;
+  const int row0 = wg_row0 + wv * kRtRowsPerWave;
+  const int nrow = max(0, min(kRtRowsPerWave, rows - row0));
 
-  bool remote[NPL], cand[NPL];
-  float zv[NPL];
-  bool any_cand = false;
+  // Score loads are unconditional (column clamped into the row).  For rows of up
+  // to 512 blocks the loads of all of this wavefront's rows are issued together
+  // up front; wider rows load one row at a time.
+  constexpr bool kAllRows = NPL <= 8;
+  constexpr int kBuf = kAllRows ? kRtRowsPerWave : 1;
+  float zb[kBuf][NPL];
+  int nb_rows[kBuf];
+  auto fetch = [&](int slot, int row) {
+    const float* zr = z + (int64_t)row * z_stride;
 #pragma unroll
-  for (int i = 0; i < NPL; ++i) {
-    const int c = lane + kWave * i;
-    zv[i] = (c < nblk) ? zr[c] : kScoreNeg;
-    remote[i] = (c < nblk) && (zv[i] > kScoreNeg * 0.5f);
-    bool cd = remote[i];
-    if (cand_in && c < nblk) cd = cd && cand_in[(int64_t)row * cand_stride + c] != 0;
-    cand[i] = cd;
-    any_cand |= cd;
+    for (int i = 0; i < NPL; ++i) zb[slot][i] = zr[min(lane + kWave * i, nblk_cols - 1)];
+    nb_rows[slot] = row_nblk ? row_nblk[row] : nblk_cols;
+  };
+  if (kAllRows) {
+#pragma unroll
+    for (int rr = 0; rr < kBuf; ++rr)
+      if (rr < nrow) fetch(rr, row0 + rr);
   }
-  // rows without any candidate fall back to every remote block
-  any_cand = __any(any_cand);
-  float v[NPL];
-  int key[NPL];
 #pragma unroll
-  for (int i = 0; i < NPL; ++i) {
-    const int c = lane + kWave * i;
-    const bool cd = any_cand ? cand[i] : remote[i];
-    float x = cd ? zv[i] * idx_scale : kEntmaxNeg;
-    if (!(fabsf(x) <= 3.402823466e38f)) x = kEntmaxNeg;
-    v[i] = (c < nblk) ? x : -INFINITY;
-    key[i] = (c < nblk) ? (c | (cd ? (1 << 30) : 0)) : 0x3fffffff;
-  }
-  const int M = topm > 0 ? max(1, min(topm, nblk)) : nblk;
-  const int Kp = max(1, min(K, M));
-
-  float bv = -INFINITY;
-  int bk = 0x3fffffff;
+  for (int rr = 0; rr < kRtRowsPerWave; ++rr) {
+    if (rr >= nrow) break;
+    const int sr = wv * kRtRowsPerWave + rr;   // row slot in the work-group
+    const int row = row0 + rr;
+    const int bs_ = kAllRows ? rr : 0;
+    if (!kAllRows) fetch(0, row);
+    float zv[NPL];
 #pragma unroll
-  for (int i = 0; i < NPL; ++i)
-    if (route_better(v[i], key[i], bv, bk)) { bv = v[i]; bk = key[i]; }
-
-  float sel_v[kMaxM];
-  int sel_k[kMaxM];
+    for (int i = 0; i < NPL; ++i) zv[i] = zb[bs_][i];
+    const int nn = nb_rows[bs_];
+    const int nblk = max(0, min(__builtin_amdgcn_readfirstlane(nn), nblk_cols));
+    uint8_t cb[NPL];
+    if (cand_in) {
 #pragma unroll
-  for (int m = 0; m < kMaxM; ++m) {
-    sel_v[m] = 0.f;
-    sel_k[m] = 0x3fffffff;
-    if (m < M) {
-      float wv = bv;
-      int wk = bk;
+      for (int i = 0; i < NPL; ++i)
+        cb[i] = cand_in[(int64_t)row * cand_stride + min(lane + kWave * i, nblk_cols - 1)];
+    }
+    bool any_cand = false;
+    if (cand_in) {
 #pragma unroll
-      for (int s = 32; s >= 1; s >>= 1) {
-        const float ov = __shfl_xor(wv, s, kWave);
-        const int ok = __shfl_xor(wk, s, kWave);
-        if (route_better(ov, ok, wv, wk)) { wv = ov; wk = ok; }
+      for (int i = 0; i < NPL; ++i)
+        any_cand |= (lane + kWave * i < nblk) && zv[i] > kScoreNeg * 0.5f && cb[i] != 0;
+    }
+    // rows without any candidate fall back to every remote block
+    const bool use_cand = cand_in && __any(any_cand);
+    uint32_t hi[NPL];
+    uint32_t cmx = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const int c = lane + kWave * i;
+      const bool remote = (c < nblk) && (zv[i] > kScoreNeg * 0.5f);
+      const bool cd = use_cand ? (remote && cb[i] != 0) : remote;
+      float x = cd ? zv[i] * idx_scale : kEntmaxNeg;
+      if (!(fabsf(x) <= 3.402823466e38f)) x = kEntmaxNeg;
+      // candidate flag in bit 0 of the key: only block ids break ties, never it
+      hi[i] = c < nblk ? ord_key(x) : 0u;
+      cb[i] = cd ? 1 : 0;
+      cmx = max(cmx, hi[i]);
+    }
+    const int M = nblk == 0 ? 0 : (topm > 0 ? max(1, min(topm, nblk)) : nblk);
+    // classes = lane quads (16 of them, all non-empty once nblk >= 61): t0 = the
+    // smallest class maximum (0 if a class is empty), kmax = the row maximum
+    cmx = quad_max_u32(cmx);
+    const uint32_t t0 = wave_min_of_quads(cmx);
+    const uint32_t kmax = wave_max_of_quads(cmx);
+    int nc = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const bool pass = hi[i] != 0u && hi[i] >= t0;
+      const uint64_t mask = __ballot(pass);
+      const int slot = nc + lane_prefix(mask);
+      const int c = lane + kWave * i;
+      if (pass && slot < kWave)
+        s_cand[wv][slot] = ((uint64_t)hi[i] << 32) | ((uint32_t)(0xffff - c) << 1) | cb[i];
+      nc += __popcll(mask);
+    }
+    if (M == 0) {
+    } else if (nc <= kWave) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const uint64_t mine = lane < nc ? s_cand[wv][lane] : 0ull;
+      const uint32_t h[1] = {(uint32_t)(mine >> 32)};
+      const uint32_t T = kth_key<1>(h, M, t0, kmax);
+      const int need_eq = M - __popcll(__ballot(h[0] > T));
+      const bool eq = h[0] == T && lane < nc;
+      const bool take = h[0] > T || (eq && lane_prefix(__ballot(eq)) < need_eq);
+      const uint64_t mt = __ballot(take);
+      if (take) s_sel[sr][lane_prefix(mt)] = mine;
+    } else {
+      const uint32_t T = kth_key<NPL>(hi, M, t0, kmax);
+      int n_gt = 0;
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) n_gt += __popcll(__ballot(hi[i] > T));
+      const int need_eq = M - n_gt;
+      int taken = 0, eq_seen = 0;
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) {
+        const bool eq = hi[i] == T;
+        const uint64_t meq = __ballot(eq);
+        const bool take = hi[i] > T || (eq && eq_seen + lane_prefix(meq) < need_eq);
+        const uint64_t mt = __ballot(take);
+        const int c = lane + kWave * i;
+        if (take)
+          s_sel[sr][taken + lane_prefix(mt)] =
+              ((uint64_t)hi[i] << 32) | ((uint32_t)(0xffff - c) << 1) | cb[i];
+        taken += __popcll(mt);
+        eq_seen += __popcll(meq);
       }
-      sel_v[m] = wv;
-      sel_k[m] = wk;
-      const int wc = wk & 0x3fffffff;
-      if ((wc & (kWave - 1)) == lane) {
-        const int wi = wc / kWave;
+    }
+    if (lane == 0) s_M[sr] = M;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  __syncthreads();
+
+  // ---- phase 2: wavefront 0, one row per lane ----
+  if (wv != 0 || lane >= kRtRows) return;
+  const int row = wg_row0 + lane;
+  if (row >= rows) return;
+  const int M = s_M[lane];
+  uint64_t k[kMaxM];
 #pragma unroll
-        for (int i = 0; i < NPL; ++i)
-          if (i == wi) { v[i] = -INFINITY; key[i] = 0x3fffffff; }
-        bv = -INFINITY;
-        bk = 0x3fffffff;
+  for (int m = 0; m < kMaxM; ++m) k[m] = m < M ? s_sel[lane][m] : 0ull;
+  // bitonic sort, descending
 #pragma unroll
-        for (int i = 0; i < NPL; ++i)
-          if (route_better(v[i], key[i], bv, bk)) { bv = v[i]; bk = key[i]; }
+  for (int kk = 2; kk <= kMaxM; kk <<= 1) {
+#pragma unroll
+    for (int j = kk >> 1; j > 0; j >>= 1) {
+#pragma unroll
+      for (int i = 0; i < kMaxM; ++i) {
+        const int l = i ^ j;
+        if (l > i) {
+          const uint64_t a = k[i], b = k[l];
+          const bool sw = ((i & kk) == 0) ? (a < b) : (a > b);
+          k[i] = sw ? b : a;
+          k[l] = sw ? a : b;
+        }
       }
     }
   }
+  float sel_v[kMaxM];
+  int sel_id[kMaxM];
+  bool sel_c[kMaxM];
+#pragma unroll
+  for (int m = 0; m < kMaxM; ++m) {
+    const uint32_t h = (uint32_t)(k[m] >> 32), l = (uint32_t)k[m];
+    sel_v[m] = m < M ? ord_key_inv(h) : 0.f;
+    sel_id[m] = 0xffff - (int)((l >> 1) & 0xffff);
+    sel_c[m] = (l & 1u) != 0;
+  }
+  const int Kp = max(1, min(K, M));
   float prior[kMaxM];
-  entmax15_sorted(sel_v, M, prior);
-
+  entmax15_sorted(sel_v, max(M, 1), prior);
   float logp[kMaxM];
   float musum = 0.f;
   int cnt = 0;
 #pragma unroll
   for (int m = 0; m < kMaxM; ++m) {
     logp[m] = logf(fmaxf(prior[m], floor_p));
-    const bool va = m < Kp && (sel_k[m] & (1 << 30));
-    if (va) { musum += logp[m]; ++cnt; }
+    if (m < Kp && m < M && sel_c[m]) { musum += logp[m]; ++cnt; }
   }
   const float mu = musum / (float)max(cnt, 1);
-  for (int m = lane; m < Kout; m += kWave) {
-    int oi = -1;
-    float ob = 0.f;
-    uint8_t ov = 0;
+  int32_t* io = idx_out + (int64_t)row * Kout;
+  float* bo = bias_out + (int64_t)row * Kout;
+  uint8_t* vo = valid_out ? valid_out + (int64_t)row * Kout : nullptr;
 #pragma unroll
-    for (int s = 0; s < kMaxM; ++s) {
-      if (s == m && s < Kp) {
-        oi = sel_k[s] & 0x3fffffff;
-        const bool va = (sel_k[s] & (1 << 30)) != 0;
-        ov = va ? 1 : 0;
-        ob = va ? (logp[s] - mu) * inv_sigma : 0.f;
-      }
+  for (int m = 0; m < kMaxM; ++m) {
+    if (m < Kout) {
+      const bool in = m < Kp && m < M;
+      const bool va = in && sel_c[m];
+      io[m] = in ? sel_id[m] : -1;
+      bo[m] = va ? (logp[m] - mu) * inv_sigma : 0.f;
+      if (vo) vo[m] = va ? 1 : 0;
     }
-    idx_out[(int64_t)row * Kout + m] = oi;
-    bias_out[(int64_t)row * Kout + m] = ob;
-    if (valid_out) valid_out[(int64_t)row * Kout + m] = ov;
+  }
+  for (int m = kMaxM; m < Kout; ++m) {
+    io[m] = -1;
+    bo[m] = 0.f;
+    if (vo) vo[m] = 0;
   }
 }
 
@@ -410,6 +711,14 @@ extern "C" int dash_kbar(const float* idx_k, int64_t ik_sb, int64_t ik_st, int64
   if (B == 0 || nblk_cap == 0) return kOk;
   SeqLayout lay{cu_seqlens, block_table, table_stride, ik_sb, ik_sp, ik_st, page_size};
   dim3 grid(tail_only ? 1 : nblk_cap, B);
+  const bool aligned = ((uintptr_t)idx_k % 16 == 0) && ((uintptr_t)head_cls % 16 == 0) &&
+                       ik_sb % 4 == 0 && ik_st % 4 == 0 && ik_sp % 4 == 0;
+  if (d == kKbD && block_size <= kKbMaxBs && aligned) {
+    hipLaunchKernelGGL(kbar128_kernel, grid, dim3(256), 0, (hipStream_t)stream, idx_k, lay,
+                       cu_seqlens, seq_lens, head_cls, S, block_size, tail_only,
+                       (float)(1.0 / sqrt((double)d)), kbar, kb_sb);
+    return launch_status();
+  }
   hipLaunchKernelGGL(kbar_kernel, grid, dim3(256), 0, (hipStream_t)stream, idx_k, lay,
                      cu_seqlens, seq_lens, head_cls, S, d, block_size, tail_only,
                      (float)(1.0 / sqrt((double)d)), kbar, kb_sb);
@@ -428,7 +737,10 @@ extern "C" int dash_block_scores(const float* idx_q, int64_t iq_sb, int64_t iq_s
   if (B == 0 || Lq == 0 || nblk_cap == 0) return kOk;
   SeqLayout lay{cu_q, nullptr, 0, iq_sb, 0, iq_st, 1};
   dim3 grid((Lq + kScTile - 1) / kScTile, (nblk_cap + kScTile - 1) / kScTile, B);
-  hipLaunchKernelGGL(scores_kernel, grid, dim3(256), 0, (hipStream_t)stream, idx_q, lay, cu_q,
+  const bool vec = d % kScK == 0 && (uintptr_t)idx_q % 16 == 0 && (uintptr_t)kbar % 16 == 0 &&
+                   iq_sb % 4 == 0 && iq_st % 4 == 0 && kb_sb % 4 == 0;
+  auto kern = vec ? scores_kernel<true> : scores_kernel<false>;
+  hipLaunchKernelGGL(kern, grid, dim3(256), 0, (hipStream_t)stream, idx_q, lay, cu_q,
                      Lq, q_pos, kbar, kb_sb, cu_k, lens_k, S, d, block_size, local_blocks,
                      nblk_cap, (float)(1.0 / sqrt((double)d)), z, z_stride);
   return launch_status();
@@ -464,14 +776,15 @@ extern "C" int dash_route(const float* z, int64_t z_stride, int rows, int nblk_c
   if (Kout < std::min(K, std::min(topm, std::max(nblk_cols, 1)))) return kErrInvalid;
   if (nblk_cols > 64 * 32) return kErrUnsupported;
   if (rows == 0) return kOk;
+  if (nblk_cols == 0) return kErrInvalid;   // top-M of an empty row
   const float inv_sigma = (float)(1.0 / (double)sigma);
-  dim3 grid((rows + 3) / 4);
+  dim3 grid((rows + kRtRows - 1) / kRtRows);
   hipStream_t st = (hipStream_t)stream;
   const int npl = (nblk_cols + 63) / 64;
 #define DASH_ROUTE(N)                                                                       \
-  hipLaunchKernelGGL(route_kernel<N>, grid, dim3(256), 0, st, z, z_stride, rows, nblk_cols, \
-                     row_nblk, cand, cand_stride, idx_scale, floor_p, inv_sigma, K, topm,   \
-                     Kout, idx, bias, valid)
+  hipLaunchKernelGGL(route_kernel<N>, grid, dim3(kRtWaves * kWave), 0, st, z, z_stride, rows, \
+                     nblk_cols, row_nblk, cand, cand_stride, idx_scale, floor_p, inv_sigma, \
+                     K, topm, Kout, idx, bias, valid)
   if (npl <= 1) DASH_ROUTE(1);
   else if (npl <= 2) DASH_ROUTE(2);
   else if (npl <= 4) DASH_ROUTE(4);
@@ -512,8 +825,13 @@ __global__ __launch_bounds__(kDrThreads) void decode_route_kernel(DecodeRouteArg
   __shared__ float s_aw[256];
   __shared__ float s_red[2];
   __shared__ float s_part[8][128];
-  __shared__ float s_x[kDrMaxBlocks + 8];
-  __shared__ int s_key[kDrMaxBlocks + 8];
+  __shared__ float s_x[kDrMaxBlocks];
+  __shared__ int s_key[kDrMaxBlocks];
+  __shared__ __attribute__((aligned(16))) float s_cx[kDrMaxBlocks + 4];
+  __shared__ __attribute__((aligned(16))) int s_ck[kDrMaxBlocks + 4];
+  __shared__ float s_cmax[kDrThreads / kWave][16];
+  __shared__ float s_t0;
+  __shared__ int s_ncand;
   __shared__ uint8_t s_flag[kDrMaxBlocks];
   __shared__ float s_selv[kMaxM];
   __shared__ int s_selk[kMaxM];
@@ -653,20 +971,62 @@ __global__ __launch_bounds__(kDrThreads) void decode_route_kernel(DecodeRouteArg
   __syncthreads();
   const int M = a.topm > 0 ? max(1, min(a.topm, nblk)) : nblk;
   const int Kp = max(1, min(a.K, M));
-  // pad to a multiple of 8 with entries that lose every comparison
-  for (int c = nblk + tid; c < ((nblk + 7) & ~7); c += kDrThreads) {
-    s_x[c] = -INFINITY;
-    s_key[c] = 0x3fffffff;
+  // Top-M prefilter: t0 = min over the 16 residue classes c mod 16 of the class
+  // maximum.  At least 16 >= M entries reach t0, so the top M all do, and every
+  // entry below t0 loses to every entry at or above it: ranking the entries
+  // >= t0 among themselves gives their rank among all entries.
+  {
+    float cm = -INFINITY;
+    for (int c = tid; c < nblk; c += kDrThreads) cm = fmaxf(cm, s_x[c]);
+    cm = fmaxf(cm, __shfl_xor(cm, 16, kWave));   // tid % 16 == lane % 16 is the class
+    cm = fmaxf(cm, __shfl_xor(cm, 32, kWave));
+    if (lane < 16) s_cmax[wv][lane] = cm;
+    if (tid == 0) s_ncand = 0;
   }
   __syncthreads();
-  // rank of every entry; an entry stops counting once it cannot be in the top M
-  for (int c = tid; c < nblk; c += kDrThreads) {
-    const float x = s_x[c];
-    const int key = s_key[c];
-    int rank = 0;
-    for (int j0 = 0; j0 < nblk && rank < M; j0 += 8) {
+  if (wv == 0) {
+    float g = INFINITY;
+    if (lane < 16) {
+      g = -INFINITY;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) rank += route_better(s_x[j0 + u], s_key[j0 + u], x, key);
+      for (int w = 0; w < kDrThreads / kWave; ++w) g = fmaxf(g, s_cmax[w][lane]);
+    }
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) g = fminf(g, __shfl_xor(g, m, kWave));
+    if (lane == 0) s_t0 = g;
+  }
+  __syncthreads();
+  {
+    const float t0v = s_t0;
+    for (int c = tid; c < nblk; c += kDrThreads) {
+      const float x = s_x[c];
+      if (x >= t0v) {
+        const int slot = atomicAdd(&s_ncand, 1);
+        s_cx[slot] = x;
+        s_ck[slot] = s_key[c];
+      }
+    }
+  }
+  __syncthreads();
+  const int nc = s_ncand;
+  // pad the candidates to a multiple of 4 with entries that lose every comparison
+  if (tid < ((nc + 3) & ~3) - nc) {
+    s_cx[nc + tid] = -INFINITY;
+    s_ck[nc + tid] = 0x3fffffff;
+  }
+  __syncthreads();
+  // exact rank among the candidates: branch-free, four entries per LDS read
+  for (int i = tid; i < nc; i += kDrThreads) {
+    const float x = s_cx[i];
+    const int key = s_ck[i], ki = key & 0x3fffffff;
+    int rank = 0;
+    for (int j0 = 0; j0 < nc; j0 += 4) {
+      const float4 xv = *reinterpret_cast<const float4*>(&s_cx[j0]);
+      const int4 kv = *reinterpret_cast<const int4*>(&s_ck[j0]);
+      rank += (int)(xv.x > x) | ((int)(xv.x == x) & (int)((kv.x & 0x3fffffff) < ki));
+      rank += (int)(xv.y > x) | ((int)(xv.y == x) & (int)((kv.y & 0x3fffffff) < ki));
+      rank += (int)(xv.z > x) | ((int)(xv.z == x) & (int)((kv.z & 0x3fffffff) < ki));
+      rank += (int)(xv.w > x) | ((int)(xv.w == x) & (int)((kv.w & 0x3fffffff) < ki));
     }
     if (rank < M) { s_selv[rank] = x; s_selk[rank] = key; }
   }

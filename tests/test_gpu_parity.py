@@ -434,6 +434,22 @@ def test_decode_route_contiguous(hc_scale, scale):
     _decode_route_check(ik_seq, iq, lens, bs, lb, 16, 16, hc)
 
 
+def test_decode_route_ties():
+    """Block-constant keys from three levels (many exactly tied scores) and one
+    sequence where every remote block ties: ids must follow (score desc, id asc)."""
+    g = _gen(502)
+    lens = [5000, 2000, 64 * 20]
+    d, bs, lb = 128, 64, 2
+    base = torch.randn(3, d, generator=g) * 0.1
+    ik_seq = []
+    for L in lens:
+        lvl = torch.randint(0, 3, ((L + bs - 1) // bs,), generator=g)
+        ik_seq.append(base[lvl].repeat_interleave(bs, 0)[:L].contiguous())
+    ik_seq[2] = torch.full((lens[2], d), 0.05)
+    iq = torch.randn(len(lens), d, generator=g)
+    _decode_route_check(ik_seq, iq, lens, bs, lb, 16, 16, torch.zeros(d))
+
+
 def test_decode_route_paged_with_candidates():
     g = _gen(501)
     lens = [3000, 2049, 700]
