@@ -57,6 +57,17 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Work-groups of a 1-D grid are dispatched to the 8 XCDs round-robin by linear
+// id, and each XCD has its own L2.  This maps linear id L of n to a logical id
+// such that every XCD runs a contiguous range of logical ids (neighbouring tiles
+// or chunks, which share K/V rows, then meet in the same L2).
+__device__ __forceinline__ int xcd_logical_id(int L, int n) {
+  constexpr int kXcd = 8;
+  const int x = L % kXcd, k = L / kXcd;
+  const int q = n / kXcd, r = n % kXcd;
+  return x * q + min(x, r) + k;
+}
+
 // Where token t of sequence b lives, for the three layouts the path uses:
 //   contiguous  row = b*stride_b + t*stride_t
 //   varlen      row = (cu[b] + t)*stride_t          (packed documents)

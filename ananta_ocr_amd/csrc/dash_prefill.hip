@@ -9,29 +9,32 @@
 // (duplicated routed blocks count once, first slot wins; rows with no key give 0).
 //
 // Work decomposition (hybrid):
+//   * plan -> scan -> scatter kernels: per 128-query tile, a routed block is
+//     "dense" if at least dense_threshold of the tile's queries selected it;
+//     the other (query, block) pairs are "sparse" and are grouped by block.
+//   * sparse kernel: one work-group per chunk of up to 512 sparse pairs of one
+//     block and head stages the block's K/V in LDS once and runs the gathered
+//     queries through the MFMA tiles, writing a normalised bf16 partial and its
+//     base-2 log-sum-exp per (pair, head).
 //   * tile kernel: one work-group of 4 wavefronts per (128-query tile, head,
-//     sequence), 32 queries per wavefront.  Keys are staged in LDS 32 at a time;
-//     S^T = K Q^T (32 keys x 32 queries, v_mfma_f32_32x32x16_bf16), masks, bias,
-//     online softmax (base 2), O^T += V^T P^T, so each lane owns one query's
-//     softmax state.  It covers the window band and the routed blocks that many
-//     queries of the tile share ("dense" blocks: every query masks the blocks it
-//     did not select), then merges the partials of the other routed blocks.
-//   * sparse kernel: routed (query, block) pairs whose block few queries of the
-//     tile selected are grouped by block (plan -> scan -> scatter kernels); one
-//     work-group stages the block's K/V in LDS once and runs up to 128 gathered
-//     queries through the same MFMA tiles, writing a normalised bf16 partial and
-//     its base-2 log-sum-exp per (pair, head).
+//     sequence), 32 queries per wavefront.  64-key items (the window band, then
+//     the tile's dense blocks) stream through double-buffered LDS stages filled
+//     by direct global->LDS loads; S^T = K Q^T with v_mfma_f32_32x32x16_bf16 so
+//     that each lane owns one query's softmax state; base-2 online softmax;
+//     O^T += V^T P^T; finally the query's sparse partials are merged in.
 // With no plan (dense_threshold <= 0) the tile kernel processes every routed
 // block of the tile as a dense block.
 
 #include "dash_common.h"
+
+#include <type_traits>
 
 namespace dash {
 
 constexpr int kPfTQ = 128;        // queries per tile work-group
 constexpr int kPfMaxK = 16;       // routed slots per query
 constexpr int kPfMaxBlocks = 2048;
-constexpr int kPfCH = 128;        // pairs per sparse chunk
+constexpr int kPfCH = 512;        // pairs per sparse chunk (work-group)
 
 struct PrefillArgs {
   const bf16* q; const bf16* k; const bf16* v;
@@ -44,6 +47,7 @@ struct PrefillArgs {
   const int32_t* cu;                   // varlen: [B+1]
   const int32_t* kmin;                 // per token row, or null
   int S, H, bs, lw, nblk_cap;
+  int ntiles;                          // 128-query tiles per sequence (of S)
   float scale_log2e;
   // hybrid plan (null kind: every routed block is processed by the tile kernel)
   uint8_t* kind;                       // [rows, K]: 0 skip, 1 tile (dense), 2 sparse
@@ -57,7 +61,8 @@ struct PrefillArgs {
   int chunk_cap;
   int32_t* pairs;                      // [rows * K] grouped by block per sequence
   float* part_lse;                     // [rows * K, H]  base-2 log-sum-exp
-  bf16* part_o;                        // [rows * K, H, D]  normalised partial output
+  bf16* part_o;                        // [rows * K, H, D]  normalised partial output, dims
+                                       // in MFMA lane order (see part_index)
 };
 
 __device__ __forceinline__ int seq_len(const PrefillArgs& a, int b) {
@@ -71,6 +76,12 @@ __device__ __forceinline__ const bf16* seq_ptr(const bf16* base, const int32_t* 
   return cu ? base + (int64_t)cu[b] * st : base + (int64_t)b * sb;
 }
 
+// Position of dim 32 dt + 8 g + 4 hl + q of a partial row: the 64 dims a lane
+// half hl owns in the MFMA accumulator layout are contiguous, in (dt, g, q) order.
+__device__ __forceinline__ int part_index(int hl, int dt, int g, int q) {
+  return hl * 64 + dt * 16 + g * 4 + q;
+}
+
 // Keep a routed slot?  The block must exist, be valid, and have keys below the
 // window start and at or above the segment start.
 __device__ __forceinline__ bool slot_usable(const PrefillArgs& a, int c, int64_t p, int t, int nblk,
@@ -81,76 +92,9 @@ __device__ __forceinline__ bool slot_usable(const PrefillArgs& a, int c, int64_t
   return c * a.bs < ls && (c + 1) * a.bs > km;
 }
 
-// ---------------------------------------------------------------------------
-// MFMA building blocks (32 queries per wavefront, lane = query n, half hl)
-// ---------------------------------------------------------------------------
-template <int D, int LDK>
-__device__ __forceinline__ floatx16 qk_tile(const bf16 (*sK)[LDK], int krow0, const bf16x8 (&qop)[D / 16],
-                                            int n, int hl) {
-  floatx16 s;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) s[r] = 0.f;
-#pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk) {
-    const bf16x8 kop = *(const bf16x8*)&sK[krow0 + n][kk * 16 + hl * 8];
-    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qop[kk], s, 0, 0, 0);
-  }
-  return s;
-}
-
-// acc_o[dt] += V^T P^T over keys kbase .. kbase+15 of a row-major LDS V tile.
-// ds_read_tr16_b64 (gfx950): within each 16-lane group, result lane i element j
-// is element (i % 4) of the 8 bytes read by lane 4j + i/4.  Lane l reads the 4
-// dims 32dt + 16((l/16)%2) + 4(l%4) .. +3 of key row kbase + 4hl + (l%16)/4 (and
-// +8), which gives every lane the 8 keys kbase + 8(e/4) + 4hl + e%4 of its dim
-// row m = l % 32: the same key order as the P^T operand built from S^T.
+// ds_read_tr16_b64 (gfx950) operands: 4 x 16-bit values read from LDS.
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4v lds_short4;
-
-template <int D, int LDV>
-__device__ __forceinline__ void pv_slice_tr(const bf16 (*sV)[LDV], int kbase, const bf16x8& pop,
-                                            floatx16 (&acc_o)[D / 32], int lane) {
-  const int hl = lane >> 5;
-  const int row = kbase + 4 * hl + ((lane & 15) >> 2);
-  const int colq = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-#pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) {
-    const int col = dt * 32 + colq;
-    const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_short4*)(__attribute__((address_space(3))) void*)&sV[row][col]);
-    const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_short4*)(__attribute__((address_space(3))) void*)&sV[row + 8][col]);
-    bf16x8 vop;
-    const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo);
-    const bf16x4 h4 = __builtin_bit_cast(bf16x4, hi);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) { vop[e] = l4[e]; vop[e + 4] = h4[e]; }
-    acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pop, acc_o[dt], 0, 0, 0);
-  }
-}
-
-// Stage rows j0 .. j0+nrows-1 of K and V (both row-major) into LDS; rows at or
-// beyond len are zero.  nrows * D / 8 chunks of 16 bytes over 256 threads.
-template <int D, int LDK, int LDV>
-__device__ __forceinline__ void stage_kv(bf16 (*sK)[LDK], bf16 (*sV)[LDV], const bf16* kb,
-                                         const bf16* vb, int64_t k_st, int64_t v_st, int j0,
-                                         int nrows, int len, int tid) {
-  const int nchunks = nrows * (D / 8);
-  for (int chunk = tid; chunk < nchunks; chunk += 256) {
-    const int kr = chunk / (D / 8), c8 = (chunk % (D / 8)) * 8;
-    const int j = j0 + kr;
-    bf16x8 kv8, vv8;
-    if (j < len) {
-      kv8 = *(const bf16x8*)(kb + (int64_t)j * k_st + c8);
-      vv8 = *(const bf16x8*)(vb + (int64_t)j * v_st + c8);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) { kv8[e] = (bf16)0.f; vv8[e] = (bf16)0.f; }
-    }
-    *(bf16x8*)&sK[kr][c8] = kv8;
-    *(bf16x8*)&sV[kr][c8] = vv8;
-  }
-}
 
 // Load the K <= 16 routed slots of one row: ids, validity and bias, with
 // vector loads where the row is 16-byte aligned.
@@ -306,160 +250,164 @@ __global__ __launch_bounds__(kPfTQ) void prefill_scatter_kernel(PrefillArgs a) {
     if (sp[s]) a.pairs[base + off[c[s]] + tb[c[s]] + pos[s]] = (int32_t)(row * a.K + s - base);
 }
 
-// ---------------------------------------------------------------------------
-// Sparse kernel: one chunk of <= 128 pairs of one routed block, one head.
-// ---------------------------------------------------------------------------
-template <int D>
-__global__ __launch_bounds__(256) void prefill_sparse_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16 sK[64][D + 8];
-  __shared__ __attribute__((aligned(16))) bf16 sV[64][D + 32];
-  const int b = blockIdx.z, h = blockIdx.y, ch = blockIdx.x;
-  if (ch >= a.num_chunks[b]) return;
-  const int4 e = a.chunk_tab[(int64_t)b * a.chunk_cap + ch];
-  const int c = e.x, start = e.y, npairs = e.z;
-  const int len = seq_len(a, b);
-  const int tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
-  const int hl = lane >> 5, n = lane & 31;
-  const int64_t r0 = row0(a, b);
-  const bf16* kb = seq_ptr(a.k, a.cu, b, a.k_sb, a.k_st) + (int64_t)h * a.k_sh;
-  const bf16* vb = seq_ptr(a.v, a.cu, b, a.v_sb, a.v_st) + (int64_t)h * a.v_sh;
-  stage_kv<D, D + 8, D + 32>(sK, sV, kb, vb, a.k_st, a.v_st, c * a.bs, a.bs, len, tid);
-
-  const int pi = wv * 32 + n;
-  const bool active = pi < npairs;
-  const int32_t pl = a.pairs[r0 * a.K + start + min(pi, npairs - 1)];   // pair index in sequence
-  const int64_t p = r0 * a.K + pl;
-  const int t = pl / a.K;
-  const int ls = t - a.lw + 1;
-  const int km = a.kmin ? a.kmin[r0 + t] : 0;
-  const float bias2 = a.bias[p] * 1.4426950408889634f;
-  const bf16* qb = seq_ptr(a.q, a.cu, b, a.q_sb, a.q_st) + (int64_t)h * a.q_sh + (int64_t)t * a.q_st;
-  bf16x8 qop[D / 16];
-#pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk) qop[kk] = *(const bf16x8*)(qb + kk * 16 + hl * 8);
-  __syncthreads();
-  if (!__any(active)) return;
-
-  const int nsub = a.bs / 32;     // 1 or 2 key sub-tiles of 32
-  floatx16 s[2];
-  float mloc = -INFINITY;
-#pragma unroll
-  for (int sub = 0; sub < 2; ++sub) {
-    if (sub < nsub) {
-      s[sub] = qk_tile<D, D + 8>(sK, sub * 32, qop, n, hl);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = c * a.bs + sub * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
-        const bool ok = active && key < ls && key >= km && key < len;
-        const float x = ok ? s[sub][r] * a.scale_log2e + bias2 : -INFINITY;
-        s[sub][r] = x;
-        mloc = fmaxf(mloc, x);
-      }
-    }
-  }
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
-  const float mu = (mloc == -INFINITY) ? 0.f : mloc;
-  floatx16 acc_o[D / 32];
-#pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc_o[dt][r] = 0.f;
-  float psum = 0.f;
-#pragma unroll
-  for (int sub = 0; sub < 2; ++sub) {
-    if (sub < nsub) {
-      bf16x8 pop[2];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pr = fast_exp2(s[sub][r] - mu);
-        psum += pr;
-        pop[r >> 3][r & 7] = (bf16)pr;
-      }
-      pv_slice_tr<D, D + 32>(sV, sub * 32, pop[0], acc_o, lane);
-      pv_slice_tr<D, D + 32>(sV, sub * 32 + 16, pop[1], acc_o, lane);
-    }
-  }
-  const float l_tot = psum + __shfl_xor(psum, 32, kWave);
-  if (!active) return;
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  bf16* po = a.part_o + (p * a.H + h) * D;
-#pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      bf16x4 w;
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) w[q4] = (bf16)(acc_o[dt][g * 4 + q4] * inv);
-      *(bf16x4*)(po + dt * 32 + 8 * g + 4 * hl) = w;
-    }
-  if (hl == 0) a.part_lse[p * a.H + h] = l_tot > 0.f ? mloc + log2f(l_tot) : -INFINITY;
-}
 
 // ---------------------------------------------------------------------------
 // Tile kernel: window band + dense routed blocks + merge of the sparse partials.
-// ---------------------------------------------------------------------------
-// Register-staged K/V rows for the software pipeline of the tile kernel:
-// thread tid holds chunks tid + 256*i (i < 4) of a 64-key x 128-dim tile.
-struct KVRegs {
-  bf16x8 k[4], v[4];
-};
-
-template <int D>
-__device__ __forceinline__ void kv_prefetch(KVRegs& r, const bf16* kb, const bf16* vb,
-                                            int64_t k_st, int64_t v_st, int j0, int nkeys,
-                                            int len, int tid) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int chunk = tid + 256 * i;
-    const int kr = chunk / (D / 8), c8 = (chunk % (D / 8)) * 8;
-    const int j = j0 + kr;
-    if (kr < nkeys && j < len) {
-      r.k[i] = *(const bf16x8*)(kb + (int64_t)j * k_st + c8);
-      r.v[i] = *(const bf16x8*)(vb + (int64_t)j * v_st + c8);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) { r.k[i][e] = (bf16)0.f; r.v[i][e] = (bf16)0.f; }
-    }
-  }
-}
-
-template <int D, int LDK, int LDV>
-__device__ __forceinline__ void kv_commit(const KVRegs& r, bf16 (*sK)[LDK], bf16 (*sV)[LDV],
-                                          int tid) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int chunk = tid + 256 * i;
-    const int kr = chunk / (D / 8), c8 = (chunk % (D / 8)) * 8;
-    *(bf16x8*)&sK[kr][c8] = r.k[i];
-    *(bf16x8*)&sV[kr][c8] = r.v[i];
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Tile kernel: window band + dense routed blocks + merge of the sparse partials.
-// Items of up to 64 keys: the window band in 64-key steps, then one item per
-// dense routed block (per 64 keys of it).  The next item's K/V is loaded into
-// registers while the current one computes.
+//
+// Items of up to 64 keys: the window band in 64-key steps, then the dense routed
+// blocks of the tile in ascending order (64 keys per item).  K and V of an item
+// are 64 x 128 bf16 tiles in LDS, double-buffered: the next item's tiles are
+// fetched straight into LDS (16-byte global_load_lds per lane) while the current
+// one computes, one barrier per item.  Rows are stored as 16 chunks of 16 bytes
+// with the chunk slot XOR-swizzled by the row, so that the K operand reads
+// (ds_read_b128: 16 lanes a clock read 16 rows at one chunk) and the
+// transposing V reads (ds_read_b64_tr_b16: 32 lanes a clock read 4 rows at 4
+// adjacent chunks) hit distinct banks of gfx950's 256-byte-per-clock LDS
+// (measured conflict-free with SQ_LDS_BANK_CONFLICT).
+// Per item and wavefront (32 queries): S^T for both 32-key halves, the
+// visible-key mask as a per-query key range (no
+// mask when the whole half is visible to every query), base-2 online softmax
+// with a lazy rescale, O^T += V^T P^T.
 // ---------------------------------------------------------------------------
 constexpr int kPfIT = 64;         // keys per item in the tile kernel
+
+__device__ __forceinline__ int k_slot(int r, int c) { return c ^ (r & 15); }
+__device__ __forceinline__ int v_slot(int r, int c) { return c ^ ((r & 3) << 2); }
+
+// Per-lane element offsets of the direct loads of a 64-key stage: wavefront wv
+// issues the 4-row groups wv, wv+4, wv+8, wv+12; lane l of a group fills slot
+// l % 16 of row 4 grp + l / 16 with chunk slot ^ swizzle(row) of that row.
+struct FetchOffsets {
+  uint32_t k[4], v[4];
+  int r[4];
+};
+
+__device__ __forceinline__ FetchOffsets fetch_offsets(int64_t k_st, int64_t v_st, int wv,
+                                                      int lane) {
+  FetchOffsets f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int grp = u * 4 + wv;
+    const int r = grp * 4 + (lane >> 4), slot = lane & 15;
+    f.r[u] = r;
+    f.k[u] = (uint32_t)(r * k_st + k_slot(r, slot) * 8);
+    f.v[u] = (uint32_t)(r * v_st + v_slot(r, slot) * 8);
+  }
+  return f;
+}
+
+// Issue the loads of K and V rows j0 .. j0+63 of one head into a swizzled
+// stage; rows at or beyond len repeat row len-1 (their keys are masked).
+template <int D>
+__device__ __forceinline__ void tile_fetch(bf16* sKs, bf16* sVs, const bf16* kb, const bf16* vb,
+                                           int64_t k_st, int64_t v_st, int j0, int len, int wv,
+                                           int lane, const FetchOffsets& f) {
+  static_assert(D == 128, "16 chunks per row");
+  const bf16* kb0 = kb + (int64_t)j0 * k_st;
+  const bf16* vb0 = vb + (int64_t)j0 * v_st;
+  const bool inside = j0 + kPfIT <= len;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int grp = u * 4 + wv;
+    const bf16* kp;
+    const bf16* vp;
+    if (inside) {
+      kp = kb0 + f.k[u];
+      vp = vb0 + f.v[u];
+    } else {
+      const int64_t dj = min(j0 + f.r[u], len - 1) - (j0 + f.r[u]);   // <= 0
+      kp = kb0 + f.k[u] + dj * k_st;
+      vp = vb0 + f.v[u] + dj * v_st;
+    }
+    __builtin_amdgcn_global_load_lds((const void*)kp,
+                                     (__attribute__((address_space(3))) void*)(sKs + grp * 4 * D),
+                                     16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)vp,
+                                     (__attribute__((address_space(3))) void*)(sVs + grp * 4 * D),
+                                     16, 0, 0);
+  }
+}
+
+// K operand of keys krow0 + (lane % 32), dims 16 kk + 8 (lane / 32) .. +7.
+__device__ __forceinline__ bf16x8 k_frag(const bf16* sKs, int krow, int kk, int hl) {
+  return *(const bf16x8*)(sKs + krow * 128 + k_slot(krow, 2 * kk + hl) * 8);
+}
+
+// acc_o[dt] += V^T P^T over keys kbase .. kbase+15 of a swizzled V stage.
+// ds_read_tr16_b64 (gfx950): within each 16-lane group, result lane i element j
+// is element (i % 4) of the 8 bytes read by lane 4j + i/4.  Lane l reads the 4
+// dims 32dt + 16((l/16)%2) + 4(l%4) .. +3 of key row kbase + 4hl + (l%16)/4 (and
+// +8), which gives every lane the 8 keys kbase + 8(e/4) + 4hl + e%4 of its dim
+// row m = l % 32: the same key order as the P^T operand built from S^T.
+__device__ __forceinline__ void pv_tr_swz(const bf16* sVs, int kbase, const bf16x8& pop,
+                                          floatx16 (&acc_o)[4], int lane) {
+  const int hl = lane >> 5;
+  const int row = kbase + 4 * hl + ((lane & 15) >> 2);
+  const int cq = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+  const int within = 4 * (lane & 1);
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    const int c = dt * 4 + cq;
+    const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_short4*)(__attribute__((address_space(3))) void*)(sVs + row * 128 + v_slot(row, c) * 8 + within));
+    const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_short4*)(__attribute__((address_space(3))) void*)(sVs + (row + 8) * 128 + v_slot(row + 8, c) * 8 + within));
+    bf16x8 vop;
+    const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo);
+    const bf16x4 h4 = __builtin_bit_cast(bf16x4, hi);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { vop[e] = l4[e]; vop[e + 4] = h4[e]; }
+    acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pop, acc_o[dt], 0, 0, 0);
+  }
+}
+
+// Maximum over lanes l and l^32, every lane gets it (v_permlane32_swap).
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// First dense block > c of the tile's bitmap (nwords 32-bit words), or -1.
+__device__ __forceinline__ int next_union(const uint32_t* sBits, int nwords, int c, int lane) {
+  const int b0 = c + 1;
+  const int w = (b0 >> 5) + lane;
+  uint32_t bits = 0;
+  if (w < nwords) {
+    bits = sBits[w];
+    if (lane == 0) bits &= ~0u << (b0 & 31);
+  }
+  const uint64_t nz = __ballot(bits != 0);
+  if (nz == 0) return -1;
+  const int f = __builtin_ctzll(nz);
+  const uint32_t fb = __builtin_amdgcn_readlane(bits, f);
+  return __builtin_amdgcn_readfirstlane((((b0 >> 5) + f) << 5) + (int)__builtin_ctz(fb));
+}
 
 template <int D>
 __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
   static_assert(D == 128, "head_dim 128");
-  __shared__ __attribute__((aligned(16))) bf16 sK[kPfIT][D + 8];
-  __shared__ __attribute__((aligned(16))) bf16 sV[kPfIT][D + 32];
-  __shared__ int32_t sIdx[kPfTQ][kPfMaxK];
+  __shared__ __attribute__((aligned(16))) bf16 sK0[kPfIT * D];
+  __shared__ __attribute__((aligned(16))) bf16 sK1[kPfIT * D];
+  __shared__ __attribute__((aligned(16))) bf16 sV0[kPfIT * D];
+  __shared__ __attribute__((aligned(16))) bf16 sV1[kPfIT * D];
+  __shared__ int16_t sIdx[kPfTQ][kPfMaxK];
   __shared__ float sBias[kPfTQ][kPfMaxK];
-  __shared__ int32_t sCnt[kPfTQ];
+  __shared__ uint8_t sCnt[kPfTQ];
   __shared__ uint32_t sBits[kPfMaxBlocks / 32];
-  __shared__ int32_t sUnion[kPfMaxBlocks];
-  __shared__ int32_t sNU;
 
-  const int b = blockIdx.z, h = blockIdx.y;
+  // logical order (sequence, head, tile), tile fastest, contiguous per XCD
+  const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int tile = lid % a.ntiles, bh = lid / a.ntiles;
+  const int h = bh % a.H, b = bh / a.H;
   const int len = seq_len(a, b);
-  const int t0 = blockIdx.x * kPfTQ;
+  const int t0 = tile * kPfTQ;
   if (t0 >= len) return;
   const int nblk = (len + a.bs - 1) / a.bs;
+  const int nwords = (nblk + 31) / 32;
   const int tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
   const int hl = lane >> 5;         // half of the wave: 0/1
   const int n = lane & 31;          // query column within the wave
@@ -472,7 +420,39 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
   if (tid < kPfTQ) {
     const int t = t0 + tid;
     int cnt = 0;
-    if (t < len) {
+    auto insert = [&](int c, float bv) {
+      int u = cnt;
+      while (u > 0 && sIdx[tid][u - 1] > c) {
+        sIdx[tid][u] = sIdx[tid][u - 1];
+        sBias[tid][u] = sBias[tid][u - 1];
+        --u;
+      }
+      sIdx[tid][u] = (int16_t)c;
+      sBias[tid][u] = bv;
+      ++cnt;
+      atomicOr(&sBits[c >> 5], 1u << (c & 31));
+    };
+    if (t < len && a.kind && a.K == kPfMaxK) {
+      // planned rows of 16 slots: kinds, ids and biases with 16-byte loads
+      const int64_t p0 = (r0 + t) * kPfMaxK;
+      const uint4 kv = *(const uint4*)(a.kind + p0);
+      int4 iv[4];
+      float4 bv4[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        iv[q] = ((const int4*)(a.idx + p0))[q];
+        bv4[q] = ((const float4*)(a.bias + p0))[q];
+      }
+      const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+      for (int s = 0; s < kPfMaxK; ++s) {
+        const uint32_t kd = (kw[s >> 2] >> (8 * (s & 3))) & 0xffu;
+        const int q = s >> 2, e = s & 3;
+        const int c = e == 0 ? iv[q].x : e == 1 ? iv[q].y : e == 2 ? iv[q].z : iv[q].w;
+        const float bv = e == 0 ? bv4[q].x : e == 1 ? bv4[q].y : e == 2 ? bv4[q].z : bv4[q].w;
+        if (kd == 1) insert(c, bv);
+      }
+    } else if (t < len) {
       const int64_t row = r0 + t;
       const int km = a.kmin ? a.kmin[row] : 0;
       for (int s = 0; s < a.K; ++s) {
@@ -486,49 +466,15 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
           for (int u = 0; u < cnt; ++u) dup |= (sIdx[tid][u] == c);
           if (dup) continue;
         }
-        const float bv = a.bias[p];
-        int u = cnt;
-        while (u > 0 && sIdx[tid][u - 1] > c) {
-          sIdx[tid][u] = sIdx[tid][u - 1];
-          sBias[tid][u] = sBias[tid][u - 1];
-          --u;
-        }
-        sIdx[tid][u] = c;
-        sBias[tid][u] = bv;
-        ++cnt;
-        atomicOr(&sBits[c >> 5], 1u << (c & 31));
+        insert(c, a.bias[p]);
       }
     }
-    sCnt[tid] = cnt;
-  }
-  __syncthreads();
-  // ---- compact the union bitmap into an ascending block list ----
-  if (wv == 0) {
-    int base = 0;
-    for (int w0 = 0; w0 < (nblk + 31) / 32; w0 += kWave) {
-      const int w = w0 + lane;
-      const uint32_t bits = (w < (nblk + 31) / 32) ? sBits[w] : 0u;
-      const int c = __popc(bits);
-      int incl = c;
-#pragma unroll
-      for (int s = 1; s < kWave; s <<= 1) {
-        const int o = __shfl_up(incl, s, kWave);
-        if (lane >= s) incl += o;
-      }
-      int off = base + incl - c;
-      uint32_t bb = bits;
-      while (bb) {
-        const int bit = __ffs(bb) - 1;
-        sUnion[off++] = w * 32 + bit;
-        bb &= bb - 1;
-      }
-      base += __shfl(incl, kWave - 1, kWave);
-    }
-    if (lane == 0) sNU = base;
+    sCnt[tid] = (uint8_t)cnt;
   }
 
   // ---- this lane's query and its Q^T operand (8 k-steps of 16 dims) ----
   const int tq = t0 + wv * 32 + n;
+  const bool qvalid = tq < len;
   const int tqc = min(tq, len - 1);
   const int64_t qrow = r0 + tqc;
   const bf16* qb = seq_ptr(a.q, a.cu, b, a.q_sb, a.q_st) + (int64_t)h * a.q_sh;
@@ -539,6 +485,7 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
   const int q_ls = tq - a.lw + 1;
   const int q_km = a.kmin ? a.kmin[qrow] : 0;
   const int q_lo = max(max(q_ls, q_km), 0);       // first window key
+  const int r_hi = min(q_ls, len) - 1;            // last key a routed block may give
 
   floatx16 acc_o[D / 32];
 #pragma unroll
@@ -547,111 +494,130 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
     for (int r = 0; r < 16; ++r) acc_o[dt][r] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  __syncthreads();
-  const int nu = sNU;
+  const bf16* kb = seq_ptr(a.k, a.cu, b, a.k_sb, a.k_st) + (int64_t)h * a.k_sh;
+  const bf16* vb = seq_ptr(a.v, a.cu, b, a.v_sb, a.v_st) + (int64_t)h * a.v_sh;
   const int t_last = min(t0 + kPfTQ - 1, len - 1);
   const int jw0 = (max(t0 - a.lw + 1, 0) / kPfIT) * kPfIT;
   const int n_win = (t_last - jw0) / kPfIT + 1;
   const int ipb = (a.bs + kPfIT - 1) / kPfIT;      // items per routed block
-  const int keys_rt = min(a.bs, kPfIT);            // keys per routed item
+  __syncthreads();
+  int nu = 0;
+  {
+    const uint32_t wbits = lane < nwords ? sBits[lane] : 0u;
+    nu = __popc(wbits);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) nu += __shfl_xor(nu, m, kWave);
+    nu = __builtin_amdgcn_readfirstlane(nu);
+  }
   const int n_items = n_win + nu * ipb;
-
-  const bf16* kb = seq_ptr(a.k, a.cu, b, a.k_sb, a.k_st) + (int64_t)h * a.k_sh;
-  const bf16* vb = seq_ptr(a.v, a.cu, b, a.v_sb, a.v_st) + (int64_t)h * a.v_sh;
-  const int myrow = wv * 32 + n;           // row within the tile
-  const int tw = t0 + wv * 32;             // first query of this wavefront
-  int ptr = 0;                             // next dense block of this query
-  bool cur_sel = false;
-  float cur_bias = 0.f;
+  const FetchOffsets fo = fetch_offsets(a.k_st, a.v_st, wv, lane);
+  const int myrow = wv * 32 + n;
+  const int my_cnt = sCnt[myrow];
   const float log2e = 1.4426950408889634f;
 
-  auto item_start = [&](int it, int& nkeys) -> int {
-    if (it < n_win) { nkeys = kPfIT; return jw0 + it * kPfIT; }
-    const int r = it - n_win;
-    nkeys = keys_rt;
-    return sUnion[r / ipb] * a.bs + (r % ipb) * kPfIT;
+  // item iterators: (block, sub-item) of the item being fetched and computed
+  int pf_c = -1, pf_sub = ipb - 1;
+  int cp_c = -1, cp_sub = ipb - 1;
+  auto advance = [&](int it, int& c, int& sub) {
+    if (it < n_win) return;
+    if (++sub >= ipb) { sub = 0; c = next_union(sBits, nwords, c, lane); }
   };
-
-  KVRegs pre;
+  auto item_j0 = [&](int it, int c, int sub) {
+    return it < n_win ? jw0 + it * kPfIT : c * a.bs + sub * kPfIT;
+  };
   if (n_items > 0) {
-    int nk0;
-    const int j00 = item_start(0, nk0);
-    kv_prefetch<D>(pre, kb, vb, a.k_st, a.v_st, j00, nk0, len, tid);
+    advance(0, pf_c, pf_sub);
+    tile_fetch<D>(sK0, sV0, kb, vb, a.k_st, a.v_st, item_j0(0, pf_c, pf_sub), len, wv, lane, fo);
   }
-  for (int it = 0; it < n_items; ++it) {
-    const bool routed = it >= n_win;
-    int nkeys;
-    const int j0 = item_start(it, nkeys);
-    int c = -1, sub_item = 0;
-    if (routed) {
-      const int r = it - n_win;
-      c = sUnion[r / ipb];
-      sub_item = r % ipb;
-    }
-    __syncthreads();                       // the previous item is done with LDS
-    kv_commit<D, D + 8, D + 32>(pre, sK, sV, tid);
-    __syncthreads();
+  int ptr = 0;                             // next dense block of this query
+  float cur_b = -INFINITY;                 // bias (base 2) of the current routed block
+  // One item on stage ST (the stages are distinct LDS arrays named at compile
+  // time, so the reads of this stage do not wait for the loads into the other).
+  auto step = [&](int it, auto stage_tag) {
+    constexpr int ST = decltype(stage_tag)::value;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();                       // item it landed; item it-1 is done with its stage
     if (it + 1 < n_items) {
-      int nk1;
-      const int j1 = item_start(it + 1, nk1);
-      kv_prefetch<D>(pre, kb, vb, a.k_st, a.v_st, j1, nk1, len, tid);
+      advance(it + 1, pf_c, pf_sub);
+      if constexpr (ST == 0)
+        tile_fetch<D>(sK1, sV1, kb, vb, a.k_st, a.v_st, item_j0(it + 1, pf_c, pf_sub), len, wv, lane, fo);
+      else
+        tile_fetch<D>(sK0, sV0, kb, vb, a.k_st, a.v_st, item_j0(it + 1, pf_c, pf_sub), len, wv, lane, fo);
     }
-
-    // ---- does any query of this wavefront use this item? ----
-    bool use;
-    float brow = 0.f;
+    const bf16* sKs;
+    const bf16* sVs;
+    if constexpr (ST == 0) { sKs = sK0; sVs = sV0; } else { sKs = sK1; sVs = sV1; }
+    advance(it, cp_c, cp_sub);
+    const bool routed = it >= n_win;
+    const int j0 = item_j0(it, cp_c, cp_sub);
+    int nkeys = kPfIT;
+    int lo, hi;
+    float bl;
     if (!routed) {
-      use = (j0 <= tq) && (j0 + nkeys - 1 >= q_lo) && (tq < len);
+      lo = q_lo; hi = tq;
+      bl = qvalid ? 0.f : -INFINITY;
     } else {
-      if (sub_item == 0) {
-        cur_sel = false;
-        if (ptr < sCnt[myrow] && sIdx[myrow][ptr] == c) {
-          cur_sel = true;
-          cur_bias = sBias[myrow][ptr];
+      if (cp_sub == 0) {
+        cur_b = -INFINITY;
+        if (ptr < my_cnt && sIdx[myrow][ptr] == cp_c) {
+          cur_b = sBias[myrow][ptr] * log2e;
           ++ptr;
         }
       }
-      use = cur_sel && (tq < len);
-      brow = cur_bias * log2e;
+      nkeys = min(kPfIT, a.bs - cp_sub * kPfIT);
+      lo = q_km; hi = r_hi;
+      bl = qvalid ? cur_b : -INFINITY;
     }
-    if (!__any(use)) continue;
+    // halves of 32 keys: skipped when no query of the wavefront sees a key of it,
+    // mask-free when every query with a finite bias sees all of it
+    const bool live = bl != -INFINITY;
+    bool do_h[2], full_h[2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int k0 = j0 + 32 * hf;
+      const bool exists = 32 * hf < nkeys;
+      do_h[hf] = exists && __any(live && lo <= k0 + 31 && hi >= k0);
+      full_h[hf] = __all(!live || (lo <= k0 && k0 + 31 <= hi));
+    }
+    if (!do_h[0] && !do_h[1]) return;
+    const uint32_t span = hi >= lo ? (uint32_t)(hi - lo) : 0u;
+    const int lo_eff = hi >= lo ? lo : 0x40000000;
 
-    // ---- per 32-key sub-tile: S^T, masks, bias, online softmax, O^T += V^T P^T ----
-    // A sub-tile is skipped when no key of it is visible to any query of the
-    // wavefront, and needs no per-element mask when every key is visible to every
-    // query (unselected routed queries carry a -inf bias instead).
-    const int nsub = nkeys / 32;
-    const float bsel = use ? brow : -INFINITY;
-    for (int sb = 0; sb < nsub; ++sb) {
-      const int k0 = j0 + sb * 32;
-      bool full;
-      if (!routed) {
-        if (k0 > tw + 31 || k0 + 31 < max(tw - a.lw + 1, 0)) continue;
-        full = !a.kmin && k0 + 31 <= tw && k0 >= tw + 31 - a.lw + 1 && tw + 31 < len;
+    // S^T of both halves first (two MFMA chains), then per half: softmax and
+    // O^T += V^T P^T.  In this order the softmax of half 0 runs on the VALU while
+    // the matrix core still works on half 1, and the softmax of half 1 while it
+    // works on the PV product of half 0.
+    floatx16 s[2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[hf][r] = 0.f;
+      if (!do_h[hf]) continue;
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk)
+        s[hf] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(sKs, 32 * hf + n, kk, hl), qop[kk],
+                                                        s[hf], 0, 0, 0);
+    }
+    const bf16x2 ones = {(bf16)1.f, (bf16)1.f};
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      if (!do_h[hf]) continue;
+      const int kq = j0 + 32 * hf + 4 * hl - lo_eff;     // key - lo for r = 0
+      // raw maximum (the scale is positive: max(fma(s, c, b)) = fma(max s, c, b));
+      // masked keys are left out here and get p = 0 below (s is not written, so
+      // both paths share its registers)
+      float mraw = -INFINITY;
+      if (full_h[hf]) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mraw = fmaxf(mraw, s[hf][r]);
       } else {
-        full = !a.kmin && k0 + 31 < tw - a.lw + 1 && k0 + 31 < len;
-      }
-      floatx16 s = qk_tile<D, D + 8>(sK, sb * 32, qop, n, hl);
-      float mloc = -INFINITY;
-      if (full) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          s[r] = fmaf(s[r], a.scale_log2e, bsel);
-          mloc = fmaxf(mloc, s[r]);
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = k0 + 8 * (r >> 2) + 4 * hl + (r & 3);
-          bool ok;
-          if (!routed) ok = use && key >= q_lo && key <= tq;
-          else ok = use && key < q_ls && key >= q_km && key < len;
-          const float x = ok ? fmaf(s[r], a.scale_log2e, brow) : -INFINITY;
-          s[r] = x;
-          mloc = fmaxf(mloc, x);
+          const uint32_t d = (uint32_t)(kq + 8 * (r >> 2) + (r & 3));
+          mraw = fmaxf(mraw, d <= span ? s[hf][r] : -INFINITY);
         }
       }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
+      const float mloc = xor32_max(mraw == -INFINITY ? -INFINITY : fmaf(mraw, a.scale_log2e, bl));
       // Lazy rescale: the exponent reference m_run only moves when some query's
       // maximum exceeds it by more than 8 (probabilities stay <= 2^8).
       if (__any(mloc > m_run + 8.f)) {
@@ -664,48 +630,116 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
           for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
         m_run = m_new;
       }
-      const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
+      // p = 2^(s c + b - m); the row sum adds the bf16 p the PV product uses
+      const float off = bl - ((m_run == -INFINITY) ? 0.f : m_run);
       bf16x8 pop[2];
+      if (full_h[hf]) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pr = fast_exp2(s[r] - m_use);
-        l_run += pr;
-        pop[r >> 3][r & 7] = (bf16)pr;
+        for (int r = 0; r < 16; ++r) pop[r >> 3][r & 7] = (bf16)fast_exp2(fmaf(s[hf][r], a.scale_log2e, off));
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t d = (uint32_t)(kq + 8 * (r >> 2) + (r & 3));
+          const float pr = fast_exp2(fmaf(s[hf][r], a.scale_log2e, off));
+          pop[r >> 3][r & 7] = (bf16)(d <= span ? pr : 0.f);
+        }
       }
-      pv_slice_tr<D, D + 32>(sV, sb * 32, pop[0], acc_o, lane);
-      pv_slice_tr<D, D + 32>(sV, sb * 32 + 16, pop[1], acc_o, lane);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const bf16x2 pp = {pop[j][e], pop[j][e + 1]};
+          l_run = __builtin_amdgcn_fdot2_f32_bf16(pp, ones, l_run, false);
+        }
+      pv_tr_swz(sVs, 32 * hf, pop[0], acc_o, lane);
+      pv_tr_swz(sVs, 32 * hf + 16, pop[1], acc_o, lane);
     }
+  };
+  for (int it = 0; it < n_items; it += 2) {
+    step(it, std::integral_constant<int, 0>{});
+    if (it + 1 < n_items) step(it + 1, std::integral_constant<int, 1>{});
   }
 
   // ---- merge the sparse partials of this query ----
-  if (a.kind && tq < len) {
-    const int64_t row = r0 + tq;
-    for (int s = 0; s < a.K; ++s) {
-      const int64_t p = row * a.K + s;
-      if (a.kind[p] != 2) continue;
-      const float lse2 = a.part_lse[p * a.H + h];
-      if (lse2 == -INFINITY) continue;
-      const float m_new = fmaxf(m_run, lse2);
-      const float alpha = fast_exp2(m_run - m_new);
-      const float w = fast_exp2(lse2 - m_new);
-      l_run = l_run * alpha + (hl == 0 ? w : 0.f);
-      m_run = m_new;
-      const bf16* po = a.part_o + (p * a.H + h) * D;
+  // All kinds and log-sum-exps are loaded first and the reference moves once to
+  // their maximum.  Then round j adds every lane's j-th sparse partial (a
+  // wave-uniform loop, so the loads of round j+1 are in flight while round j is
+  // accumulated); partial rows are lane-contiguous and read with 16-byte loads.
+  if (a.kind) {
+    const int64_t p0 = (r0 + tqc) * a.K;
+    float l2[kPfMaxK];
+    uint32_t smask = 0;
+    if (a.K == kPfMaxK) {
+      const uint4 kv = *(const uint4*)(a.kind + p0);
+      const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+      for (int s = 0; s < kPfMaxK; ++s)
+        if (qvalid && ((kw[s >> 2] >> (8 * (s & 3))) & 0xffu) == 2) smask |= 1u << s;
+    } else {
+      for (int s = 0; s < a.K; ++s)
+        if (qvalid && a.kind[p0 + s] == 2) smask |= 1u << s;
+    }
+#pragma unroll
+    for (int s = 0; s < kPfMaxK; ++s)
+      l2[s] = ((smask >> s) & 1u) ? a.part_lse[(p0 + s) * a.H + h] : -INFINITY;
+    float mx = m_run;
+#pragma unroll
+    for (int s = 0; s < kPfMaxK; ++s) mx = fmaxf(mx, l2[s]);
+    if (mx > m_run) {
+      const float alpha = fast_exp2(m_run - mx);
+      l_run *= alpha;
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const bf16x4 ov = *(const bf16x4*)(po + dt * 32 + 8 * g + 4 * hl);
+        for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
+      m_run = mx;
+    }
+    // partials with a finite log-sum-exp, in slot order
+    uint32_t live = 0;
 #pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4)
-            acc_o[dt][g * 4 + q4] = acc_o[dt][g * 4 + q4] * alpha + w * bf2f(ov[q4]);
-        }
+    for (int s = 0; s < kPfMaxK; ++s)
+      if (l2[s] != -INFINITY) live |= 1u << s;
+    const int nlive = __popc(live);
+    int rounds = nlive;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) rounds = max(rounds, __shfl_xor(rounds, m, kWave));
+    rounds = __builtin_amdgcn_readfirstlane(rounds);
+    auto slot_of = [&](uint32_t msk) { return msk ? __builtin_ctz(msk) : 0; };
+    auto fetch_part = [&](int s, bf16x8 (&buf)[8]) {
+      const bf16* po = a.part_o + ((p0 + s) * a.H + h) * D + part_index(hl, 0, 0, 0);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) buf[q] = *(const bf16x8*)(po + q * 8);
+    };
+    bf16x8 cur[8], nxt[8];
+    uint32_t rem = live;
+    int s_cur = slot_of(rem);
+    if (rounds > 0 && nlive > 0) fetch_part(s_cur, cur);
+    for (int j = 0; j < rounds; ++j) {
+      const bool have = j < nlive;
+      const uint32_t rem_next = have ? (rem & (rem - 1)) : 0u;
+      const int s_next = slot_of(rem_next);
+      if (j + 1 < nlive) fetch_part(s_next, nxt);
+      if (have) {
+        const float w = fast_exp2(l2[s_cur] - m_run);
+        if (hl == 0) l_run += w;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+          for (int g = 0; g < 4; g += 2)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              acc_o[dt][g * 4 + e] += w * bf2f(cur[dt * 2 + g / 2][e]);
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) cur[q] = nxt[q];
+      rem = rem_next;
+      s_cur = s_next;
     }
   }
 
   // ---- epilogue: normalise and store ----
-  const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
-  if (tq < len) {
+  const float l_tot = xor32_sum(l_run);
+  if (qvalid) {
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     bf16* ob = (a.cu ? a.o + (int64_t)a.cu[b] * a.o_st : a.o + (int64_t)b * a.o_sb) +
                (int64_t)h * a.o_sh + (int64_t)tq * a.o_st;
@@ -722,6 +756,152 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
       const float lse = l_tot > 0.f ? (m_run + log2f(l_tot)) * 0.6931471805599453f : -INFINITY;
       a.lse[(r0 + tq) * a.lse_row + (int64_t)h * a.lse_sh] = lse;
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Sparse kernel: one chunk of up to 512 (query, block) pairs of one routed
+// block, one head.  The block's K and V rows are staged in LDS once (swizzled
+// like the tile kernel's stages); then each wavefront runs rounds of 32 gathered
+// queries (pairs 32 wv + 128 j + lane of the chunk): S^T = K Q^T, the query's
+// visible keys of the block with its routed bias, softmax, O^T = V^T P^T, and
+// writes the normalised bf16 partial (lane order, see part_index) and its
+// base-2 log-sum-exp per (pair, head).  No barrier after the staging; the pair
+// ids and Q rows of the next round are loaded while the current one computes.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void prefill_sparse_kernel(PrefillArgs a) {
+  static_assert(D == 128, "head_dim 128");
+  __shared__ __attribute__((aligned(16))) bf16 sKs[kPfIT * D];
+  __shared__ __attribute__((aligned(16))) bf16 sVs[kPfIT * D];
+  // logical order (sequence, head, chunk), chunk fastest, contiguous per XCD
+  const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int ch = lid % a.chunk_cap, bh = lid / a.chunk_cap;
+  const int h = bh % a.H, b = bh / a.H;
+  if (ch >= a.num_chunks[b]) return;
+  const int4 e = a.chunk_tab[(int64_t)b * a.chunk_cap + ch];
+  const int c = e.x, start = e.y, npairs = e.z;
+  const int len = seq_len(a, b);
+  const int tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
+  const int hl = lane >> 5, n = lane & 31;
+  const int64_t r0 = row0(a, b);
+  const bf16* kb = seq_ptr(a.k, a.cu, b, a.k_sb, a.k_st) + (int64_t)h * a.k_sh;
+  const bf16* vb = seq_ptr(a.v, a.cu, b, a.v_sb, a.v_st) + (int64_t)h * a.v_sh;
+  const FetchOffsets fo = fetch_offsets(a.k_st, a.v_st, wv, lane);
+  tile_fetch<D>(sKs, sVs, kb, vb, a.k_st, a.v_st, c * a.bs, len, wv, lane, fo);
+
+  const bf16* qb = seq_ptr(a.q, a.cu, b, a.q_sb, a.q_st) + (int64_t)h * a.q_sh;
+  const int32_t* plist = a.pairs + r0 * a.K + start;
+  const int nkeys = min(a.bs, kPfIT);
+  const int kfirst = c * a.bs;
+  const int nrounds = npairs > wv * 32 ? (npairs - wv * 32 + 127) / 128 : 0;
+  auto pair_id = [&](int j) {
+    const int pi = wv * 32 + 128 * j + n;
+    return plist[min(pi, npairs - 1)];
+  };
+  auto load_q = [&](int pid, bf16x8 (&q)[D / 16]) {
+    const int t = pid / a.K;
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk)
+      q[kk] = *(const bf16x8*)(qb + (int64_t)t * a.q_st + kk * 16 + hl * 8);
+  };
+  int pid_cur = 0, pid_nxt = 0;
+  bf16x8 qcur[D / 16], qnxt[D / 16];
+  if (nrounds > 0) {
+    pid_cur = pair_id(0);
+    load_q(pid_cur, qcur);
+    if (nrounds > 1) pid_nxt = pair_id(1);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  const bf16x2 ones = {(bf16)1.f, (bf16)1.f};
+
+  for (int j = 0; j < nrounds; ++j) {
+    // next round's Q rows and the id after it, in flight during this round
+    int pid_after = 0;
+    if (j + 1 < nrounds) load_q(pid_nxt, qnxt);
+    if (j + 2 < nrounds) pid_after = pair_id(j + 2);
+
+    const bool active = wv * 32 + 128 * j + n < npairs;
+    const int t = pid_cur / a.K;
+    const int64_t p = r0 * a.K + pid_cur;
+    const int q_ls = t - a.lw + 1;
+    const int lo = a.kmin ? a.kmin[r0 + t] : 0;
+    const int hi = min(q_ls, len) - 1;
+    const uint32_t span = (active && hi >= lo) ? (uint32_t)(hi - lo) : 0u;
+    const int lo_eff = (active && hi >= lo) ? lo : 0x40000000;
+    const float bl = a.bias[p] * 1.4426950408889634f;
+
+    floatx16 s[2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[hf][r] = 0.f;
+      if (32 * hf >= nkeys) continue;
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk)
+        s[hf] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(sKs, 32 * hf + n, kk, hl), qcur[kk],
+                                                        s[hf], 0, 0, 0);
+    }
+    float mraw = -INFINITY;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      if (32 * hf >= nkeys) continue;
+      const int kq = kfirst + 32 * hf + 4 * hl - lo_eff;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t d = (uint32_t)(kq + 8 * (r >> 2) + (r & 3));
+        mraw = fmaxf(mraw, d <= span ? s[hf][r] : -INFINITY);
+      }
+    }
+    const float mloc = xor32_max(mraw == -INFINITY ? -INFINITY : fmaf(mraw, a.scale_log2e, bl));
+    const float off = bl - (mloc == -INFINITY ? 0.f : mloc);
+    floatx16 acc_o[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc_o[dt][r] = 0.f;
+    float psum = 0.f;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      if (32 * hf >= nkeys) continue;
+      const int kq = kfirst + 32 * hf + 4 * hl - lo_eff;
+      bf16x8 pop[2];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t d = (uint32_t)(kq + 8 * (r >> 2) + (r & 3));
+        const float pr = fast_exp2(fmaf(s[hf][r], a.scale_log2e, off));
+        pop[r >> 3][r & 7] = (bf16)(d <= span ? pr : 0.f);
+      }
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+        for (int e2 = 0; e2 < 8; e2 += 2) {
+          const bf16x2 pp = {pop[jj][e2], pop[jj][e2 + 1]};
+          psum = __builtin_amdgcn_fdot2_f32_bf16(pp, ones, psum, false);
+        }
+      pv_tr_swz(sVs, 32 * hf, pop[0], acc_o, lane);
+      pv_tr_swz(sVs, 32 * hf + 16, pop[1], acc_o, lane);
+    }
+    const float l_tot = xor32_sum(psum);
+    if (active) {
+      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+      bf16* po = a.part_o + (p * a.H + h) * D;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; g += 2) {
+          bf16x8 w;
+#pragma unroll
+          for (int e2 = 0; e2 < 8; ++e2) w[e2] = (bf16)(acc_o[dt][g * 4 + e2] * inv);
+          *(bf16x8*)(po + part_index(hl, dt, g, 0)) = w;
+        }
+      if (hl == 0) a.part_lse[p * a.H + h] = l_tot > 0.f ? mloc + log2f(l_tot) : -INFINITY;
+    }
+    pid_cur = pid_nxt;
+    pid_nxt = pid_after;
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) qcur[kk] = qnxt[kk];
   }
 }
 
@@ -809,6 +989,7 @@ extern "C" int dash_attn_prefill(
   a.scale_log2e = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
   const int ntiles = (S + kPfTQ - 1) / kPfTQ;
+  a.ntiles = ntiles;
   const bool hybrid = dense_threshold > 0 && K > 0 && block_size <= 64;
   if (hybrid) {
     if (total_rows <= 0) return kErrInvalid;
@@ -831,9 +1012,9 @@ extern "C" int dash_attn_prefill(
     hipLaunchKernelGGL(prefill_plan_kernel, dim3(ntiles, B), dim3(kPfTQ), 0, st, a);
     hipLaunchKernelGGL(prefill_scan_kernel, dim3(B), dim3(1024), 0, st, a);
     hipLaunchKernelGGL(prefill_scatter_kernel, dim3(ntiles, B), dim3(kPfTQ), 0, st, a);
-    hipLaunchKernelGGL(prefill_sparse_kernel<128>, dim3(L.chunk_cap, H, B), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(prefill_sparse_kernel<128>, dim3(L.chunk_cap * H * B), dim3(256), 0, st, a);
   }
-  hipLaunchKernelGGL(prefill_tile_kernel<128>, dim3(ntiles, H, B), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(prefill_tile_kernel<128>, dim3(ntiles * H * B), dim3(256), 0, st, a);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? kOk : (int)e;
 }

@@ -166,7 +166,7 @@ def route(z, cand, idx_scale, floor, sigma, K, topm, row_nblk=None, width=None):
     return idx.view(*lead, Kp), bias.view(*lead, Kp), valid.view(*lead, Kp).bool()
 
 
-DENSE_THRESHOLD = 24   # of the 128 queries of a tile; below it a routed block goes sparse
+DENSE_THRESHOLD = 32   # of the 128 queries of a tile; below it a routed block goes sparse
 
 _WORKSPACES = {}
 
