@@ -12,7 +12,7 @@
 //   * plan -> scan -> scatter kernels: per 128-query tile, a routed block is
 //     "dense" if at least dense_threshold of the tile's queries selected it;
 //     the other (query, block) pairs are "sparse" and are grouped by block.
-//   * sparse kernel: one work-group per chunk of up to 512 sparse pairs of one
+//   * sparse kernel: one work-group per chunk of up to 256 sparse pairs of one
 //     block and head stages the block's K/V in LDS once and runs the gathered
 //     queries through the MFMA tiles, writing a normalised bf16 partial and its
 //     base-2 log-sum-exp per (pair, head).
@@ -34,7 +34,7 @@ namespace dash {
 constexpr int kPfTQ = 128;        // queries per tile work-group
 constexpr int kPfMaxK = 16;       // routed slots per query
 constexpr int kPfMaxBlocks = 2048;
-constexpr int kPfCH = 512;        // pairs per sparse chunk (work-group)
+constexpr int kPfCH = 256;        // pairs per sparse chunk (work-group)
 
 struct PrefillArgs {
   const bf16* q; const bf16* k; const bf16* v;
@@ -760,17 +760,16 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Sparse kernel: one chunk of up to 512 (query, block) pairs of one routed
+// Sparse kernel: one chunk of up to 256 (query, block) pairs of one routed
 // block, one head.  The block's K and V rows are staged in LDS once (swizzled
 // like the tile kernel's stages); then each wavefront runs rounds of 32 gathered
 // queries (pairs 32 wv + 128 j + lane of the chunk): S^T = K Q^T, the query's
 // visible keys of the block with its routed bias, softmax, O^T = V^T P^T, and
 // writes the normalised bf16 partial (lane order, see part_index) and its
-// base-2 log-sum-exp per (pair, head).  No barrier after the staging; the pair
-// ids and Q rows of the next round are loaded while the current one computes.
+// base-2 log-sum-exp per (pair, head).  No barrier after the staging.
 // ---------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(256) void prefill_sparse_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
   static_assert(D == 128, "head_dim 128");
   __shared__ __attribute__((aligned(16))) bf16 sKs[kPfIT * D];
   __shared__ __attribute__((aligned(16))) bf16 sVs[kPfIT * D];
@@ -778,8 +777,9 @@ __global__ __launch_bounds__(256) void prefill_sparse_kernel(PrefillArgs a) {
   const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
   const int ch = lid % a.chunk_cap, bh = lid / a.chunk_cap;
   const int h = bh % a.H, b = bh / a.H;
-  if (ch >= a.num_chunks[b]) return;
+  // the table entry is read together with the count (entries past it are unused)
   const int4 e = a.chunk_tab[(int64_t)b * a.chunk_cap + ch];
+  if (ch >= a.num_chunks[b]) return;
   const int c = e.x, start = e.y, npairs = e.z;
   const int len = seq_len(a, b);
   const int tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
@@ -799,39 +799,46 @@ __global__ __launch_bounds__(256) void prefill_sparse_kernel(PrefillArgs a) {
     const int pi = wv * 32 + 128 * j + n;
     return plist[min(pi, npairs - 1)];
   };
-  auto load_q = [&](int pid, bf16x8 (&q)[D / 16]) {
+  // a round's per-query inputs: Q rows, routed bias, segment start
+  struct RoundIn {
+    bf16x8 q[D / 16];
+    float bias;
+    int km;
+  };
+  auto load_round = [&](int pid, RoundIn& in) {
     const int t = pid / a.K;
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk)
-      q[kk] = *(const bf16x8*)(qb + (int64_t)t * a.q_st + kk * 16 + hl * 8);
+      in.q[kk] = *(const bf16x8*)(qb + (int64_t)t * a.q_st + kk * 16 + hl * 8);
+    in.bias = a.bias[r0 * a.K + pid];
+    in.km = a.kmin ? a.kmin[r0 + t] : 0;
   };
-  int pid_cur = 0, pid_nxt = 0;
-  bf16x8 qcur[D / 16], qnxt[D / 16];
-  if (nrounds > 0) {
-    pid_cur = pair_id(0);
-    load_q(pid_cur, qcur);
-    if (nrounds > 1) pid_nxt = pair_id(1);
-  }
+  // Both rounds' inputs (pair ids, Q rows, biases) are loaded before the first
+  // partial store: loads and stores share one counter on gfx9 and may complete
+  // out of order, so a load issued before a store cannot be waited for alone.
+  constexpr int kMaxRounds = kPfCH / 128;
+  static_assert(kMaxRounds == 2, "two rounds of 128 pairs per chunk");
+  int pids[kMaxRounds];
+#pragma unroll
+  for (int j = 0; j < kMaxRounds; ++j) pids[j] = j < nrounds ? pair_id(j) : 0;
+  RoundIn inA, inB;
+  if (nrounds > 0) load_round(pids[0], inA);
+  if (nrounds > 1) load_round(pids[1], inB);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   const bf16x2 ones = {(bf16)1.f, (bf16)1.f};
 
-  for (int j = 0; j < nrounds; ++j) {
-    // next round's Q rows and the id after it, in flight during this round
-    int pid_after = 0;
-    if (j + 1 < nrounds) load_q(pid_nxt, qnxt);
-    if (j + 2 < nrounds) pid_after = pair_id(j + 2);
-
+  auto round = [&](int j, const RoundIn& cur) {
+    const int pid_cur = pids[j];
     const bool active = wv * 32 + 128 * j + n < npairs;
     const int t = pid_cur / a.K;
     const int64_t p = r0 * a.K + pid_cur;
     const int q_ls = t - a.lw + 1;
-    const int lo = a.kmin ? a.kmin[r0 + t] : 0;
+    const int lo = cur.km;
     const int hi = min(q_ls, len) - 1;
     const uint32_t span = (active && hi >= lo) ? (uint32_t)(hi - lo) : 0u;
     const int lo_eff = (active && hi >= lo) ? lo : 0x40000000;
-    const float bl = a.bias[p] * 1.4426950408889634f;
-
+    const float bl = cur.bias * 1.4426950408889634f;
     floatx16 s[2];
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
@@ -840,7 +847,7 @@ __global__ __launch_bounds__(256) void prefill_sparse_kernel(PrefillArgs a) {
       if (32 * hf >= nkeys) continue;
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk)
-        s[hf] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(sKs, 32 * hf + n, kk, hl), qcur[kk],
+        s[hf] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(sKs, 32 * hf + n, kk, hl), cur.q[kk],
                                                         s[hf], 0, 0, 0);
     }
     float mraw = -INFINITY;
@@ -898,11 +905,9 @@ __global__ __launch_bounds__(256) void prefill_sparse_kernel(PrefillArgs a) {
         }
       if (hl == 0) a.part_lse[p * a.H + h] = l_tot > 0.f ? mloc + log2f(l_tot) : -INFINITY;
     }
-    pid_cur = pid_nxt;
-    pid_nxt = pid_after;
-#pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) qcur[kk] = qnxt[kk];
-  }
+  };
+  if (nrounds > 0) round(0, inA);
+  if (nrounds > 1) round(1, inB);
 }
 
 // Workspace layout of the hybrid plan (byte offsets, 256-byte aligned pieces).
