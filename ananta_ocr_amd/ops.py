@@ -308,11 +308,13 @@ def attn_decode(q, k, v, idx, bias, valid, block_size, local_window, scale, seq_
 
 def decode_route(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, idx_scale,
                  floor, sigma, K, topm, seq_lens=None, block_table=None, page_size=None,
-                 cand=None, refresh_tail=True, width=None, return_scores=False):
+                 cand=None, refresh_tail=True, width=None, return_scores=False,
+                 valid_dtype=torch.bool):
     """Decode routing for one query per sequence (the last cached token): refreshes the
     tail block of `kbar_cache` [B, nblk_cap, d] in place, scores and routes.
     idx_q [B,d] or [B,1,d]; idx_k contiguous [B,S,d] or paged [pages, page_size, d].
-    Returns idx int32 [B,1,K'], bias fp32, valid bool (and the scores [B,nblk_cap])."""
+    Returns idx int32 [B,1,K'], bias fp32, valid (bool, or valid_dtype) and with
+    return_scores the scores [B,nblk_cap]."""
     _need_gpu(idx_q, idx_k, kbar_cache)
     lib = _lib.load()
     if idx_q.dim() == 3:
@@ -349,7 +351,7 @@ def decode_route(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, i
         float(idx_scale), float(floor), float(sigma), int(K), int(topm), Kw, _ptr(idx),
         _ptr(bias), _ptr(valid), _ptr(z), z.stride(0), _stream())
     _lib.check(st_, "dash_decode_route")
-    res = (idx[:, None], bias[:, None], valid[:, None].bool())
+    res = (idx[:, None], bias[:, None], valid[:, None].to(valid_dtype))
     return res + (z,) if return_scores else res
 
 

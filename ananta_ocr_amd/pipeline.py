@@ -35,7 +35,7 @@ def prefill(q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks, idx_scale
     out = ops.attn_prefill(q, k, v, idx, bias, valid, block_size, local_blocks * block_size,
                            scale, cu_seqlens=cu_seqlens)
     if return_routing:
-        return out, (idx, bias, valid)
+        return out, (idx, bias, valid.bool())
     return out
 
 
@@ -67,11 +67,42 @@ def decode_step(state, q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks
     idx, bias, valid = ops.decode_route(idx_q, idx_k, head_cls, state.kbar, block_size,
                                         local_blocks, idx_scale, floor, sigma, K, topm,
                                         seq_lens=seq_lens, block_table=block_table,
-                                        page_size=page_size, cand=block_cand, width=width)
+                                        page_size=page_size, cand=block_cand, width=width,
+                                        valid_dtype=torch.uint8)
     out = ops.attn_decode(q, k, v, idx[:, 0], bias[:, 0], valid[:, 0], block_size,
                           local_blocks * block_size, scale, seq_lens=seq_lens,
                           block_table=block_table, page_size=page_size, out_dtype=out_dtype,
                           nsplit=nsplit)
     if return_routing:
-        return out, (idx, bias, valid)
+        return out, (idx, bias, valid.bool())
     return out
+
+
+class DecodeGraph:
+    """One ``decode_step`` captured into a HIP graph for fixed buffers.
+
+    The router, the split-K attention and the merge of a step (and the small
+    tensor ops between them) are recorded once; ``replay()`` relaunches them all
+    with one host call, which is what a serving loop does for every token.  The
+    inputs are the captured tensors themselves: write the new query (and the new
+    cache rows) into them in place before each replay.  Outputs live in buffers
+    owned by the graph and are overwritten by the next replay.
+    """
+
+    def __init__(self, state, q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks,
+                 idx_scale, floor, sigma, K, topm, scale=None, warmup=2, **kw):
+        args = (state, q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks, idx_scale,
+                floor, sigma, K, topm, scale)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                decode_step(*args, **kw)
+        torch.cuda.current_stream().wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.out, self.routing = decode_step(*args, return_routing=True, **kw)
+
+    def replay(self):
+        self.graph.replay()
+        return self.out

@@ -495,3 +495,39 @@ def test_decode_step_pipeline_matches_oracle():
     assert torch.equal(va.cpu(), v_r)
     assert torch.equal(ti.cpu().long(), t_r)
     _close(out, ref[:, :, 0], "decode step")
+
+
+def test_decode_graph_replays_match_eager():
+    """decode_step captured in a HIP graph: every replay (with eager work and
+    synchronisations between replays, and after the query buffer is rewritten in
+    place) equals the eager step bit for bit."""
+    from ananta_ocr_amd import pipeline
+    cfg = W.Decode("small", 3, 4000, 64, 1024, 16, seed=12)
+    d = W.make_decode(cfg)
+    hc = torch.zeros(128, device=DEV)
+    nblk = (cfg.S + cfg.bs - 1) // cfg.bs
+    q, k, v = d["q"].to(DEV), d["k"].to(DEV), d["v"].to(DEV)
+    iq, ik = d["idx_q"].to(DEV), d["idx_k"].to(DEV)
+    st = pipeline.init_decode_state(ik, hc, cfg.bs, nblk)
+    args = (hc, cfg.bs, cfg.lw // cfg.bs, W.IDX_SCALE * 50, W.FLOOR, W.SIGMA, cfg.cap, cfg.cap,
+            1 / math.sqrt(128))
+    eager = pipeline.decode_step(st, q, k, v, iq, ik, *args).clone()
+    g = pipeline.DecodeGraph(st, q, k, v, iq, ik, *args)
+    for i in range(4):
+        out = g.replay().clone()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        again = pipeline.decode_step(st, q, k, v, iq, ik, *args)      # eager work in between
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager)
+    # a new query written into the captured buffer
+    gen = torch.Generator().manual_seed(13)
+    q2 = (torch.randn(q.shape, generator=gen) * 0.5).to(DEV, q.dtype)
+    iq2 = torch.randn(iq.shape, generator=gen).to(DEV, iq.dtype)
+    ref2 = pipeline.decode_step(st, q2, k, v, iq2, ik, *args).clone()
+    q.copy_(q2)
+    iq.copy_(iq2)
+    for i in range(2):
+        out = g.replay().clone()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref2), f"replay with new query {i}"
