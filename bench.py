@@ -292,6 +292,60 @@ def cpu_decode_baseline(res, cfg, reps=3):
 
 # ------------------------------------------------------------------ main
 
+# HBM bytes per launch of the measured kernel groups, from two hardware-counter
+# runs of ``bench.py --traffic-probe`` under rocprofv3 --pmc (FETCH_SIZE, then
+# WRITE_SIZE), each divided by the counter's reading for a 256 MiB device copy
+# (FETCH_SIZE reads 0.500 of the copied bytes, WRITE_SIZE 1.000).  Re-measure when
+# the kernels change.
+PREFILL_ATTN_TRAFFIC_BYTES = int((1787.6 + 767.1) * 1e6)
+DECODE_ATTN_TRAFFIC_BYTES = int((87.2 + 1.5) * 1e6)
+
+
+def traffic_probe():
+    """One launch of each measured kernel group, for hardware-counter runs: after
+    warm-up, a 256 MiB device-to-device copy (the counters' calibration), then one
+    27,300-token prefill attention launch and one B=8 decode attention launch,
+    separated by synchronisations.  The last dispatch of each kernel name is the
+    measured one."""
+    dev = "cuda"
+    cfg = W.PREFILL_27300
+    d = W.make_prefill(cfg, device=dev)
+    hc = torch.zeros(W.D, device=dev)
+    scale = 1.0 / math.sqrt(W.D)
+    _, (idx, bias, valid) = pipeline.prefill(d["q"], d["k"], d["v"], d["idx_q"], d["idx_k"], hc,
+                                             cfg.bs, cfg.lw // cfg.bs, W.IDX_SCALE, W.FLOOR,
+                                             W.SIGMA, cfg.cap, cfg.cap, return_routing=True)
+    dc = W.DECODE_B8
+    dd = W.make_decode(dc, device=dev)
+    nblk = (dc.S + dc.bs - 1) // dc.bs
+    st = pipeline.init_decode_state(dd["idx_k"], hc, dc.bs, nblk)
+    _, (didx, dbias, dvalid) = pipeline.decode_step(st, dd["q"], dd["k"], dd["v"], dd["idx_q"],
+                                                    dd["idx_k"], hc, dc.bs, dc.lw // dc.bs,
+                                                    W.IDX_SCALE, W.FLOOR, W.SIGMA, dc.cap,
+                                                    dc.cap, scale, return_routing=True)
+
+    def prefill_attn():
+        ops.attn_prefill(d["q"], d["k"], d["v"], idx, bias, valid, cfg.bs, cfg.lw, scale)
+
+    def decode_attn():
+        ops.attn_decode(dd["q"], dd["k"], dd["v"], didx[:, 0], dbias[:, 0], dvalid[:, 0], dc.bs,
+                        dc.lw, scale)
+
+    for _ in range(2):
+        prefill_attn()
+        decode_attn()
+    src = torch.ones(64 * 2 ** 20, dtype=torch.float32, device=dev)      # 256 MiB
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    prefill_attn()
+    torch.cuda.synchronize()
+    decode_attn()
+    torch.cuda.synchronize()
+    log("[bench] traffic probe: copy 268435456 B, then prefill attention, then decode attention")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -300,7 +354,13 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--extras", action="store_true",
                     help="also time the 2,730-token, packed and 12-layer paged workloads")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run one launch of each measured kernel for counter runs and exit")
     args = ap.parse_args()
+    if args.traffic_probe:
+        torch.cuda.set_device(0)
+        traffic_probe()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (no multi-GPU path); "
               "run with --gpus 1", file=sys.stderr)
@@ -332,7 +392,8 @@ def main():
                    "parallelism": "single-gpu"},
         "roofline": {"bound": "mfma", "achieved": round(tflops_attn, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops_attn / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(tflops_attn / PEAK_BF16_TFLOPS, 4),
+                     "traffic": PREFILL_ATTN_TRAFFIC_BYTES,
                      "kernel": "prefill attention", "flop_per_launch": pre["flops"],
                      "avg_launch_ms": round(pre["t_attn"] * 1e3, 4)},
         "decode": {"workload": W.DECODE_B8.name, "us_per_step": round(dec["t_step"] * 1e6, 2),
@@ -340,7 +401,8 @@ def main():
                    "step": "routing + attention, replayed as one HIP graph per cache set",
                    "roofline": {"bound": "hbm", "achieved": round(dec_gbs, 1),
                                 "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                "frac": round(dec_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                                "frac": round(dec_gbs / PEAK_HBM_GBS, 4),
+                                "traffic": DECODE_ATTN_TRAFFIC_BYTES,
                                 "kernel": "decode attention (split + merge)",
                                 "bytes_per_launch": dec["kv_bytes"] + dec["qo_bytes"],
                                 "avg_launch_us": round(dec["t_attn"] * 1e6, 2)}},
