@@ -34,6 +34,10 @@ namespace dash {
 constexpr int kPfTQ = 128;        // queries per tile work-group
 constexpr int kPfMaxK = 16;       // routed slots per query
 constexpr int kPfMaxBlocks = 2048;
+// Keys per tile-kernel item (a double-buffered LDS stage) and the work-groups per
+// CU that the stage size and the register budget allow.
+constexpr int kTileIT = 64;
+constexpr int kTileOcc = 2;
 constexpr int kPfCH = 256;        // pairs per sparse chunk (work-group)
 
 struct PrefillArgs {
@@ -269,24 +273,27 @@ __global__ __launch_bounds__(kPfTQ) void prefill_scatter_kernel(PrefillArgs a) {
 // mask when the whole half is visible to every query), base-2 online softmax
 // with a lazy rescale, O^T += V^T P^T.
 // ---------------------------------------------------------------------------
-constexpr int kPfIT = 64;         // keys per item in the tile kernel
+constexpr int kPfIT = 64;         // keys of a sparse-kernel stage (one routed block)
 
 __device__ __forceinline__ int k_slot(int r, int c) { return c ^ (r & 15); }
 __device__ __forceinline__ int v_slot(int r, int c) { return c ^ ((r & 3) << 2); }
 
-// Per-lane element offsets of the direct loads of a 64-key stage: wavefront wv
-// issues the 4-row groups wv, wv+4, wv+8, wv+12; lane l of a group fills slot
-// l % 16 of row 4 grp + l / 16 with chunk slot ^ swizzle(row) of that row.
+// Per-lane element offsets of the direct loads of a stage of ROWS keys by 4
+// wavefronts: wavefront wv issues the 4-row groups wv, wv+4, ...; lane l of a
+// group fills slot l % 16 of row 4 grp + l / 16 with chunk slot ^ swizzle(row).
+template <int ROWS>
 struct FetchOffsets {
-  uint32_t k[4], v[4];
-  int r[4];
+  static constexpr int kN = ROWS / 16;     // 4-row groups per wavefront
+  uint32_t k[kN], v[kN];
+  int r[kN];
 };
 
-__device__ __forceinline__ FetchOffsets fetch_offsets(int64_t k_st, int64_t v_st, int wv,
-                                                      int lane) {
-  FetchOffsets f;
+template <int ROWS>
+__device__ __forceinline__ FetchOffsets<ROWS> fetch_offsets(int64_t k_st, int64_t v_st, int wv,
+                                                            int lane) {
+  FetchOffsets<ROWS> f;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < FetchOffsets<ROWS>::kN; ++u) {
     const int grp = u * 4 + wv;
     const int r = grp * 4 + (lane >> 4), slot = lane & 15;
     f.r[u] = r;
@@ -296,18 +303,18 @@ __device__ __forceinline__ FetchOffsets fetch_offsets(int64_t k_st, int64_t v_st
   return f;
 }
 
-// Issue the loads of K and V rows j0 .. j0+63 of one head into a swizzled
+// Issue the loads of K and V rows j0 .. j0+ROWS-1 of one head into a swizzled
 // stage; rows at or beyond len repeat row len-1 (their keys are masked).
-template <int D>
+template <int D, int ROWS>
 __device__ __forceinline__ void tile_fetch(bf16* sKs, bf16* sVs, const bf16* kb, const bf16* vb,
                                            int64_t k_st, int64_t v_st, int j0, int len, int wv,
-                                           int lane, const FetchOffsets& f) {
+                                           int lane, const FetchOffsets<ROWS>& f) {
   static_assert(D == 128, "16 chunks per row");
   const bf16* kb0 = kb + (int64_t)j0 * k_st;
   const bf16* vb0 = vb + (int64_t)j0 * v_st;
-  const bool inside = j0 + kPfIT <= len;
+  const bool inside = j0 + ROWS <= len;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < FetchOffsets<ROWS>::kN; ++u) {
     const int grp = u * 4 + wv;
     const bf16* kp;
     const bf16* vp;
@@ -387,15 +394,15 @@ __device__ __forceinline__ int next_union(const uint32_t* sBits, int nwords, int
   return __builtin_amdgcn_readfirstlane((((b0 >> 5) + f) << 5) + (int)__builtin_ctz(fb));
 }
 
-template <int D>
-__global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
+template <int D, int IT, int OCC>
+__global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
   static_assert(D == 128, "head_dim 128");
-  __shared__ __attribute__((aligned(16))) bf16 sK0[kPfIT * D];
-  __shared__ __attribute__((aligned(16))) bf16 sK1[kPfIT * D];
-  __shared__ __attribute__((aligned(16))) bf16 sV0[kPfIT * D];
-  __shared__ __attribute__((aligned(16))) bf16 sV1[kPfIT * D];
-  __shared__ int16_t sIdx[kPfTQ][kPfMaxK];
-  __shared__ float sBias[kPfTQ][kPfMaxK];
+  __shared__ __attribute__((aligned(16))) bf16 sK0[IT * D];
+  __shared__ __attribute__((aligned(16))) bf16 sK1[IT * D];
+  __shared__ __attribute__((aligned(16))) bf16 sV0[IT * D];
+  __shared__ __attribute__((aligned(16))) bf16 sV1[IT * D];
+  __shared__ __attribute__((aligned(16))) int16_t sIdx[kPfTQ][kPfMaxK];
+  __shared__ __attribute__((aligned(16))) float sBias[kPfTQ][kPfMaxK];
   __shared__ uint8_t sCnt[kPfTQ];
   __shared__ uint32_t sBits[kPfMaxBlocks / 32];
 
@@ -433,7 +440,11 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
       atomicOr(&sBits[c >> 5], 1u << (c & 31));
     };
     if (t < len && a.kind && a.K == kPfMaxK) {
-      // planned rows of 16 slots: kinds, ids and biases with 16-byte loads
+      // Planned rows of 16 slots (kinds, ids and biases read with 16-byte loads;
+      // the plan has already dropped duplicate and unusable slots).  The dense
+      // slots are sorted by block id with a bitonic network on the keys
+      // id << 5 | slot in registers (ids < 2048; other slots take id 2048 and
+      // sort last); the biases, stored in slot order, are then gathered by slot.
       const int64_t p0 = (r0 + t) * kPfMaxK;
       const uint4 kv = *(const uint4*)(a.kind + p0);
       int4 iv[4];
@@ -443,15 +454,56 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
         iv[q] = ((const int4*)(a.idx + p0))[q];
         bv4[q] = ((const float4*)(a.bias + p0))[q];
       }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ((float4*)&sBias[tid][0])[q] = bv4[q];
       const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
+      uint32_t key[kPfMaxK];
 #pragma unroll
       for (int s = 0; s < kPfMaxK; ++s) {
         const uint32_t kd = (kw[s >> 2] >> (8 * (s & 3))) & 0xffu;
         const int q = s >> 2, e = s & 3;
         const int c = e == 0 ? iv[q].x : e == 1 ? iv[q].y : e == 2 ? iv[q].z : iv[q].w;
-        const float bv = e == 0 ? bv4[q].x : e == 1 ? bv4[q].y : e == 2 ? bv4[q].z : bv4[q].w;
-        if (kd == 1) insert(c, bv);
+        key[s] = ((kd == 1 ? (uint32_t)c : (uint32_t)kPfMaxBlocks) << 5) | (uint32_t)s;
       }
+#pragma unroll
+      for (int k = 2; k <= kPfMaxK; k <<= 1)
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1)
+#pragma unroll
+          for (int i = 0; i < kPfMaxK; ++i) {
+            const int l = i ^ j;
+            if (l > i) {
+              const uint32_t x = key[i], y = key[l];
+              const bool asc = (i & k) == 0;
+              key[i] = asc ? min(x, y) : max(x, y);
+              key[l] = asc ? max(x, y) : min(x, y);
+            }
+          }
+      float sb[kPfMaxK];
+#pragma unroll
+      for (int p = 0; p < kPfMaxK; ++p) sb[p] = sBias[tid][key[p] & 31u];
+      int16_t ids[kPfMaxK];
+#pragma unroll
+      for (int p = 0; p < kPfMaxK; ++p) {
+        const int c = (int)(key[p] >> 5);
+        ids[p] = (int16_t)c;
+        if (c < kPfMaxBlocks) {
+          ++cnt;
+          atomicOr(&sBits[c >> 5], 1u << (c & 31));
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        int4 w;
+        w.x = (uint16_t)ids[8 * q + 0] | ((uint32_t)(uint16_t)ids[8 * q + 1] << 16);
+        w.y = (uint16_t)ids[8 * q + 2] | ((uint32_t)(uint16_t)ids[8 * q + 3] << 16);
+        w.z = (uint16_t)ids[8 * q + 4] | ((uint32_t)(uint16_t)ids[8 * q + 5] << 16);
+        w.w = (uint16_t)ids[8 * q + 6] | ((uint32_t)(uint16_t)ids[8 * q + 7] << 16);
+        ((int4*)&sIdx[tid][0])[q] = w;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        ((float4*)&sBias[tid][0])[q] = make_float4(sb[4 * q], sb[4 * q + 1], sb[4 * q + 2], sb[4 * q + 3]);
     } else if (t < len) {
       const int64_t row = r0 + t;
       const int km = a.kmin ? a.kmin[row] : 0;
@@ -497,9 +549,10 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
   const bf16* kb = seq_ptr(a.k, a.cu, b, a.k_sb, a.k_st) + (int64_t)h * a.k_sh;
   const bf16* vb = seq_ptr(a.v, a.cu, b, a.v_sb, a.v_st) + (int64_t)h * a.v_sh;
   const int t_last = min(t0 + kPfTQ - 1, len - 1);
-  const int jw0 = (max(t0 - a.lw + 1, 0) / kPfIT) * kPfIT;
-  const int n_win = (t_last - jw0) / kPfIT + 1;
-  const int ipb = (a.bs + kPfIT - 1) / kPfIT;      // items per routed block
+  constexpr int kH = IT / 32;                      // 32-key halves per item
+  const int jw0 = (max(t0 - a.lw + 1, 0) / IT) * IT;
+  const int n_win = (t_last - jw0) / IT + 1;
+  const int ipb = (a.bs + IT - 1) / IT;            // items per routed block
   __syncthreads();
   int nu = 0;
   {
@@ -510,7 +563,7 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
     nu = __builtin_amdgcn_readfirstlane(nu);
   }
   const int n_items = n_win + nu * ipb;
-  const FetchOffsets fo = fetch_offsets(a.k_st, a.v_st, wv, lane);
+  const FetchOffsets<IT> fo = fetch_offsets<IT>(a.k_st, a.v_st, wv, lane);
   const int myrow = wv * 32 + n;
   const int my_cnt = sCnt[myrow];
   const float log2e = 1.4426950408889634f;
@@ -523,11 +576,11 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
     if (++sub >= ipb) { sub = 0; c = next_union(sBits, nwords, c, lane); }
   };
   auto item_j0 = [&](int it, int c, int sub) {
-    return it < n_win ? jw0 + it * kPfIT : c * a.bs + sub * kPfIT;
+    return it < n_win ? jw0 + it * IT : c * a.bs + sub * IT;
   };
   if (n_items > 0) {
     advance(0, pf_c, pf_sub);
-    tile_fetch<D>(sK0, sV0, kb, vb, a.k_st, a.v_st, item_j0(0, pf_c, pf_sub), len, wv, lane, fo);
+    tile_fetch<D, IT>(sK0, sV0, kb, vb, a.k_st, a.v_st, item_j0(0, pf_c, pf_sub), len, wv, lane, fo);
   }
   int ptr = 0;                             // next dense block of this query
   float cur_b = -INFINITY;                 // bias (base 2) of the current routed block
@@ -540,9 +593,9 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
     if (it + 1 < n_items) {
       advance(it + 1, pf_c, pf_sub);
       if constexpr (ST == 0)
-        tile_fetch<D>(sK1, sV1, kb, vb, a.k_st, a.v_st, item_j0(it + 1, pf_c, pf_sub), len, wv, lane, fo);
+        tile_fetch<D, IT>(sK1, sV1, kb, vb, a.k_st, a.v_st, item_j0(it + 1, pf_c, pf_sub), len, wv, lane, fo);
       else
-        tile_fetch<D>(sK0, sV0, kb, vb, a.k_st, a.v_st, item_j0(it + 1, pf_c, pf_sub), len, wv, lane, fo);
+        tile_fetch<D, IT>(sK0, sV0, kb, vb, a.k_st, a.v_st, item_j0(it + 1, pf_c, pf_sub), len, wv, lane, fo);
     }
     const bf16* sKs;
     const bf16* sVs;
@@ -550,7 +603,7 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
     advance(it, cp_c, cp_sub);
     const bool routed = it >= n_win;
     const int j0 = item_j0(it, cp_c, cp_sub);
-    int nkeys = kPfIT;
+    int nkeys = IT;
     int lo, hi;
     float bl;
     if (!routed) {
@@ -564,22 +617,25 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
           ++ptr;
         }
       }
-      nkeys = min(kPfIT, a.bs - cp_sub * kPfIT);
+      nkeys = min(IT, a.bs - cp_sub * IT);
       lo = q_km; hi = r_hi;
       bl = qvalid ? cur_b : -INFINITY;
     }
     // halves of 32 keys: skipped when no query of the wavefront sees a key of it,
     // mask-free when every query with a finite bias sees all of it
     const bool live = bl != -INFINITY;
-    bool do_h[2], full_h[2];
+    bool do_h[kH], full_h[kH];
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
+    for (int hf = 0; hf < kH; ++hf) {
       const int k0 = j0 + 32 * hf;
       const bool exists = 32 * hf < nkeys;
       do_h[hf] = exists && __any(live && lo <= k0 + 31 && hi >= k0);
       full_h[hf] = __all(!live || (lo <= k0 && k0 + 31 <= hi));
     }
-    if (!do_h[0] && !do_h[1]) return;
+    bool any_h = false;
+#pragma unroll
+    for (int hf = 0; hf < kH; ++hf) any_h |= do_h[hf];
+    if (!any_h) return;
     const uint32_t span = hi >= lo ? (uint32_t)(hi - lo) : 0u;
     const int lo_eff = hi >= lo ? lo : 0x40000000;
 
@@ -587,9 +643,9 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
     // O^T += V^T P^T.  In this order the softmax of half 0 runs on the VALU while
     // the matrix core still works on half 1, and the softmax of half 1 while it
     // works on the PV product of half 0.
-    floatx16 s[2];
+    floatx16 s[kH];
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
+    for (int hf = 0; hf < kH; ++hf) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[hf][r] = 0.f;
       if (!do_h[hf]) continue;
@@ -600,7 +656,7 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
     }
     const bf16x2 ones = {(bf16)1.f, (bf16)1.f};
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
+    for (int hf = 0; hf < kH; ++hf) {
       if (!do_h[hf]) continue;
       const int kq = j0 + 32 * hf + 4 * hl - lo_eff;     // key - lo for r = 0
       // raw maximum (the scale is positive: max(fma(s, c, b)) = fma(max s, c, b));
@@ -662,9 +718,7 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
 
   // ---- merge the sparse partials of this query ----
   // All kinds and log-sum-exps are loaded first and the reference moves once to
-  // their maximum.  Then round j adds every lane's j-th sparse partial (a
-  // wave-uniform loop, so the loads of round j+1 are in flight while round j is
-  // accumulated); partial rows are lane-contiguous and read with 16-byte loads.
+  // their maximum; partial rows are lane-contiguous and read with 16-byte loads.
   if (a.kind) {
     const int64_t p0 = (r0 + tqc) * a.K;
     float l2[kPfMaxK];
@@ -694,46 +748,39 @@ __global__ __launch_bounds__(256, 2) void prefill_tile_kernel(PrefillArgs a) {
         for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
       m_run = mx;
     }
-    // partials with a finite log-sum-exp, in slot order
+    // Slots in 4 batches of 4: a batch's loads (the lanes' live slots only) are
+    // all in flight before any is accumulated, so the merge waits on memory at
+    // most four times.
     uint32_t live = 0;
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s)
       if (l2[s] != -INFINITY) live |= 1u << s;
-    const int nlive = __popc(live);
-    int rounds = nlive;
+    const bf16* po = a.part_o + (p0 * a.H + h) * D + part_index(hl, 0, 0, 0);
+    const int64_t pstride = (int64_t)a.H * D;
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) rounds = max(rounds, __shfl_xor(rounds, m, kWave));
-    rounds = __builtin_amdgcn_readfirstlane(rounds);
-    auto slot_of = [&](uint32_t msk) { return msk ? __builtin_ctz(msk) : 0; };
-    auto fetch_part = [&](int s, bf16x8 (&buf)[8]) {
-      const bf16* po = a.part_o + ((p0 + s) * a.H + h) * D + part_index(hl, 0, 0, 0);
+    for (int sb = 0; sb < kPfMaxK; sb += 4) {
+      const uint32_t gm = (live >> sb) & 15u;
+      if (!__any(gm != 0u)) continue;
+      bf16x8 buf[4][8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) buf[q] = *(const bf16x8*)(po + q * 8);
-    };
-    bf16x8 cur[8], nxt[8];
-    uint32_t rem = live;
-    int s_cur = slot_of(rem);
-    if (rounds > 0 && nlive > 0) fetch_part(s_cur, cur);
-    for (int j = 0; j < rounds; ++j) {
-      const bool have = j < nlive;
-      const uint32_t rem_next = have ? (rem & (rem - 1)) : 0u;
-      const int s_next = slot_of(rem_next);
-      if (j + 1 < nlive) fetch_part(s_next, nxt);
-      if (have) {
-        const float w = fast_exp2(l2[s_cur] - m_run);
-        if (hl == 0) l_run += w;
+      for (int u = 0; u < 4; ++u)
+        if ((gm >> u) & 1u) {
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
+          for (int q = 0; q < 8; ++q) buf[u][q] = *(const bf16x8*)(po + (sb + u) * pstride + q * 8);
+        }
 #pragma unroll
-          for (int g = 0; g < 4; g += 2)
+      for (int u = 0; u < 4; ++u)
+        if ((gm >> u) & 1u) {
+          const float w = fast_exp2(l2[sb + u] - m_run);
+          if (hl == 0) l_run += w;
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-              acc_o[dt][g * 4 + e] += w * bf2f(cur[dt * 2 + g / 2][e]);
-      }
+          for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-      for (int q = 0; q < 8; ++q) cur[q] = nxt[q];
-      rem = rem_next;
-      s_cur = s_next;
+            for (int g = 0; g < 4; g += 2)
+#pragma unroll
+              for (int e = 0; e < 8; ++e)
+                acc_o[dt][g * 4 + e] += w * bf2f(buf[u][dt * 2 + g / 2][e]);
+        }
     }
   }
 
@@ -787,8 +834,8 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
   const int64_t r0 = row0(a, b);
   const bf16* kb = seq_ptr(a.k, a.cu, b, a.k_sb, a.k_st) + (int64_t)h * a.k_sh;
   const bf16* vb = seq_ptr(a.v, a.cu, b, a.v_sb, a.v_st) + (int64_t)h * a.v_sh;
-  const FetchOffsets fo = fetch_offsets(a.k_st, a.v_st, wv, lane);
-  tile_fetch<D>(sKs, sVs, kb, vb, a.k_st, a.v_st, c * a.bs, len, wv, lane, fo);
+  const FetchOffsets<kPfIT> fo = fetch_offsets<kPfIT>(a.k_st, a.v_st, wv, lane);
+  tile_fetch<D, kPfIT>(sKs, sVs, kb, vb, a.k_st, a.v_st, c * a.bs, len, wv, lane, fo);
 
   const bf16* qb = seq_ptr(a.q, a.cu, b, a.q_sb, a.q_st) + (int64_t)h * a.q_sh;
   const int32_t* plist = a.pairs + r0 * a.K + start;
@@ -1019,7 +1066,7 @@ extern "C" int dash_attn_prefill(
     hipLaunchKernelGGL(prefill_scatter_kernel, dim3(ntiles, B), dim3(kPfTQ), 0, st, a);
     hipLaunchKernelGGL(prefill_sparse_kernel<128>, dim3(L.chunk_cap * H * B), dim3(256), 0, st, a);
   }
-  hipLaunchKernelGGL(prefill_tile_kernel<128>, dim3(ntiles * H * B), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((prefill_tile_kernel<128, kTileIT, kTileOcc>), dim3(ntiles * H * B), dim3(256), 0, st, a);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? kOk : (int)e;
 }
