@@ -335,6 +335,75 @@ __device__ __forceinline__ void tile_fetch(bf16* sKs, bf16* sVs, const bf16* kb,
   }
 }
 
+// Issue the loads of rows j0 .. j0+ROWS-1 of one matrix (K or V) into a
+// swizzled stage by 4 wavefronts; rows at or beyond len repeat row len-1.
+// Wavefront wv fills rows 16u + r0 (r0 = 4 wv + lane/16), chunk slot lane % 16,
+// for u = 0 .. ROWS/16-1.  The swizzles of both matrices depend on the row only
+// through row % 16 = r0, so the lane's swizzled chunk is one byte offset cb for
+// every u; lane_off = 2 r0 x_st + cb.
+template <int D, int ROWS>
+__device__ __forceinline__ void rows_fetch(bf16* sX, const bf16* xb, int64_t x_st, uint32_t lane_off,
+                                           uint32_t cb, int r0, int j0, int len, int wv) {
+  static_assert(D == 128, "16 chunks per row");
+  const char* xb0 = (const char*)(xb + (int64_t)j0 * x_st);
+  const uint32_t row_b = (uint32_t)x_st * 2u;
+  if (j0 + ROWS <= len) {
+#pragma unroll
+    for (int u = 0; u < ROWS / 16; ++u)
+      __builtin_amdgcn_global_load_lds((const void*)(xb0 + (lane_off + (uint32_t)(16 * u) * row_b)),
+                                       (__attribute__((address_space(3))) void*)(sX + (4 * u + wv) * 4 * D),
+                                       16, 0, 0);
+  } else {
+#pragma unroll
+    for (int u = 0; u < ROWS / 16; ++u) {
+      const int dr = min(j0 + 16 * u + r0, len - 1) - j0;     // >= 0: j0 < len
+      __builtin_amdgcn_global_load_lds((const void*)(xb0 + ((uint32_t)dr * row_b + cb)),
+                                       (__attribute__((address_space(3))) void*)(sX + (4 * u + wv) * 4 * D),
+                                       16, 0, 0);
+    }
+  }
+}
+
+// Lane part of the byte offset of the K operand reads (see k_frag): row n of a
+// stage and, for k-step kk, chunk ((2 kk + hl) ^ (n % 16)), whose byte offset
+// 16 ((2 kk + hl) ^ (n % 16)) = 32 kk ^ (16 hl ^ 16 (n % 16)).  So the read of
+// half hf, k-step kk is at 8192 hf + (kl ^ 32 kk): one XOR per k-step.
+__device__ __forceinline__ uint32_t k_lane_off(int n, int hl) {
+  return (uint32_t)(n * 256) | (uint32_t)((hl << 4) ^ ((n & 15) << 4));
+}
+__device__ __forceinline__ bf16x8 k_frag_at(const bf16* sKs, uint32_t kl, int hf, int kk) {
+  return *(const bf16x8*)((const char*)sKs + hf * 8192 + (kl ^ (uint32_t)(kk << 5)));
+}
+
+// Lane part of the byte offset of the transposing V reads (see pv_tr_swz): row
+// 4 hl + rr (rr = (lane % 16) / 4, which is also the row's swizzle row % 4),
+// bytes 8 (lane % 2) within chunk 4 dt + cq, whose swizzled slot gives byte
+// offset 16 cq + 64 (dt ^ rr).  The read of tile dt is at (vl ^ 64 dt), plus
+// 256 kbase (and 2048 for the rows 8 further).
+__device__ __forceinline__ uint32_t v_lane_off(int lane) {
+  const int hl = lane >> 5;
+  const int rr = (lane & 15) >> 2;
+  const int cq = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+  return (uint32_t)((4 * hl + rr) * 256 + 8 * (lane & 1) + 16 * cq + 64 * rr);
+}
+__device__ __forceinline__ void pv_at(const bf16* sVs, uint32_t vl, int kbase, const bf16x8& pop,
+                                      floatx16 (&acc_o)[4]) {
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    const char* p = (const char*)sVs + kbase * 256 + (vl ^ (uint32_t)(dt << 6));
+    const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_short4*)(__attribute__((address_space(3))) void*)p);
+    const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_short4*)(__attribute__((address_space(3))) void*)(p + 2048));
+    bf16x8 vop;
+    const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo);
+    const bf16x4 h4 = __builtin_bit_cast(bf16x4, hi);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { vop[e] = l4[e]; vop[e + 4] = h4[e]; }
+    acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pop, acc_o[dt], 0, 0, 0);
+  }
+}
+
 // K operand of keys krow0 + (lane % 32), dims 16 kk + 8 (lane / 32) .. +7.
 __device__ __forceinline__ bf16x8 k_frag(const bf16* sKs, int krow, int kk, int hl) {
   return *(const bf16x8*)(sKs + krow * 128 + k_slot(krow, 2 * kk + hl) * 8);
@@ -403,7 +472,6 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 sV1[IT * D];
   __shared__ __attribute__((aligned(16))) int16_t sIdx[kPfTQ][kPfMaxK];
   __shared__ __attribute__((aligned(16))) float sBias[kPfTQ][kPfMaxK];
-  __shared__ uint8_t sCnt[kPfTQ];
   __shared__ uint32_t sBits[kPfMaxBlocks / 32];
 
   // logical order (sequence, head, tile), tile fastest, contiguous per XCD
@@ -521,7 +589,8 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
         insert(c, a.bias[p]);
       }
     }
-    sCnt[tid] = (uint8_t)cnt;
+    // id 2048 (no block) ends every list
+    for (int u = cnt; u < kPfMaxK; ++u) sIdx[tid][u] = (int16_t)kPfMaxBlocks;
   }
 
   // ---- this lane's query and its Q^T operand (8 k-steps of 16 dims) ----
@@ -549,7 +618,6 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
   const bf16* kb = seq_ptr(a.k, a.cu, b, a.k_sb, a.k_st) + (int64_t)h * a.k_sh;
   const bf16* vb = seq_ptr(a.v, a.cu, b, a.v_sb, a.v_st) + (int64_t)h * a.v_sh;
   const int t_last = min(t0 + kPfTQ - 1, len - 1);
-  constexpr int kH = IT / 32;                      // 32-key halves per item
   const int jw0 = (max(t0 - a.lw + 1, 0) / IT) * IT;
   const int n_win = (t_last - jw0) / IT + 1;
   const int ipb = (a.bs + IT - 1) / IT;            // items per routed block
@@ -563,179 +631,214 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
     nu = __builtin_amdgcn_readfirstlane(nu);
   }
   const int n_items = n_win + nu * ipb;
-  const FetchOffsets<IT> fo = fetch_offsets<IT>(a.k_st, a.v_st, wv, lane);
+  // fetch byte offsets: row r0 of a 16-row group and its swizzled chunk
+  const int fr0 = wv * 4 + (lane >> 4);
+  const uint32_t fkc = (uint32_t)(k_slot(fr0, lane & 15) * 16), fvc = (uint32_t)(v_slot(fr0, lane & 15) * 16);
+  const uint32_t fk0 = (uint32_t)(fr0 * a.k_st * 2) + fkc, fv0 = (uint32_t)(fr0 * a.v_st * 2) + fvc;
+  const uint32_t kl0 = k_lane_off(n, hl), vl0 = v_lane_off(lane);
   const int myrow = wv * 32 + n;
-  const int my_cnt = sCnt[myrow];
   const float log2e = 1.4426950408889634f;
+  const float csc = a.scale_log2e;
 
-  // item iterators: (block, sub-item) of the item being fetched and computed
+  // Fetch iterator: block and sub-item of the last item whose K rows were fetched.
   int pf_c = -1, pf_sub = ipb - 1;
-  int cp_c = -1, cp_sub = ipb - 1;
-  auto advance = [&](int it, int& c, int& sub) {
-    if (it < n_win) return;
-    if (++sub >= ipb) { sub = 0; c = next_union(sBits, nwords, c, lane); }
-  };
-  auto item_j0 = [&](int it, int c, int sub) {
-    return it < n_win ? jw0 + it * IT : c * a.bs + sub * IT;
+  int jk = 0, ck = -1, subk = 0;           // that item's first key, block, sub-item
+  auto advance = [&](int it) {
+    if (it >= n_win && ++pf_sub >= ipb) { pf_sub = 0; pf_c = next_union(sBits, nwords, pf_c, lane); }
+    jk = it < n_win ? jw0 + it * IT : pf_c * a.bs + pf_sub * IT;
+    ck = pf_c;
+    subk = pf_sub;
   };
   if (n_items > 0) {
-    advance(0, pf_c, pf_sub);
-    tile_fetch<D, IT>(sK0, sV0, kb, vb, a.k_st, a.v_st, item_j0(0, pf_c, pf_sub), len, wv, lane, fo);
+    advance(0);
+    rows_fetch<D, IT>(sK0, kb, a.k_st, fk0, fkc, fr0, jk, len, wv);
   }
-  int ptr = 0;                             // next dense block of this query
+  // Cursor into this query's ascending dense-block list (ended by id 2048): the
+  // next candidate block is read one match ahead.
+  int ptr = 0;
+  int cand_c = sIdx[myrow][0];
   float cur_b = -INFINITY;                 // bias (base 2) of the current routed block
-  // One item on stage ST (the stages are distinct LDS arrays named at compile
-  // time, so the reads of this stage do not wait for the loads into the other).
-  auto step = [&](int it, auto stage_tag) {
-    constexpr int ST = decltype(stage_tag)::value;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();                       // item it landed; item it-1 is done with its stage
-    if (it + 1 < n_items) {
-      advance(it + 1, pf_c, pf_sub);
-      if constexpr (ST == 0)
-        tile_fetch<D, IT>(sK1, sV1, kb, vb, a.k_st, a.v_st, item_j0(it + 1, pf_c, pf_sub), len, wv, lane, fo);
-      else
-        tile_fetch<D, IT>(sK0, sV0, kb, vb, a.k_st, a.v_st, item_j0(it + 1, pf_c, pf_sub), len, wv, lane, fo);
-    }
-    const bf16* sKs;
-    const bf16* sVs;
-    if constexpr (ST == 0) { sKs = sK0; sVs = sV0; } else { sKs = sK1; sVs = sV1; }
-    advance(it, cp_c, cp_sub);
-    const bool routed = it >= n_win;
-    const int j0 = item_j0(it, cp_c, cp_sub);
-    int nkeys = IT;
-    int lo, hi;
-    float bl;
-    if (!routed) {
-      lo = q_lo; hi = tq;
-      bl = qvalid ? 0.f : -INFINITY;
-    } else {
-      if (cp_sub == 0) {
-        cur_b = -INFINITY;
-        if (ptr < my_cnt && sIdx[myrow][ptr] == cp_c) {
-          cur_b = sBias[myrow][ptr] * log2e;
-          ++ptr;
-        }
-      }
-      nkeys = min(IT, a.bs - cp_sub * IT);
-      lo = q_km; hi = r_hi;
-      bl = qvalid ? cur_b : -INFINITY;
-    }
-    // halves of 32 keys: skipped when no query of the wavefront sees a key of it,
-    // mask-free when every query with a finite bias sees all of it
-    const bool live = bl != -INFINITY;
-    bool do_h[kH], full_h[kH];
-#pragma unroll
-    for (int hf = 0; hf < kH; ++hf) {
-      const int k0 = j0 + 32 * hf;
-      const bool exists = 32 * hf < nkeys;
-      do_h[hf] = exists && __any(live && lo <= k0 + 31 && hi >= k0);
-      full_h[hf] = __all(!live || (lo <= k0 && k0 + 31 <= hi));
-    }
-    bool any_h = false;
-#pragma unroll
-    for (int hf = 0; hf < kH; ++hf) any_h |= do_h[hf];
-    if (!any_h) return;
-    const uint32_t span = hi >= lo ? (uint32_t)(hi - lo) : 0u;
-    const int lo_eff = hi >= lo ? lo : 0x40000000;
 
-    // S^T of both halves first (two MFMA chains), then per half: softmax and
-    // O^T += V^T P^T.  In this order the softmax of half 0 runs on the VALU while
-    // the matrix core still works on half 1, and the softmax of half 1 while it
-    // works on the PV product of half 0.
-    floatx16 s[kH];
+  // Software pipeline over the items: step i computes S^T of item i, its row
+  // maximum and its probabilities P, and O^T += V^T P^T of item i-1 (whose P the
+  // previous step left in registers), so that the VALU work on item i runs while
+  // the matrix core multiplies item i-1.  K of item i sits in stage sK[i % 2], V in
+  // sV[i % 2]; step i fetches K(i+1) and V(i).  A lazy rescale (the reference
+  // m_run only moves when some query's maximum exceeds it by more than 8, so
+  // probabilities stay <= 2^8) applies its factor to O at the start of the next
+  // step, after O^T(i-1) is complete.
+  // Per item: the visible-key range of the query as (kq, span) (key j is visible
+  // when j - lo, as unsigned, is <= span) and its bias; whether some query of the
+  // wavefront sees a key of the item (need) and whether every query with a finite
+  // bias sees all of them (full).  An item nobody needs gets S = -inf, so P = 0;
+  // the V stage read before item 0 is zero-filled, so that every step runs the
+  // same straight-line O^T update.
+  bf16x8 pP[2][2][2];                      // [parity][half][16-key group]
 #pragma unroll
-    for (int hf = 0; hf < kH; ++hf) {
+  for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[hf][r] = 0.f;
-      if (!do_h[hf]) continue;
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) pP[1][hf][j][q] = (bf16)0.f;
+  for (int i = tid; i < IT * D / 8; i += 256) ((uint4*)sV1)[i] = make_uint4(0u, 0u, 0u, 0u);
+  float alpha_o = 1.f;                     // pending factor of acc_o
+  bool o_pending = false;
+  const bf16x2 ones = {(bf16)1.f, (bf16)1.f};
+
+  auto step = [&](int it, auto par_tag) {
+    constexpr int P = decltype(par_tag)::value;
+    // parity P is a compile-time constant, so that every LDS array is named
+    // statically and the reads of one stage do not wait for the loads into another
+    bf16* const sKc = P == 0 ? sK0 : sK1;     // K(it)
+    bf16* const sKn = P == 0 ? sK1 : sK0;     // K(it+1) is fetched here
+    bf16* const sVc = P == 0 ? sV0 : sV1;     // V(it) is fetched here
+    const bf16* const sVp = P == 0 ? sV1 : sV0;  // V(it-1)
+    // Lane offsets pass through an empty asm each step, so that the compiler
+    // derives the per-read addresses here instead of keeping them all live.
+    uint32_t kl = kl0, vl = vl0, fk = fk0, fv = fv0;
+    asm volatile("" : "+v"(kl), "+v"(vl), "+v"(fk), "+v"(fv));
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();                       // K(it), V(it-1) landed; step it-1 is done
+    // S^T of item it first, so that its reads and MFMAs overlap the fetches and
+    // the bookkeeping below (an item nobody needs, or the drain step, computes a
+    // discarded S^T from whatever the stage holds)
+    floatx16 sc[2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[hf][r] = 0.f;
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk)
-        s[hf] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(sKs, 32 * hf + n, kk, hl), qop[kk],
-                                                        s[hf], 0, 0, 0);
+        sc[hf] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag_at(sKc, kl, hf, kk), qop[kk], sc[hf],
+                                                         0, 0, 0);
     }
-    const bf16x2 ones = {(bf16)1.f, (bf16)1.f};
-#pragma unroll
-    for (int hf = 0; hf < kH; ++hf) {
-      if (!do_h[hf]) continue;
-      const int kq = j0 + 32 * hf + 4 * hl - lo_eff;     // key - lo for r = 0
-      // raw maximum (the scale is positive: max(fma(s, c, b)) = fma(max s, c, b));
-      // masked keys are left out here and get p = 0 below (s is not written, so
-      // both paths share its registers)
-      float mraw = -INFINITY;
-      if (full_h[hf]) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mraw = fmaxf(mraw, s[hf][r]);
+    bool need = false, full = false;
+    float bl = -INFINITY;
+    int kq = 0;
+    uint32_t span = 0;
+    if (it < n_items) {
+      rows_fetch<D, IT>(sVc, vb, a.v_st, fv, fvc, fr0, jk, len, wv);
+      // item it: visible keys and bias of this query
+      int lo, hi;
+      if (it < n_win) {
+        lo = q_lo; hi = tq;
+        bl = qvalid ? 0.f : -INFINITY;
       } else {
+        if (subk == 0) {
+          cur_b = -INFINITY;
+          if (cand_c == ck) {
+            cur_b = sBias[myrow][ptr] * log2e;
+            ++ptr;
+            cand_c = ptr < kPfMaxK ? sIdx[myrow][ptr] : kPfMaxBlocks;
+          }
+        }
+        lo = q_km; hi = min(r_hi, ck * a.bs + a.bs - 1);
+        bl = qvalid ? cur_b : -INFINITY;
+      }
+      const int j0 = jk;
+      const bool live = bl != -INFINITY && lo <= hi;
+      need = __any(live && lo <= j0 + IT - 1 && hi >= j0);
+      full = __all(!live || (lo <= j0 && j0 + IT - 1 <= hi));
+      span = lo <= hi ? (uint32_t)(hi - lo) : 0u;
+      kq = j0 + 4 * hl - (lo <= hi ? lo : 0x40000000);
+      if (it + 1 < n_items) {
+        advance(it + 1);
+        rows_fetch<D, IT>(sKn, kb, a.k_st, fk, fkc, fr0, jk, len, wv);
+      }
+    }
+    if (o_pending) {                       // O^T(it-2) is complete
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha_o;
+      alpha_o = 1.f;
+      o_pending = false;
+    }
+    if (!need) {
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[hf][r] = -INFINITY;
+    } else if (!full) {
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const uint32_t d = (uint32_t)(kq + 8 * (r >> 2) + (r & 3));
-          mraw = fmaxf(mraw, d <= span ? s[hf][r] : -INFINITY);
+          const uint32_t d = (uint32_t)(kq + 32 * hf + 8 * (r >> 2) + (r & 3));
+          sc[hf][r] = d <= span ? sc[hf][r] : -INFINITY;
         }
-      }
-      const float mloc = xor32_max(mraw == -INFINITY ? -INFINITY : fmaf(mraw, a.scale_log2e, bl));
-      // Lazy rescale: the exponent reference m_run only moves when some query's
-      // maximum exceeds it by more than 8 (probabilities stay <= 2^8).
-      if (__any(mloc > m_run + 8.f)) {
-        const float m_new = fmaxf(m_run, mloc);
-        const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run - m_new);
-        l_run *= alpha;
+    }
+    // O^T += V^T P^T of item it-1
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
+    for (int hf = 0; hf < 2; ++hf) {
+      pv_at(sVp, vl, 32 * hf, pP[P ^ 1][hf][0], acc_o);
+      pv_at(sVp, vl, 32 * hf + 16, pP[P ^ 1][hf][1], acc_o);
+    }
+    // row maximum in base 2 (the scale is positive: max(fma(s, c, b)) =
+    // fma(max s, c, b)), the rescale decision, p = 2^(s c + b - m) in bf16 and
+    // the row sum of the bf16 p
+    float mraw = -INFINITY;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
-        m_run = m_new;
-      }
-      // p = 2^(s c + b - m); the row sum adds the bf16 p the PV product uses
-      const float off = bl - ((m_run == -INFINITY) ? 0.f : m_run);
-      bf16x8 pop[2];
-      if (full_h[hf]) {
+    for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) pop[r >> 3][r & 7] = (bf16)fast_exp2(fmaf(s[hf][r], a.scale_log2e, off));
-      } else {
+      for (int r = 0; r < 16; ++r) mraw = fmaxf(mraw, sc[hf][r]);
+    const float mloc = xor32_max(fmaf(mraw, a.scale_log2e, bl));
+    const bool up = mloc > m_run + 8.f;
+    const float alpha = up ? fast_exp2(m_run - mloc) : 1.f;   // 0 when m_run = -inf
+    l_run *= alpha;
+    alpha_o *= alpha;
+    o_pending = o_pending || __any(up);
+    m_run = up ? mloc : m_run;
+    const float off = bl - ((m_run == -INFINITY) ? 0.f : m_run);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const uint32_t d = (uint32_t)(kq + 8 * (r >> 2) + (r & 3));
-          const float pr = fast_exp2(fmaf(s[hf][r], a.scale_log2e, off));
-          pop[r >> 3][r & 7] = (bf16)(d <= span ? pr : 0.f);
-        }
-      }
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        pP[P][hf][r >> 3][r & 7] = (bf16)fast_exp2(fmaf(sc[hf][r], a.scale_log2e, off));
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          const bf16x2 pp = {pop[j][e], pop[j][e + 1]};
+        for (int q = 0; q < 8; q += 2) {
+          const bf16x2 pp = {pP[P][hf][j][q], pP[P][hf][j][q + 1]};
           l_run = __builtin_amdgcn_fdot2_f32_bf16(pp, ones, l_run, false);
         }
-      pv_tr_swz(sVs, 32 * hf, pop[0], acc_o, lane);
-      pv_tr_swz(sVs, 32 * hf + 16, pop[1], acc_o, lane);
-    }
   };
-  for (int it = 0; it < n_items; it += 2) {
+  for (int it = 0; it <= n_items; it += 2) {
     step(it, std::integral_constant<int, 0>{});
-    if (it + 1 < n_items) step(it + 1, std::integral_constant<int, 1>{});
+    if (it + 1 <= n_items) step(it + 1, std::integral_constant<int, 1>{});
   }
+
+  // Arguments used only from here on are read again through an opaque copy of
+  // the kernel-argument pointer, so that they occupy no scalar registers during
+  // the item loop.
+  const __attribute__((address_space(4))) char* kap =
+      (const __attribute__((address_space(4))) char*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(kap));
+  const __attribute__((address_space(4))) PrefillArgs& pa =
+      *(const __attribute__((address_space(4))) PrefillArgs*)kap;
 
   // ---- merge the sparse partials of this query ----
   // All kinds and log-sum-exps are loaded first and the reference moves once to
   // their maximum; partial rows are lane-contiguous and read with 16-byte loads.
-  if (a.kind) {
-    const int64_t p0 = (r0 + tqc) * a.K;
+  if (pa.kind) {
+    const int64_t p0 = (r0 + tqc) * pa.K;
     float l2[kPfMaxK];
     uint32_t smask = 0;
-    if (a.K == kPfMaxK) {
-      const uint4 kv = *(const uint4*)(a.kind + p0);
+    if (pa.K == kPfMaxK) {
+      const uint4 kv = *(const uint4*)(pa.kind + p0);
       const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
       for (int s = 0; s < kPfMaxK; ++s)
         if (qvalid && ((kw[s >> 2] >> (8 * (s & 3))) & 0xffu) == 2) smask |= 1u << s;
     } else {
-      for (int s = 0; s < a.K; ++s)
-        if (qvalid && a.kind[p0 + s] == 2) smask |= 1u << s;
+      for (int s = 0; s < pa.K; ++s)
+        if (qvalid && pa.kind[p0 + s] == 2) smask |= 1u << s;
     }
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s)
-      l2[s] = ((smask >> s) & 1u) ? a.part_lse[(p0 + s) * a.H + h] : -INFINITY;
+      l2[s] = ((smask >> s) & 1u) ? pa.part_lse[(p0 + s) * pa.H + h] : -INFINITY;
     float mx = m_run;
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s) mx = fmaxf(mx, l2[s]);
@@ -755,8 +858,8 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s)
       if (l2[s] != -INFINITY) live |= 1u << s;
-    const bf16* po = a.part_o + (p0 * a.H + h) * D + part_index(hl, 0, 0, 0);
-    const int64_t pstride = (int64_t)a.H * D;
+    const bf16* po = pa.part_o + (p0 * pa.H + h) * D + part_index(hl, 0, 0, 0);
+    const int64_t pstride = (int64_t)pa.H * D;
 #pragma unroll
     for (int sb = 0; sb < kPfMaxK; sb += 4) {
       const uint32_t gm = (live >> sb) & 15u;
@@ -788,8 +891,8 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
   const float l_tot = xor32_sum(l_run);
   if (qvalid) {
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    bf16* ob = (a.cu ? a.o + (int64_t)a.cu[b] * a.o_st : a.o + (int64_t)b * a.o_sb) +
-               (int64_t)h * a.o_sh + (int64_t)tq * a.o_st;
+    bf16* ob = (pa.cu ? pa.o + (int64_t)pa.cu[b] * pa.o_st : pa.o + (int64_t)b * pa.o_sb) +
+               (int64_t)h * pa.o_sh + (int64_t)tq * pa.o_st;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
@@ -799,9 +902,9 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
         for (int e = 0; e < 4; ++e) w[e] = (bf16)(acc_o[dt][g * 4 + e] * inv);
         *(bf16x4*)(ob + dt * 32 + 8 * g + 4 * hl) = w;
       }
-    if (a.lse && hl == 0) {
+    if (pa.lse && hl == 0) {
       const float lse = l_tot > 0.f ? (m_run + log2f(l_tot)) * 0.6931471805599453f : -INFINITY;
-      a.lse[(r0 + tq) * a.lse_row + (int64_t)h * a.lse_sh] = lse;
+      pa.lse[(r0 + tq) * pa.lse_row + (int64_t)h * pa.lse_sh] = lse;
     }
   }
 }
