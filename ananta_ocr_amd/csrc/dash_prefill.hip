@@ -64,8 +64,10 @@ struct PrefillArgs {
   int4* chunk_tab;                     // [B, chunk_cap]: block, start, count
   int chunk_cap;
   int32_t* pairs;                      // [rows * K] grouped by block per sequence
-  float* part_lse;                     // [rows * K, H]  base-2 log-sum-exp
-  bf16* part_o;                        // [rows * K, H, D]  normalised partial output, dims
+  // sparse partials, one per (head, slot, token row) in that order (see part_row)
+  int64_t prows;                       // token rows of the partial arrays
+  float* part_lse;                     // [H, K, prows]  base-2 log-sum-exp
+  bf16* part_o;                        // [H, K, prows, D]  normalised partial output, dims
                                        // in MFMA lane order (see part_index)
 };
 
@@ -84,6 +86,14 @@ __device__ __forceinline__ const bf16* seq_ptr(const bf16* base, const int32_t* 
 // half hl owns in the MFMA accumulator layout are contiguous, in (dt, g, q) order.
 __device__ __forceinline__ int part_index(int hl, int dt, int g, int q) {
   return hl * 64 + dt * 16 + g * 4 + q;
+}
+
+// Index of the sparse partial of (token row, routed slot, head): head, slot,
+// row order, so that the partials of one slot of neighbouring queries, which a
+// wavefront merges together, are neighbours in memory.
+template <typename Args>
+__device__ __forceinline__ int64_t part_row(const Args& a, int64_t row, int slot, int h) {
+  return ((int64_t)h * a.K + slot) * a.prows + row;
 }
 
 // Keep a routed slot?  The block must exist, be valid, and have keys below the
@@ -838,7 +848,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
     }
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s)
-      l2[s] = ((smask >> s) & 1u) ? pa.part_lse[(p0 + s) * pa.H + h] : -INFINITY;
+      l2[s] = ((smask >> s) & 1u) ? pa.part_lse[part_row(pa, r0 + tqc, s, h)] : -INFINITY;
     float mx = m_run;
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s) mx = fmaxf(mx, l2[s]);
@@ -858,8 +868,8 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s)
       if (l2[s] != -INFINITY) live |= 1u << s;
-    const bf16* po = pa.part_o + (p0 * pa.H + h) * D + part_index(hl, 0, 0, 0);
-    const int64_t pstride = (int64_t)pa.H * D;
+    const bf16* po = pa.part_o + part_row(pa, r0 + tqc, 0, h) * D + part_index(hl, 0, 0, 0);
+    const int64_t pstride = pa.prows * D;
 #pragma unroll
     for (int sb = 0; sb < kPfMaxK; sb += 4) {
       const uint32_t gm = (live >> sb) & 15u;
@@ -982,7 +992,6 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
     const int pid_cur = pids[j];
     const bool active = wv * 32 + 128 * j + n < npairs;
     const int t = pid_cur / a.K;
-    const int64_t p = r0 * a.K + pid_cur;
     const int q_ls = t - a.lw + 1;
     const int lo = cur.km;
     const int hi = min(q_ls, len) - 1;
@@ -1043,7 +1052,8 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
     const float l_tot = xor32_sum(psum);
     if (active) {
       const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-      bf16* po = a.part_o + (p * a.H + h) * D;
+      const int64_t pr = part_row(a, r0 + t, pid_cur - t * a.K, h);
+      bf16* po = a.part_o + pr * D;
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
@@ -1053,7 +1063,7 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
           for (int e2 = 0; e2 < 8; ++e2) w[e2] = (bf16)(acc_o[dt][g * 4 + e2] * inv);
           *(bf16x8*)(po + part_index(hl, dt, g, 0)) = w;
         }
-      if (hl == 0) a.part_lse[p * a.H + h] = l_tot > 0.f ? mloc + log2f(l_tot) : -INFINITY;
+      if (hl == 0) a.part_lse[pr] = l_tot > 0.f ? mloc + log2f(l_tot) : -INFINITY;
     }
   };
   if (nrounds > 0) round(0, inA);
@@ -1162,6 +1172,7 @@ extern "C" int dash_attn_prefill(
     a.chunk_tab = (int4*)(w + L.tab);
     a.chunk_cap = L.chunk_cap;
     a.pairs = (int32_t*)(w + L.pairs);
+    a.prows = total_rows;
     a.part_lse = (float*)(w + L.plse);
     a.part_o = (bf16*)(w + L.po);
     hipLaunchKernelGGL(prefill_plan_kernel, dim3(ntiles, B), dim3(kPfTQ), 0, st, a);
