@@ -61,6 +61,9 @@ struct PrefillArgs {
   int ntiles_cap;
   int32_t* blk_off;                    // [B, nblk_cap]
   int32_t* num_chunks;                 // [B]
+  int32_t* chunk_pref;                 // [B+1] prefix sums of num_chunks
+  int32_t* done;                       // arrival counter of the scan, zero between calls
+  int B;
   int4* chunk_tab;                     // [B, chunk_cap]: block, start, count
   int chunk_cap;
   int32_t* pairs;                      // [rows * K] grouped by block per sequence
@@ -220,7 +223,12 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
   const int xp = bp + ip - sp, xc = bc + ic - sc;   // exclusive prefix of this thread
   if (e0 < kPfMaxBlocks) { sC[e0] = v0; sOff[e0] = xp; sCh[e0] = xc; }
   if (e1 < kPfMaxBlocks) { sC[e1] = v1; sOff[e1] = xp + v0; sCh[e1] = xc + c0; }
-  if (tid == 1023) a.num_chunks[b] = bc + ic;
+  __shared__ int sLast;
+  if (tid == 1023) {
+    a.num_chunks[b] = bc + ic;
+    __threadfence();
+    sLast = atomicAdd(a.done, 1) == (int)gridDim.x - 1;
+  }
   __syncthreads();
   int4* tab = a.chunk_tab + (int64_t)b * a.chunk_cap;
   for (int c = tid; c < nblk; c += 1024) {
@@ -228,6 +236,39 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
     const int n = sC[c];
     for (int i = 0; i * kPfCH < n; ++i)
       tab[sCh[c] + i] = make_int4(c, sOff[c] + i * kPfCH, min(kPfCH, n - i * kPfCH), 0);
+  }
+  // The sequence that finishes last writes the prefix sums of the chunk counts
+  // (the sparse kernel maps its grid onto the real chunks with them) and resets
+  // the arrival counter.
+  if (sLast) {
+    __threadfence();
+    const int nseq = (int)gridDim.x;
+    int carry = 0;
+    for (int base = 0; base < nseq; base += 1024) {
+      const int i = base + tid;
+      const int v = i < nseq ? __hip_atomic_load(&a.num_chunks[i], __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT) : 0;
+      int x = v;
+#pragma unroll
+      for (int s2 = 1; s2 < kWave; s2 <<= 1) {
+        const int y = __shfl_up(x, s2, kWave);
+        if (lane >= s2) x += y;
+      }
+      __syncthreads();
+      if (lane == kWave - 1) sWave[0][wv] = x;
+      __syncthreads();
+      int wb = 0, tot = 0;
+      for (int w = 0; w < 16; ++w) {
+        if (w < wv) wb += sWave[0][w];
+        tot += sWave[0][w];
+      }
+      if (i < nseq) a.chunk_pref[i + 1] = carry + wb + x;
+      carry += tot;
+    }
+    if (tid == 0) {
+      a.chunk_pref[0] = 0;
+      atomicExch(a.done, 0);
+    }
   }
 }
 
@@ -933,13 +974,25 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
   static_assert(D == 128, "head_dim 128");
   __shared__ __attribute__((aligned(16))) bf16 sKs[kPfIT * D];
   __shared__ __attribute__((aligned(16))) bf16 sVs[kPfIT * D];
-  // logical order (sequence, head, chunk), chunk fastest, contiguous per XCD
-  const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
-  const int ch = lid % a.chunk_cap, bh = lid / a.chunk_cap;
-  const int h = bh % a.H, b = bh / a.H;
-  // the table entry is read together with the count (entries past it are unused)
+  // The first H * (total chunks) work-groups of the grid take the real chunks
+  // (the hardware deals consecutive work-groups to the 8 XCDs in turn, so every
+  // XCD gets an equal share); the rest exit.  Logical order (sequence, head,
+  // chunk), chunk fastest, contiguous per XCD.
+  const int nreal = a.H * a.chunk_pref[a.B];
+  if ((int)blockIdx.x >= nreal) return;
+  const int lid = xcd_logical_id(blockIdx.x, nreal);
+  int b = 0;
+  {
+    int hi = a.B;                          // the last sequence b with H * pref[b] <= lid
+    while (hi - b > 1) {
+      const int mid = (b + hi) >> 1;
+      if (a.H * a.chunk_pref[mid] <= lid) b = mid; else hi = mid;
+    }
+  }
+  const int pb = a.chunk_pref[b], nc = a.chunk_pref[b + 1] - pb;
+  const int hc = lid - a.H * pb;
+  const int h = hc / nc, ch = hc % nc;
   const int4 e = a.chunk_tab[(int64_t)b * a.chunk_cap + ch];
-  if (ch >= a.num_chunks[b]) return;
   const int c = e.x, start = e.y, npairs = e.z;
   const int len = seq_len(a, b);
   const int tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
@@ -1072,7 +1125,7 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
 
 // Workspace layout of the hybrid plan (byte offsets, 256-byte aligned pieces).
 struct PlanLayout {
-  int64_t count, tbase, off, nchunks, tab, pairs, kind, plse, po, total;
+  int64_t count, done, tbase, off, nchunks, cpref, tab, pairs, kind, plse, po, total;
   int chunk_cap, ntiles_cap;
 };
 
@@ -1085,10 +1138,12 @@ inline PlanLayout plan_layout(int B, int H, int S_max, int64_t rows, int K, int 
   L.ntiles_cap = (S_max + kPfTQ - 1) / kPfTQ;
   const int64_t nbc = (int64_t)B * nblk_cap;
   int64_t o = 0;
-  L.count = o; o = align256(o + nbc * 4);
+  L.count = o; o += nbc * 4;
+  L.done = o; o = align256(o + 4);
   L.tbase = o; o = align256(o + nbc * L.ntiles_cap * 4);
   L.off = o; o = align256(o + nbc * 4);
   L.nchunks = o; o = align256(o + (int64_t)B * 4);
+  L.cpref = o; o = align256(o + (int64_t)(B + 1) * 4);
   L.tab = o; o = align256(o + (int64_t)B * L.chunk_cap * 16);
   L.pairs = o; o = align256(o + rows * K * 4);
   L.kind = o; o = align256(o + rows * K);
@@ -1169,6 +1224,9 @@ extern "C" int dash_attn_prefill(
     a.ntiles_cap = L.ntiles_cap;
     a.blk_off = (int32_t*)(w + L.off);
     a.num_chunks = (int32_t*)(w + L.nchunks);
+    a.chunk_pref = (int32_t*)(w + L.cpref);
+    a.done = (int32_t*)(w + L.done);
+    a.B = B;
     a.chunk_tab = (int4*)(w + L.tab);
     a.chunk_cap = L.chunk_cap;
     a.pairs = (int32_t*)(w + L.pairs);

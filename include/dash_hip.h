@@ -113,8 +113,8 @@ int dash_route(const float* z, int64_t z_stride, int rows, int nblk_cols,
  * dense_threshold > 0 (block_size <= 64): routed blocks selected by fewer than
  * dense_threshold of the 128 queries of a tile go through the block-major sparse path,
  * which needs `workspace` (dash_attn_prefill_workspace_size bytes, 256-byte aligned; its
- * leading block counters must be zero before the first call and are left zero by every
- * call) and total_rows (B*S, or cu_seqlens[B]).  dense_threshold <= 0: no workspace,
+ * leading counters (per-block pair counts and one arrival counter) must be zero before
+ * the first call and are left zero by every call) and total_rows (B*S, or cu_seqlens[B]).  dense_threshold <= 0: no workspace,
  * every routed block of a tile is processed with the tile.  Calls sharing a workspace
  * must not overlap.
  */
