@@ -39,6 +39,11 @@ constexpr int kPfMaxBlocks = 2048;
 constexpr int kTileIT = 64;
 constexpr int kTileOcc = 2;
 constexpr int kPfCH = 256;        // pairs per sparse chunk (work-group)
+// A chunk record: block id, pair count, 2 unused words, then up to kPfCH pair ids
+// (token * K + slot within the sequence), so that a work-group reads its chunk's
+// header and pair ids in one round trip.
+constexpr int kRecHead = 4;
+constexpr int kRec = kRecHead + kPfCH;
 
 struct PrefillArgs {
   const bf16* q; const bf16* k; const bf16* v;
@@ -59,14 +64,13 @@ struct PrefillArgs {
   int32_t* blk_count;                  // [B, nblk_cap]  zero between calls
   int32_t* tile_base;                  // [B, ntiles_cap, nblk_cap] offset of a tile's pairs
   int ntiles_cap;
-  int32_t* blk_off;                    // [B, nblk_cap]
+  int32_t* blk_chunk;                  // [B, nblk_cap] first chunk of each block
   int32_t* num_chunks;                 // [B]
   int32_t* chunk_pref;                 // [B+1] prefix sums of num_chunks
   int32_t* done;                       // arrival counter of the scan, zero between calls
   int B;
-  int4* chunk_tab;                     // [B, chunk_cap]: block, start, count
+  int32_t* chunk_rec;                  // [B, chunk_cap, kRec] chunk records
   int chunk_cap;
-  int32_t* pairs;                      // [rows * K] grouped by block per sequence
   // sparse partials, one per (head, slot, token row) in that order (see part_row)
   int64_t prows;                       // token rows of the partial arrays
   float* part_lse;                     // [H, K, prows]  base-2 log-sum-exp
@@ -191,12 +195,11 @@ __global__ __launch_bounds__(kPfTQ) void prefill_plan_kernel(PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Scan: per sequence, block offsets of the sparse pairs and the chunk table.
-// Resets the block counters (they are zero between calls).
+// Scan: per sequence, the first chunk of every block and the chunk record
+// headers.  Resets the block counters (they are zero between calls).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
   __shared__ int32_t sC[kPfMaxBlocks];
-  __shared__ int32_t sOff[kPfMaxBlocks];
   __shared__ int32_t sCh[kPfMaxBlocks];
   __shared__ int32_t sWave[2][16];
   const int b = blockIdx.x, tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
@@ -209,20 +212,20 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
   if (e0 < a.nblk_cap) { v0 = e0 < nblk ? cnt[e0] : 0; cnt[e0] = 0; }
   if (e1 < a.nblk_cap) { v1 = e1 < nblk ? cnt[e1] : 0; cnt[e1] = 0; }
   const int c0 = (v0 + kPfCH - 1) / kPfCH, c1 = (v1 + kPfCH - 1) / kPfCH;
-  int sp = v0 + v1, sc = c0 + c1;
-  int ip = sp, ic = sc;
+  const int sc = c0 + c1;
+  int ic = sc;
 #pragma unroll
   for (int s = 1; s < kWave; s <<= 1) {
-    const int op = __shfl_up(ip, s, kWave), oc = __shfl_up(ic, s, kWave);
-    if (lane >= s) { ip += op; ic += oc; }
+    const int oc = __shfl_up(ic, s, kWave);
+    if (lane >= s) ic += oc;
   }
-  if (lane == kWave - 1) { sWave[0][wv] = ip; sWave[1][wv] = ic; }
+  if (lane == kWave - 1) sWave[1][wv] = ic;
   __syncthreads();
-  int bp = 0, bc = 0;
-  for (int w = 0; w < wv; ++w) { bp += sWave[0][w]; bc += sWave[1][w]; }
-  const int xp = bp + ip - sp, xc = bc + ic - sc;   // exclusive prefix of this thread
-  if (e0 < kPfMaxBlocks) { sC[e0] = v0; sOff[e0] = xp; sCh[e0] = xc; }
-  if (e1 < kPfMaxBlocks) { sC[e1] = v1; sOff[e1] = xp + v0; sCh[e1] = xc + c0; }
+  int bc = 0;
+  for (int w = 0; w < wv; ++w) bc += sWave[1][w];
+  const int xc = bc + ic - sc;                       // exclusive prefix of this thread
+  if (e0 < kPfMaxBlocks) { sC[e0] = v0; sCh[e0] = xc; }
+  if (e1 < kPfMaxBlocks) { sC[e1] = v1; sCh[e1] = xc + c0; }
   __shared__ int sLast;
   if (tid == 1023) {
     a.num_chunks[b] = bc + ic;
@@ -230,12 +233,12 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
     sLast = atomicAdd(a.done, 1) == (int)gridDim.x - 1;
   }
   __syncthreads();
-  int4* tab = a.chunk_tab + (int64_t)b * a.chunk_cap;
+  int32_t* rec = a.chunk_rec + (int64_t)b * a.chunk_cap * kRec;
   for (int c = tid; c < nblk; c += 1024) {
-    a.blk_off[(int64_t)b * a.nblk_cap + c] = sOff[c];
+    a.blk_chunk[(int64_t)b * a.nblk_cap + c] = sCh[c];
     const int n = sC[c];
     for (int i = 0; i * kPfCH < n; ++i)
-      tab[sCh[c] + i] = make_int4(c, sOff[c] + i * kPfCH, min(kPfCH, n - i * kPfCH), 0);
+      *(int2*)(rec + (int64_t)(sCh[c] + i) * kRec) = make_int2(c, min(kPfCH, n - i * kPfCH));
   }
   // The sequence that finishes last writes the prefix sums of the chunk counts
   // (the sparse kernel maps its grid onto the real chunks with them) and resets
@@ -273,7 +276,8 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Scatter: sparse pairs into per-block lists (order within a block is free).
+// Scatter: sparse pairs into the chunk records of their block (order within a
+// block is free).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kPfTQ) void prefill_scatter_kernel(PrefillArgs a) {
   __shared__ int32_t sFill[kPfMaxBlocks];
@@ -289,7 +293,8 @@ __global__ __launch_bounds__(kPfTQ) void prefill_scatter_kernel(PrefillArgs a) {
   const int64_t row = row0(a, b) + t;
   const int64_t base = row0(a, b) * a.K;
   const int32_t* tb = a.tile_base + ((int64_t)b * a.ntiles_cap + blockIdx.x) * a.nblk_cap;
-  const int32_t* off = a.blk_off + (int64_t)b * a.nblk_cap;
+  const int32_t* bch = a.blk_chunk + (int64_t)b * a.nblk_cap;
+  int32_t* rec = a.chunk_rec + (int64_t)b * a.chunk_cap * kRec;
   int32_t c[kPfMaxK];
   uint32_t vmask;
   load_row_slots(a, row, c, vmask);
@@ -302,7 +307,11 @@ __global__ __launch_bounds__(kPfTQ) void prefill_scatter_kernel(PrefillArgs a) {
   }
 #pragma unroll
   for (int s = 0; s < kPfMaxK; ++s)
-    if (sp[s]) a.pairs[base + off[c[s]] + tb[c[s]] + pos[s]] = (int32_t)(row * a.K + s - base);
+    if (sp[s]) {
+      const int q = tb[c[s]] + pos[s];               // position in the block's pair list
+      rec[(int64_t)(bch[c[s]] + q / kPfCH) * kRec + kRecHead + q % kPfCH] =
+          (int32_t)(row * a.K + s - base);
+    }
 }
 
 
@@ -992,11 +1001,16 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
   const int pb = a.chunk_pref[b], nc = a.chunk_pref[b + 1] - pb;
   const int hc = lid - a.H * pb;
   const int h = hc / nc, ch = hc % nc;
-  const int4 e = a.chunk_tab[(int64_t)b * a.chunk_cap + ch];
-  const int c = e.x, start = e.y, npairs = e.z;
-  const int len = seq_len(a, b);
   const int tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
   const int hl = lane >> 5, n = lane & 31;
+  // header and pair ids in one round trip: lanes past the count take the first id
+  const int32_t* rec = a.chunk_rec + ((int64_t)b * a.chunk_cap + ch) * kRec;
+  const int c = rec[0], npairs = rec[1];
+  const int pid_first = rec[kRecHead];
+  int pid_raw[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) pid_raw[j] = rec[kRecHead + wv * 32 + 128 * j + n];
+  const int len = seq_len(a, b);
   const int64_t r0 = row0(a, b);
   const bf16* kb = seq_ptr(a.k, a.cu, b, a.k_sb, a.k_st) + (int64_t)h * a.k_sh;
   const bf16* vb = seq_ptr(a.v, a.cu, b, a.v_sb, a.v_st) + (int64_t)h * a.v_sh;
@@ -1004,13 +1018,11 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
   tile_fetch<D, kPfIT>(sKs, sVs, kb, vb, a.k_st, a.v_st, c * a.bs, len, wv, lane, fo);
 
   const bf16* qb = seq_ptr(a.q, a.cu, b, a.q_sb, a.q_st) + (int64_t)h * a.q_sh;
-  const int32_t* plist = a.pairs + r0 * a.K + start;
   const int nkeys = min(a.bs, kPfIT);
   const int kfirst = c * a.bs;
   const int nrounds = npairs > wv * 32 ? (npairs - wv * 32 + 127) / 128 : 0;
   auto pair_id = [&](int j) {
-    const int pi = wv * 32 + 128 * j + n;
-    return plist[min(pi, npairs - 1)];
+    return wv * 32 + 128 * j + n < npairs ? pid_raw[j] : pid_first;
   };
   // a round's per-query inputs: Q rows, routed bias, segment start
   struct RoundIn {
@@ -1125,7 +1137,7 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
 
 // Workspace layout of the hybrid plan (byte offsets, 256-byte aligned pieces).
 struct PlanLayout {
-  int64_t count, done, tbase, off, nchunks, cpref, tab, pairs, kind, plse, po, total;
+  int64_t count, done, tbase, bch, nchunks, cpref, rec, kind, plse, po, total;
   int chunk_cap, ntiles_cap;
 };
 
@@ -1141,11 +1153,10 @@ inline PlanLayout plan_layout(int B, int H, int S_max, int64_t rows, int K, int 
   L.count = o; o += nbc * 4;
   L.done = o; o = align256(o + 4);
   L.tbase = o; o = align256(o + nbc * L.ntiles_cap * 4);
-  L.off = o; o = align256(o + nbc * 4);
+  L.bch = o; o = align256(o + nbc * 4);
   L.nchunks = o; o = align256(o + (int64_t)B * 4);
   L.cpref = o; o = align256(o + (int64_t)(B + 1) * 4);
-  L.tab = o; o = align256(o + (int64_t)B * L.chunk_cap * 16);
-  L.pairs = o; o = align256(o + rows * K * 4);
+  L.rec = o; o = align256(o + (int64_t)B * L.chunk_cap * kRec * 4);
   L.kind = o; o = align256(o + rows * K);
   L.plse = o; o = align256(o + rows * K * H * 4);
   L.po = o; o = align256(o + rows * K * H * D * 2);
@@ -1222,14 +1233,13 @@ extern "C" int dash_attn_prefill(
     a.blk_count = (int32_t*)(w + L.count);
     a.tile_base = (int32_t*)(w + L.tbase);
     a.ntiles_cap = L.ntiles_cap;
-    a.blk_off = (int32_t*)(w + L.off);
+    a.blk_chunk = (int32_t*)(w + L.bch);
     a.num_chunks = (int32_t*)(w + L.nchunks);
     a.chunk_pref = (int32_t*)(w + L.cpref);
     a.done = (int32_t*)(w + L.done);
     a.B = B;
-    a.chunk_tab = (int4*)(w + L.tab);
+    a.chunk_rec = (int32_t*)(w + L.rec);
     a.chunk_cap = L.chunk_cap;
-    a.pairs = (int32_t*)(w + L.pairs);
     a.prows = total_rows;
     a.part_lse = (float*)(w + L.plse);
     a.part_o = (bf16*)(w + L.po);
