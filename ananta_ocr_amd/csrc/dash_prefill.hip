@@ -229,8 +229,14 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
   __shared__ int sLast;
   if (tid == 1023) {
     a.num_chunks[b] = bc + ic;
-    __threadfence();
-    sLast = atomicAdd(a.done, 1) == (int)gridDim.x - 1;
+    if (gridDim.x == 1) {                  // one sequence: its count is the prefix
+      a.chunk_pref[0] = 0;
+      a.chunk_pref[1] = bc + ic;
+      sLast = 0;
+    } else {
+      __threadfence();
+      sLast = atomicAdd(a.done, 1) == (int)gridDim.x - 1;
+    }
   }
   __syncthreads();
   int32_t* rec = a.chunk_rec + (int64_t)b * a.chunk_cap * kRec;
