@@ -819,6 +819,64 @@ struct DecodeRouteArgs {
   float* z; int64_t z_stride;
 };
 
+// 1.5-entmax of the sorted top M, the log-prior bias and the output slots of one
+// decode row, by one wavefront with lane m holding entry m: the operations of
+// entmax15_sorted in the same order (each lane forms its own prefix sums
+// serially), so the result is bit-for-bit the serial one.
+__device__ __forceinline__ void decode_route_finish(const DecodeRouteArgs& a, int b, int lane, int M,
+                                                    int Kp, const float* s_selv, const int* s_selk) {
+#pragma clang fp contract(off)
+  const float xv = lane < M ? s_selv[lane] : 0.f;
+  const int kv = lane < M ? s_selk[lane] : 0x3fffffff;
+  const float x0 = s_selv[0];
+  const float X = __fdiv_rn(__fsub_rn(xv, x0), 2.0f);
+  double cs = 0.0, cs2 = 0.0;
+#pragma unroll
+  for (int j = 0; j < kMaxM; ++j) {
+    const float Xj = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(X), j));
+    if (j <= lane) {
+      cs += (double)Xj;
+      cs2 += (double)__fmul_rn(Xj, Xj);
+    }
+  }
+  float tau = 0.f;
+  bool sup = false;
+  if (lane < M) {
+    const float rho = (float)(lane + 1);
+    const float mean = __fdiv_rn((float)cs, rho);
+    const float mean_sq = __fdiv_rn((float)cs2, rho);
+    const float ss = __fmul_rn(rho, __fsub_rn(mean_sq, __fmul_rn(mean, mean)));
+    const float delta = __fdiv_rn(__fsub_rn(1.0f, ss), rho);
+    const float delta_nz = delta > 0.f ? delta : 0.f;
+    tau = __fsub_rn(mean, __fsqrt_rn(delta_nz));
+    sup = tau <= X;
+  }
+  const int support = max(__popcll(__ballot(sup)), 1);
+  const float tau_star = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(tau), support - 1));
+  const float tt = __fsub_rn(X, tau_star);
+  const float cc = tt > 0.f ? tt : 0.f;
+  const float prior = lane < M ? __fmul_rn(cc, cc) : 0.f;
+  const float logp = logf(fmaxf(prior, a.floor_p));
+  const bool va = (kv & (1 << 30)) != 0;
+  // mean log-prior of the kept valid slots, summed in slot order
+  float musum = 0.f;
+  int cnt = 0;
+  const uint64_t keep = __ballot(lane < Kp && va);
+#pragma unroll
+  for (int j = 0; j < kMaxM; ++j)
+    if ((keep >> j) & 1ull) {
+      musum += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(logp), j));
+      ++cnt;
+    }
+  const float mu = musum / (float)max(cnt, 1);
+  for (int m = lane; m < a.Kout; m += kWave) {
+    const bool kept = m < Kp;                   // m < Kp <= 16: lane m holds slot m
+    a.idx[(int64_t)b * a.Kout + m] = kept ? (kv & 0x3fffffff) : -1;
+    a.bias[(int64_t)b * a.Kout + m] = kept && va ? (logp - mu) * a.inv_sigma : 0.f;
+    if (a.valid) a.valid[(int64_t)b * a.Kout + m] = kept && va ? 1 : 0;
+  }
+}
+
 __global__ __launch_bounds__(kDrThreads) void decode_route_kernel(DecodeRouteArgs a) {
   __shared__ __attribute__((aligned(16))) float s_q[256];
   __shared__ __attribute__((aligned(16))) float s_tail[256];
@@ -852,17 +910,34 @@ __global__ __launch_bounds__(kDrThreads) void decode_route_kernel(DecodeRouteArg
     return;
   }
   for (int i = tid; i < a.d; i += kDrThreads) s_q[i] = a.idx_q[(int64_t)b * a.iq_sb + i];
+  // d = 128 and up to 512 blocks: every block's k_bar row is loaded now, 16 lanes
+  // per row, so that the loads are in flight during the tail refresh
+  const bool fast_scores = a.d == 128 && nblk <= 8 * (kDrThreads / 16);
+  const int l16 = lane & 15, slot16 = tid >> 4;
+  float4 kp[8][2];
+  auto prefetch = [&](int r0, int r1) {
+    if (!fast_scores) return;
+#pragma unroll
+    for (int r = r0; r < r1; ++r) {
+      const int c = min(slot16 + r * (kDrThreads / 16), nblk - 1);
+      const float* kr = a.kbar + (int64_t)b * a.kb_sb + (int64_t)c * 128;
+      kp[r][0] = *(const float4*)(kr + l16 * 4);
+      kp[r][1] = *(const float4*)(kr + 64 + l16 * 4);
+    }
+  };
+  prefetch(0, 4);
   if (a.refresh_tail) {
     const int t0 = ct * a.bs, n = len - t0;
     const float* hcp = a.head_cls;
-    // logits of the tail tokens: 4 lanes per token, a quarter of the dims each
-    for (int j0 = 0; j0 < n; j0 += kDrThreads / 4) {
-      const int j = j0 + tid / 4, part = tid % 4;
+    // logits of the tail tokens: 8 lanes per token, an eighth of the dims each
+    // (the k_bar rows of the scores are already in flight)
+    for (int j0 = 0; j0 < n; j0 += kDrThreads / 8) {
+      const int j = j0 + tid / 8, part = tid % 8;
       float acc = 0.f;
       if (j < n) {
         const float* kr = a.idx_k + a.lay_k.row(b, t0 + j);
-        const int q4 = a.d / 4;
-        for (int i = part * q4; i < (part + 1) * q4; i += 4) {
+        const int q8 = a.d / 8;
+        for (int i = part * q8; i < (part + 1) * q8; i += 4) {
           const float4 kv = *(const float4*)(kr + i);
           const float4 hv = *(const float4*)(hcp + i);
           acc += kv.x * hv.x + kv.y * hv.y + kv.z * hv.z + kv.w * hv.w;
@@ -870,8 +945,10 @@ __global__ __launch_bounds__(kDrThreads) void decode_route_kernel(DecodeRouteArg
       }
       acc += __shfl_xor(acc, 1, kWave);
       acc += __shfl_xor(acc, 2, kWave);
+      acc += __shfl_xor(acc, 4, kWave);
       if (j < n && part == 0) s_aw[j] = fminf(fmaxf(acc * a.inv_sqrt_d, -kActClamp), kActClamp);
     }
+    prefetch(4, 8);
     __syncthreads();
     if (wv == 0) {
       float m = -INFINITY;
@@ -907,10 +984,31 @@ __global__ __launch_bounds__(kDrThreads) void decode_route_kernel(DecodeRouteArg
       __syncthreads();
     }
   }
+  if (!a.refresh_tail) prefetch(4, 8);
   __syncthreads();
-  // scores: 32 lanes per block (4 dims per lane per step), 32 blocks per pass,
-  // loads of 8 passes issued before use; the refreshed tail block from LDS
-  {
+  // scores, the refreshed tail block from LDS
+  if (fast_scores) {
+    const float4 qa = *(const float4*)(s_q + l16 * 4), qb = *(const float4*)(s_q + 64 + l16 * 4);
+    const float4 ta = *(const float4*)(s_tail + l16 * 4), tb = *(const float4*)(s_tail + 64 + l16 * 4);
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int c = slot16 + r * (kDrThreads / 16);
+      const bool tl = a.refresh_tail && c == ct;
+      const float4 ka = tl ? ta : kp[r][0], kb = tl ? tb : kp[r][1];
+      float v = qa.x * ka.x + qa.y * ka.y + qa.z * ka.z + qa.w * ka.w +
+                qb.x * kb.x + qb.y * kb.y + qb.z * kb.z + qb.w * kb.w;
+#pragma unroll
+      for (int m = 8; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+      if (l16 == 0 && c < nblk) {
+        float zz = kScoreNeg;
+        if (c <= lim) zz = fminf(fmaxf(v * a.inv_sqrt_d, -kActClamp), kActClamp);
+        s_x[c] = zz;
+        a.z[(int64_t)b * a.z_stride + c] = zz;
+      }
+    }
+  } else {
+    // 32 lanes per block (4 dims per lane per step), 32 blocks per pass, loads of
+    // 8 passes issued before use
     const int l32 = lane & 31, row0 = tid / 32;
     for (int cb = 0; cb < nblk; cb += 8 * (kDrThreads / 32)) {
       float acc[8];
@@ -1032,42 +1130,9 @@ __global__ __launch_bounds__(kDrThreads) void decode_route_kernel(DecodeRouteArg
   }
   __syncthreads();
   if (wv != 0) return;
-  float sel_v[kMaxM];
-  int sel_k[kMaxM];
-#pragma unroll
-  for (int m = 0; m < kMaxM; ++m) {
-    sel_v[m] = m < M ? s_selv[m] : 0.f;
-    sel_k[m] = m < M ? s_selk[m] : 0x3fffffff;
-  }
-  float prior[kMaxM];
-  entmax15_sorted(sel_v, M, prior);
-  float logp[kMaxM];
-  float musum = 0.f;
-  int cnt = 0;
-#pragma unroll
-  for (int m = 0; m < kMaxM; ++m) {
-    logp[m] = logf(fmaxf(prior[m], a.floor_p));
-    if (m < Kp && (sel_k[m] & (1 << 30))) { musum += logp[m]; ++cnt; }
-  }
-  const float mu = musum / (float)max(cnt, 1);
-  for (int m = lane; m < a.Kout; m += kWave) {
-    int oi = -1;
-    float ob = 0.f;
-    uint8_t ov = 0;
-#pragma unroll
-    for (int s = 0; s < kMaxM; ++s) {
-      if (s == m && s < Kp) {
-        oi = sel_k[s] & 0x3fffffff;
-        const bool va = (sel_k[s] & (1 << 30)) != 0;
-        ov = va ? 1 : 0;
-        ob = va ? (logp[s] - mu) * a.inv_sigma : 0.f;
-      }
-    }
-    a.idx[(int64_t)b * a.Kout + m] = oi;
-    a.bias[(int64_t)b * a.Kout + m] = ob;
-    if (a.valid) a.valid[(int64_t)b * a.Kout + m] = ov;
-  }
+  decode_route_finish(a, b, lane, M, Kp, s_selv, s_selk);
 }
+
 
 }  // namespace dash
 
