@@ -768,6 +768,9 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
     // S^T of item it first, so that its reads and MFMAs overlap the fetches and
     // the bookkeeping below (an item nobody needs, or the drain step, computes a
     // discarded S^T from whatever the stage holds)
+    // raised wave priority over the compute of the step (two wavefronts of other
+    // work-groups share each SIMD: the one in its MFMA stretch is preferred)
+    __builtin_amdgcn_s_setprio(1);
     floatx16 sc[2];
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
@@ -870,6 +873,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
           const bf16x2 pp = {pP[P][hf][j][q], pP[P][hf][j][q + 1]};
           l_run = __builtin_amdgcn_fdot2_f32_bf16(pp, ones, l_run, false);
         }
+    __builtin_amdgcn_s_setprio(0);
   };
   for (int it = 0; it <= n_items; it += 2) {
     step(it, std::integral_constant<int, 0>{});
