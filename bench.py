@@ -297,7 +297,7 @@ def cpu_decode_baseline(res, cfg, reps=3):
 # WRITE_SIZE), each divided by the counter's reading for a 256 MiB device copy
 # (FETCH_SIZE reads 0.500 of the copied bytes, WRITE_SIZE 1.000).  Re-measure when
 # the kernels change.
-PREFILL_ATTN_TRAFFIC_BYTES = int((1684.6 + 776.3) * 1e6)
+PREFILL_ATTN_TRAFFIC_BYTES = int((1664.4 + 776.1) * 1e6)
 DECODE_ATTN_TRAFFIC_BYTES = int((87.2 + 1.5) * 1e6)
 
 
