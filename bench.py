@@ -298,6 +298,10 @@ def cpu_decode_baseline(res, cfg, reps=3):
 # (FETCH_SIZE reads 0.500 of the copied bytes, WRITE_SIZE 1.000).  Re-measure when
 # the kernels change.
 PREFILL_ATTN_TRAFFIC_BYTES = int((1664.4 + 776.1) * 1e6)
+# Executed bf16 MFMA FLOP of one prefill attention launch (tile + sparse kernels), from
+# SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 in a counter run of ``bench.py --traffic-probe``
+# (re-measure when the kernels change).
+PREFILL_ATTN_EXECUTED_FLOP = (293.7 + 79.4) * 1e9
 DECODE_ATTN_TRAFFIC_BYTES = int((87.2 + 1.5) * 1e6)
 
 
@@ -395,7 +399,10 @@ def main():
                      "frac": round(tflops_attn / PEAK_BF16_TFLOPS, 4),
                      "traffic": PREFILL_ATTN_TRAFFIC_BYTES,
                      "kernel": "prefill attention", "flop_per_launch": pre["flops"],
-                     "avg_launch_ms": round(pre["t_attn"] * 1e3, 4)},
+                     "avg_launch_ms": round(pre["t_attn"] * 1e3, 4),
+                     "executed_flop_per_launch": PREFILL_ATTN_EXECUTED_FLOP,
+                     "executed_frac": round(PREFILL_ATTN_EXECUTED_FLOP / pre["t_attn"] / 1e12 /
+                                            PEAK_BF16_TFLOPS, 4)},
         "decode": {"workload": W.DECODE_B8.name, "us_per_step": round(dec["t_step"] * 1e6, 2),
                    "us_per_step_eager": round(dec["t_step_eager"] * 1e6, 2),
                    "step": "routing + attention, replayed as one HIP graph per cache set",
