@@ -71,10 +71,12 @@ struct PrefillArgs {
   int B;
   int32_t* chunk_rec;                  // [B, chunk_cap, kRec] chunk records
   int chunk_cap;
-  // sparse partials, one per (head, slot, token row) in that order (see part_row)
-  int64_t prows;                       // token rows of the partial arrays
-  float* part_lse;                     // [H, K, prows]  base-2 log-sum-exp
-  bf16* part_o;                        // [H, K, prows, D]  normalised partial output, dims
+  // sparse partials, one per (head, pair position) (see part_row): a pair's
+  // position is its place in the chunk records, chunk-major over all sequences
+  int32_t* spos;                       // [rows, K] position of each sparse pair
+  int64_t ppos;                        // positions per head
+  float* part_lse;                     // [H, ppos]  base-2 log-sum-exp
+  bf16* part_o;                        // [H, ppos, D]  normalised partial output, dims
                                        // in MFMA lane order (see part_index)
 };
 
@@ -95,12 +97,12 @@ __device__ __forceinline__ int part_index(int hl, int dt, int g, int q) {
   return hl * 64 + dt * 16 + g * 4 + q;
 }
 
-// Index of the sparse partial of (token row, routed slot, head): head, slot,
-// row order, so that the partials of one slot of neighbouring queries, which a
-// wavefront merges together, are neighbours in memory.
+// Index of the sparse partial of (pair position, head): head, then position, so
+// that the partials a sparse wavefront writes (32 consecutive pairs of a chunk)
+// are neighbours in memory.
 template <typename Args>
-__device__ __forceinline__ int64_t part_row(const Args& a, int64_t row, int slot, int h) {
-  return ((int64_t)h * a.K + slot) * a.prows + row;
+__device__ __forceinline__ int64_t part_row(const Args& a, int64_t pos, int h) {
+  return (int64_t)h * a.ppos + pos;
 }
 
 // Keep a routed slot?  The block must exist, be valid, and have keys below the
@@ -301,6 +303,7 @@ __global__ __launch_bounds__(kPfTQ) void prefill_scatter_kernel(PrefillArgs a) {
   const int32_t* tb = a.tile_base + ((int64_t)b * a.ntiles_cap + blockIdx.x) * a.nblk_cap;
   const int32_t* bch = a.blk_chunk + (int64_t)b * a.nblk_cap;
   int32_t* rec = a.chunk_rec + (int64_t)b * a.chunk_cap * kRec;
+  const int64_t pos0 = (int64_t)a.chunk_pref[b] * kPfCH;   // first pair position of the sequence
   int32_t c[kPfMaxK];
   uint32_t vmask;
   load_row_slots(a, row, c, vmask);
@@ -317,6 +320,7 @@ __global__ __launch_bounds__(kPfTQ) void prefill_scatter_kernel(PrefillArgs a) {
       const int q = tb[c[s]] + pos[s];               // position in the block's pair list
       rec[(int64_t)(bch[c[s]] + q / kPfCH) * kRec + kRecHead + q % kPfCH] =
           (int32_t)(row * a.K + s - base);
+      a.spos[row * a.K + s] = (int32_t)(pos0 + (int64_t)bch[c[s]] * kPfCH + q);
     }
 }
 
@@ -890,25 +894,37 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
       *(const __attribute__((address_space(4))) PrefillArgs*)kap;
 
   // ---- merge the sparse partials of this query ----
-  // All kinds and log-sum-exps are loaded first and the reference moves once to
-  // their maximum; partial rows are lane-contiguous and read with 16-byte loads.
+  // All kinds, pair positions and log-sum-exps are loaded first and the
+  // reference moves once to their maximum; partial rows are lane-contiguous and
+  // read with 16-byte loads.
   if (pa.kind) {
     const int64_t p0 = (r0 + tqc) * pa.K;
     float l2[kPfMaxK];
+    int32_t sp[kPfMaxK];                   // positions (read for sparse slots only)
     uint32_t smask = 0;
     if (pa.K == kPfMaxK) {
       const uint4 kv = *(const uint4*)(pa.kind + p0);
+#pragma unroll
+      for (int g = 0; g < kPfMaxK / 4; ++g) {
+        const int4 pv = *(const int4*)(pa.spos + p0 + 4 * g);
+        sp[4 * g] = pv.x; sp[4 * g + 1] = pv.y; sp[4 * g + 2] = pv.z; sp[4 * g + 3] = pv.w;
+      }
       const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
       for (int s = 0; s < kPfMaxK; ++s)
         if (qvalid && ((kw[s >> 2] >> (8 * (s & 3))) & 0xffu) == 2) smask |= 1u << s;
     } else {
+#pragma unroll
+      for (int s = 0; s < kPfMaxK; ++s) sp[s] = 0;
       for (int s = 0; s < pa.K; ++s)
-        if (qvalid && pa.kind[p0 + s] == 2) smask |= 1u << s;
+        if (qvalid && pa.kind[p0 + s] == 2) {
+          smask |= 1u << s;
+          sp[s] = pa.spos[p0 + s];
+        }
     }
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s)
-      l2[s] = ((smask >> s) & 1u) ? pa.part_lse[part_row(pa, r0 + tqc, s, h)] : -INFINITY;
+      l2[s] = ((smask >> s) & 1u) ? pa.part_lse[part_row(pa, sp[s], h)] : -INFINITY;
     float mx = m_run;
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s) mx = fmaxf(mx, l2[s]);
@@ -928,8 +944,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s)
       if (l2[s] != -INFINITY) live |= 1u << s;
-    const bf16* po = pa.part_o + part_row(pa, r0 + tqc, 0, h) * D + part_index(hl, 0, 0, 0);
-    const int64_t pstride = pa.prows * D;
+    const bf16* po = pa.part_o + part_row(pa, 0, h) * D + part_index(hl, 0, 0, 0);
 #pragma unroll
     for (int sb = 0; sb < kPfMaxK; sb += 4) {
       const uint32_t gm = (live >> sb) & 15u;
@@ -939,7 +954,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
       for (int u = 0; u < 4; ++u)
         if ((gm >> u) & 1u) {
 #pragma unroll
-          for (int q = 0; q < 8; ++q) buf[u][q] = *(const bf16x8*)(po + (sb + u) * pstride + q * 8);
+          for (int q = 0; q < 8; ++q) buf[u][q] = *(const bf16x8*)(po + (int64_t)sp[sb + u] * D + q * 8);
         }
 #pragma unroll
       for (int u = 0; u < 4; ++u)
@@ -1127,7 +1142,7 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
     const float l_tot = xor32_sum(psum);
     if (active) {
       const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-      const int64_t pr = part_row(a, r0 + t, pid_cur - t * a.K, h);
+      const int64_t pr = part_row(a, (int64_t)(pb + ch) * kPfCH + wv * 32 + 128 * j + n, h);
       bf16* po = a.part_o + pr * D;
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt)
@@ -1147,14 +1162,15 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
 
 // Workspace layout of the hybrid plan (byte offsets, 256-byte aligned pieces).
 struct PlanLayout {
-  int64_t count, done, tbase, bch, nchunks, cpref, rec, kind, plse, po, total;
+  int64_t count, done, tbase, bch, nchunks, cpref, rec, kind, spos, plse, po, total;
+  int64_t ppos;
   int chunk_cap, ntiles_cap;
 };
 
 inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
 inline PlanLayout plan_layout(int B, int H, int S_max, int64_t rows, int K, int D,
-                              int nblk_cap) {
+                              int nblk_cap, int bs) {
   PlanLayout L;
   L.chunk_cap = (int)((int64_t)S_max * K / kPfCH) + nblk_cap + 1;
   L.ntiles_cap = (S_max + kPfTQ - 1) / kPfTQ;
@@ -1168,8 +1184,12 @@ inline PlanLayout plan_layout(int B, int H, int S_max, int64_t rows, int K, int 
   L.cpref = o; o = align256(o + (int64_t)(B + 1) * 4);
   L.rec = o; o = align256(o + (int64_t)B * L.chunk_cap * kRec * 4);
   L.kind = o; o = align256(o + rows * K);
-  L.plse = o; o = align256(o + rows * K * H * 4);
-  L.po = o; o = align256(o + rows * K * H * D * 2);
+  L.spos = o; o = align256(o + rows * K * 4);
+  // chunks over all sequences: at most (pairs / kPfCH) full ones plus one partly
+  // filled chunk per block, and a sequence of len rows has ceil(len / bs) blocks
+  L.ppos = (rows * K / kPfCH + rows / bs + B + 2) * kPfCH;
+  L.plse = o; o = align256(o + L.ppos * H * 4);
+  L.po = o; o = align256(o + L.ppos * H * D * 2);
   L.total = o;
   return L;
 }
@@ -1185,7 +1205,7 @@ extern "C" int dash_attn_prefill_workspace_size(int B, int H, int S_max, int64_t
   if (!bytes || B < 0 || H <= 0 || S_max < 0 || total_rows < 0 || K < 0 || block_size <= 0)
     return kErrInvalid;
   const int nblk_cap = (S_max + block_size - 1) / block_size;
-  *bytes = plan_layout(B, H, S_max, total_rows, K, D, nblk_cap).total;
+  *bytes = plan_layout(B, H, S_max, total_rows, K, D, nblk_cap, block_size).total;
   return kOk;
 }
 
@@ -1234,7 +1254,7 @@ extern "C" int dash_attn_prefill(
   const bool hybrid = dense_threshold > 0 && K > 0 && block_size <= 64;
   if (hybrid) {
     if (total_rows <= 0) return kErrInvalid;
-    const PlanLayout L = plan_layout(B, H, S, total_rows, K, D, nblk_cap);
+    const PlanLayout L = plan_layout(B, H, S, total_rows, K, D, nblk_cap, block_size);
     if (!workspace || workspace_bytes < L.total || (uintptr_t)workspace % 256 != 0)
       return kErrWorkspace;
     char* w = (char*)workspace;
@@ -1250,7 +1270,8 @@ extern "C" int dash_attn_prefill(
     a.B = B;
     a.chunk_rec = (int32_t*)(w + L.rec);
     a.chunk_cap = L.chunk_cap;
-    a.prows = total_rows;
+    a.spos = (int32_t*)(w + L.spos);
+    a.ppos = L.ppos;
     a.part_lse = (float*)(w + L.plse);
     a.part_o = (bf16*)(w + L.po);
     hipLaunchKernelGGL(prefill_plan_kernel, dim3(ntiles, B), dim3(kPfTQ), 0, st, a);
