@@ -507,6 +507,15 @@ __device__ __forceinline__ void pv_tr_swz(const bf16* sVs, int kbase, const bf16
   }
 }
 
+// Orders a wavefront's LDS writes before its later LDS reads of other lanes'
+// data (and reads before later writes): the compiler otherwise treats each lane's
+// LDS accesses as independent of the other lanes'.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Maximum over lanes l and l^32, every lane gets it (v_permlane32_swap).
 __device__ __forceinline__ float xor32_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -1008,6 +1017,7 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
   static_assert(D == 128, "head_dim 128");
   __shared__ __attribute__((aligned(16))) bf16 sKs[kPfIT * D];
   __shared__ __attribute__((aligned(16))) bf16 sVs[kPfIT * D];
+  __shared__ __attribute__((aligned(16))) bf16 sTr[4 * 16 * D];   // per wavefront: 16 partial rows
   // The first H * (total chunks) work-groups of the grid take the real chunks
   // (the hardware deals consecutive work-groups to the 8 XCDs in turn, so every
   // XCD gets an equal share); the rest exit.  Logical order (sequence, head,
@@ -1140,21 +1150,35 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
       pv_tr_swz(sVs, 32 * hf + 16, pop[1], acc_o, lane);
     }
     const float l_tot = xor32_sum(psum);
-    if (active) {
-      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-      const int64_t pr = part_row(a, (int64_t)(pb + ch) * kPfCH + wv * 32 + 128 * j + n, h);
-      bf16* po = a.part_o + pr * D;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    // The wavefront's 32 partial rows (consecutive positions) leave through LDS in
+    // two pieces of 16 rows, so that every store instruction writes 1 KB
+    // contiguously (whole 128-byte lines) instead of 16 bytes of 64 different
+    // rows.  Rows of lanes past the chunk's pair count are written too: their
+    // positions belong to this chunk and are never read.
+    const int64_t pw = part_row(a, (int64_t)(pb + ch) * kPfCH + wv * 32 + 128 * j, h);
+    bf16* const st = sTr + wv * 16 * D;
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
+    for (int piece = 0; piece < 2; ++piece) {
+      if ((n >> 4) == piece) {
 #pragma unroll
-        for (int g = 0; g < 4; g += 2) {
-          bf16x8 w;
+        for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-          for (int e2 = 0; e2 < 8; ++e2) w[e2] = (bf16)(acc_o[dt][g * 4 + e2] * inv);
-          *(bf16x8*)(po + part_index(hl, dt, g, 0)) = w;
-        }
-      if (hl == 0) a.part_lse[pr] = l_tot > 0.f ? mloc + log2f(l_tot) : -INFINITY;
+          for (int g = 0; g < 4; g += 2) {
+            bf16x8 w;
+#pragma unroll
+            for (int e2 = 0; e2 < 8; ++e2) w[e2] = (bf16)(acc_o[dt][g * 4 + e2] * inv);
+            *(bf16x8*)(st + (n & 15) * D + part_index(hl, dt, g, 0)) = w;
+          }
+      }
+      wave_lds_sync();                     // other lanes' rows are read below
+      char* const dst = (char*)(a.part_o + (pw + 16 * piece) * D);
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        *(bf16x8*)(dst + k * 1024 + lane * 16) = *(const bf16x8*)((const char*)st + k * 1024 + lane * 16);
+      wave_lds_sync();                     // and overwritten by the next piece
     }
+    if (active && hl == 0) a.part_lse[pw + n] = l_tot > 0.f ? mloc + log2f(l_tot) : -INFINITY;
   };
   if (nrounds > 0) round(0, inA);
   if (nrounds > 1) round(1, inB);
