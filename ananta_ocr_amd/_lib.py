@@ -36,6 +36,11 @@ SIGNATURES = {
     "dash_attn_decode": (_i, [_p, _l, _l, _p, _l, _l, _l, _l, _p, _l, _l, _l, _l, _p, _l, _i,
                               _p, _p, _p, _p, _p, _i, _p, _i, _l, _l, _p, _l, _l, _i, _i, _i,
                               _i, _i, _i, _f, _i, _p, _l, _p]),
+    "dash_decode_step_workspace_size": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_l)]),
+    "dash_decode_step": (_i, [_p, _l, _p, _l, _l, _l, _p, _l, _i, _p, _i, _p, _i, _p, _l, _i,
+                              _p, _l, _i, _i, _f, _f, _f, _i, _i, _i, _p, _p, _p, _p, _l,
+                              _p, _l, _l, _p, _l, _l, _l, _l, _p, _l, _l, _l, _l,
+                              _p, _i, _l, _l, _p, _l, _l, _i, _i, _i, _i, _i, _f, _p, _l, _p]),
 }
 
 _LIB = None

@@ -12,45 +12,9 @@
 // online softmax in base 2.  Every wavefront writes an (o, m, l) partial; a
 // merge kernel (one wavefront per (b, h)) combines them with a log-sum-exp.
 
-#include "dash_common.h"
+#include "dash_decode_unit.h"
 
 namespace dash {
-
-constexpr int kDcMaxK = 16;
-constexpr int kDcMaxSplit = 64;
-
-struct DecodeArgs {
-  const bf16* q; int64_t q_sb, q_sh;
-  const bf16* k; const bf16* v;
-  int64_t k_sb, k_sh, k_st, k_sp;
-  int64_t v_sb, v_sh, v_st, v_sp;
-  const int32_t* table; int64_t table_stride; int page;
-  const int32_t* lens; const int32_t* q_pos;
-  const int32_t* idx; const uint8_t* valid; const float* bias; int K;
-  void* out; int out_bf16; int64_t o_sb, o_sh;
-  float* lse; int64_t lse_sb, lse_sh;
-  float* part;                   // [B*H*nsplit, D + 2]: o[D], m, l
-  int S, H, bs, lw, nsplit;
-  float scale_log2e;
-};
-
-__device__ __forceinline__ int64_t dc_row(const DecodeArgs& a, int b, int j, int64_t sb,
-                                          int64_t st, int64_t sp) {
-  if (a.table) {
-    const int p = a.table[(int64_t)b * a.table_stride + j / a.page];
-    return (int64_t)p * sp + (int64_t)(j % a.page) * st;
-  }
-  return (int64_t)b * sb + (int64_t)j * st;
-}
-
-// Sum over the 16 lanes of a DPP row; every lane of the row gets the sum.
-__device__ __forceinline__ float row16_sum(float v) {
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x122, 0xf, 0xf, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x121, 0xf, 0xf, false));
-  return v;
-}
 
 template <int D>
 __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeArgs a) {
@@ -61,127 +25,26 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeArgs a) {
 
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x;
-  const int len = a.lens ? a.lens[b] : a.S;
-  const int qp = a.q_pos ? a.q_pos[b] : len - 1;
-  const int ls = qp - a.lw + 1;
-  const int lo = max(ls, 0);
-  const int nblk = len > 0 ? (len + a.bs - 1) / a.bs : 0;
-  const float log2e = 1.4426950408889634f;
-  const int w0 = lo / a.bs;
-  const int n_win = (len > 0 && qp >= 0) ? qp / a.bs - w0 + 1 : 0;
-  // ---- routed blocks (only wavefronts that own a routed unit need them): lanes < K
-  // load the slots; keep valid, remote, first occurrence, in slot order ----
+  const DcSpan sp = dc_span(a, b);
+  // ---- routed blocks (only wavefronts that own a routed unit need them) ----
   int n_r = 0;
   // first unit index >= n_win in this wavefront's sequence split, split + nsplit, ...
   const int u_first_routed =
-      split >= n_win ? split : split + a.nsplit * ((n_win - split + a.nsplit - 1) / a.nsplit);
-  if (u_first_routed < n_win + a.K) {
-    int c = -1;
-    float bl = 0.f;
-    bool keep = false;
-    if (lane < a.K && len > 0) {
-      const int64_t o = (int64_t)b * a.K + lane;
-      c = a.idx[o];
-      keep = c >= 0 && c < nblk && c * a.bs < ls && (!a.valid || a.valid[o] != 0);
-      bl = a.bias[o] * log2e;
-    }
-    sTmp[lane] = keep ? c : -1;
-    __syncthreads();
-    if (keep)
-      for (int j = 0; j < lane; ++j) keep &= (sTmp[j] != c);
-    const uint64_t mask = __ballot(keep);
-    if (keep) {
-      const int pos = __popcll(mask & ((1ull << lane) - 1ull));
-      sRC[pos] = c;
-      sRB[pos] = bl;
-    }
-    __syncthreads();
-    n_r = __popcll(mask);
-  }
-  const int n_units = n_win + n_r;
+      split >= sp.n_win ? split : split + a.nsplit * ((sp.n_win - split + a.nsplit - 1) / a.nsplit);
+  if (u_first_routed < sp.n_win + a.K)
+    n_r = dc_routed(a, b, sp, lane, sTmp, sRC, sRB, [] { __syncthreads(); });
+  const int n_units = sp.n_win + n_r;
 
-  const int g = lane >> 4, dl = (lane & 15) * 8;
-  const bf16x8 qv8 = *(const bf16x8*)(a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + dl);
-  bf16x2 qp2[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) { qp2[e][0] = qv8[2 * e]; qp2[e][1] = qv8[2 * e + 1]; }
-
-  float m_run = -INFINITY, l_run = 0.f, o[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = 0.f;
-
-  const bf16* kh = a.k + (int64_t)h * a.k_sh;
-  const bf16* vh = a.v + (int64_t)h * a.v_sh;
+  DcState st;
+  dc_init(st, a, b, h, lane);
   for (int u = split; u < n_units; u += a.nsplit) {
-    const bool routed = u >= n_win;
-    const int cu = routed ? sRC[u - n_win] : w0 + u;
-    const float blog = routed ? sRB[u - n_win] : 0.f;
-    const int jend = min((cu + 1) * a.bs, len);
-    for (int jb = cu * a.bs; jb < jend; jb += 64) {
-      bf16x8 kr[16], vr[16];
-#pragma unroll
-      for (int st = 0; st < 16; ++st) {
-        const int j = min(jb + 4 * st + g, len - 1);
-        kr[st] = *(const bf16x8*)(kh + dc_row(a, b, j, a.k_sb, a.k_st, a.k_sp) + dl);
-      }
-#pragma unroll
-      for (int st = 0; st < 16; ++st) {
-        const int j = min(jb + 4 * st + g, len - 1);
-        vr[st] = *(const bf16x8*)(vh + dc_row(a, b, j, a.v_sb, a.v_st, a.v_sp) + dl);
-      }
-      float s[16];
-      float mloc = -INFINITY;
-#pragma unroll
-      for (int st = 0; st < 16; ++st) {
-        float acc = 0.f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          bf16x2 kk;
-          kk[0] = kr[st][2 * e];
-          kk[1] = kr[st][2 * e + 1];
-          acc = __builtin_amdgcn_fdot2_f32_bf16(qp2[e], kk, acc, false);
-        }
-        acc = row16_sum(acc);
-        const int key = jb + 4 * st + g;
-        bool ok = key < jend;
-        ok = ok && (routed ? (key < ls) : (key >= lo && key <= qp));
-        s[st] = ok ? acc * a.scale_log2e + blog : -INFINITY;
-        mloc = fmaxf(mloc, s[st]);
-      }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 16, kWave));
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
-      const float m_new = fmaxf(m_run, mloc);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run - m_use);
-      l_run *= alpha;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] *= alpha;
-#pragma unroll
-      for (int st = 0; st < 16; ++st) {
-        const float p = fast_exp2(s[st] - m_use);
-        l_run += p;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = fmaf(p, bf2f(vr[st][e]), o[e]);
-      }
-      m_run = m_new;
-    }
-  }
-  // ---- this wavefront's partial: sum the four lane groups (they share m_run) ----
-  l_run += __shfl_xor(l_run, 16, kWave);
-  l_run += __shfl_xor(l_run, 32, kWave);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    o[e] += __shfl_xor(o[e], 16, kWave);
-    o[e] += __shfl_xor(o[e], 32, kWave);
+    const bool routed = u >= sp.n_win;
+    const int cu = routed ? sRC[u - sp.n_win] : sp.w0 + u;
+    const float blog = routed ? sRB[u - sp.n_win] : 0.f;
+    dc_block(st, a, b, h, sp, cu, routed, blog);
   }
   const int bh = b * a.H + h;
-  float* part = a.part + ((int64_t)bh * a.nsplit + split) * (D + 2);
-  if (lane < 16) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) part[dl + e] = o[e];
-  }
-  if (lane == 0) { part[D] = m_run; part[D + 1] = l_run; }
-
+  dc_store_partial<D>(st, a.part + ((int64_t)bh * a.nsplit + split) * (D + 2), lane);
 }
 
 // Merge of the nsplit partials of every (b, h): one wavefront per (b, h).
@@ -193,31 +56,8 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
   const float* pb = a.part + (int64_t)bh * a.nsplit * (D + 2);
   float ms = -INFINITY, lsum = 0.f;
   if (lane < a.nsplit) { ms = pb[lane * (D + 2) + D]; lsum = pb[lane * (D + 2) + D + 1]; }
-  const float M = wave_max(ms);
-  const float Mu = (M == -INFINITY) ? 0.f : M;
-  const float w = lane < a.nsplit ? fast_exp2(ms - Mu) : 0.f;
-  const float L = wave_sum(lsum * w);
-  sW[lane] = w;
-  __syncthreads();
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  float acc0 = 0.f, acc1 = 0.f;
-  for (int s = 0; s < a.nsplit; ++s) {
-    const float2 ov = *(const float2*)(pb + s * (D + 2) + lane * 2);
-    acc0 += ov.x * sW[s];
-    acc1 += ov.y * sW[s];
-  }
-  const int64_t off = (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + lane * 2;
-  if (a.out_bf16) {
-    bf16x2 r;
-    r[0] = (bf16)(acc0 * inv);
-    r[1] = (bf16)(acc1 * inv);
-    *(bf16x2*)((bf16*)a.out + off) = r;
-  } else {
-    *(float2*)((float*)a.out + off) = make_float2(acc0 * inv, acc1 * inv);
-  }
-  if (a.lse && lane == 0)
-    a.lse[(int64_t)b * a.lse_sb + (int64_t)h * a.lse_sh] =
-        L > 0.f ? (M + log2f(L)) * 0.6931471805599453f : -INFINITY;
+  dc_merge<D>(a, b, h, lane, a.nsplit, ms, lsum, sW,
+              [&](int s) { return pb + s * (D + 2); });
 }
 
 }  // namespace dash

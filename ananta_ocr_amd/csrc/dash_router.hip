@@ -11,6 +11,7 @@
 //                      (modeling_deepseekv2.py:309-333, dash_attention.py:615-662)
 
 #include "dash_common.h"
+#include "dash_decode_unit.h"
 
 namespace dash {
 
@@ -877,7 +878,7 @@ __device__ __forceinline__ void decode_route_finish(const DecodeRouteArgs& a, in
   }
 }
 
-__global__ __launch_bounds__(kDrThreads) void decode_route_kernel(DecodeRouteArgs a) {
+__device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int b) {
   __shared__ __attribute__((aligned(16))) float s_q[256];
   __shared__ __attribute__((aligned(16))) float s_tail[256];
   __shared__ float s_aw[256];
@@ -894,7 +895,6 @@ __global__ __launch_bounds__(kDrThreads) void decode_route_kernel(DecodeRouteArg
   __shared__ float s_selv[kMaxM];
   __shared__ int s_selk[kMaxM];
 
-  const int b = blockIdx.x;
   const int tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
   const int len = a.lens ? a.lens[b] : a.S;
   const int nblk = len > 0 ? (len + a.bs - 1) / a.bs : 0;
@@ -1133,10 +1133,85 @@ __global__ __launch_bounds__(kDrThreads) void decode_route_kernel(DecodeRouteArg
   decode_route_finish(a, b, lane, M, Kp, s_selv, s_selk);
 }
 
+__global__ __launch_bounds__(kDrThreads) void decode_route_kernel(DecodeRouteArgs a) {
+  decode_route_body(a, blockIdx.x);
+}
+
+// ---------------------------------------------------------------------------
+// Fused decode step.  The window part of the attention does not depend on the
+// routing, so it runs in the router's launch: work-groups 0 .. B-1 route one
+// sequence each (as decode_route_kernel), the rest are 16 wavefronts of window
+// pieces, one 32-key piece of the window of one (sequence, head) per wavefront,
+// each writing an (o, m, l) partial (32 keys per round trip keep a wavefront
+// within the 128 registers a 1024-thread work-group allows).  A second launch
+// takes one wavefront per routed slot of (sequence, head), a third merges.
+// ---------------------------------------------------------------------------
+constexpr int kDsPiece = 32;              // keys per window piece
+
+__device__ __forceinline__ int ds_pieces(const DecodeArgs& da, const DcSpan& sp) {
+  return sp.n_win > 0 ? (sp.qp + 1 - sp.w0 * da.bs + kDsPiece - 1) / kDsPiece : 0;
+}
+
+__global__ __launch_bounds__(kDrThreads) void decode_route_window_kernel(DecodeRouteArgs ra,
+                                                                         DecodeArgs da, int B,
+                                                                         int npw) {
+  if ((int)blockIdx.x < B) {
+    decode_route_body(ra, blockIdx.x);
+    return;
+  }
+  const int task = ((int)blockIdx.x - B) * (kDrThreads / kWave) + (int)threadIdx.x / kWave;
+  if (task >= B * da.H * npw) return;
+  const int piece = task % npw, bh = task / npw;
+  const int h = bh % da.H, b = bh / da.H;
+  const int lane = wave_lane();
+  const DcSpan sp = dc_span(da, b);
+  if (piece >= ds_pieces(da, sp)) return;
+  DcState st;
+  dc_init(st, da, b, h, lane);
+  const int j0 = sp.w0 * da.bs + piece * kDsPiece;
+  dc_keys<kDsPiece>(st, da, b, h, sp, j0, min(j0 + kDsPiece, sp.len), false, 0.f);
+  dc_store_partial<128>(st, da.part + ((int64_t)bh * (npw + da.K) + piece) * (128 + 2), lane);
+}
+
+// Routed blocks of the fused step: one wavefront per routed slot of (b, h), 64 keys
+// per round trip; slot npw + r of the partials (an empty partial past the routed
+// count).
+__global__ __launch_bounds__(64) void decode_routed_kernel(DecodeArgs da, int npw) {
+  __shared__ int sTmp[kWave];
+  __shared__ int sRC[kDcMaxK];
+  __shared__ float sRB[kDcMaxK];
+  const int r = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x;
+  const DcSpan sp = dc_span(da, b);
+  const int n_r = dc_routed(da, b, sp, lane, sTmp, sRC, sRB, [] { __syncthreads(); });
+  DcState st;
+  dc_init(st, da, b, h, lane);
+  if (r < n_r) dc_block<64>(st, da, b, h, sp, sRC[r], true, sRB[r]);
+  dc_store_partial<128>(st, da.part + ((int64_t)(b * da.H + h) * (npw + da.K) + npw + r) * (128 + 2),
+                        lane);
+}
+
+// Merge of the fused step: the window pieces of (b, h) (slots below its piece count)
+// and its K routed slots (npw ..), one wavefront per (b, h).
+__global__ __launch_bounds__(64) void decode_step_merge_kernel(DecodeArgs da, int npw) {
+  __shared__ float sW[kWave];
+  const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  const DcSpan sp = dc_span(da, b);
+  const int nw = ds_pieces(da, sp);
+  const int n = nw + da.K;
+  const float* pb = da.part + (int64_t)(b * da.H + h) * (npw + da.K) * (128 + 2);
+  auto part_at = [&](int s) -> const float* { return pb + (s < nw ? s : npw + s - nw) * (128 + 2); };
+  float ms = -INFINITY, lsum = 0.f;
+  if (lane < n) { ms = part_at(lane)[128]; lsum = part_at(lane)[129]; }
+  dc_merge<128>(da, b, h, lane, n, ms, lsum, sW, part_at);
+}
 
 }  // namespace dash
 
-extern "C" int dash_decode_route(const float* idx_q, int64_t iq_sb, const float* idx_k,
+namespace dash {
+// Checks and packs the arguments of the decode router (shared by the router entry
+// and the fused decode step).
+static int decode_route_args(const float* idx_q, int64_t iq_sb, const float* idx_k,
                                  int64_t ik_sb, int64_t ik_st, int64_t ik_sp,
                                  const int32_t* block_table, int64_t table_stride,
                                  int page_size, const int32_t* seq_lens, int S,
@@ -1145,8 +1220,7 @@ extern "C" int dash_decode_route(const float* idx_q, int64_t iq_sb, const float*
                                  int64_t cand_stride, int B, int d, int block_size,
                                  int local_blocks, float idx_scale, float floor_p, float sigma,
                                  int K, int topm, int Kout, int32_t* idx, float* bias,
-                                 uint8_t* valid, float* z, int64_t z_stride, void* stream) {
-  using namespace dash;
+                                 uint8_t* valid, float* z, int64_t z_stride, DecodeRouteArgs& a) {
   if (!idx_q || !idx_k || !head_cls || !kbar || !idx || !bias || !z) return kErrInvalid;
   if (B < 0 || d <= 0 || d > 256 || block_size <= 0 || block_size > 256) return kErrUnsupported;
   if (topm < 1 || topm > kMaxM) return kErrUnsupported;
@@ -1157,8 +1231,6 @@ extern "C" int dash_decode_route(const float* idx_q, int64_t iq_sb, const float*
   if (ik_st % 4 != 0 || ik_sp % 4 != 0 || ik_sb % 4 != 0 || (uintptr_t)idx_k % 16 != 0 ||
       (uintptr_t)head_cls % 16 != 0)
     return kErrUnsupported;
-  if (B == 0) return kOk;
-  DecodeRouteArgs a;
   a.idx_q = idx_q; a.iq_sb = iq_sb;
   a.idx_k = idx_k;
   a.lay_k = SeqLayout{nullptr, block_table, table_stride, ik_sb, ik_sp, ik_st, page_size};
@@ -1172,6 +1244,102 @@ extern "C" int dash_decode_route(const float* idx_q, int64_t iq_sb, const float*
   a.K = K; a.topm = topm; a.Kout = Kout;
   a.idx = idx; a.bias = bias; a.valid = valid;
   a.z = z; a.z_stride = z_stride;
+  return kOk;
+}
+}  // namespace dash
+
+extern "C" int dash_decode_route(const float* idx_q, int64_t iq_sb, const float* idx_k,
+                                 int64_t ik_sb, int64_t ik_st, int64_t ik_sp,
+                                 const int32_t* block_table, int64_t table_stride,
+                                 int page_size, const int32_t* seq_lens, int S,
+                                 const float* head_cls, int refresh_tail, float* kbar,
+                                 int64_t kb_sb, int nblk_cap, const uint8_t* cand,
+                                 int64_t cand_stride, int B, int d, int block_size,
+                                 int local_blocks, float idx_scale, float floor_p, float sigma,
+                                 int K, int topm, int Kout, int32_t* idx, float* bias,
+                                 uint8_t* valid, float* z, int64_t z_stride, void* stream) {
+  using namespace dash;
+  DecodeRouteArgs a;
+  const int st = decode_route_args(idx_q, iq_sb, idx_k, ik_sb, ik_st, ik_sp, block_table, table_stride,
+                                   page_size, seq_lens, S, head_cls, refresh_tail, kbar, kb_sb,
+                                   nblk_cap, cand, cand_stride, B, d, block_size, local_blocks,
+                                   idx_scale, floor_p, sigma, K, topm, Kout, idx, bias, valid, z,
+                                   z_stride, a);
+  if (st != kOk || B == 0) return st;
   hipLaunchKernelGGL(decode_route_kernel, dim3(B), dim3(kDrThreads), 0, (hipStream_t)stream, a);
+  return launch_status();
+}
+
+extern "C" int dash_decode_step_workspace_size(int B, int H, int D, int block_size,
+                                               int local_window, int64_t* bytes) {
+  using namespace dash;
+  if (!bytes || B < 0 || H < 0 || D <= 0 || block_size <= 0 || local_window < 1) return kErrInvalid;
+  const int npw = (local_window + block_size - 1 + kDsPiece - 1) / kDsPiece;
+  *bytes = (int64_t)B * H * (npw + kDcMaxK) * (D + 2) * (int64_t)sizeof(float);
+  return kOk;
+}
+
+extern "C" int dash_decode_step(
+    const float* idx_q, int64_t iq_sb, const float* idx_k, int64_t ik_sb, int64_t ik_st,
+    int64_t ik_sp, const int32_t* block_table, int64_t table_stride, int page_size,
+    const int32_t* seq_lens, int S, const float* head_cls, int refresh_tail, float* kbar,
+    int64_t kb_sb, int nblk_cap, const uint8_t* cand, int64_t cand_stride, int d,
+    int local_blocks, float idx_scale, float floor_p, float sigma, int K, int topm, int Kout,
+    int32_t* idx, float* bias, uint8_t* valid, float* z, int64_t z_stride,
+    const void* q, int64_t q_sb, int64_t q_sh,
+    const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t k_sp,
+    const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t v_sp,
+    void* out, int out_bf16, int64_t o_sb, int64_t o_sh, float* lse, int64_t lse_sb,
+    int64_t lse_sh, int B, int H, int D, int block_size, int local_window, float scale,
+    void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace dash;
+  DecodeRouteArgs ra;
+  const int rs = decode_route_args(idx_q, iq_sb, idx_k, ik_sb, ik_st, ik_sp, block_table,
+                                   table_stride, page_size, seq_lens, S, head_cls, refresh_tail,
+                                   kbar, kb_sb, nblk_cap, cand, cand_stride, B, d, block_size,
+                                   local_blocks, idx_scale, floor_p, sigma, K, topm, Kout, idx, bias,
+                                   valid, z, z_stride, ra);
+  if (rs != kOk) return rs;
+  if (!q || !k || !v || !out || H <= 0) return kErrInvalid;
+  if (D != 128) return kErrUnsupported;
+  if (Kout > kDcMaxK) return kErrUnsupported;
+  if (block_size % 64 != 0 && block_size != 32) return kErrUnsupported;
+  if (local_window < 1) return kErrInvalid;
+  if (block_table && page_size % block_size != 0) return kErrUnsupported;
+  const int npw = (local_window + block_size - 1 + kDsPiece - 1) / kDsPiece;
+  if (npw + Kout > kWave) return kErrUnsupported;     // partials of one merge wavefront
+  if (B == 0) return kOk;
+  const int64_t strides[] = {q_sb, q_sh, k_sb, k_sh, k_st, k_sp, v_sb, v_sh, v_st, v_sp};
+  for (int64_t s : strides)
+    if (s % 8 != 0) return kErrUnsupported;
+  const void* ptrs[] = {q, k, v};
+  for (const void* p : ptrs)
+    if ((uintptr_t)p % 16 != 0) return kErrUnsupported;
+  int64_t need = 0;
+  dash_decode_step_workspace_size(B, H, D, block_size, local_window, &need);
+  if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 16 != 0) return kErrWorkspace;
+  DecodeArgs a;
+  a.q = (const bf16*)q; a.q_sb = q_sb; a.q_sh = q_sh;
+  a.k = (const bf16*)k; a.v = (const bf16*)v;
+  a.k_sb = k_sb; a.k_sh = k_sh; a.k_st = k_st; a.k_sp = k_sp;
+  a.v_sb = v_sb; a.v_sh = v_sh; a.v_st = v_st; a.v_sp = v_sp;
+  a.table = block_table; a.table_stride = table_stride; a.page = page_size;
+  a.lens = seq_lens; a.q_pos = nullptr;
+  a.idx = idx; a.valid = valid; a.bias = bias; a.K = Kout;
+  a.out = out; a.out_bf16 = out_bf16; a.o_sb = o_sb; a.o_sh = o_sh;
+  a.lse = lse; a.lse_sb = lse_sb; a.lse_sh = lse_sh;
+  a.part = (float*)workspace;
+  a.S = S; a.H = H; a.bs = block_size; a.lw = local_window; a.nsplit = npw;
+  a.scale_log2e = scale * 1.4426950408889634f;
+  const int64_t tasks = (int64_t)B * H * npw;
+  const int64_t wgs = B + (tasks + kDrThreads / kWave - 1) / (kDrThreads / kWave);
+  if (wgs > 0x7fffffff) return kErrUnsupported;
+  hipLaunchKernelGGL(decode_route_window_kernel, dim3((unsigned)wgs), dim3(kDrThreads), 0,
+                     (hipStream_t)stream, ra, a, B, npw);
+  if (Kout > 0)
+    hipLaunchKernelGGL(decode_routed_kernel, dim3(Kout, H, B), dim3(64), 0, (hipStream_t)stream, a,
+                       npw);
+  hipLaunchKernelGGL(decode_step_merge_kernel, dim3(H, B), dim3(64), 0, (hipStream_t)stream, a,
+                     npw);
   return launch_status();
 }

@@ -355,5 +355,80 @@ def decode_route(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, i
     return res + (z,) if return_scores else res
 
 
+def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks,
+                      idx_scale, floor, sigma, K, topm, scale, seq_lens=None, block_table=None,
+                      page_size=None, cand=None, width=None, out_dtype=torch.float32,
+                      return_lse=False):
+    """decode_route followed by attn_decode of its routing, in two launches: the window
+    part of the attention runs beside the router.  Same arguments and results as those
+    two calls (q [B,H,D] or [B,H,1,D]; out [B,H,D]); returns (out, (idx, bias, valid))
+    with idx/bias/valid [B,1,K'] (valid uint8), or (out, lse, routing) with return_lse."""
+    _need_gpu(q, k, v, idx_q, idx_k, kbar_cache)
+    lib = _lib.load()
+    squeeze = q.dim() == 4
+    if squeeze:
+        q = q[:, :, 0]
+    q = _rows(q.to(torch.bfloat16))
+    k = _rows(k.to(torch.bfloat16))
+    v = _rows(v.to(torch.bfloat16))
+    if idx_q.dim() == 3:
+        idx_q = idx_q[:, 0]
+    idx_q = idx_q.float().contiguous()
+    idx_k = idx_k.float()
+    if idx_k.stride(-1) != 1:
+        idx_k = idx_k.contiguous()
+    B, H, D = q.shape
+    d = idx_q.shape[1]
+    nblk_cap = kbar_cache.shape[1]
+    if block_table is not None:
+        bt = _i32(block_table)
+        S = bt.shape[1] * page_size
+        isb, ist, isp = 0, idx_k.stride(1), idx_k.stride(0)
+        k_sb, k_sh, k_st, k_sp = 0, k.stride(2), k.stride(1), k.stride(0)
+        v_sb, v_sh, v_st, v_sp = 0, v.stride(2), v.stride(1), v.stride(0)
+        bt_stride = bt.stride(0)
+    else:
+        bt = None
+        S = idx_k.shape[1]
+        isb, ist, isp = idx_k.stride(0), idx_k.stride(1), 0
+        k_sb, k_sh, k_st, k_sp = k.stride(0), k.stride(1), k.stride(2), 0
+        v_sb, v_sh, v_st, v_sp = v.stride(0), v.stride(1), v.stride(2), 0
+        bt_stride = 0
+    Kw = max(1, min(int(K), int(topm))) if width is None else int(width)
+    if seq_lens is None and width is None:
+        Kw = max(1, min(int(K), max(1, min(int(topm), (S + block_size - 1) // block_size))))
+    dev = q.device
+    idx = torch.empty(B, Kw, dtype=torch.int32, device=dev)
+    bias = torch.empty(B, Kw, dtype=torch.float32, device=dev)
+    valid = torch.empty(B, Kw, dtype=torch.uint8, device=dev)
+    z = torch.empty(B, nblk_cap, dtype=torch.float32, device=dev)
+    out = torch.empty(B, H, D, dtype=out_dtype, device=dev)
+    lse = torch.empty(B, H, dtype=torch.float32, device=dev) if return_lse else None
+    lens = _i32(seq_lens)
+    c2 = None if cand is None else _u8(cand.reshape(B, -1))
+    hc = head_cls.float().contiguous()
+    lw = int(local_blocks) * int(block_size)
+    ws_bytes = ctypes.c_int64(0)
+    _lib.check(lib.dash_decode_step_workspace_size(B, H, D, int(block_size), lw, ws_bytes),
+               "workspace")
+    ws = torch.empty((ws_bytes.value + 3) // 4, dtype=torch.float32, device=dev)
+    st_ = lib.dash_decode_step(
+        _ptr(idx_q), idx_q.stride(0), _ptr(idx_k), isb, ist, isp, _ptr(bt), bt_stride,
+        int(page_size or 0), _ptr(lens), S, _ptr(hc), 1, _ptr(kbar_cache), kbar_cache.stride(0),
+        nblk_cap, _ptr(c2), 0 if c2 is None else c2.stride(0), d, int(local_blocks),
+        float(idx_scale), float(floor), float(sigma), int(K), int(topm), Kw, _ptr(idx),
+        _ptr(bias), _ptr(valid), _ptr(z), z.stride(0),
+        _ptr(q), q.stride(0), q.stride(1),
+        _ptr(k), k_sb, k_sh, k_st, k_sp, _ptr(v), v_sb, v_sh, v_st, v_sp,
+        _ptr(out), int(out_dtype == torch.bfloat16), out.stride(0), out.stride(1),
+        _ptr(lse), 0 if lse is None else lse.stride(0), 1,
+        B, H, D, int(block_size), lw, float(scale), _ptr(ws), ws.numel() * 4, _stream())
+    _lib.check(st_, "dash_decode_step")
+    if squeeze:
+        out = out[:, :, None]
+    routing = (idx[:, None], bias[:, None], valid[:, None])
+    return (out, lse, routing) if return_lse else (out, routing)
+
+
 def inv_sqrt(d):
     return 1.0 / math.sqrt(d)

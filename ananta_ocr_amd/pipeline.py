@@ -56,14 +56,28 @@ def init_decode_state(idx_k, head_cls, block_size, nblk_cap, seq_lens=None, bloc
 def decode_step(state, q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks, idx_scale,
                 floor, sigma, K, topm, scale=None, seq_lens=None, block_table=None,
                 page_size=None, out_dtype=torch.float32, nsplit=None, block_cand=None,
-                return_routing=False):
+                return_routing=False, fused=None):
     """One decode step for the query at the last cached token of each sequence.
     The newest token is already in k/v and idx_k; its block's summary is refreshed
-    inside the fused decode router."""
+    inside the fused decode router.  fused (default: whenever nsplit is not given and
+    the shapes allow it) runs the window part of the attention beside the router
+    (ops.decode_step_fused); otherwise decode_route then attn_decode."""
     D = q.shape[-1]
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     width = None if seq_lens is None else max(1, min(int(K), int(topm)))
+    if fused is None:
+        npw = (local_blocks * block_size + block_size - 1 + 31) // 32
+        fused = nsplit is None and D == 128 and min(int(K), int(topm)) <= 16 and \
+            npw + max(1, min(int(K), int(topm))) <= 64
+    if fused:
+        out, (idx, bias, valid) = ops.decode_step_fused(
+            q, k, v, idx_q, idx_k, head_cls, state.kbar, block_size, local_blocks, idx_scale,
+            floor, sigma, K, topm, scale, seq_lens=seq_lens, block_table=block_table,
+            page_size=page_size, cand=block_cand, width=width, out_dtype=out_dtype)
+        if return_routing:
+            return out, (idx, bias, valid.bool())
+        return out
     idx, bias, valid = ops.decode_route(idx_q, idx_k, head_cls, state.kbar, block_size,
                                         local_blocks, idx_scale, floor, sigma, K, topm,
                                         seq_lens=seq_lens, block_table=block_table,

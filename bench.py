@@ -80,14 +80,17 @@ def time_kernel(fn, reps):
     """Average duration of fn's launches with HIP events on the current stream
     (the stream the kernels are enqueued on)."""
     st = torch.cuda.current_stream()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(reps)]
-    for i, (a, b) in enumerate(evs):
-        a.record(st)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # A spin kernel first keeps the GPU busy while the host enqueues every launch, so
+    # that the event pair around the back-to-back launches brackets GPU work only (an
+    # event pair per launch would add its own gaps).
+    torch.cuda._sleep(int(2.4e9 * 2e-3 + reps * 2.4e9 * 100e-6))
+    a.record(st)
+    for i in range(reps):
         fn(i)
-        b.record(st)
+    b.record(st)
     torch.cuda.synchronize()
-    return statistics.mean(a.elapsed_time(b) for a, b in evs) * 1e-3
+    return a.elapsed_time(b) * 1e-3 / reps
 
 
 # ------------------------------------------------------------------ prefill
@@ -171,6 +174,8 @@ def bench_decode(cfg, steps, warmup, copies=8):
     graphs = [pipeline.DecodeGraph(states[i], *sets[i], hc, cfg.bs, lb, W.IDX_SCALE, W.FLOOR,
                                    W.SIGMA, cfg.cap, cfg.cap, scale) for i in range(len(sets))]
     t_step = time_steps(lambda i: graphs[i % len(graphs)].replay(), max(steps, 20), warmup)
+    # the same replays timed on the device (the host enqueues ahead of the GPU)
+    t_step_dev = time_kernel(lambda i: graphs[i % len(graphs)].replay(), max(steps, 20))
 
     def attn(i):
         qq, kk, vv, _, _ = sets[i % len(sets)]
@@ -178,7 +183,7 @@ def bench_decode(cfg, steps, warmup, copies=8):
 
     t_attn = time_kernel(attn, max(steps, 20))
     return dict(kv_bytes=kv_bytes, qo_bytes=qo_bytes, kbar_bytes=kbar_bytes, t_step=t_step,
-                t_step_eager=t_step_eager,
+                t_step_eager=t_step_eager, t_step_dev=t_step_dev,
                 t_attn=t_attn, data=d, routing=(idx, bias, valid))
 
 
@@ -405,7 +410,10 @@ def main():
                                             PEAK_BF16_TFLOPS, 4)},
         "decode": {"workload": W.DECODE_B8.name, "us_per_step": round(dec["t_step"] * 1e6, 2),
                    "us_per_step_eager": round(dec["t_step_eager"] * 1e6, 2),
+                   "us_per_step_device": round(dec["t_step_dev"] * 1e6, 2),
                    "step": "routing + attention, replayed as one HIP graph per cache set",
+                   "step_hbm_gbs_device": round((dec["kv_bytes"] + dec["qo_bytes"] +
+                                                 dec["kbar_bytes"]) / dec["t_step_dev"] / 1e9, 1),
                    "roofline": {"bound": "hbm", "achieved": round(dec_gbs, 1),
                                 "peak": PEAK_HBM_GBS, "unit": "GB/s",
                                 "frac": round(dec_gbs / PEAK_HBM_GBS, 4),

@@ -179,6 +179,37 @@ int dash_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
                      float scale, int nsplit, void* workspace, int64_t workspace_bytes,
                      void* stream);
 
+/* Workspace bytes dash_decode_step needs (the window partials). */
+int dash_decode_step_workspace_size(int B, int H, int D, int block_size, int local_window,
+                                    int64_t* bytes);
+
+/*
+ * One decode step: dash_decode_route followed by dash_attn_decode of its routing for
+ * the query at seq_lens[b]-1, the way _dash_decode_forward (modeling_deepseekv2.py:
+ * 454-500) chains _infer_route_select and _decode_attend.  The router arguments are
+ * those of dash_decode_route (idx/bias/valid/z are its outputs, [B, Kout]); the
+ * attention arguments those of dash_attn_decode with K = Kout.  The window part of the
+ * attention runs in the router's launch (it does not depend on the routing), the routed
+ * blocks and the merge in a second launch.  Kout <= 16; ceil((local_window + block_size
+ * - 1) / 32) + Kout <= 64.  workspace: dash_decode_step_workspace_size bytes, 16-byte
+ * aligned.
+ */
+int dash_decode_step(const float* idx_q, int64_t iq_sb, const float* idx_k, int64_t ik_sb,
+                     int64_t ik_st, int64_t ik_sp, const int32_t* block_table,
+                     int64_t table_stride, int page_size, const int32_t* seq_lens, int S,
+                     const float* head_cls, int refresh_tail, float* kbar, int64_t kb_sb,
+                     int nblk_cap, const uint8_t* cand, int64_t cand_stride, int d,
+                     int local_blocks, float idx_scale, float floor_p, float sigma, int K,
+                     int topm, int Kout, int32_t* idx, float* bias, uint8_t* valid, float* z,
+                     int64_t z_stride,
+                     const void* q, int64_t q_sb, int64_t q_sh,
+                     const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t k_sp,
+                     const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t v_sp,
+                     void* out, int out_bf16, int64_t o_sb, int64_t o_sh,
+                     float* lse, int64_t lse_sb, int64_t lse_sh,
+                     int B, int H, int D, int block_size, int local_window, float scale,
+                     void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

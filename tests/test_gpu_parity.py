@@ -527,6 +527,59 @@ def test_decode_step_pipeline_matches_oracle():
     _close(out, ref[:, :, 0], "decode step")
 
 
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("bs", [32, 64, 128])
+def test_decode_step_fused_matches_two_launch_path(paged, bs):
+    """The fused decode step (window attention beside the router, routed blocks and
+    merge in a second launch) against decode_route + attn_decode: routing bit for bit,
+    outputs to fp32 rounding (the window is cut into 32-key pieces instead of blocks)."""
+    from ananta_ocr_amd import pipeline
+    H, d, lw, K = 3, 128, 512, 8
+    lens = [2900, 1, 33, 511, 1300]
+    B, S = len(lens), max(lens)
+    g = _gen(470 + bs + int(paged))
+    k = (torch.randn(B, H, S, 128, generator=g) / math.sqrt(128)).bfloat16()
+    v = torch.randn(B, H, S, 128, generator=g).bfloat16()
+    q = (torch.randn(B, H, 128, generator=g) * 2).bfloat16()
+    ik = torch.randn(B, S, d, generator=g)
+    iq = torch.randn(B, d, generator=g)
+    hc = torch.randn(d, generator=g) * 0.1
+    nblk = (S + bs - 1) // bs
+    kw = dict(seq_lens=torch.tensor(lens, dtype=torch.int32).to(DEV))
+    if paged:
+        npg = [(L + bs - 1) // bs for L in lens]
+        perm = torch.randperm(sum(npg), generator=g)
+        table = torch.zeros(B, max(npg), dtype=torch.int32)
+        kp = torch.zeros(sum(npg), bs, H, 128, dtype=torch.bfloat16)
+        vp = torch.zeros_like(kp)
+        ikp = torch.zeros(sum(npg), bs, d)
+        o = 0
+        for b in range(B):
+            for pg in range(npg[b]):
+                phys = int(perm[o + pg])
+                table[b, pg] = phys
+                seg = slice(pg * bs, min((pg + 1) * bs, lens[b]))
+                n = seg.stop - seg.start
+                kp[phys, :n] = k[b, :, seg].transpose(0, 1)
+                vp[phys, :n] = v[b, :, seg].transpose(0, 1)
+                ikp[phys, :n] = ik[b, seg]
+            o += npg[b]
+        kd, vd, ikd = kp.to(DEV), vp.to(DEV), ikp.to(DEV)
+        kw.update(block_table=table.to(DEV), page_size=bs)
+        nblk = max(npg)
+    else:
+        kd, vd, ikd = k.to(DEV), v.to(DEV), ik.to(DEV)
+    st = pipeline.init_decode_state(ikd, hc.to(DEV), bs, nblk, **kw)
+    args = (hc.to(DEV), bs, lw // bs, W.IDX_SCALE * 50, W.FLOOR, W.SIGMA, K, K, 1 / math.sqrt(128))
+    out_f, (ti_f, bi_f, va_f) = pipeline.decode_step(st, q.to(DEV), kd, vd, iq.to(DEV), ikd, *args,
+                                                     return_routing=True, fused=True, **kw)
+    out_s, (ti_s, bi_s, va_s) = pipeline.decode_step(st, q.to(DEV), kd, vd, iq.to(DEV), ikd, *args,
+                                                     return_routing=True, fused=False, **kw)
+    assert torch.equal(ti_f, ti_s) and torch.equal(va_f, va_s) and torch.equal(bi_f, bi_s)
+    assert va_f.any()
+    torch.testing.assert_close(out_f, out_s, atol=2e-5, rtol=2e-5)
+
+
 def test_decode_graph_replays_match_eager():
     """decode_step captured in a HIP graph: every replay (with eager work and
     synchronisations between replays, and after the query buffer is rewritten in
