@@ -212,7 +212,19 @@ __device__ __forceinline__ void dc_merge(const DecodeArgs& a, int b, int h, int 
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const float inv = L > 0.f ? 1.f / L : 0.f;
   float acc0 = 0.f, acc1 = 0.f;
-  for (int s = 0; s < n; ++s) {
+  // eight partials' loads in flight at a time
+  int s = 0;
+  for (; s + 8 <= n; s += 8) {
+    float2 ov[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) ov[u] = *(const float2*)(part_at(s + u) + lane * 2);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      acc0 += ov[u].x * sW[s + u];
+      acc1 += ov[u].y * sW[s + u];
+    }
+  }
+  for (; s < n; ++s) {
     const float2 ov = *(const float2*)(part_at(s) + lane * 2);
     acc0 += ov.x * sW[s];
     acc1 += ov.y * sW[s];
