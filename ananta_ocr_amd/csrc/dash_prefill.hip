@@ -1059,7 +1059,10 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
   auto pair_id = [&](int j) {
     return wv * 32 + 128 * j + n < npairs ? pid_raw[j] : pid_first;
   };
-  // a round's per-query inputs: Q rows, routed bias, segment start
+  // a round's per-query inputs: Q rows, routed bias, segment start.  The Q rows
+  // of the wavefront's 32 pairs are loaded row-contiguously, 16 lanes per row and
+  // 4 rows per load (q[kk] of lane l: 16 bytes l % 16 of the row of pair 4 kk +
+  // l / 16), and rearranged into the MFMA operand layout through LDS per round.
   struct RoundIn {
     bf16x8 q[D / 16];
     float bias;
@@ -1068,8 +1071,10 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
   auto load_round = [&](int pid, RoundIn& in) {
     const int t = pid / a.K;
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk)
-      in.q[kk] = *(const bf16x8*)(qb + (int64_t)t * a.q_st + kk * 16 + hl * 8);
+    for (int kk = 0; kk < D / 16; ++kk) {
+      const int tk = __shfl(t, 4 * kk + (lane >> 4), kWave);
+      in.q[kk] = *(const bf16x8*)(qb + (int64_t)tk * a.q_st + (lane & 15) * 8);
+    }
     in.bias = a.bias[r0 * a.K + pid];
     in.km = a.kmin ? a.kmin[r0 + t] : 0;
   };
@@ -1088,7 +1093,27 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
   __syncthreads();
   const bf16x2 ones = {(bf16)1.f, (bf16)1.f};
 
+  bf16* const st = sTr + wv * 16 * D;
   auto round = [&](int j, const RoundIn& cur) {
+    // Q^T operand of this lane's pair: rows pass through the wavefront's 16-row LDS
+    // scratch in two pieces, 16-byte chunk c of row r at slot c ^ (r % 16)
+    bf16x8 qop[D / 16];
+#pragma unroll
+    for (int piece = 0; piece < 2; ++piece) {
+#pragma unroll
+      for (int kk = 4 * piece; kk < 4 * piece + 4; ++kk) {
+        const int rr = 4 * (kk - 4 * piece) + (lane >> 4);
+        *(bf16x8*)(st + (rr * 16 + ((lane & 15) ^ rr)) * 8) = cur.q[kk];
+      }
+      wave_lds_sync();
+      if ((n >> 4) == piece) {
+        const int rr = n & 15;
+#pragma unroll
+        for (int kk = 0; kk < D / 16; ++kk)
+          qop[kk] = *(const bf16x8*)(st + (rr * 16 + ((2 * kk + hl) ^ rr)) * 8);
+      }
+      wave_lds_sync();
+    }
     const int pid_cur = pids[j];
     const bool active = wv * 32 + 128 * j + n < npairs;
     const int t = pid_cur / a.K;
@@ -1106,7 +1131,7 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
       if (32 * hf >= nkeys) continue;
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk)
-        s[hf] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(sKs, 32 * hf + n, kk, hl), cur.q[kk],
+        s[hf] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(sKs, 32 * hf + n, kk, hl), qop[kk],
                                                         s[hf], 0, 0, 0);
     }
     float mraw = -INFINITY;
@@ -1157,7 +1182,6 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
     // rows.  Rows of lanes past the chunk's pair count are written too: their
     // positions belong to this chunk and are never read.
     const int64_t pw = part_row(a, (int64_t)(pb + ch) * kPfCH + wv * 32 + 128 * j, h);
-    bf16* const st = sTr + wv * 16 * D;
 #pragma unroll
     for (int piece = 0; piece < 2; ++piece) {
       if ((n >> 4) == piece) {
