@@ -359,45 +359,12 @@ __global__ __launch_bounds__(256) void blockmax_kernel(
 constexpr int kMaxM = 16;
 
 
-// 1.5-entmax over M values sorted in descending order, bit-for-bit the fp32
-// sequence of dash_attention.py:623-647 on the CPU: X = (x - max)/2, cumsums
-// accumulated in double and rounded to fp32, every other operation a single
-// correctly rounded fp32 operation (no contraction).
-__device__ __forceinline__ void entmax15_sorted(const float (&x)[kMaxM], int M,
-                                                float (&p)[kMaxM]) {
-#pragma clang fp contract(off)
-  float X[kMaxM], tau[kMaxM];
-  double cs = 0.0, cs2 = 0.0;
-  int support = 0;
-#pragma unroll
-  for (int m = 0; m < kMaxM; ++m) {
-    X[m] = __fdiv_rn(__fsub_rn(x[m], x[0]), 2.0f);
-    tau[m] = 0.f;
-    if (m < M) {
-      const float rho = (float)(m + 1);
-      cs += (double)X[m];
-      cs2 += (double)__fmul_rn(X[m], X[m]);
-      const float mean = __fdiv_rn((float)cs, rho);
-      const float mean_sq = __fdiv_rn((float)cs2, rho);
-      const float ss = __fmul_rn(rho, __fsub_rn(mean_sq, __fmul_rn(mean, mean)));
-      const float delta = __fdiv_rn(__fsub_rn(1.0f, ss), rho);
-      const float delta_nz = delta > 0.f ? delta : 0.f;
-      tau[m] = __fsub_rn(mean, __fsqrt_rn(delta_nz));
-      if (tau[m] <= X[m]) ++support;
-    }
-  }
-  support = max(support, 1);
-  float tau_star = tau[0];
-#pragma unroll
-  for (int m = 1; m < kMaxM; ++m)
-    if (m == support - 1) tau_star = tau[m];
-#pragma unroll
-  for (int m = 0; m < kMaxM; ++m) {
-    const float t = __fsub_rn(X[m], tau_star);
-    const float c = t > 0.f ? t : 0.f;
-    p[m] = (m < M) ? __fmul_rn(c, c) : 0.f;
-  }
-}
+// 1.5-entmax over M values sorted in descending order follows the fp32 sequence
+// of dash_attention.py:623-647 on the CPU: X = (x - max)/2, cumsums accumulated in
+// double and rounded to fp32, every other operation a single correctly rounded fp32
+// operation (no contraction).  The kernels below hold entry m on lane m, each lane
+// forming its own prefix sums in the serial order, so the result is the serial one
+// bit for bit.
 
 // Order-preserving key of a finite float: larger value -> larger key; -0 and +0
 // share a key (they compare equal).
@@ -479,8 +446,8 @@ __device__ __forceinline__ uint32_t kth_key(const uint32_t (&h)[NV], int M, uint
 //     blocks) run the same bisection over all their entries.
 //  The entries above T and the lowest-id entries at T form the set, parked in
 //  LDS.
-//  Phase 2, wavefront 0 with one row per lane: bitonic sort of the M keys,
-//  1.5-entmax, first K, centred log-prior bias.
+//  Phase 2, each wavefront for its own rows, 16 lanes per row: rank sort of the M
+//  keys, 1.5-entmax with entry m on lane m, first K, centred log-prior bias.
 constexpr int kRtRowsPerWave = 4;
 constexpr int kRtWaves = 4;
 constexpr int kRtRows = kRtRowsPerWave * kRtWaves;
@@ -618,72 +585,98 @@ __global__ __launch_bounds__(kRtWaves * kWave) void route_kernel(
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
-  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- phase 2: wavefront 0, one row per lane ----
-  if (wv != 0 || lane >= kRtRows) return;
-  const int row = wg_row0 + lane;
-  if (row >= rows) return;
-  const int M = s_M[lane];
-  uint64_t k[kMaxM];
+  // ---- phase 2: each wavefront finishes its own rows, 16 lanes per row (lane
+  // group gi = row rr, lane m = entry m): rank sort, then 1.5-entmax with entry m
+  // on lane m (each lane forms its prefix sums in the serial order, so the result
+  // is the serial one bit for bit), first K, centred log-prior bias ----
+  {
+#pragma clang fp contract(off)
+  const int gi = lane >> 4, m = lane & 15, gbase = lane & ~15;
+  const bool row_ok = gi < nrow;
+  const int sr = wv * kRtRowsPerWave + gi;
+  const int row = row0 + gi;
+  const int M = row_ok ? s_M[sr] : 0;
+  const uint64_t key = m < M ? s_sel[sr][m] : 0ull;
+  int rank = 0;
 #pragma unroll
-  for (int m = 0; m < kMaxM; ++m) k[m] = m < M ? s_sel[lane][m] : 0ull;
-  // bitonic sort, descending
+  for (int j = 0; j < kMaxM; ++j) {
+    const uint64_t kj = row_ok ? s_sel[sr][j] : 0ull;
+    rank += (j < M && kj > key) ? 1 : 0;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (m < M) s_sel[sr][rank] = key;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const uint64_t ks = m < M ? s_sel[sr][m] : 0ull;     // entry m of the descending order
+  const uint32_t kh = (uint32_t)(ks >> 32), kl = (uint32_t)ks;
+  const float xv = m < M ? ord_key_inv(kh) : 0.f;
+  const int sel_id = 0xffff - (int)((kl >> 1) & 0xffff);
+  const bool sel_c = (kl & 1u) != 0;
+  const float x0 = __shfl(xv, gbase, kWave);
+  const float X = __fdiv_rn(__fsub_rn(xv, x0), 2.0f);
+  double cs = 0.0, cs2 = 0.0;
 #pragma unroll
-  for (int kk = 2; kk <= kMaxM; kk <<= 1) {
-#pragma unroll
-    for (int j = kk >> 1; j > 0; j >>= 1) {
-#pragma unroll
-      for (int i = 0; i < kMaxM; ++i) {
-        const int l = i ^ j;
-        if (l > i) {
-          const uint64_t a = k[i], b = k[l];
-          const bool sw = ((i & kk) == 0) ? (a < b) : (a > b);
-          k[i] = sw ? b : a;
-          k[l] = sw ? a : b;
-        }
-      }
+  for (int j = 0; j < kMaxM; ++j) {
+    const float Xj = __shfl(X, gbase + j, kWave);
+    if (j <= m) {
+      cs += (double)Xj;
+      cs2 += (double)__fmul_rn(Xj, Xj);
     }
   }
-  float sel_v[kMaxM];
-  int sel_id[kMaxM];
-  bool sel_c[kMaxM];
-#pragma unroll
-  for (int m = 0; m < kMaxM; ++m) {
-    const uint32_t h = (uint32_t)(k[m] >> 32), l = (uint32_t)k[m];
-    sel_v[m] = m < M ? ord_key_inv(h) : 0.f;
-    sel_id[m] = 0xffff - (int)((l >> 1) & 0xffff);
-    sel_c[m] = (l & 1u) != 0;
+  const int Me = max(M, 1);                  // entmax over at least one entry
+  float tau = 0.f;
+  bool sup = false;
+  if (m < Me) {
+    const float rho = (float)(m + 1);
+    const float mean = __fdiv_rn((float)cs, rho);
+    const float mean_sq = __fdiv_rn((float)cs2, rho);
+    const float ss = __fmul_rn(rho, __fsub_rn(mean_sq, __fmul_rn(mean, mean)));
+    const float delta = __fdiv_rn(__fsub_rn(1.0f, ss), rho);
+    const float delta_nz = delta > 0.f ? delta : 0.f;
+    tau = __fsub_rn(mean, __fsqrt_rn(delta_nz));
+    sup = tau <= X;
   }
+  const uint32_t grp = (uint32_t)(__ballot(sup) >> gbase) & 0xffffu;
+  const int support = max(__popc(grp), 1);
+  const float tau_star = __shfl(tau, gbase + support - 1, kWave);
+  const float tt = __fsub_rn(X, tau_star);
+  const float cc = tt > 0.f ? tt : 0.f;
+  const float prior = m < M ? __fmul_rn(cc, cc) : 0.f;
+  const float logp = logf(fmaxf(prior, floor_p));
   const int Kp = max(1, min(K, M));
-  float prior[kMaxM];
-  entmax15_sorted(sel_v, max(M, 1), prior);
-  float logp[kMaxM];
+  // mean log-prior of the kept candidate slots, summed in slot order
+  const uint32_t keep = (uint32_t)(__ballot(m < Kp && m < M && sel_c) >> gbase) & 0xffffu;
   float musum = 0.f;
   int cnt = 0;
 #pragma unroll
-  for (int m = 0; m < kMaxM; ++m) {
-    logp[m] = logf(fmaxf(prior[m], floor_p));
-    if (m < Kp && m < M && sel_c[m]) { musum += logp[m]; ++cnt; }
+  for (int j = 0; j < kMaxM; ++j) {
+    const float lj = __shfl(logp, gbase + j, kWave);
+    if ((keep >> j) & 1u) { musum += lj; ++cnt; }
   }
   const float mu = musum / (float)max(cnt, 1);
+  if (!row_ok) return;
   int32_t* io = idx_out + (int64_t)row * Kout;
   float* bo = bias_out + (int64_t)row * Kout;
   uint8_t* vo = valid_out ? valid_out + (int64_t)row * Kout : nullptr;
-#pragma unroll
-  for (int m = 0; m < kMaxM; ++m) {
-    if (m < Kout) {
-      const bool in = m < Kp && m < M;
-      const bool va = in && sel_c[m];
-      io[m] = in ? sel_id[m] : -1;
-      bo[m] = va ? (logp[m] - mu) * inv_sigma : 0.f;
-      if (vo) vo[m] = va ? 1 : 0;
-    }
+  if (m < Kout) {
+    const bool in = m < Kp && m < M;
+    const bool va = in && sel_c;
+    io[m] = in ? sel_id : -1;
+    bo[m] = va ? (logp - mu) * inv_sigma : 0.f;
+    if (vo) vo[m] = va ? 1 : 0;
   }
-  for (int m = kMaxM; m < Kout; ++m) {
-    io[m] = -1;
-    bo[m] = 0.f;
-    if (vo) vo[m] = 0;
+  for (int mm = kMaxM + m; mm < Kout; mm += kMaxM) {
+    io[mm] = -1;
+    bo[mm] = 0.f;
+    if (vo) vo[mm] = 0;
+  }
   }
 }
 
@@ -821,9 +814,8 @@ struct DecodeRouteArgs {
 };
 
 // 1.5-entmax of the sorted top M, the log-prior bias and the output slots of one
-// decode row, by one wavefront with lane m holding entry m: the operations of
-// entmax15_sorted in the same order (each lane forms its own prefix sums
-// serially), so the result is bit-for-bit the serial one.
+// decode row, by one wavefront with lane m holding entry m (each lane forms its own
+// prefix sums serially), so the result is bit-for-bit the serial one.
 __device__ __forceinline__ void decode_route_finish(const DecodeRouteArgs& a, int b, int lane, int M,
                                                     int Kp, const float* s_selv, const int* s_selk) {
 #pragma clang fp contract(off)

@@ -34,7 +34,11 @@ def _i32(t):
 
 
 def _u8(t):
-    return None if t is None else t.to(torch.uint8).contiguous()
+    if t is None:
+        return None
+    if t.dtype == torch.bool:                  # same bytes (0/1): no conversion kernel
+        return t.contiguous().view(torch.uint8)
+    return t.to(torch.uint8).contiguous()
 
 
 def _rows(x):
@@ -73,7 +77,12 @@ def kbar(idx_k, head_cls, block_size, cu_seqlens=None, seq_lens=None, nblk_cap=N
     if nblk_cap is None:
         nblk_cap = (S + block_size - 1) // block_size
     if out is None:
-        out = torch.zeros(B, nblk_cap, d, dtype=torch.float32, device=idx_k.device)
+        # every block of every sequence has tokens (and is written) only for full-length
+        # contiguous sequences; otherwise the rows past a sequence's blocks stay zero
+        full = cu is None and seq_lens is None and block_table is None and not tail_only \
+            and nblk_cap == (S + block_size - 1) // block_size
+        out = (torch.empty if full else torch.zeros)(B, nblk_cap, d, dtype=torch.float32,
+                                                     device=idx_k.device)
     hc = head_cls.float().contiguous()
     bt = _i32(block_table)
     st_ = lib.dash_kbar(_ptr(idx_k), sb, st, sp, _ptr(cu), _ptr(seq_lens), _ptr(bt),
@@ -163,7 +172,7 @@ def route(z, cand, idx_scale, floor, sigma, K, topm, row_nblk=None, width=None):
                          float(sigma), int(K), int(topm), Kp, _ptr(idx), _ptr(bias),
                          _ptr(valid), _stream())
     _lib.check(st_, "dash_route")
-    return idx.view(*lead, Kp), bias.view(*lead, Kp), valid.view(*lead, Kp).bool()
+    return idx.view(*lead, Kp), bias.view(*lead, Kp), valid.view(*lead, Kp).view(torch.bool)
 
 
 DENSE_THRESHOLD = 32   # of the 128 queries of a tile; below it a routed block goes sparse
@@ -351,7 +360,8 @@ def decode_route(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, i
         float(idx_scale), float(floor), float(sigma), int(K), int(topm), Kw, _ptr(idx),
         _ptr(bias), _ptr(valid), _ptr(z), z.stride(0), _stream())
     _lib.check(st_, "dash_decode_route")
-    res = (idx[:, None], bias[:, None], valid[:, None].to(valid_dtype))
+    vd = valid[:, None].view(torch.bool) if valid_dtype == torch.bool else valid[:, None].to(valid_dtype)
+    res = (idx[:, None], bias[:, None], vd)
     return res + (z,) if return_scores else res
 
 
