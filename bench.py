@@ -302,7 +302,7 @@ def cpu_decode_baseline(res, cfg, reps=3):
 # WRITE_SIZE), each divided by the counter's reading for a 256 MiB device copy
 # (FETCH_SIZE reads 0.500 of the copied bytes, WRITE_SIZE 1.000).  Re-measure when
 # the kernels change.
-PREFILL_ATTN_TRAFFIC_BYTES = int((1664.4 + 776.1) * 1e6)
+PREFILL_ATTN_TRAFFIC_BYTES = int((1659.8 + 703.1) * 1e6)
 # Executed bf16 MFMA FLOP of one prefill attention launch (tile + sparse kernels), from
 # SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 in a counter run of ``bench.py --traffic-probe``
 # (re-measure when the kernels change).
