@@ -269,6 +269,174 @@ __global__ __launch_bounds__(256) void scores_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Block scores for d = 128 on the matrix cores.  Every fp32 operand is split into
+// three bf16 parts x = x_h + x_m + x_l (each part the round-to-nearest of what the
+// previous ones leave; together they hold the 24-bit significand), and q.k is
+// the fp32-accumulated sum of the six products with x_i y_j for i + j <= 2
+// (h = 0, m = 1, l = 2); the dropped ones are below 2^-24 of the product, so the
+// result is an fp32-accurate dot product.  A work-group covers 128 query rows x 64
+// blocks: the 64 k_bar rows are split once into three swizzled LDS planes (16-byte
+// chunk c of block row n at slot c ^ (n % 16)), and each wavefront multiplies its
+// 32 rows, split in registers 8 dims at a time, with v_mfma_f32_32x32x16_bf16.
+// Tiles beyond every row's causal limit only write the sentinel.
+// ---------------------------------------------------------------------------
+constexpr int kSmRows = 128, kSmBlk = 64;
+
+__device__ __forceinline__ void split3(float x, __bf16& h, __bf16& m, __bf16& l) {
+  h = (__bf16)x;
+  const float r1 = x - (float)h;
+  m = (__bf16)r1;
+  l = (__bf16)(r1 - (float)m);
+}
+
+__global__ __launch_bounds__(256) void scores_mfma_kernel(
+    const float* __restrict__ idx_q, SeqLayout lay_q, const int32_t* __restrict__ cu_q, int Lq,
+    const int32_t* __restrict__ q_pos, const float* __restrict__ kbar, int64_t kb_sb,
+    const int32_t* __restrict__ cu_k, const int32_t* __restrict__ lens_k, int S, int bs,
+    int local_blocks, int nblk_cap, float inv_sqrt_d, float* __restrict__ z, int64_t z_stride) {
+  __shared__ __attribute__((aligned(16))) bf16 sK[3][kSmBlk * 128];
+  __shared__ int sLim[kSmRows];
+  const int b = blockIdx.z;
+  const int nq = cu_q ? (cu_q[b + 1] - cu_q[b]) : Lq;
+  const int r0 = blockIdx.x * kSmRows;
+  const int c0 = blockIdx.y * kSmBlk;
+  if (r0 >= nq) return;
+  const int klen = seq_length(cu_k, lens_k, b, S);
+  const int nblk_b = (klen + bs - 1) / bs;
+  const int tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
+  int my_max = INT_MIN;
+  if (tid < kSmRows) {
+    const int r = r0 + tid;
+    int lim = INT_MIN;
+    if (r < nq) {
+      const int pos = q_pos ? q_pos[token_row(cu_q, b, r, Lq)] : r;
+      lim = (pos >= 0 ? pos / bs : -((-pos + bs - 1) / bs)) - local_blocks;
+    }
+    sLim[tid] = lim;
+    my_max = lim;
+  }
+  if (!__syncthreads_or(c0 <= my_max && c0 < nblk_b)) {
+    for (int e = tid; e < kSmRows * kSmBlk; e += 256) {
+      const int r = r0 + e / kSmBlk, c = c0 + e % kSmBlk;
+      if (r < nq && c < nblk_cap) z[token_row(cu_q, b, r, Lq) * z_stride + c] = kScoreNeg;
+    }
+    return;
+  }
+  // this wavefront's 32 query rows: lane (m, half) holds dims 16 kk + 8 half .. +7;
+  // its 64 dims are loaded now, in flight during the k_bar split
+  const int mrow = lane & 31, half = lane >> 5;
+  const int rq = min(r0 + wv * 32 + mrow, nq - 1);
+  const float* qr = idx_q + lay_q.row(b, rq) + 8 * half;
+  float4 qv[16];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    qv[2 * kk] = *(const float4*)(qr + 16 * kk);
+    qv[2 * kk + 1] = *(const float4*)(qr + 16 * kk + 4);
+  }
+  // the 64 k_bar rows, split into the three planes (rows past nblk_cap are zero)
+  float4 kv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int e = (tid + 256 * j) * 4;          // element of the 64 x 128 tile
+    const int n = e / 128, k = e % 128;
+    kv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c0 + n < nblk_cap) kv[j] = *(const float4*)(kbar + (int64_t)b * kb_sb + (int64_t)(c0 + n) * 128 + k);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int e = (tid + 256 * j) * 4;
+    const int n = e / 128, k = e % 128;
+    const float4 v = kv[j];
+    const float xs[4] = {v.x, v.y, v.z, v.w};
+    bf16x4 ph, pm, pl;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      __bf16 h, m, l;
+      split3(xs[u], h, m, l);
+      ph[u] = h; pm[u] = m; pl[u] = l;
+    }
+    const int off = n * 128 + (((k >> 3) ^ (n & 15)) << 3) + (k & 7);
+    *(bf16x4*)(&sK[0][off]) = ph;
+    *(bf16x4*)(&sK[1][off]) = pm;
+    *(bf16x4*)(&sK[2][off]) = pl;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(qv[i].x), "+v"(qv[i].y), "+v"(qv[i].z), "+v"(qv[i].w));
+  floatx16 acc[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    const float4 qa = qv[2 * kk], qb = qv[2 * kk + 1];
+    const float xs[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    bf16x8 ah, am, al;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      __bf16 h, m, l;
+      split3(xs[u], h, m, l);
+      ah[u] = h; am[u] = m; al[u] = l;
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int n = t * 32 + mrow;
+      const int off = n * 128 + (((2 * kk + half) ^ (n & 15)) << 3);
+      const bf16x8 bh = *(const bf16x8*)(&sK[0][off]);
+      const bf16x8 bm = *(const bf16x8*)(&sK[1][off]);
+      const bf16x8 bl = *(const bf16x8*)(&sK[2][off]);
+      // smallest terms first
+      acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bm, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bm, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, acc[t], 0, 0, 0);
+    }
+  }
+  // C layout: lane l holds block column l % 32 of each 32-block tile, rows
+  // 8 (i / 4) + 4 (l / 32) + i % 4.  The wavefront's 32 x 64 scores pass through
+  // its 8 KB of the (now idle) k_bar planes, so that each store writes four whole
+  // 256-byte row pieces.
+  __syncthreads();                         // every wavefront is done with the planes
+  float* const so = (float*)&sK[0][0] + wv * 32 * kSmBlk;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int cl = t * 32 + mrow, c = c0 + cl;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int rr = 8 * (i >> 2) + 4 * half + (i & 3);
+      float v = kScoreNeg;
+      if (c <= sLim[wv * 32 + rr] && c < nblk_b)
+        v = fminf(fmaxf(acc[t][i] * inv_sqrt_d, -kActClamp), kActClamp);
+      so[rr * kSmBlk + cl] = v;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int cq = (lane & 15) * 4;          // four columns per lane
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int rr = 4 * k + (lane >> 4);
+    const int r = r0 + wv * 32 + rr;
+    const float4 v = *(const float4*)(so + rr * kSmBlk + cq);
+    if (r < nq) {
+      float* zr = z + token_row(cu_q, b, r, Lq) * z_stride + c0 + cq;
+      if (c0 + cq + 3 < nblk_cap && ((uintptr_t)zr & 15) == 0) {
+        *(float4*)zr = v;
+      } else {
+        const float vs[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (c0 + cq + u < nblk_cap) zr[u] = vs[u];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Indexer stage-0 block scores: per-block max of q.k_j over keys j < ls(t)
 // (ls = pos - LW + 1), optionally j >= seg[t].  mode 0: torch form (clamp to
 // +-1e4, SCORE_NEG for empty blocks); mode 1: fused-kernel form (no clamp,
@@ -733,6 +901,13 @@ extern "C" int dash_block_scores(const float* idx_q, int64_t iq_sb, int64_t iq_s
   dim3 grid((Lq + kScTile - 1) / kScTile, (nblk_cap + kScTile - 1) / kScTile, B);
   const bool vec = d % kScK == 0 && (uintptr_t)idx_q % 16 == 0 && (uintptr_t)kbar % 16 == 0 &&
                    iq_sb % 4 == 0 && iq_st % 4 == 0 && kb_sb % 4 == 0;
+  if (vec && d == 128) {
+    dim3 g2((Lq + kSmRows - 1) / kSmRows, (nblk_cap + kSmBlk - 1) / kSmBlk, B);
+    hipLaunchKernelGGL(scores_mfma_kernel, g2, dim3(256), 0, (hipStream_t)stream, idx_q, lay, cu_q,
+                       Lq, q_pos, kbar, kb_sb, cu_k, lens_k, S, block_size, local_blocks, nblk_cap,
+                       (float)(1.0 / sqrt((double)d)), z, z_stride);
+    return launch_status();
+  }
   auto kern = vec ? scores_kernel<true> : scores_kernel<false>;
   hipLaunchKernelGGL(kern, grid, dim3(256), 0, (hipStream_t)stream, idx_q, lay, cu_q,
                      Lq, q_pos, kbar, kb_sb, cu_k, lens_k, S, d, block_size, local_blocks,

@@ -104,24 +104,27 @@ def block_scores(idx_q, kb, block_size, local_blocks, q_pos=None, cu_seqlens=Non
         idx_q = idx_q.contiguous()
     kb = kb.contiguous()
     B, nblk, d = kb.shape
+    # rows padded to whole 128-byte lines, so that the kernel's 64-block tiles write
+    # full lines (returned as a view of the first nblk columns)
+    zs = max(32, (nblk + 31) // 32 * 32)
     if cu_seqlens is not None:
         cu = _i32(cu_seqlens)
         T = idx_q.shape[-2]
         Lq = int((cu[1:] - cu[:-1]).max().item()) if B > 0 else 0
-        z = torch.empty(T, nblk, dtype=torch.float32, device=idx_q.device)
+        z = torch.empty(T, zs, dtype=torch.float32, device=idx_q.device)[:, :nblk]
         sb, st = 0, idx_q.stride(-2)
         Sk = Lq if S is None else S
     else:
         cu = None
         Lq = idx_q.shape[1]
-        z = torch.empty(B, Lq, nblk, dtype=torch.float32, device=idx_q.device)
+        z = torch.empty(B, Lq, zs, dtype=torch.float32, device=idx_q.device)[:, :, :nblk]
         sb, st = idx_q.stride(0), idx_q.stride(1)
         Sk = Lq if S is None else S
     qp = _i32(q_pos)
     lens = _i32(seq_lens)
     st_ = lib.dash_block_scores(_ptr(idx_q), sb, st, _ptr(cu), Lq, _ptr(qp), _ptr(kb),
                                 kb.stride(0), nblk, _ptr(cu), _ptr(lens), Sk, B, d, block_size,
-                                local_blocks, _ptr(z), nblk, _stream())
+                                local_blocks, _ptr(z), zs, _stream())
     _lib.check(st_, "dash_block_scores")
     return z
 
