@@ -1,0 +1,173 @@
+"""GPU parity at the workloads' full sizes: the 27,300-token prefill (block 64,
+window 1,024, cap 16, 5 % offset key blocks), the 16-document packed prefill
+(78,078 tokens for seed 4, block-diagonal varlen) and one layer of the 32-sequence
+paged decode (lengths 2,730..27,300, pages of 64 tokens in a random physical order).
+
+Every stage is checked against the CPU oracle on the same inputs: the block
+summaries and scores within fp32 tolerance, the routing bit-exact on the GPU's own
+scores, the attention on every query row (prefill) or sequence (decode) within the
+output tolerance.
+"""
+
+import math
+
+import pytest
+import torch
+
+from ananta_ocr_amd import ops, pipeline
+from ananta_ocr_amd import workloads as W
+from oracle import dash_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+ATOL, RTOL = 2e-2, 1e-2          # bf16 output, fp32 accumulation
+SCALE = 1 / math.sqrt(128)
+
+
+def _close(out, ref, what, tight=1.5e-2):
+    out = out.float().cpu()
+    ref = ref.float().cpu()
+    err = (out - ref).abs()
+    assert torch.all(err <= ATOL + RTOL * ref.abs()), f"{what}: max err {err.max().item()}"
+    assert err.max().item() <= tight * ref.abs().max().item() + 1e-6, \
+        f"{what}: max err {err.max().item():.3e}"
+
+
+def _scores_close(z, z_ref, what):
+    sent = z_ref < -5e8
+    assert torch.equal(z < -5e8, sent), f"{what}: sentinel pattern differs"
+    torch.testing.assert_close(z[~sent], z_ref[~sent], atol=2e-5, rtol=2e-5)
+
+
+def _route_equal(z, ti, bi, va, K, topm, what):
+    """GPU routing of z against the oracle routing of the same fp32 scores."""
+    t_r, b_r, v_r = O.infer_route_select(z, None, W.IDX_SCALE, W.FLOOR, W.SIGMA, K, topm)
+    kp = t_r.shape[-1]
+    assert torch.equal(va[..., :kp], v_r), f"{what}: valid differs"
+    mism = (ti[..., :kp] != t_r).nonzero()
+    assert mism.numel() == 0, f"{what}: routed ids differ at {mism[:5].tolist()}"
+    torch.testing.assert_close(bi[..., :kp], b_r, atol=2e-5, rtol=1e-5)
+    # slots past K' = min(K, M') are empty
+    assert bool((ti[..., kp:] == -1).all()) and not bool(va[..., kp:].any())
+    return t_r, b_r, v_r
+
+
+def test_prefill_27300_tokens_full_size():
+    cfg = W.PREFILL_27300
+    d = W.make_prefill(cfg)
+    S, lb = d["S"], cfg.lw // cfg.bs
+    hc = torch.zeros(128)
+    print(f"prefill {cfg.name}: S={S}", flush=True)
+    kb = ops.kbar(d["idx_k"].to(DEV), hc.to(DEV), cfg.bs)
+    z = ops.block_scores(d["idx_q"].to(DEV), kb, cfg.bs, lb)
+    ti, bi, va = ops.route(z, None, W.IDX_SCALE, W.FLOOR, W.SIGMA, cfg.cap, cfg.cap)
+    out = ops.attn_prefill(d["q"].to(DEV), d["k"].to(DEV), d["v"].to(DEV), ti, bi, va,
+                           cfg.bs, cfg.lw, SCALE)
+    kb_r, cv = O.kbar_headcls(d["idx_k"], hc, cfg.bs)
+    torch.testing.assert_close(kb.cpu(), kb_r, atol=1e-6, rtol=1e-5)
+    pos = torch.arange(S)[None]
+    z_r = O.block_scores_headcls(d["idx_q"], kb_r, cv, pos, cfg.bs, lb)
+    z = z.cpu()
+    _scores_close(z, z_r, "scores")
+    t_r, b_r, v_r = _route_equal(z, ti.cpu().long(), bi.cpu(), va.cpu(), cfg.cap, cfg.cap,
+                                 "route")
+    # the offset blocks must actually be routed (the workload's point)
+    assert int(v_r.sum()) > 0
+    ref = O.dense_attend(d["q"], d["k"], d["v"], t_r, b_r, v_r, cfg.bs, cfg.lw, SCALE,
+                         q_chunk=1024)
+    _close(out, ref, "prefill 27300")
+
+
+def test_packed_16_documents_full_size():
+    cfg = W.PACKED_16DOC
+    d = W.make_prefill(cfg)
+    cu = d["cu_list"]
+    T, lb = d["S"], cfg.lw // cfg.bs
+    hc = torch.zeros(128)
+    print(f"packed {cfg.name}: T={T}, docs={len(cu) - 1}", flush=True)
+    out, (ti, bi, va) = pipeline.prefill(
+        d["q"].to(DEV), d["k"].to(DEV), d["v"].to(DEV), d["idx_q"].to(DEV),
+        d["idx_k"].to(DEV), hc.to(DEV), cfg.bs, lb, W.IDX_SCALE, W.FLOOR, W.SIGMA,
+        cfg.cap, cfg.cap, SCALE, cu_seqlens=d["cu_seqlens"].to(DEV), return_routing=True)
+    # the GPU's own scores, to route them on the CPU as well
+    kb = ops.kbar(d["idx_k"].to(DEV), hc.to(DEV), cfg.bs, cu_seqlens=d["cu_seqlens"].to(DEV))
+    z = ops.block_scores(d["idx_q"].to(DEV), kb, cfg.bs, lb,
+                         cu_seqlens=d["cu_seqlens"].to(DEV)).cpu()
+    kb = kb.cpu()
+    out = out.cpu()
+    ti, bi, va = ti.cpu().long(), bi.cpu(), va.cpu()
+    for b in range(len(cu) - 1):
+        s0, s1 = cu[b], cu[b + 1]
+        L = s1 - s0
+        nblk = (L + cfg.bs - 1) // cfg.bs
+        kb_r, cv = O.kbar_headcls(d["idx_k"][:, s0:s1], hc, cfg.bs)
+        torch.testing.assert_close(kb[b:b + 1, :nblk], kb_r, atol=1e-6, rtol=1e-5)
+        zd = z[s0:s1, :nblk][None]
+        z_r = O.block_scores_headcls(d["idx_q"][:, s0:s1], kb_r, cv, torch.arange(L)[None],
+                                     cfg.bs, lb)
+        _scores_close(zd, z_r, f"scores doc {b}")
+        t_r, b_r, v_r = _route_equal(zd, ti[None, s0:s1], bi[None, s0:s1], va[None, s0:s1],
+                                     cfg.cap, cfg.cap, f"route doc {b}")
+        ref = O.dense_attend(d["q"][:, :, s0:s1], d["k"][:, :, s0:s1], d["v"][:, :, s0:s1],
+                             t_r, b_r, v_r, cfg.bs, cfg.lw, SCALE, q_chunk=1024)
+        _close(out[:, :, s0:s1], ref, f"document {b} ({L} tokens)")
+
+
+def _gather_pages(x, table_row, L):
+    """[pages, bs, ...] paged tensor -> [L, ...] contiguous rows of one sequence."""
+    npg = (L + x.shape[1] - 1) // x.shape[1]
+    return x[table_row[:npg].long()].reshape(-1, *x.shape[2:])[:L]
+
+
+def test_paged_decode_32_sequences_full_size():
+    cfg = W.PAGED_12L
+    lens, table = W.paged_layout(cfg)
+    d = W.make_paged_decode(cfg, DEV, 0, lens, table)
+    lb = cfg.lw // cfg.bs
+    hc = torch.zeros(128)
+    print(f"paged decode {cfg.name}: B={cfg.B}, tokens={int(lens.sum())}", flush=True)
+    st = pipeline.init_decode_state(d["idx_k"], hc.to(DEV), cfg.bs, table.shape[1],
+                                    seq_lens=d["seq_lens"], block_table=d["block_table"],
+                                    page_size=cfg.bs)
+    out, (ti, bi, va) = pipeline.decode_step(
+        st, d["q"], d["k"], d["v"], d["idx_q"], d["idx_k"], hc.to(DEV), cfg.bs, lb,
+        W.IDX_SCALE, W.FLOOR, W.SIGMA, cfg.cap, cfg.cap, SCALE, seq_lens=d["seq_lens"],
+        block_table=d["block_table"], page_size=cfg.bs, return_routing=True)
+    out = out.cpu()
+    ti, bi, va = ti.cpu().long(), bi.cpu(), va.cpu()
+    q, iq = d["q"].cpu(), d["idx_q"].cpu()
+    kp, vp, ikp = d["k"].cpu(), d["v"].cpu(), d["idx_k"].cpu()
+    del d, st
+    ties = 0
+    for b in range(cfg.B):
+        L = int(lens[b])
+        ik = _gather_pages(ikp, table[b], L)[None]                       # [1, L, d]
+        k = _gather_pages(kp, table[b], L).permute(1, 0, 2)[None]       # [1, H, L, D]
+        v = _gather_pages(vp, table[b], L).permute(1, 0, 2)[None]
+        kb_r, cv = O.kbar_headcls(ik, hc, cfg.bs)
+        z_r = O.block_scores_headcls(iq[b:b + 1], kb_r, cv, torch.tensor([[L - 1]]), cfg.bs,
+                                     lb)
+        t_r, b_r, v_r = O.infer_route_select(z_r, None, W.IDX_SCALE, W.FLOOR, W.SIGMA,
+                                             cfg.cap, cfg.cap)
+        kp_ = t_r.shape[-1]
+        g_ids = set(ti[b, 0, :kp_][va[b, 0, :kp_]].tolist())
+        r_ids = set(t_r[0, 0][v_r[0, 0]].tolist())
+        if g_ids != r_ids:
+            # scores are computed in a different order on the two sides: only blocks
+            # tied with the last selected one (to fp32 rounding) may swap
+            zz = z_r[0, 0]
+            edge = zz[t_r[0, 0, kp_ - 1]].item()
+            for c in g_ids ^ r_ids:
+                assert abs(zz[c].item() - edge) <= 1e-5 * abs(edge) + 1e-6, \
+                    f"sequence {b}: block {c} routed on one side only"
+            ties += 1
+        else:
+            assert torch.equal(ti[b, 0, :kp_], t_r[0, 0]), f"sequence {b}: slot order"
+            torch.testing.assert_close(bi[b, 0, :kp_], b_r[0, 0], atol=1e-4, rtol=1e-4)
+        # attention on the GPU's routing
+        ref = O.decode_attend(q[b:b + 1, :, None], k, v, ti[b:b + 1, :, :kp_],
+                              bi[b:b + 1, :, :kp_], va[b:b + 1, :, :kp_],
+                              torch.tensor([[L - 1]]), cfg.bs, cfg.lw, SCALE)
+        _close(out[b:b + 1], ref[:, :, 0], f"decode sequence {b} ({L} tokens)")
+    assert ties <= 2, f"{ties} sequences with near-tied routing"
