@@ -61,13 +61,13 @@ struct PrefillArgs {
   // hybrid plan (null kind: every routed block is processed by the tile kernel)
   uint8_t* kind;                       // [rows, K]: 0 skip, 1 tile (dense), 2 sparse
   int dense_threshold;
-  int32_t* blk_count;                  // [B, nblk_cap]  zero between calls
+  int32_t* blk_count;                  // [B, nblk_cap], cleared at the start of a call
   int32_t* tile_base;                  // [B, ntiles_cap, nblk_cap] offset of a tile's pairs
   int ntiles_cap;
   int32_t* blk_chunk;                  // [B, nblk_cap] first chunk of each block
   int32_t* num_chunks;                 // [B]
   int32_t* chunk_pref;                 // [B+1] prefix sums of num_chunks
-  int32_t* done;                       // arrival counter of the scan, zero between calls
+  int32_t* done;                       // arrival counter of the scan (follows blk_count)
   int B;
   int32_t* chunk_rec;                  // [B, chunk_cap, kRec] chunk records
   int chunk_cap;
@@ -197,8 +197,17 @@ __global__ __launch_bounds__(kPfTQ) void prefill_plan_kernel(PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// The block counters and the arrival counter are cleared at the start of every
+// call: a workspace reused by calls of other shapes holds other data there.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void prefill_clear_kernel(int32_t* p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// ---------------------------------------------------------------------------
 // Scan: per sequence, the first chunk of every block and the chunk record
-// headers.  Resets the block counters (they are zero between calls).
+// headers.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
   __shared__ int32_t sC[kPfMaxBlocks];
@@ -211,8 +220,8 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
   // two entries per thread
   int v0 = 0, v1 = 0;
   const int e0 = tid * 2, e1 = tid * 2 + 1;
-  if (e0 < a.nblk_cap) { v0 = e0 < nblk ? cnt[e0] : 0; cnt[e0] = 0; }
-  if (e1 < a.nblk_cap) { v1 = e1 < nblk ? cnt[e1] : 0; cnt[e1] = 0; }
+  if (e0 < nblk) v0 = cnt[e0];
+  if (e1 < nblk) v1 = cnt[e1];
   const int c0 = (v0 + kPfCH - 1) / kPfCH, c1 = (v1 + kPfCH - 1) / kPfCH;
   const int sc = c0 + c1;
   int ic = sc;
@@ -249,8 +258,7 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
       *(int2*)(rec + (int64_t)(sCh[c] + i) * kRec) = make_int2(c, min(kPfCH, n - i * kPfCH));
   }
   // The sequence that finishes last writes the prefix sums of the chunk counts
-  // (the sparse kernel maps its grid onto the real chunks with them) and resets
-  // the arrival counter.
+  // (the sparse kernel maps its grid onto the real chunks with them).
   if (sLast) {
     __threadfence();
     const int nseq = (int)gridDim.x;
@@ -276,10 +284,7 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
       if (i < nseq) a.chunk_pref[i + 1] = carry + wb + x;
       carry += tot;
     }
-    if (tid == 0) {
-      a.chunk_pref[0] = 0;
-      atomicExch(a.done, 0);
-    }
+    if (tid == 0) a.chunk_pref[0] = 0;
   }
 }
 
@@ -1322,6 +1327,9 @@ extern "C" int dash_attn_prefill(
     a.ppos = L.ppos;
     a.part_lse = (float*)(w + L.plse);
     a.part_o = (bf16*)(w + L.po);
+    const int ncount = (int)((L.done - L.count) / 4) + 1;     // block counters + arrival
+    hipLaunchKernelGGL(prefill_clear_kernel, dim3((ncount + 255) / 256), dim3(256), 0, st,
+                       a.blk_count, ncount);
     hipLaunchKernelGGL(prefill_plan_kernel, dim3(ntiles, B), dim3(kPfTQ), 0, st, a);
     hipLaunchKernelGGL(prefill_scan_kernel, dim3(B), dim3(1024), 0, st, a);
     hipLaunchKernelGGL(prefill_scatter_kernel, dim3(ntiles, B), dim3(kPfTQ), 0, st, a);

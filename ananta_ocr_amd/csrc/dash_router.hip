@@ -979,6 +979,7 @@ struct DecodeRouteArgs {
   const float* idx_k; SeqLayout lay_k;
   const int32_t* lens; int S;
   const float* head_cls; int refresh_tail;
+  int skip_tail;                     // the scores read no k_bar row past the last remote block
   float* kbar; int64_t kb_sb; int nblk_cap;
   const uint8_t* cand; int64_t cand_stride;
   int d, bs, local_blocks;
@@ -1045,7 +1046,17 @@ __device__ __forceinline__ void decode_route_finish(const DecodeRouteArgs& a, in
   }
 }
 
+// Modes of decode_route_body.  The tail block holds the query, so with a window of
+// at least one block (local_blocks >= 1) it is never a remote candidate: its summary
+// is needed only by later steps, and its refresh can run in another work-group
+// (kTailOnly) beside the routing, which then runs with refresh_tail = 0 and
+// skip_tail = 1 (no read of the tail row).
+constexpr int kRouteAll = 0;         // refresh (if refresh_tail), then route
+constexpr int kTailOnly = 1;         // refresh only
+
+template <int MODE = kRouteAll>
 __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int b) {
+  constexpr int mode = MODE;
   __shared__ __attribute__((aligned(16))) float s_q[256];
   __shared__ __attribute__((aligned(16))) float s_tail[256];
   __shared__ float s_aw[256];
@@ -1068,6 +1079,8 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
   const int qp = len - 1;
   const int lim = (qp >= 0 ? qp / a.bs : -1) - a.local_blocks;
   const int ct = nblk - 1;               // tail block
+  constexpr bool own_refresh = mode == kRouteAll;   // and a.refresh_tail, at each use
+  if (mode == kTailOnly && (!a.refresh_tail || nblk == 0)) return;
   if (nblk == 0) {
     for (int m = tid; m < a.Kout; m += kDrThreads) {
       a.idx[(int64_t)b * a.Kout + m] = -1;
@@ -1076,24 +1089,30 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
     }
     return;
   }
-  for (int i = tid; i < a.d; i += kDrThreads) s_q[i] = a.idx_q[(int64_t)b * a.iq_sb + i];
+  if (mode != kTailOnly)
+    for (int i = tid; i < a.d; i += kDrThreads) s_q[i] = a.idx_q[(int64_t)b * a.iq_sb + i];
+  // The k_bar rows the scores read: every block, or (skip_tail) the remote ones only, so
+  // that the tail row being rewritten elsewhere is never read (rows past the last
+  // remote block read that block again, and a sequence with no remote block reads
+  // head_cls, d floats, instead; those scores are masked).
+  const int c_clamp = a.skip_tail ? max(lim, 0) : nblk - 1;
   // d = 128 and up to 512 blocks: every block's k_bar row is loaded now, 16 lanes
   // per row, so that the loads are in flight during the tail refresh
-  const bool fast_scores = a.d == 128 && nblk <= 8 * (kDrThreads / 16);
+  const bool fast_scores = mode != kTailOnly && a.d == 128 && nblk <= 8 * (kDrThreads / 16);
   const int l16 = lane & 15, slot16 = tid >> 4;
   float4 kp[8][2];
   auto prefetch = [&](int r0, int r1) {
     if (!fast_scores) return;
 #pragma unroll
     for (int r = r0; r < r1; ++r) {
-      const int c = min(slot16 + r * (kDrThreads / 16), nblk - 1);
-      const float* kr = a.kbar + (int64_t)b * a.kb_sb + (int64_t)c * 128;
+      const int c = min(slot16 + r * (kDrThreads / 16), c_clamp);
+      const float* kr = (a.skip_tail && lim < 0) ? a.head_cls : a.kbar + (int64_t)b * a.kb_sb + (int64_t)c * 128;
       kp[r][0] = *(const float4*)(kr + l16 * 4);
       kp[r][1] = *(const float4*)(kr + 64 + l16 * 4);
     }
   };
   prefetch(0, 4);
-  if (a.refresh_tail) {
+  if ((own_refresh && a.refresh_tail) || mode == kTailOnly) {
     const int t0 = ct * a.bs, n = len - t0;
     const float* hcp = a.head_cls;
     // logits of the tail tokens: 8 lanes per token, an eighth of the dims each
@@ -1150,8 +1169,9 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
       }
       __syncthreads();
     }
+    if (mode == kTailOnly) return;
   }
-  if (!a.refresh_tail) prefetch(4, 8);
+  if (!(own_refresh && a.refresh_tail)) prefetch(4, 8);
   __syncthreads();
   // scores, the refreshed tail block from LDS
   if (fast_scores) {
@@ -1160,7 +1180,7 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       const int c = slot16 + r * (kDrThreads / 16);
-      const bool tl = a.refresh_tail && c == ct;
+      const bool tl = own_refresh && a.refresh_tail && c == ct;
       const float4 ka = tl ? ta : kp[r][0], kb = tl ? tb : kp[r][1];
       float v = qa.x * ka.x + qa.y * ka.y + qa.z * ka.z + qa.w * ka.w +
                 qb.x * kb.x + qb.y * kb.y + qb.z * kb.z + qb.w * kb.w;
@@ -1185,15 +1205,15 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
         float4 kv[8];
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
-          const int c = min(cb + row0 + r * (kDrThreads / 32), nblk - 1);
-          kv[r] = *(const float4*)(a.kbar + (int64_t)b * a.kb_sb + (int64_t)c * a.d + i);
+          const int c = min(cb + row0 + r * (kDrThreads / 32), c_clamp);
+          kv[r] = *(const float4*)(((a.skip_tail && lim < 0) ? a.head_cls : a.kbar + (int64_t)b * a.kb_sb + (int64_t)c * a.d) + i);
         }
         const float4 qv = *(const float4*)(s_q + i);
         const float4 tv = *(const float4*)(s_tail + i);
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
           const int c = cb + row0 + r * (kDrThreads / 32);
-          const float4 k4 = (a.refresh_tail && c == ct) ? tv : kv[r];
+          const float4 k4 = (own_refresh && a.refresh_tail && c == ct) ? tv : kv[r];
           acc[r] += qv.x * k4.x + qv.y * k4.y + qv.z * k4.z + qv.w * k4.w;
         }
       }
@@ -1300,14 +1320,22 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
   decode_route_finish(a, b, lane, M, Kp, s_selv, s_selk);
 }
 
-__global__ __launch_bounds__(kDrThreads) void decode_route_kernel(DecodeRouteArgs a) {
-  decode_route_body(a, blockIdx.x);
+// Work-groups 0 .. B-1 route one sequence each; with nrw = 2, a routes without the
+// tail refresh (refresh_tail 0, skip_tail 1) and B .. 2B-1 refresh with rt.
+__global__ __launch_bounds__(kDrThreads) void decode_route_kernel(DecodeRouteArgs a,
+                                                                  DecodeRouteArgs rt, int B) {
+  if ((int)blockIdx.x < B)
+    decode_route_body<kRouteAll>(a, blockIdx.x);
+  else
+    decode_route_body<kTailOnly>(rt, (int)blockIdx.x - B);
 }
 
 // ---------------------------------------------------------------------------
 // Fused decode step.  The window part of the attention does not depend on the
 // routing, so it runs in the router's launch: work-groups 0 .. B-1 route one
-// sequence each (as decode_route_kernel), the rest are 16 wavefronts of window
+// sequence each (as decode_route_kernel), B .. 2B-1 refresh the tail block's
+// summary of one sequence each (beside its routing, which does not read it once
+// the window spans a block), the rest are 16 wavefronts of window
 // pieces, one 32-key piece of the window of one (sequence, head) per wavefront,
 // each writing an (o, m, l) partial (32 keys per round trip keep a wavefront
 // within the 128 registers a 1024-thread work-group allows).  A second launch
@@ -1319,14 +1347,21 @@ __device__ __forceinline__ int ds_pieces(const DecodeArgs& da, const DcSpan& sp)
   return sp.n_win > 0 ? (sp.qp + 1 - sp.w0 * da.bs + kDsPiece - 1) / kDsPiece : 0;
 }
 
+// With nrw = 2 (split), ra routes without the refresh (refresh_tail 0, skip_tail 1)
+// and rt refreshes the tail blocks in work-groups B .. 2B-1.
 __global__ __launch_bounds__(kDrThreads) void decode_route_window_kernel(DecodeRouteArgs ra,
+                                                                         DecodeRouteArgs rt,
                                                                          DecodeArgs da, int B,
-                                                                         int npw) {
+                                                                         int nrw, int npw) {
   if ((int)blockIdx.x < B) {
-    decode_route_body(ra, blockIdx.x);
+    decode_route_body<kRouteAll>(ra, blockIdx.x);
     return;
   }
-  const int task = ((int)blockIdx.x - B) * (kDrThreads / kWave) + (int)threadIdx.x / kWave;
+  if ((int)blockIdx.x < nrw * B) {
+    decode_route_body<kTailOnly>(rt, (int)blockIdx.x - B);
+    return;
+  }
+  const int task = ((int)blockIdx.x - nrw * B) * (kDrThreads / kWave) + (int)threadIdx.x / kWave;
   if (task >= B * da.H * npw) return;
   const int piece = task % npw, bh = task / npw;
   const int h = bh % da.H, b = bh / da.H;
@@ -1402,7 +1437,7 @@ static int decode_route_args(const float* idx_q, int64_t iq_sb, const float* idx
   a.idx_k = idx_k;
   a.lay_k = SeqLayout{nullptr, block_table, table_stride, ik_sb, ik_sp, ik_st, page_size};
   a.lens = seq_lens; a.S = S;
-  a.head_cls = head_cls; a.refresh_tail = refresh_tail;
+  a.head_cls = head_cls; a.refresh_tail = refresh_tail; a.skip_tail = 0;
   a.kbar = kbar; a.kb_sb = kb_sb; a.nblk_cap = nblk_cap;
   a.cand = cand; a.cand_stride = cand_stride;
   a.d = d; a.bs = block_size; a.local_blocks = local_blocks;
@@ -1433,7 +1468,12 @@ extern "C" int dash_decode_route(const float* idx_q, int64_t iq_sb, const float*
                                    idx_scale, floor_p, sigma, K, topm, Kout, idx, bias, valid, z,
                                    z_stride, a);
   if (st != kOk || B == 0) return st;
-  hipLaunchKernelGGL(decode_route_kernel, dim3(B), dim3(kDrThreads), 0, (hipStream_t)stream, a);
+  // the tail refresh beside the routing when the tail block cannot be remote
+  const int nrw = (refresh_tail && local_blocks >= 1) ? 2 : 1;
+  const DecodeRouteArgs rt = a;
+  if (nrw == 2) { a.refresh_tail = 0; a.skip_tail = 1; }
+  hipLaunchKernelGGL(decode_route_kernel, dim3(nrw * B), dim3(kDrThreads), 0, (hipStream_t)stream,
+                     a, rt, B);
   return launch_status();
 }
 
@@ -1499,10 +1539,14 @@ extern "C" int dash_decode_step(
   a.S = S; a.H = H; a.bs = block_size; a.lw = local_window; a.nsplit = npw;
   a.scale_log2e = scale * 1.4426950408889634f;
   const int64_t tasks = (int64_t)B * H * npw;
-  const int64_t wgs = B + (tasks + kDrThreads / kWave - 1) / (kDrThreads / kWave);
+  // the tail refresh beside the routing when the tail block cannot be remote
+  const int nrw = (refresh_tail && local_blocks >= 1) ? 2 : 1;
+  const DecodeRouteArgs rt = ra;
+  if (nrw == 2) { ra.refresh_tail = 0; ra.skip_tail = 1; }
+  const int64_t wgs = nrw * (int64_t)B + (tasks + kDrThreads / kWave - 1) / (kDrThreads / kWave);
   if (wgs > 0x7fffffff) return kErrUnsupported;
   hipLaunchKernelGGL(decode_route_window_kernel, dim3((unsigned)wgs), dim3(kDrThreads), 0,
-                     (hipStream_t)stream, ra, a, B, npw);
+                     (hipStream_t)stream, ra, rt, a, B, nrw, npw);
   if (Kout > 0)
     hipLaunchKernelGGL(decode_routed_kernel, dim3(Kout, H, B), dim3(64), 0, (hipStream_t)stream, a,
                        npw);

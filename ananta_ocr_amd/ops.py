@@ -183,17 +183,16 @@ DENSE_THRESHOLD = 32   # of the 128 queries of a tile; below it a routed block g
 _WORKSPACES = {}
 
 
-def zeroed_workspace(key, nbytes, device):
-    """A cached device buffer of at least `nbytes`, zero-filled when (re)allocated.
-    The kernels using it leave their counters at zero, so it is reused as is.
-    Calls that share it are ordered on the current stream."""
+def cached_workspace(key, nbytes, device):
+    """A cached device buffer of at least `nbytes` (contents undefined; the kernels
+    clear what they count in).  Calls that share it are ordered on the current stream."""
     k = (key, str(device))
     buf = _WORKSPACES.get(k)
     if buf is None or buf.numel() < nbytes:
         if buf is not None:
             del _WORKSPACES[k]
             del buf
-        buf = torch.zeros(int(nbytes * 1.1) + 4096, dtype=torch.uint8, device=device)
+        buf = torch.empty(int(nbytes * 1.1) + 4096, dtype=torch.uint8, device=device)
         _WORKSPACES[k] = buf
     return buf
 
@@ -239,7 +238,7 @@ def attn_prefill(q, k, v, idx, bias, valid, block_size, local_window, scale,
         nbytes = ctypes.c_int64(0)
         _lib.check(lib.dash_attn_prefill_workspace_size(nb, H, Smax, rows, K, D, int(block_size),
                                                         nbytes), "workspace")
-        ws = zeroed_workspace("prefill", nbytes.value, q.device)
+        ws = cached_workspace("prefill", nbytes.value, q.device)
         ws_n = ws.numel()
     km = _i32(kmin)
     st_ = lib.dash_attn_prefill(

@@ -112,9 +112,8 @@ int dash_route(const float* z, int64_t z_stride, int rows, int nblk_cols,
  * block_size in {32, 64, ..., 256}, K <= 16.
  * dense_threshold > 0 (block_size <= 64): routed blocks selected by fewer than
  * dense_threshold of the 128 queries of a tile go through the block-major sparse path,
- * which needs `workspace` (dash_attn_prefill_workspace_size bytes, 256-byte aligned; its
- * leading counters (per-block pair counts and one arrival counter) must be zero before
- * the first call and are left zero by every call) and total_rows (B*S, or cu_seqlens[B]).  dense_threshold <= 0: no workspace,
+ * which needs `workspace` (dash_attn_prefill_workspace_size bytes, 256-byte aligned, any
+ * contents: the call clears its counters first) and total_rows (B*S, or cu_seqlens[B]).  dense_threshold <= 0: no workspace,
  * every routed block of a tile is processed with the tile.  Calls sharing a workspace
  * must not overlap.
  */
@@ -142,7 +141,10 @@ int dash_attn_prefill_workspace_size(int B, int H, int S_max, int64_t total_rows
  *   idx_q    fp32 [B, d] rows (iq_sb); idx_k index-key cache addressed like dash_kbar
  *   kbar     [B, nblk_cap, d] fp32 cache (updated in place at the tail block)
  *   z        [B, z_stride] fp32 scores (written, for inspection)
- *   One 1024-thread work-group per sequence.  nblk_cap <= 2048, d <= 256.
+ *   One 1024-thread work-group per sequence; with refresh_tail and local_blocks >= 1 a
+ *   second one per sequence refreshes the tail block beside the routing (the tail block
+ *   holds the query, so it is never remote and the routing does not read its row).
+ *   nblk_cap <= 2048, d <= 256.
  */
 int dash_decode_route(const float* idx_q, int64_t iq_sb, const float* idx_k,
                       int64_t ik_sb, int64_t ik_st, int64_t ik_sp,

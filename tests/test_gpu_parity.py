@@ -296,6 +296,37 @@ def test_prefill_varlen_many_documents(thr):
         _close(out[:, :, s0:s1], ref, f"document {b}")
 
 
+def test_prefill_workspace_any_contents():
+    """The sparse path's workspace may hold anything, as a cached buffer last used by a
+    call of another shape does: the call clears its own counters first."""
+    g = _gen(345)
+    lens = (torch.rand(300, generator=g) * 90 + 20).long().tolist()
+    cu = [0]
+    for L in lens:
+        cu.append(cu[-1] + L)
+    T, H, bs, lw, K = cu[-1], 1, 32, 16, 3
+    q, k, v, idx, bias, valid = _attn_inputs(346, 1, H, T, bs, lw, K)
+    for b in range(len(lens)):
+        L = lens[b]
+        t = torch.arange(L)
+        lb = (lw + bs - 1) // bs
+        hi = (t // bs - lb).clamp(min=0)
+        idx[0, cu[b]:cu[b + 1]] = (torch.rand(L, K, generator=g) * (hi[:, None] + 1)).floor().long()
+        valid[0, cu[b]:cu[b + 1]] &= (t // bs - lb >= 0)[:, None]
+    qd = q.to(DEV)
+    ws = ops.cached_workspace("prefill", 256 << 20, qd.device)     # the buffer the call takes
+    ws.fill_(0x5A)                       # every counter starts at 0x5A5A5A5A
+    out = ops.attn_prefill(qd, k.to(DEV), v.to(DEV), idx[0].to(DEV), bias[0].to(DEV),
+                           valid[0].to(DEV), bs, lw, 1 / math.sqrt(128),
+                           cu_seqlens=torch.tensor(cu, dtype=torch.int32).to(DEV),
+                           dense_threshold=24).cpu()
+    for b in range(len(lens)):
+        s0, s1 = cu[b], cu[b + 1]
+        ref = O.dense_attend(q[:, :, s0:s1], k[:, :, s0:s1], v[:, :, s0:s1], idx[:, s0:s1],
+                             bias[:, s0:s1], valid[:, s0:s1], bs, lw, 1 / math.sqrt(128))
+        _close(out[:, :, s0:s1], ref, f"document {b}")
+
+
 def test_prefill_pipeline_2730_tokens():
     """Prefill at 2,730 tokens (10 pages): GPU k_bar -> scores -> route -> attention.
     Routing is bit-exact against the oracle on the GPU's scores; the attention is
