@@ -24,6 +24,8 @@ SIGNATURES = {
                                _p, _l, _p]),
     "dash_block_max_score": (_i, [_p, _l, _l, _i, _p, _p, _l, _p, _l, _l, _i, _i, _i, _i, _i,
                                   _i, _i, _p, _l, _l, _p]),
+    "dash_router_qk_norm": (_i, [_p, _i, _l, _l, _i, _i, _p, _p, _f, _p, _p, _i, _l, _l, _p, _p,
+                                 _p]),
     "dash_route": (_i, [_p, _l, _i, _i, _p, _p, _l, _f, _f, _f, _i, _i, _i, _p, _p, _p, _p]),
     "dash_attn_prefill": (_i, [_p, _l, _l, _l, _p, _l, _l, _l, _p, _l, _l, _l, _p, _l, _l, _l,
                                _p, _l, _l, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _f,

@@ -1554,3 +1554,112 @@ extern "C" int dash_decode_step(
                      npw);
   return launch_status();
 }
+
+// ---------------------------------------------------------------------------
+// Router front end: the index projections' Gemma RMSNorm, optional RoPE and the
+// finiteness guards (dash_attention.py:680-700 and the q/k path of
+// modeling_deepseekv2.py:336-348), one wavefront per (row, q or k), two dims per
+// lane.  The projection of both sides comes from one GEMM, [rows, 2d] (q then k).
+// Every elementwise step is one correctly rounded operation as in the unfused
+// sequence; in bf16 (bf16 projection and bf16 cos/sin) each RoPE product and the
+// sum are rounded to bf16 as separate tensor ops round them.
+// ---------------------------------------------------------------------------
+namespace dash {
+
+struct RouterQkArgs {
+  const void* proj; int proj_bf16; int64_t proj_row; int64_t rows; int S;
+  const float* wq; const float* wk; float eps;
+  const void* cos; const void* sin; int cs_bf16; int64_t cs_sb, cs_st;
+  float* iq; float* ik;
+};
+
+__device__ __forceinline__ float rb16(float x) { return (float)(bf16)x; }
+__device__ __forceinline__ float finite_or_zero(float x) {
+  return (fabsf(x) <= 3.402823466e38f) ? x : 0.f;
+}
+
+__global__ __launch_bounds__(256) void router_qk_kernel(RouterQkArgs a) {
+#pragma clang fp contract(off)
+  const int64_t task = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+  if (task >= a.rows * 2) return;
+  const int64_t row = task >> 1;
+  const int side = (int)(task & 1);            // 0: q, 1: k
+  const int lane = wave_lane(), i0 = 2 * lane;
+  constexpr int d = 128;
+  float x0, x1;
+  if (a.proj_bf16) {
+    const bf16x2 v = *(const bf16x2*)((const bf16*)a.proj + row * a.proj_row + side * d + i0);
+    x0 = (float)v[0]; x1 = (float)v[1];
+  } else {
+    const float2 v = *(const float2*)((const float*)a.proj + row * a.proj_row + side * d + i0);
+    x0 = v.x; x1 = v.y;
+  }
+  x0 = finite_or_zero(x0);
+  x1 = finite_or_zero(x1);
+  const float ss = wave_sum(__fadd_rn(__fmul_rn(x0, x0), __fmul_rn(x1, x1)));
+  const float r = rsqrtf(__fadd_rn(__fmul_rn(ss, 1.0f / d), a.eps));
+  const float* w = side ? a.wk : a.wq;
+  const float2 wv = *(const float2*)(w + i0);
+  float y0 = fminf(fmaxf(__fmul_rn(x0, r), -kActClamp), kActClamp);
+  float y1 = fminf(fmaxf(__fmul_rn(x1, r), -kActClamp), kActClamp);
+  y0 = fminf(fmaxf(__fmul_rn(y0, __fadd_rn(1.0f, wv.x)), -kActClamp), kActClamp);
+  y1 = fminf(fmaxf(__fmul_rn(y1, __fadd_rn(1.0f, wv.y)), -kActClamp), kActClamp);
+  if (a.proj_bf16) { y0 = rb16(y0); y1 = rb16(y1); }
+  if (a.cos) {
+    const int64_t b = row / a.S, t = row % a.S;
+    const int64_t co = b * a.cs_sb + t * a.cs_st + i0;
+    float c0, c1, s0, s1;
+    if (a.cs_bf16) {
+      const bf16x2 cv = *(const bf16x2*)((const bf16*)a.cos + co);
+      const bf16x2 sv = *(const bf16x2*)((const bf16*)a.sin + co);
+      c0 = (float)cv[0]; c1 = (float)cv[1]; s0 = (float)sv[0]; s1 = (float)sv[1];
+    } else {
+      const float2 cv = *(const float2*)((const float*)a.cos + co);
+      const float2 sv = *(const float2*)((const float*)a.sin + co);
+      c0 = cv.x; c1 = cv.y; s0 = sv.x; s1 = sv.y;
+    }
+    // rotate_half: dim i < d/2 takes -y[i + d/2], dim i >= d/2 takes y[i - d/2]
+    const float p0 = __shfl_xor(y0, 32, kWave), p1 = __shfl_xor(y1, 32, kWave);
+    const float h0 = lane < 32 ? -p0 : p0, h1 = lane < 32 ? -p1 : p1;
+    const bool bf = a.proj_bf16 && a.cs_bf16;
+    float t0 = __fmul_rn(y0, c0), t1 = __fmul_rn(y1, c1);
+    float u0 = __fmul_rn(h0, s0), u1 = __fmul_rn(h1, s1);
+    if (bf) { t0 = rb16(t0); t1 = rb16(t1); u0 = rb16(u0); u1 = rb16(u1); }
+    y0 = __fadd_rn(t0, u0);
+    y1 = __fadd_rn(t1, u1);
+    if (bf) { y0 = rb16(y0); y1 = rb16(y1); }
+  }
+  float* out = (side ? a.ik : a.iq) + row * d + i0;
+  *(float2*)out = make_float2(finite_or_zero(y0), finite_or_zero(y1));
+}
+
+}  // namespace dash
+
+extern "C" int dash_router_qk_norm(const void* proj, int proj_bf16, int64_t proj_row,
+                                   int64_t rows, int S, int d, const float* wq,
+                                   const float* wk, float eps, const void* cos,
+                                   const void* sin, int cs_bf16, int64_t cs_sb, int64_t cs_st,
+                                   float* idx_q, float* idx_k, void* stream) {
+  using namespace dash;
+  if (!proj || !wq || !wk || !idx_q || !idx_k || rows < 0 || S <= 0) return kErrInvalid;
+  if (d != 128) return kErrUnsupported;
+  if ((cos == nullptr) != (sin == nullptr)) return kErrInvalid;
+  const int es = proj_bf16 ? 2 : 4, cs = cs_bf16 ? 2 : 4;
+  if (proj_row % 2 != 0 || (uintptr_t)proj % (2 * es) != 0) return kErrUnsupported;
+  if ((uintptr_t)wq % 8 != 0 || (uintptr_t)wk % 8 != 0 || (uintptr_t)idx_q % 8 != 0 ||
+      (uintptr_t)idx_k % 8 != 0)
+    return kErrUnsupported;
+  if (cos && ((uintptr_t)cos % (2 * cs) != 0 || (uintptr_t)sin % (2 * cs) != 0 ||
+              cs_sb % 2 != 0 || cs_st % 2 != 0))
+    return kErrUnsupported;
+  if (rows == 0) return kOk;
+  RouterQkArgs a;
+  a.proj = proj; a.proj_bf16 = proj_bf16; a.proj_row = proj_row; a.rows = rows; a.S = S;
+  a.wq = wq; a.wk = wk; a.eps = eps;
+  a.cos = cos; a.sin = sin; a.cs_bf16 = cs_bf16; a.cs_sb = cs_sb; a.cs_st = cs_st;
+  a.iq = idx_q; a.ik = idx_k;
+  const int64_t grid = (rows * 2 + 3) / 4;
+  if (grid > 0x7fffffff) return kErrUnsupported;
+  hipLaunchKernelGGL(router_qk_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a);
+  return launch_status();
+}

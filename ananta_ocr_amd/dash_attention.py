@@ -93,6 +93,16 @@ class DashAttention(nn.Module):
         B, S, _ = hidden_states.shape
         d = self.index_dim
         hs = torch.nan_to_num(hidden_states, nan=0.0, posinf=0.0, neginf=0.0)
+        if d == 128 and hs.is_cuda and self.q_norm.eps == self.k_norm.eps:
+            # one GEMM for both projections, then the fused norm / RoPE / guards
+            w = torch.cat([self.q_proj.weight, self.k_proj.weight], 0)
+            proj = torch.nn.functional.linear(hs, w)
+            cos = sin = None
+            if position_embeddings is not None:
+                cos, sin = position_embeddings
+                cos, sin = cos[..., :d], sin[..., :d]
+            return ops.router_qk_norm(proj, self.q_norm.weight, self.k_norm.weight,
+                                      self.q_norm.eps, cos, sin)
         iq = self.q_norm(self.q_proj(hs).view(B, S, 1, d)).transpose(1, 2)
         ik = self.k_norm(self.k_proj(hs).view(B, S, 1, d)).transpose(1, 2)
         if position_embeddings is not None:

@@ -150,6 +150,40 @@ def block_max_score(q, k, pos, seg, block_size, num_key_blocks, local_window, mo
     return out
 
 
+def router_qk_norm(proj, wq, wk, eps, cos=None, sin=None):
+    """Gemma RMSNorm (+ RoPE) of the stacked index projections proj [B,S,2d] (q then k,
+    bf16 or fp32); cos/sin [B,S,>=d] (or [1,S,>=d]) bf16/fp32 or None.
+    Returns (idx_q, idx_k) fp32 [B,S,d] (modeling_deepseekv2.py:336-348)."""
+    _need_gpu(proj, wq, wk)
+    lib = _lib.load()
+    B, S, d2 = proj.shape
+    d = d2 // 2
+    if proj.dtype not in (torch.bfloat16, torch.float32):
+        proj = proj.float()
+    if proj.stride(-1) != 1 or proj.stride(0) != S * proj.stride(1):
+        proj = proj.contiguous()
+    iq = torch.empty(B, S, d, dtype=torch.float32, device=proj.device)
+    ik = torch.empty_like(iq)
+    wq = wq.float().contiguous()
+    wk = wk.float().contiguous()
+    cs_bf16, cs_sb, cs_st = 0, 0, 0
+    if cos is not None:
+        dt = torch.bfloat16 if (cos.dtype == torch.bfloat16 and sin.dtype == torch.bfloat16) \
+            else torch.float32
+        cos = cos.to(dt)
+        sin = sin.to(dt)
+        if cos.stride(-1) != 1 or cos.stride() != sin.stride():
+            cos, sin = cos.contiguous(), sin.contiguous()
+        cs_bf16 = int(dt == torch.bfloat16)
+        cs_sb = 0 if cos.shape[0] == 1 else cos.stride(0)
+        cs_st = cos.stride(1)
+    st_ = lib.dash_router_qk_norm(_ptr(proj), int(proj.dtype == torch.bfloat16), proj.stride(1),
+                                  B * S, S, d, _ptr(wq), _ptr(wk), float(eps), _ptr(cos),
+                                  _ptr(sin), cs_bf16, cs_sb, cs_st, _ptr(iq), _ptr(ik), _stream())
+    _lib.check(st_, "dash_router_qk_norm")
+    return iq, ik
+
+
 def route(z, cand, idx_scale, floor, sigma, K, topm, row_nblk=None, width=None):
     """Inference routing of every row of z [..., nblk] fp32.
     Returns (idx int32 [..., K'], bias fp32, valid bool) with K' = max(1, min(K, M'))."""

@@ -84,6 +84,22 @@ int dash_block_max_score(const float* q, int64_t q_sb, int64_t q_st, int C,
                          float* out, int64_t o_sb, int64_t o_sc, void* stream);
 
 /*
+ * Router front end after the index projections: Gemma RMSNorm (scale 1 + w, eps,
+ * activations clamped to +-1e4), optional RoPE (rotate-half, cos/sin rows of the
+ * first d dims) and the finiteness guards of _router_qk (modeling_deepseekv2.py:336-348)
+ * with GemmaRMSNorm (dash_attention.py:680-700).  proj [rows, proj_row] holds both
+ * projections of a row, q at [0, d) and k at [d, 2d) (one GEMM with the two weights
+ * stacked), bf16 or fp32; cos/sin (optional, both or neither) at b*cs_sb + t*cs_st for
+ * row = b*S + t, bf16 or fp32.  Steps round as the unfused tensor ops do: fp32 math,
+ * the normed rows rounded to the projection dtype, RoPE in bf16 when both the
+ * projection and cos/sin are bf16, else fp32.  idx_q/idx_k fp32 [rows, d].  d == 128.
+ */
+int dash_router_qk_norm(const void* proj, int proj_bf16, int64_t proj_row, int64_t rows, int S,
+                        int d, const float* wq, const float* wk, float eps, const void* cos,
+                        const void* sin, int cs_bf16, int64_t cs_sb, int64_t cs_st,
+                        float* idx_q, float* idx_k, void* stream);
+
+/*
  * Inference routing of every score row: candidates (remote, optionally AND cand,
  * falling back to remote), x = z*idx_scale, top-M by (value desc, block id asc),
  * 1.5-entmax prior over the M values, first K' = max(1,min(K,M)) slots, bias =

@@ -149,3 +149,69 @@ def test_decode_attend_helper_matches_oracle():
                             valid.to(DEV), qp.to(DEV), bs, lw, 0.1)
     ref = O.decode_attend(q, k, v, topi, bias, valid, qp, bs, lw, 0.1)
     _close(out, ref, "decode helper")
+
+
+def _qk_norm_ref(x, w, eps, cos, sin):
+    """Plain torch restatement of the router's index path for one side
+    (GemmaRMSNorm dash_attention.py:680-700, rotate-half RoPE, finiteness guards),
+    on the CPU in the projection's dtype."""
+    x32 = torch.nan_to_num(x.float(), nan=0.0, posinf=0.0, neginf=0.0)
+    x32 = x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + eps)
+    x32 = x32.clamp(-1e4, 1e4)
+    y = (x32 * (1.0 + w.float())).clamp(-1e4, 1e4).to(x.dtype)
+    if cos is not None:
+        y1, y2 = y.chunk(2, dim=-1)
+        y = y * cos + torch.cat((-y2, y1), dim=-1) * sin
+    return torch.nan_to_num(y.float(), nan=0.0, posinf=0.0, neginf=0.0)
+
+
+@pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("cdt", [None, torch.float32, torch.bfloat16])
+def test_router_qk_norm_matches_torch(pdt, cdt):
+    from ananta_ocr_amd import ops
+    g = torch.Generator().manual_seed(7)
+    B, S, d = 2, 301, 128
+    proj = torch.randn(B, S, 2 * d, generator=g) * 3
+    proj[0, 5, 7] = float("nan")
+    proj[1, 9, 130] = float("inf")
+    proj[0, 11] *= 1e6                                  # norm clamps
+    proj = proj.to(pdt)
+    wq = torch.randn(d, generator=g) * 0.3
+    wk = torch.randn(d, generator=g) * 0.3
+    cos = sin = None
+    if cdt is not None:
+        ang = torch.arange(S)[:, None] * (1e4 ** (-torch.arange(0, 160, 2) / 160))[None]
+        emb = torch.cat([ang, ang], -1)                 # [S, 160]: the first d dims are used
+        cos, sin = emb.cos()[None].to(cdt), emb.sin()[None].to(cdt)
+    iq, ik = ops.router_qk_norm(proj.to(DEV), wq.to(DEV), wk.to(DEV), 1e-6,
+                                None if cos is None else cos[..., :d].to(DEV),
+                                None if sin is None else sin[..., :d].to(DEV))
+    c = None if cos is None else cos[..., :d]
+    s = None if sin is None else sin[..., :d]
+    for side, (out, w) in enumerate(((iq, wq), (ik, wk))):
+        ref = _qk_norm_ref(proj[..., side * d:(side + 1) * d], w, 1e-6, c, s)
+        out = out.cpu()
+        assert torch.isfinite(out).all()
+        if pdt == torch.float32:
+            torch.testing.assert_close(out, ref, atol=1e-5, rtol=1e-5)
+        else:
+            # one bf16 rounding may flip on the ulp-level difference of the row norm
+            err = (out - ref).abs()
+            assert torch.all(err <= 2 ** -7 * ref.abs() + 1e-6), f"side {side}: {err.max().item()}"
+            assert (err > 0).float().mean().item() < 0.01
+
+
+def test_router_qk_fused_matches_unfused_module_path():
+    torch.manual_seed(3)
+    cfg = _config("head_cls")
+    mod = DashAttention(cfg).eval().to(DEV)
+    with torch.no_grad():
+        mod.q_norm.weight.normal_(0, 0.2)
+        mod.k_norm.weight.normal_(0, 0.2)
+        hs = torch.randn(1, 257, cfg.hidden_size, device=DEV)
+        iq, ik = mod.router_qk(hs)
+        d = mod.index_dim
+        hq = mod.q_norm(mod.q_proj(hs).view(1, 257, 1, d))[:, :, 0].float()
+        hk = mod.k_norm(mod.k_proj(hs).view(1, 257, 1, d))[:, :, 0].float()
+    torch.testing.assert_close(iq, hq, atol=2e-5, rtol=2e-5)
+    torch.testing.assert_close(ik, hk, atol=2e-5, rtol=2e-5)
