@@ -296,6 +296,38 @@ def test_prefill_varlen_many_documents(thr):
         _close(out[:, :, s0:s1], ref, f"document {b}")
 
 
+@pytest.mark.parametrize("thr", [0, 24])
+@pytest.mark.parametrize("K", [0, 4])
+def test_prefill_empty_documents_single_tokens_no_routing(thr, K):
+    """Packed documents of 0, 5, 0, 295, 1 and 0 tokens; with and without routed slots."""
+    g = _gen(350 + K)
+    cu = [0, 0, 5, 5, 300, 301, 301]
+    T, H, bs, lw = cu[-1], 2, 64, 128
+    q, k, v, idx, bias, valid = _attn_inputs(351 + K, 1, H, T, bs, lw, max(K, 1))
+    if K == 0:
+        idx, bias, valid = idx[..., :0], bias[..., :0], valid[..., :0]
+    else:
+        for b in range(len(cu) - 1):
+            L = cu[b + 1] - cu[b]
+            t = torch.arange(L)
+            hi = (t // bs - lw // bs).clamp(min=0)
+            idx[0, cu[b]:cu[b + 1]] = (torch.rand(L, K, generator=g) * (hi[:, None] + 1)).floor().long()
+            valid[0, cu[b]:cu[b + 1]] &= (t // bs - lw // bs >= 0)[:, None]
+    scale = 1 / math.sqrt(128)
+    out = ops.attn_prefill(q.to(DEV), k.to(DEV), v.to(DEV), idx[0].to(DEV), bias[0].to(DEV),
+                           valid[0].to(DEV), bs, lw, scale,
+                           cu_seqlens=torch.tensor(cu, dtype=torch.int32).to(DEV),
+                           dense_threshold=thr).cpu()
+    assert out.shape == (1, H, T, 128)
+    for b in range(len(cu) - 1):
+        s0, s1 = cu[b], cu[b + 1]
+        if s1 == s0:
+            continue
+        ref = O.dense_attend(q[:, :, s0:s1], k[:, :, s0:s1], v[:, :, s0:s1], idx[:, s0:s1],
+                             bias[:, s0:s1], valid[:, s0:s1], bs, lw, scale)
+        _close(out[:, :, s0:s1], ref, f"document {b}")
+
+
 def test_prefill_workspace_any_contents():
     """The sparse path's workspace may hold anything, as a cached buffer last used by a
     call of another shape does: the call clears its own counters first."""
@@ -389,6 +421,19 @@ def test_decode_contiguous_matches_oracle(nsplit):
     out = ops.attn_decode(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), bias.to(DEV),
                           valid.to(DEV), bs, lw, scale, seq_lens=lens.to(DEV), nsplit=nsplit)
     _close(out, ref, "decode")
+
+
+def test_decode_without_routed_blocks_and_single_token():
+    B, H, bs, lw = 3, 2, 64, 512
+    lens = torch.tensor([1, 64, 1500], dtype=torch.int32)
+    q, k, v, idx, bias, valid, lens = _decode_inputs(420, B, H, 1500, bs, lw, 1, lens)
+    idx, bias, valid = idx[:, :0], bias[:, :0], valid[:, :0]
+    scale = 1 / math.sqrt(128)
+    ref = _decode_ref(q, k, v, idx, bias, valid, lens, bs, lw, scale)
+    out = ops.attn_decode(q.to(DEV), k.to(DEV), v.to(DEV), None, None, None, bs, lw, scale,
+                          seq_lens=lens.to(DEV))
+    _close(out, ref, "decode, window only")
+    torch.testing.assert_close(out[0].cpu(), v[0, :, 0].float(), atol=1e-6, rtol=0)   # one key
 
 
 def test_decode_paged_matches_contiguous_oracle():
