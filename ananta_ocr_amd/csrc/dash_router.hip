@@ -599,8 +599,9 @@ __device__ __forceinline__ uint32_t kth_key(const uint32_t (&h)[NV], int M, uint
   return T;
 }
 
-// Routing: work-groups of four wavefronts own 16 consecutive score rows, four
-// per wavefront.
+// Routing: work-groups of four wavefronts own 8 consecutive score rows, two per
+// wavefront (more rows per wavefront lengthen each wavefront's serial chain; one
+// row leaves three quarters of the lanes idle in phase 2).
 //  Phase 1, one row at a time over the whole wavefront: every entry gets the
 //  64-bit key  ord_key(x) << 32 | (0xffff - block id) << 1 | candidate  whose
 //  descending order is (value desc, block id asc).  The top-M set is found
@@ -616,7 +617,7 @@ __device__ __forceinline__ uint32_t kth_key(const uint32_t (&h)[NV], int M, uint
 //  LDS.
 //  Phase 2, each wavefront for its own rows, 16 lanes per row: rank sort of the M
 //  keys, 1.5-entmax with entry m on lane m, first K, centred log-prior bias.
-constexpr int kRtRowsPerWave = 4;
+constexpr int kRtRowsPerWave = 2;
 constexpr int kRtWaves = 4;
 constexpr int kRtRows = kRtRowsPerWave * kRtWaves;
 
