@@ -1,6 +1,6 @@
 """CPU oracle for the DASH attention hot path.  TEST INFRASTRUCTURE ONLY.
 
-This module is the checker, never the product: only ``tests/``, the entry
+This module is test infrastructure, never the product: only ``tests/``, the entry
 point's ``smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may import it.
 The shipped package (``ananta_ocr_amd``) never imports it and has no CPU path.
 

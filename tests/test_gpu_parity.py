@@ -15,7 +15,7 @@ from oracle import dash_oracle as O
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-# north-star output tolerance (bf16 output, fp32 accumulation)
+# output tolerance of the path (bf16 output, fp32 accumulation)
 ATOL, RTOL = 2e-2, 1e-2
 
 
@@ -24,7 +24,7 @@ def _gen(seed):
 
 
 def _close(out, ref, what, tight=1.5e-2):
-    """north-star allclose plus a scale-aware bound: the max error must also be
+    """The output tolerance plus a scale-aware bound: the max error must also be
     below `tight` x max|ref| (bf16 rounding of P and of the output)."""
     out = out.float().cpu()
     ref = ref.float().cpu()
