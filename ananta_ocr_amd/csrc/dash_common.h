@@ -26,7 +26,7 @@ constexpr int kWave = 64;
 // Status codes returned by every C entry point.
 enum Status : int {
   kOk = 0,
-  kErrUnsupported = -2,   // a shape or parameter this build does not implement
+  kErrUnsupported = -2,   // a shape or parameter the library does not implement
   kErrInvalid = -3,       // inconsistent arguments (null pointer, negative size...)
   kErrWorkspace = -4,     // caller-provided workspace too small
 };

@@ -60,7 +60,7 @@ def gather_attention(query_states, key_states, value_states, block_indices, posi
     """[B,HQ,T,D] block-sparse attention without bias; packed rows (position_ids
     restarting at 0) keep every query inside its segment [t - position_ids[t], t].
     Returns None where the reference does (mask, prefix cache, index heads that do
-    not divide the heads); several index heads are not supported by this build and
+    not divide the heads); several index heads are not supported by this library and
     raise NotImplementedError."""
     if attention_mask is not None:
         return None

@@ -371,7 +371,7 @@ def main():
         traffic_probe()
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only (no multi-GPU path); "
+        print("bench.py: this benchmark measures one GPU only (no multi-GPU path); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     torch.cuda.set_device(0)
