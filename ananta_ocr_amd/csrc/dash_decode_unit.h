@@ -55,8 +55,8 @@ struct DcSpan {
 
 __device__ __forceinline__ DcSpan dc_span(const DecodeArgs& a, int b) {
   DcSpan s;
-  s.len = a.lens ? a.lens[b] : a.S;
-  s.qp = a.q_pos ? a.q_pos[b] : s.len - 1;
+  s.len = a.lens ? min(max(a.lens[b], 0), a.S) : a.S;
+  s.qp = a.q_pos ? min(a.q_pos[b], s.len - 1) : s.len - 1;   // at most the last cached token
   s.ls = s.qp - a.lw + 1;
   s.lo = max(s.ls, 0);
   s.nblk = s.len > 0 ? (s.len + a.bs - 1) / a.bs : 0;
@@ -96,12 +96,12 @@ __device__ __forceinline__ void dc_keys(DcState& st, const DecodeArgs& a, int b,
     bf16x8 kr[NT], vr[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int j = min(jb + 4 * t + st.g, sp.len - 1);
+      const int j = min(jb + 4 * t + st.g, j1 - 1);
       kr[t] = *(const bf16x8*)(kh + dc_row(a, b, j, a.k_sb, a.k_st, a.k_sp) + st.dl);
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int j = min(jb + 4 * t + st.g, sp.len - 1);
+      const int j = min(jb + 4 * t + st.g, j1 - 1);
       vr[t] = *(const bf16x8*)(vh + dc_row(a, b, j, a.v_sb, a.v_st, a.v_sp) + st.dl);
     }
     float s[NT];
@@ -142,11 +142,16 @@ __device__ __forceinline__ void dc_keys(DcState& st, const DecodeArgs& a, int b,
   }
 }
 
-// Stream key block cu (a routed block with log2 bias blog, or a window block).
+// Stream key block cu (a routed block with log2 bias blog, or a window block);
+// blocks of at most 32 keys take one 32-row round trip.
 template <int ROWS = 64>
 __device__ __forceinline__ void dc_block(DcState& st, const DecodeArgs& a, int b, int h,
                                          const DcSpan& sp, int cu, bool routed, float blog) {
-  dc_keys<ROWS>(st, a, b, h, sp, cu * a.bs, min((cu + 1) * a.bs, sp.len), routed, blog);
+  const int j0 = cu * a.bs, j1 = min((cu + 1) * a.bs, sp.len);
+  if (ROWS > 32 && a.bs <= 32)
+    dc_keys<32>(st, a, b, h, sp, j0, j1, routed, blog);
+  else
+    dc_keys<ROWS>(st, a, b, h, sp, j0, j1, routed, blog);
 }
 
 // Sum the four lane groups (they share m_run) and store the wavefront's partial

@@ -68,6 +68,7 @@ struct PrefillArgs {
   int32_t* num_chunks;                 // [B]
   int32_t* chunk_pref;                 // [B+1] prefix sums of num_chunks
   int32_t* done;                       // arrival counter of the scan (follows blk_count)
+  int32_t* err;                        // nonzero: a plan count exceeded its capacity (follows done)
   int B;
   int32_t* chunk_rec;                  // [B, chunk_cap, kRec] chunk records
   int chunk_cap;
@@ -103,6 +104,19 @@ __device__ __forceinline__ int part_index(int hl, int dt, int g, int q) {
 template <typename Args>
 __device__ __forceinline__ int64_t part_row(const Args& a, int64_t pos, int h) {
   return (int64_t)h * a.ppos + pos;
+}
+
+// Where the scatter kernel stores the q-th sparse pair of a block whose chunks start
+// at chunk bch of its sequence: the index of its chunk record (within the
+// sequence's chunk_cap records) and its partial position (pair positions of the
+// sequence start at pos0).  False if either falls outside the workspace, which
+// consistent plan counts never produce.
+__host__ __device__ inline bool scatter_target(int64_t chunk_cap, int64_t ppos, int64_t pos0,
+                                               int64_t bch, int64_t q, int64_t* rec_chunk,
+                                               int64_t* pair_pos) {
+  *rec_chunk = bch + q / kPfCH;
+  *pair_pos = pos0 + bch * kPfCH + q;
+  return bch >= 0 && q >= 0 && *rec_chunk < chunk_cap && *pair_pos < ppos;
 }
 
 // Keep a routed slot?  The block must exist, be valid, and have keys below the
@@ -239,10 +253,11 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
   if (e1 < kPfMaxBlocks) { sC[e1] = v1; sCh[e1] = xc + c0; }
   __shared__ int sLast;
   if (tid == 1023) {
-    a.num_chunks[b] = bc + ic;
+    // the sparse grid covers no chunk past the sequence's records
+    a.num_chunks[b] = min(bc + ic, a.chunk_cap);
     if (gridDim.x == 1) {                  // one sequence: its count is the prefix
       a.chunk_pref[0] = 0;
-      a.chunk_pref[1] = bc + ic;
+      a.chunk_pref[1] = min(bc + ic, a.chunk_cap);
       sLast = 0;
     } else {
       __threadfence();
@@ -254,8 +269,13 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
   for (int c = tid; c < nblk; c += 1024) {
     a.blk_chunk[(int64_t)b * a.nblk_cap + c] = sCh[c];
     const int n = sC[c];
-    for (int i = 0; i * kPfCH < n; ++i)
+    for (int i = 0; i * kPfCH < n; ++i) {
+      if (sCh[c] + i >= a.chunk_cap) {       // never with consistent counts
+        atomicOr(a.err, 1);
+        break;
+      }
       *(int2*)(rec + (int64_t)(sCh[c] + i) * kRec) = make_int2(c, min(kPfCH, n - i * kPfCH));
+    }
   }
   // The sequence that finishes last writes the prefix sums of the chunk counts
   // (the sparse kernel maps its grid onto the real chunks with them).
@@ -323,9 +343,14 @@ __global__ __launch_bounds__(kPfTQ) void prefill_scatter_kernel(PrefillArgs a) {
   for (int s = 0; s < kPfMaxK; ++s)
     if (sp[s]) {
       const int q = tb[c[s]] + pos[s];               // position in the block's pair list
-      rec[(int64_t)(bch[c[s]] + q / kPfCH) * kRec + kRecHead + q % kPfCH] =
-          (int32_t)(row * a.K + s - base);
-      a.spos[row * a.K + s] = (int32_t)(pos0 + (int64_t)bch[c[s]] * kPfCH + q);
+      int64_t rc, pp;
+      if (scatter_target(a.chunk_cap, a.ppos, pos0, bch[c[s]], q, &rc, &pp)) {
+        rec[rc * kRec + kRecHead + q % kPfCH] = (int32_t)(row * a.K + s - base);
+        a.spos[row * a.K + s] = (int32_t)pp;
+      } else {                                       // never with consistent counts
+        atomicOr(a.err, 2);
+        a.spos[row * a.K + s] = -1;                  // the tile kernel skips the slot
+      }
     }
 }
 
@@ -938,7 +963,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
     }
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s)
-      l2[s] = ((smask >> s) & 1u) ? pa.part_lse[part_row(pa, sp[s], h)] : -INFINITY;
+      l2[s] = (((smask >> s) & 1u) && sp[s] >= 0) ? pa.part_lse[part_row(pa, sp[s], h)] : -INFINITY;
     float mx = m_run;
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s) mx = fmaxf(mx, l2[s]);
@@ -1041,6 +1066,7 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
   const int pb = a.chunk_pref[b], nc = a.chunk_pref[b + 1] - pb;
   const int hc = lid - a.H * pb;
   const int h = hc / nc, ch = hc % nc;
+  if ((int64_t)(pb + ch + 1) * kPfCH > a.ppos) return;     // never with consistent counts
   const int tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
   const int hl = lane >> 5, n = lane & 31;
   // header and pair ids in one round trip: lanes past the count take the first id
@@ -1074,7 +1100,7 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
     int km;
   };
   auto load_round = [&](int pid, RoundIn& in) {
-    const int t = pid / a.K;
+    const int t = pid / a.K;                   // pid is in [0, len * K): see pids below
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
       const int tk = __shfl(t, 4 * kk + (lane >> 4), kWave);
@@ -1090,7 +1116,8 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
   static_assert(kMaxRounds == 2, "two rounds of 128 pairs per chunk");
   int pids[kMaxRounds];
 #pragma unroll
-  for (int j = 0; j < kMaxRounds; ++j) pids[j] = j < nrounds ? pair_id(j) : 0;
+  for (int j = 0; j < kMaxRounds; ++j)
+    pids[j] = j < nrounds ? min(max(pair_id(j), 0), len * a.K - 1) : 0;
   RoundIn inA, inB;
   if (nrounds > 0) load_round(pids[0], inA);
   if (nrounds > 1) load_round(pids[1], inB);
@@ -1215,7 +1242,7 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
 
 // Workspace layout of the hybrid plan (byte offsets, 256-byte aligned pieces).
 struct PlanLayout {
-  int64_t count, done, tbase, bch, nchunks, cpref, rec, kind, spos, plse, po, total;
+  int64_t count, done, err, tbase, bch, nchunks, cpref, rec, kind, spos, plse, po, total;
   int64_t ppos;
   int chunk_cap, ntiles_cap;
 };
@@ -1230,7 +1257,8 @@ inline PlanLayout plan_layout(int B, int H, int S_max, int64_t rows, int K, int 
   const int64_t nbc = (int64_t)B * nblk_cap;
   int64_t o = 0;
   L.count = o; o += nbc * 4;
-  L.done = o; o = align256(o + 4);
+  L.done = o;
+  L.err = o + 4; o = align256(o + 8);
   L.tbase = o; o = align256(o + nbc * L.ntiles_cap * 4);
   L.bch = o; o = align256(o + nbc * 4);
   L.nchunks = o; o = align256(o + (int64_t)B * 4);
@@ -1252,6 +1280,25 @@ inline PlanLayout plan_layout(int B, int H, int S_max, int64_t rows, int K, int 
 // ---------------------------------------------------------------------------
 // C entry points
 // ---------------------------------------------------------------------------
+extern "C" int dash_attn_prefill_error_offset(int B, int H, int S_max, int64_t total_rows,
+                                              int K, int D, int block_size, int64_t* offset) {
+  using namespace dash;
+  if (!offset || B < 0 || H <= 0 || S_max < 0 || total_rows < 0 || K < 0 || block_size <= 0)
+    return kErrInvalid;
+  const int nblk_cap = (S_max + block_size - 1) / block_size;
+  *offset = plan_layout(B, H, S_max, total_rows, K, D, nblk_cap, block_size).err;
+  return kOk;
+}
+
+extern "C" int dash_prefill_plan_target(int64_t chunk_cap, int64_t ppos, int64_t pos0,
+                                        int64_t block_chunk, int64_t q, int64_t* rec_chunk,
+                                        int64_t* pair_pos) {
+  using namespace dash;
+  if (!rec_chunk || !pair_pos) return kErrInvalid;
+  return scatter_target(chunk_cap, ppos, pos0, block_chunk, q, rec_chunk, pair_pos) ? kOk
+                                                                                    : kErrInvalid;
+}
+
 extern "C" int dash_attn_prefill_workspace_size(int B, int H, int S_max, int64_t total_rows,
                                                 int K, int D, int block_size, int64_t* bytes) {
   using namespace dash;
@@ -1320,6 +1367,7 @@ extern "C" int dash_attn_prefill(
     a.num_chunks = (int32_t*)(w + L.nchunks);
     a.chunk_pref = (int32_t*)(w + L.cpref);
     a.done = (int32_t*)(w + L.done);
+    a.err = (int32_t*)(w + L.err);
     a.B = B;
     a.chunk_rec = (int32_t*)(w + L.rec);
     a.chunk_cap = L.chunk_cap;
@@ -1327,7 +1375,7 @@ extern "C" int dash_attn_prefill(
     a.ppos = L.ppos;
     a.part_lse = (float*)(w + L.plse);
     a.part_o = (bf16*)(w + L.po);
-    const int ncount = (int)((L.done - L.count) / 4) + 1;     // block counters + arrival
+    const int ncount = (int)((L.err - L.count) / 4) + 1;  // block counters, arrival, error
     hipLaunchKernelGGL(prefill_clear_kernel, dim3((ncount + 255) / 256), dim3(256), 0, st,
                        a.blk_count, ncount);
     hipLaunchKernelGGL(prefill_plan_kernel, dim3(ntiles, B), dim3(kPfTQ), 0, st, a);

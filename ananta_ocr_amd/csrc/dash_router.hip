@@ -978,7 +978,7 @@ constexpr int kDrMaxBlocks = 2048;
 struct DecodeRouteArgs {
   const float* idx_q; int64_t iq_sb;
   const float* idx_k; SeqLayout lay_k;
-  const int32_t* lens; int S;
+  const int32_t* lens; const int32_t* q_pos; int S;
   const float* head_cls; int refresh_tail;
   int skip_tail;                     // the scores read no k_bar row past the last remote block
   float* kbar; int64_t kb_sb; int nblk_cap;
@@ -1075,9 +1075,10 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
   __shared__ int s_selk[kMaxM];
 
   const int tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
-  const int len = a.lens ? a.lens[b] : a.S;
-  const int nblk = len > 0 ? (len + a.bs - 1) / a.bs : 0;
-  const int qp = len - 1;
+  const int len = a.lens ? min(max(a.lens[b], 0), a.S) : a.S;
+  const int nblk = len > 0 ? (len + a.bs - 1) / a.bs : 0;     // <= nblk_cap (host check)
+  // the query position, at most the last cached token (so the tail block is never remote)
+  const int qp = a.q_pos ? min(a.q_pos[b], len - 1) : len - 1;
   const int lim = (qp >= 0 ? qp / a.bs : -1) - a.local_blocks;
   const int ct = nblk - 1;               // tail block
   constexpr bool own_refresh = mode == kRouteAll;   // and a.refresh_tail, at each use
@@ -1417,8 +1418,8 @@ namespace dash {
 static int decode_route_args(const float* idx_q, int64_t iq_sb, const float* idx_k,
                                  int64_t ik_sb, int64_t ik_st, int64_t ik_sp,
                                  const int32_t* block_table, int64_t table_stride,
-                                 int page_size, const int32_t* seq_lens, int S,
-                                 const float* head_cls, int refresh_tail, float* kbar,
+                                 int page_size, const int32_t* seq_lens, const int32_t* q_pos,
+                                 int S, const float* head_cls, int refresh_tail, float* kbar,
                                  int64_t kb_sb, int nblk_cap, const uint8_t* cand,
                                  int64_t cand_stride, int B, int d, int block_size,
                                  int local_blocks, float idx_scale, float floor_p, float sigma,
@@ -1430,6 +1431,9 @@ static int decode_route_args(const float* idx_q, int64_t iq_sb, const float* idx
   if (K < 1 || Kout < std::min(K, topm)) return kErrInvalid;
   if (nblk_cap <= 0 || nblk_cap > kDrMaxBlocks) return kErrUnsupported;
   if (block_table && page_size <= 0) return kErrInvalid;
+  // S bounds every sequence's length (the kernels clamp lens to it), so the k_bar
+  // cache and the score rows must hold ceil(S / block_size) blocks
+  if (S < 0 || ((int64_t)S + block_size - 1) / block_size > nblk_cap) return kErrInvalid;
   if (d % 16 != 0 || kb_sb % 4 != 0 || (uintptr_t)kbar % 16 != 0) return kErrUnsupported;
   if (ik_st % 4 != 0 || ik_sp % 4 != 0 || ik_sb % 4 != 0 || (uintptr_t)idx_k % 16 != 0 ||
       (uintptr_t)head_cls % 16 != 0)
@@ -1437,7 +1441,7 @@ static int decode_route_args(const float* idx_q, int64_t iq_sb, const float* idx
   a.idx_q = idx_q; a.iq_sb = iq_sb;
   a.idx_k = idx_k;
   a.lay_k = SeqLayout{nullptr, block_table, table_stride, ik_sb, ik_sp, ik_st, page_size};
-  a.lens = seq_lens; a.S = S;
+  a.lens = seq_lens; a.q_pos = q_pos; a.S = S;
   a.head_cls = head_cls; a.refresh_tail = refresh_tail; a.skip_tail = 0;
   a.kbar = kbar; a.kb_sb = kb_sb; a.nblk_cap = nblk_cap;
   a.cand = cand; a.cand_stride = cand_stride;
@@ -1454,8 +1458,8 @@ static int decode_route_args(const float* idx_q, int64_t iq_sb, const float* idx
 extern "C" int dash_decode_route(const float* idx_q, int64_t iq_sb, const float* idx_k,
                                  int64_t ik_sb, int64_t ik_st, int64_t ik_sp,
                                  const int32_t* block_table, int64_t table_stride,
-                                 int page_size, const int32_t* seq_lens, int S,
-                                 const float* head_cls, int refresh_tail, float* kbar,
+                                 int page_size, const int32_t* seq_lens, const int32_t* q_pos,
+                                 int S, const float* head_cls, int refresh_tail, float* kbar,
                                  int64_t kb_sb, int nblk_cap, const uint8_t* cand,
                                  int64_t cand_stride, int B, int d, int block_size,
                                  int local_blocks, float idx_scale, float floor_p, float sigma,
@@ -1464,7 +1468,7 @@ extern "C" int dash_decode_route(const float* idx_q, int64_t iq_sb, const float*
   using namespace dash;
   DecodeRouteArgs a;
   const int st = decode_route_args(idx_q, iq_sb, idx_k, ik_sb, ik_st, ik_sp, block_table, table_stride,
-                                   page_size, seq_lens, S, head_cls, refresh_tail, kbar, kb_sb,
+                                   page_size, seq_lens, q_pos, S, head_cls, refresh_tail, kbar, kb_sb,
                                    nblk_cap, cand, cand_stride, B, d, block_size, local_blocks,
                                    idx_scale, floor_p, sigma, K, topm, Kout, idx, bias, valid, z,
                                    z_stride, a);
@@ -1490,7 +1494,8 @@ extern "C" int dash_decode_step_workspace_size(int B, int H, int D, int block_si
 extern "C" int dash_decode_step(
     const float* idx_q, int64_t iq_sb, const float* idx_k, int64_t ik_sb, int64_t ik_st,
     int64_t ik_sp, const int32_t* block_table, int64_t table_stride, int page_size,
-    const int32_t* seq_lens, int S, const float* head_cls, int refresh_tail, float* kbar,
+    const int32_t* seq_lens, const int32_t* q_pos, int S, const float* head_cls,
+    int refresh_tail, float* kbar,
     int64_t kb_sb, int nblk_cap, const uint8_t* cand, int64_t cand_stride, int d,
     int local_blocks, float idx_scale, float floor_p, float sigma, int K, int topm, int Kout,
     int32_t* idx, float* bias, uint8_t* valid, float* z, int64_t z_stride,
@@ -1503,7 +1508,7 @@ extern "C" int dash_decode_step(
   using namespace dash;
   DecodeRouteArgs ra;
   const int rs = decode_route_args(idx_q, iq_sb, idx_k, ik_sb, ik_st, ik_sp, block_table,
-                                   table_stride, page_size, seq_lens, S, head_cls, refresh_tail,
+                                   table_stride, page_size, seq_lens, q_pos, S, head_cls, refresh_tail,
                                    kbar, kb_sb, nblk_cap, cand, cand_stride, B, d, block_size,
                                    local_blocks, idx_scale, floor_p, sigma, K, topm, Kout, idx, bias,
                                    valid, z, z_stride, ra);
@@ -1532,7 +1537,7 @@ extern "C" int dash_decode_step(
   a.k_sb = k_sb; a.k_sh = k_sh; a.k_st = k_st; a.k_sp = k_sp;
   a.v_sb = v_sb; a.v_sh = v_sh; a.v_st = v_st; a.v_sp = v_sp;
   a.table = block_table; a.table_stride = table_stride; a.page = page_size;
-  a.lens = seq_lens; a.q_pos = nullptr;
+  a.lens = seq_lens; a.q_pos = q_pos;
   a.idx = idx; a.valid = valid; a.bias = bias; a.K = Kout;
   a.out = out; a.out_bf16 = out_bf16; a.o_sb = o_sb; a.o_sh = o_sh;
   a.lse = lse; a.lse_sb = lse_sb; a.lse_sh = lse_sh;

@@ -112,13 +112,15 @@ class DashAttention(nn.Module):
         ik = torch.nan_to_num(ik[:, 0].float(), nan=0.0, posinf=0.0, neginf=0.0)
         return iq, ik
 
-    def block_scores(self, idx_q, idx_k, q_pos=None, nblk=None):
-        """[B,Lq,nblk] fp32 remote block scores (modeling_deepseekv2.py:351-400)."""
+    def block_scores(self, idx_q, idx_k, q_pos=None, nblk=None, kbar=None):
+        """[B,Lq,nblk] fp32 remote block scores (modeling_deepseekv2.py:351-400).
+        kbar: the block summaries of idx_k when the caller already holds them."""
         B, S, d = idx_k.shape
         if nblk is None:
             nblk = (S + self.block_size - 1) // self.block_size
         if self.stage0 == "head_cls":
-            kb = ops.kbar(idx_k, self.head_cls.detach(), self.block_size, nblk_cap=nblk)
+            kb = kbar[:, :nblk] if kbar is not None else \
+                ops.kbar(idx_k, self.head_cls.detach(), self.block_size, nblk_cap=nblk)
             return ops.block_scores(idx_q, kb, self.block_size, self.local_blocks, q_pos=q_pos,
                                     S=S)
         Lq = idx_q.shape[1]
@@ -133,33 +135,50 @@ class DashAttention(nn.Module):
         return ops.route(block_scores, block_cand, p["idx_scale"], p["floor"], p["sigma"],
                          p["K"], p["topm"])
 
+    # ---------------------------------------------------------------- attend
+    def _forward_triton(self, q, k, v, topi, blk_bias, valid, S, nblk, position_ids):
+        """Fused block-sparse attention of routed (topi, blk_bias, valid) [B,S,K] plus the
+        token window (dash_attention.py:962-978): invalid slots become -1 and the call
+        goes to the gather-attention entry point, which returns None on the inputs the
+        reference's kernel refuses (non-arange positions, key length != query length)."""
+        from .sparse_gather import triton_gather_attention_e2e
+        block_indices = topi.masked_fill(~valid.bool(), -1).to(torch.int32).unsqueeze(1)
+        if position_ids is None:
+            position_ids = torch.arange(S, device=q.device)[None].expand(q.shape[0], -1)
+        return triton_gather_attention_e2e(q, k, v, block_indices, blk_bias, position_ids, None,
+                                           self.block_size, self._scale, self.local_window)
+
+    def _forward_dense(self, q, k, v, topi, blk_bias, valid, S, nblk, attention_mask):
+        """The same attention over token positions 0..S-1 (dash_attention.py:980-1006:
+        window keys with bias 0, keys of valid routed blocks below the window with the
+        block's bias).  An additive attention_mask is not supported by the kernels and
+        raises NotImplementedError (there is no second code path)."""
+        if attention_mask is not None:
+            raise NotImplementedError("additive attention_mask is not supported by the HIP path")
+        if k.shape[2] != S or q.shape[2] != S:
+            raise NotImplementedError("query and key lengths must both be S")
+        if k.shape[1] != q.shape[1]:
+            rep = q.shape[1] // k.shape[1]
+            k = k.repeat_interleave(rep, dim=1)
+            v = v.repeat_interleave(rep, dim=1)
+        out = ops.attn_prefill(q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16),
+                               topi, blk_bias, valid, self.block_size, self.local_window,
+                               self._scale)
+        return out.to(q.dtype)
+
     # ---------------------------------------------------------------- forward
     def forward(self, hidden_states, q, k, v, position_embeddings=None, position_ids=None,
                 attention_mask=None, image_block_mask=None, block_cand=None, page_ids=None):
         """hidden_states [B,S,hidden]; q,k,v [B,H,S,D] (RoPE'd, GQA-expanded).
-        Returns [B,H,S,D] in q.dtype (dash_attention.py:1008-1071).  page_ids is
-        accepted for signature compatibility (the reference uses it for logs only)."""
-        if attention_mask is not None:
-            raise NotImplementedError("additive attention_mask is not supported by the HIP path")
-        if torch.is_grad_enabled() and any(t.requires_grad for t in (hidden_states, q, k, v)):
-            raise NotImplementedError("DASH HIP attention is forward-only")
-        if not q.is_cuda:
-            raise ValueError("DashAttention runs on the GPU (no CPU path)")
-        B, H, S, D = q.shape
-        nblk = (S + self.block_size - 1) // self.block_size
-        if position_ids is not None:
-            ar = torch.arange(S, device=q.device)
-            if not bool((position_ids == ar).all()):
-                raise NotImplementedError("position_ids must be 0..S-1 (packed rows: use "
-                                          "ops.attn_prefill with cu_seqlens)")
-        with torch.no_grad():
-            iq, ik = self.router_qk(hidden_states, position_embeddings)
-            sc = self.block_scores(iq, ik, nblk=nblk)
-            cand = block_cand
-            if cand is None and self.image_only and image_block_mask is not None:
-                cand = image_block_mask[:, None, :].expand(B, S, nblk)
-            topi, bias, valid = self.route(sc, cand)
-            out = ops.attn_prefill(q.to(torch.bfloat16), k.to(torch.bfloat16),
-                                   v.to(torch.bfloat16), topi, bias, valid, self.block_size,
-                                   self.local_window, self._scale)
-        return out.to(q.dtype)
+        Returns [B,H,S,D] in q.dtype (dash_attention.py:1008-1071).
+
+        The reference's forward routes with its training router: 1.5-entmax over
+        every block of the row (dash_attention.py:906-930) and the top k of the masked
+        prior under a global k schedule (:932-960).  This module implements the
+        inference router only (modeling_deepseekv2.py:403-421, reached through
+        ``modeling_deepseekv2._infer_prefill_attend``), so ``forward`` raises
+        NotImplementedError instead of silently routing another way."""
+        raise NotImplementedError(
+            "DashAttention.forward routes with the training router (full-width entmax, "
+            "k schedule), which the HIP path does not implement; enable inference routing "
+            "(configure_dash_inference) and call _infer_prefill_attend")

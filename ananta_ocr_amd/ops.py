@@ -354,8 +354,9 @@ def attn_decode(q, k, v, idx, bias, valid, block_size, local_window, scale, seq_
 def decode_route(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, idx_scale,
                  floor, sigma, K, topm, seq_lens=None, block_table=None, page_size=None,
                  cand=None, refresh_tail=True, width=None, return_scores=False,
-                 valid_dtype=torch.bool):
-    """Decode routing for one query per sequence (the last cached token): refreshes the
+                 valid_dtype=torch.bool, q_pos=None):
+    """Decode routing for one query per sequence (at q_pos [B], default the last cached
+    token; positions past it are taken as it): refreshes the
     tail block of `kbar_cache` [B, nblk_cap, d] in place, scores and routes.
     idx_q [B,d] or [B,1,d]; idx_k contiguous [B,S,d] or paged [pages, page_size, d].
     Returns idx int32 [B,1,K'], bias fp32, valid (bool, or valid_dtype) and with
@@ -388,9 +389,11 @@ def decode_route(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, i
     lens = _i32(seq_lens)
     c2 = None if cand is None else _u8(cand.reshape(B, -1))
     hc = head_cls.float().contiguous()
+    qp = None if q_pos is None else _i32(q_pos.reshape(B))
     st_ = lib.dash_decode_route(
         _ptr(idx_q), idx_q.stride(0), _ptr(idx_k), sb, st, sp, _ptr(bt),
-        0 if bt is None else bt.stride(0), int(page_size or 0), _ptr(lens), S, _ptr(hc),
+        0 if bt is None else bt.stride(0), int(page_size or 0), _ptr(lens), _ptr(qp), S,
+        _ptr(hc),
         int(bool(refresh_tail)), _ptr(kbar_cache), kbar_cache.stride(0), nblk_cap, _ptr(c2),
         0 if c2 is None else c2.stride(0), B, d, int(block_size), int(local_blocks),
         float(idx_scale), float(floor), float(sigma), int(K), int(topm), Kw, _ptr(idx),
@@ -404,11 +407,12 @@ def decode_route(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, i
 def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks,
                       idx_scale, floor, sigma, K, topm, scale, seq_lens=None, block_table=None,
                       page_size=None, cand=None, width=None, out_dtype=torch.float32,
-                      return_lse=False):
+                      return_lse=False, q_pos=None, workspace=None, return_scores=False):
     """decode_route followed by attn_decode of its routing, in two launches: the window
     part of the attention runs beside the router.  Same arguments and results as those
     two calls (q [B,H,D] or [B,H,1,D]; out [B,H,D]); returns (out, (idx, bias, valid))
-    with idx/bias/valid [B,1,K'] (valid uint8), or (out, lse, routing) with return_lse."""
+    with idx/bias/valid [B,1,K'] (valid uint8), or (out, lse, routing) with return_lse;
+    return_scores appends the block scores z [B, nblk_cap] the router computed."""
     _need_gpu(q, k, v, idx_q, idx_k, kbar_cache)
     lib = _lib.load()
     squeeze = q.dim() == 4
@@ -457,10 +461,17 @@ def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, l
     ws_bytes = ctypes.c_int64(0)
     _lib.check(lib.dash_decode_step_workspace_size(B, H, D, int(block_size), lw, ws_bytes),
                "workspace")
-    ws = torch.empty((ws_bytes.value + 3) // 4, dtype=torch.float32, device=dev)
+    if workspace is None:
+        ws = torch.empty((ws_bytes.value + 3) // 4, dtype=torch.float32, device=dev)
+    else:
+        ws = workspace
+        if ws.numel() * ws.element_size() < ws_bytes.value:
+            raise ValueError("decode step workspace too small")
+    qp = None if q_pos is None else _i32(q_pos.reshape(B))
     st_ = lib.dash_decode_step(
         _ptr(idx_q), idx_q.stride(0), _ptr(idx_k), isb, ist, isp, _ptr(bt), bt_stride,
-        int(page_size or 0), _ptr(lens), S, _ptr(hc), 1, _ptr(kbar_cache), kbar_cache.stride(0),
+        int(page_size or 0), _ptr(lens), _ptr(qp), S, _ptr(hc), 1, _ptr(kbar_cache),
+        kbar_cache.stride(0),
         nblk_cap, _ptr(c2), 0 if c2 is None else c2.stride(0), d, int(local_blocks),
         float(idx_scale), float(floor), float(sigma), int(K), int(topm), Kw, _ptr(idx),
         _ptr(bias), _ptr(valid), _ptr(z), z.stride(0),
@@ -468,12 +479,14 @@ def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, l
         _ptr(k), k_sb, k_sh, k_st, k_sp, _ptr(v), v_sb, v_sh, v_st, v_sp,
         _ptr(out), int(out_dtype == torch.bfloat16), out.stride(0), out.stride(1),
         _ptr(lse), 0 if lse is None else lse.stride(0), 1,
-        B, H, D, int(block_size), lw, float(scale), _ptr(ws), ws.numel() * 4, _stream())
+        B, H, D, int(block_size), lw, float(scale), _ptr(ws), ws.numel() * ws.element_size(),
+        _stream())
     _lib.check(st_, "dash_decode_step")
     if squeeze:
         out = out[:, :, None]
     routing = (idx[:, None], bias[:, None], valid[:, None])
-    return (out, lse, routing) if return_lse else (out, routing)
+    res = (out, lse, routing) if return_lse else (out, routing)
+    return res + (z,) if return_scores else res
 
 
 def inv_sqrt(d):

@@ -56,12 +56,13 @@ def init_decode_state(idx_k, head_cls, block_size, nblk_cap, seq_lens=None, bloc
 def decode_step(state, q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks, idx_scale,
                 floor, sigma, K, topm, scale=None, seq_lens=None, block_table=None,
                 page_size=None, out_dtype=torch.float32, nsplit=None, block_cand=None,
-                return_routing=False, fused=None):
+                return_routing=False, fused=None, return_scores=False):
     """One decode step for the query at the last cached token of each sequence.
     The newest token is already in k/v and idx_k; its block's summary is refreshed
     inside the fused decode router.  fused (default: whenever nsplit is not given and
     the shapes allow it) runs the window part of the attention beside the router
-    (ops.decode_step_fused); otherwise decode_route then attn_decode."""
+    (ops.decode_step_fused); otherwise decode_route then attn_decode.  return_scores
+    (with return_routing) also returns the block scores [B, nblk_cap] of the router."""
     D = q.shape[-1]
     if scale is None:
         scale = 1.0 / math.sqrt(D)
@@ -71,24 +72,27 @@ def decode_step(state, q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks
         fused = nsplit is None and D == 128 and min(int(K), int(topm)) <= 16 and \
             npw + max(1, min(int(K), int(topm))) <= 64
     if fused:
-        out, (idx, bias, valid) = ops.decode_step_fused(
+        out, (idx, bias, valid), z = ops.decode_step_fused(
             q, k, v, idx_q, idx_k, head_cls, state.kbar, block_size, local_blocks, idx_scale,
             floor, sigma, K, topm, scale, seq_lens=seq_lens, block_table=block_table,
-            page_size=page_size, cand=block_cand, width=width, out_dtype=out_dtype)
+            page_size=page_size, cand=block_cand, width=width, out_dtype=out_dtype,
+            return_scores=True)
         if return_routing:
-            return out, (idx, bias, valid.bool())
+            res = (out, (idx, bias, valid.bool()))
+            return res + (z,) if return_scores else res
         return out
-    idx, bias, valid = ops.decode_route(idx_q, idx_k, head_cls, state.kbar, block_size,
-                                        local_blocks, idx_scale, floor, sigma, K, topm,
-                                        seq_lens=seq_lens, block_table=block_table,
-                                        page_size=page_size, cand=block_cand, width=width,
-                                        valid_dtype=torch.uint8)
+    idx, bias, valid, z = ops.decode_route(idx_q, idx_k, head_cls, state.kbar, block_size,
+                                           local_blocks, idx_scale, floor, sigma, K, topm,
+                                           seq_lens=seq_lens, block_table=block_table,
+                                           page_size=page_size, cand=block_cand, width=width,
+                                           valid_dtype=torch.uint8, return_scores=True)
     out = ops.attn_decode(q, k, v, idx[:, 0], bias[:, 0], valid[:, 0], block_size,
                           local_blocks * block_size, scale, seq_lens=seq_lens,
                           block_table=block_table, page_size=page_size, out_dtype=out_dtype,
                           nsplit=nsplit)
     if return_routing:
-        return out, (idx, bias, valid.bool())
+        res = (out, (idx, bias, valid.bool()))
+        return res + (z,) if return_scores else res
     return out
 
 

@@ -149,9 +149,31 @@ int dash_attn_prefill_workspace_size(int B, int H, int S_max, int64_t total_rows
                                      int block_size, int64_t* bytes);
 
 /*
- * Decode router, one query per sequence (the last cached token, q_pos = seq_lens[b]-1):
+ * Byte offset, inside a dash_attn_prefill workspace of these sizes, of the plan's int32
+ * error word: 0 after a call whose pair counts fit the workspace; nonzero if a chunk
+ * record or partial position would have fallen outside it (such writes are skipped and
+ * the affected pairs contribute nothing).  Cleared at the start of every call.  No
+ * counterpart in the reference (its Triton kernels keep no plan).
+ */
+int dash_attn_prefill_error_offset(int B, int H, int S_max, int64_t total_rows, int K, int D,
+                                   int block_size, int64_t* offset);
+
+/*
+ * Host-side form of the scatter kernel's bounds rule (the same function runs in the
+ * kernel): the chunk record and partial position of the q-th sparse pair of a block whose
+ * chunks start at block_chunk, for a sequence whose pair positions start at pos0.
+ * Returns 0 if both fall inside (chunk_cap records, ppos positions), else -3.  Host code
+ * only (no device pointers): for checks of the plan arithmetic without a GPU.
+ */
+int dash_prefill_plan_target(int64_t chunk_cap, int64_t ppos, int64_t pos0, int64_t block_chunk,
+                             int64_t q, int64_t* rec_chunk, int64_t* pair_pos);
+
+/*
+ * Decode router, one query per sequence at q_pos[b] (NULL: the last cached token,
+ * seq_lens[b]-1; a position past the last cached token is taken as that token):
  * refreshes k_bar of the tail block (refresh_tail = 1), scores every block of the
- * sequence and routes the row exactly as dash_route does.  Replaces the decode routing of
+ * sequence (remote: c <= q_pos[b] / block_size - local_blocks) and routes the row exactly
+ * as dash_route does.  Replaces the decode routing of
  * _dash_decode_forward (modeling_deepseekv2.py:481-496: _block_scores_infer over the whole
  * index-key cache + _infer_route_select), keeping the summaries of complete blocks cached.
  *   idx_q    fp32 [B, d] rows (iq_sb); idx_k index-key cache addressed like dash_kbar
@@ -165,7 +187,8 @@ int dash_attn_prefill_workspace_size(int B, int H, int S_max, int64_t total_rows
 int dash_decode_route(const float* idx_q, int64_t iq_sb, const float* idx_k,
                       int64_t ik_sb, int64_t ik_st, int64_t ik_sp,
                       const int32_t* block_table, int64_t table_stride, int page_size,
-                      const int32_t* seq_lens, int S, const float* head_cls, int refresh_tail,
+                      const int32_t* seq_lens, const int32_t* q_pos, int S,
+                      const float* head_cls, int refresh_tail,
                       float* kbar, int64_t kb_sb, int nblk_cap, const uint8_t* cand,
                       int64_t cand_stride, int B, int d, int block_size, int local_blocks,
                       float idx_scale, float floor_p, float sigma, int K, int topm, int Kout,
@@ -203,7 +226,7 @@ int dash_decode_step_workspace_size(int B, int H, int D, int block_size, int loc
 
 /*
  * One decode step: dash_decode_route followed by dash_attn_decode of its routing for
- * the query at seq_lens[b]-1, the way _dash_decode_forward (modeling_deepseekv2.py:
+ * the query at q_pos[b] (NULL: seq_lens[b]-1), the way _dash_decode_forward (modeling_deepseekv2.py:
  * 454-500) chains _infer_route_select and _decode_attend.  The router arguments are
  * those of dash_decode_route (idx/bias/valid/z are its outputs, [B, Kout]); the
  * attention arguments those of dash_attn_decode with K = Kout.  The window part of the
@@ -214,7 +237,8 @@ int dash_decode_step_workspace_size(int B, int H, int D, int block_size, int loc
  */
 int dash_decode_step(const float* idx_q, int64_t iq_sb, const float* idx_k, int64_t ik_sb,
                      int64_t ik_st, int64_t ik_sp, const int32_t* block_table,
-                     int64_t table_stride, int page_size, const int32_t* seq_lens, int S,
+                     int64_t table_stride, int page_size, const int32_t* seq_lens,
+                     const int32_t* q_pos, int S,
                      const float* head_cls, int refresh_tail, float* kbar, int64_t kb_sb,
                      int nblk_cap, const uint8_t* cand, int64_t cand_stride, int d,
                      int local_blocks, float idx_scale, float floor_p, float sigma, int K,

@@ -46,8 +46,11 @@ def test_dash_attention_forward_matches_oracle(stage0):
     k = (torch.randn(B, H, S, 128, generator=g) * 0.5).bfloat16()
     v = torch.randn(B, H, S, 128, generator=g).bfloat16()
     mod_gpu = mod.to(DEV)
+    layer = SimpleNamespace(layer_idx=0)
+    pos = torch.arange(S, device=DEV)[None]
     with torch.no_grad():
-        out = mod_gpu(hs.to(DEV), q.to(DEV), k.to(DEV), v.to(DEV))
+        out = MD._infer_prefill_attend(layer, mod_gpu, hs.to(DEV), q.to(DEV), k.to(DEV),
+                                       v.to(DEV), None, pos, None, None, None)
         iq, ik = mod_gpu.router_qk(hs.to(DEV))
         sc = mod_gpu.block_scores(iq, ik)
         ti, bi, va = mod_gpu.route(sc)
@@ -81,8 +84,10 @@ def test_dash_attention_candidate_mask_and_errors():
     v = torch.randn(B, H, S, 128, device=DEV).bfloat16()
     nblk = (S + 63) // 64
     cand = torch.rand(B, S, nblk, device=DEV) < 0.5
+    layer = SimpleNamespace(layer_idx=0)
+    pos = torch.arange(S, device=DEV)[None]
     with torch.no_grad():
-        out = mod(hs, q, k, v, block_cand=cand)
+        out = MD._infer_prefill_attend(layer, mod, hs, q, k, v, None, pos, cand, None, None)
         iq, ik = mod.router_qk(hs)
         sc = mod.block_scores(iq, ik)
     p = mod._infer_params
@@ -91,7 +96,10 @@ def test_dash_attention_candidate_mask_and_errors():
     ref = O.dense_attend(q.cpu(), k.cpu(), v.cpu(), t_r, b_r, v_r, 64, 256, 1 / math.sqrt(128))
     _close(out, ref, "DashAttention block_cand")
     with pytest.raises(NotImplementedError):
-        mod(hs, q, k, v, attention_mask=torch.zeros(1, 1, S, S, device=DEV))
+        MD._infer_prefill_attend(layer, mod, hs, q, k, v, None, pos, None,
+                                 torch.zeros(1, 1, S, S, device=DEV), None)
+    with pytest.raises(NotImplementedError):          # the training router is not provided
+        mod(hs, q, k, v)
 
 
 def test_gather_attention_e2e_matches_oracle_and_returns_none():

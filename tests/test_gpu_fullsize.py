@@ -171,3 +171,33 @@ def test_paged_decode_32_sequences_full_size():
                               torch.tensor([[L - 1]]), cfg.bs, cfg.lw, SCALE)
         _close(out[b:b + 1], ref[:, :, 0], f"decode sequence {b} ({L} tokens)")
     assert ties <= 2, f"{ties} sequences with near-tied routing"
+
+
+def test_decode_b8_27300_full_size():
+    """The B = 8 decode step at its full size (8 x 27,300 contiguous cached tokens,
+    block 64, window 1,024, cap 16) through pipeline.decode_step, the fused step the
+    benchmark times: block summaries and scores within fp32 tolerance, routing bit for
+    bit on the GPU's own scores, attention within the output tolerance."""
+    cfg = W.DECODE_B8
+    d = W.make_decode(cfg)
+    lb = cfg.lw // cfg.bs
+    hc = torch.zeros(128)
+    nblk = (cfg.S + cfg.bs - 1) // cfg.bs
+    print(f"decode {cfg.name}: B={cfg.B}, S={cfg.S}", flush=True)
+    st = pipeline.init_decode_state(d["idx_k"].to(DEV), hc.to(DEV), cfg.bs, nblk)
+    out, (ti, bi, va), z = pipeline.decode_step(
+        st, d["q"].to(DEV), d["k"].to(DEV), d["v"].to(DEV), d["idx_q"].to(DEV),
+        d["idx_k"].to(DEV), hc.to(DEV), cfg.bs, lb, W.IDX_SCALE, W.FLOOR, W.SIGMA, cfg.cap,
+        cfg.cap, SCALE, return_routing=True, return_scores=True)
+    kb_r, cv = O.kbar_headcls(d["idx_k"], hc, cfg.bs)
+    torch.testing.assert_close(st.kbar.cpu(), kb_r, atol=1e-6, rtol=1e-5)
+    qpos = torch.full((cfg.B, 1), cfg.S - 1)
+    z_r = O.block_scores_headcls(d["idx_q"], kb_r, cv, qpos, cfg.bs, lb)
+    zg = z.cpu()[:, None, :nblk]
+    _scores_close(zg, z_r, "decode scores")
+    t_r, b_r, v_r = _route_equal(zg, ti.cpu().long(), bi.cpu(), va.cpu(), cfg.cap, cfg.cap,
+                                 "decode routing")
+    assert v_r.any()
+    ref = O.decode_attend(d["q"][:, :, None], d["k"], d["v"], t_r, b_r, v_r, qpos, cfg.bs,
+                          cfg.lw, SCALE)
+    _close(out, ref[:, :, 0], "decode B=8 x 27,300")

@@ -690,3 +690,79 @@ def test_decode_graph_replays_match_eager():
         out = g.replay().clone()
         torch.cuda.synchronize()
         assert torch.equal(out, ref2), f"replay with new query {i}"
+
+
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("paged", [False, True])
+def test_decode_checkpoint_config_matches_oracle(paged, fused):
+    """Decode at the shipped checkpoint's router configuration (config.json: block 32,
+    local blocks 4 = window 128, dash_topk_blocks 12, topm 16, learned head_cls) on
+    sequences of several lengths, contiguous or paged (pages of 32 tokens in a random
+    physical order), fused step or router + split-K: block summaries and scores within
+    fp32 tolerance, routing bit for bit on the GPU's own scores, attention within the
+    output tolerance."""
+    from ananta_ocr_amd import pipeline
+    bs, lb, K, topm, H, d = 32, 4, 12, 16, 4, 128
+    lw = lb * bs
+    lens = [5000, 97, 129, 1, 2048, 3333]
+    B, S = len(lens), max(lens)
+    g = _gen(880 + 2 * int(paged) + int(fused))
+    k = (torch.randn(B, H, S, 128, generator=g) / math.sqrt(128)).bfloat16()
+    v = torch.randn(B, H, S, 128, generator=g).bfloat16()
+    q = (torch.randn(B, H, 128, generator=g) * 2).bfloat16()
+    ik = torch.randn(B, S, d, generator=g)
+    iq = torch.randn(B, d, generator=g)
+    hc = torch.randn(d, generator=g) * 0.3
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    kw = dict(seq_lens=lens_t.to(DEV))
+    nblk = (S + bs - 1) // bs
+    if paged:
+        npg = [(L + bs - 1) // bs for L in lens]
+        perm = torch.randperm(sum(npg), generator=g)
+        table = torch.zeros(B, max(npg), dtype=torch.int32)
+        kp = torch.zeros(sum(npg), bs, H, 128, dtype=torch.bfloat16)
+        vp = torch.zeros_like(kp)
+        ikp = torch.zeros(sum(npg), bs, d)
+        o = 0
+        for b in range(B):
+            for pg in range(npg[b]):
+                phys = int(perm[o + pg])
+                table[b, pg] = phys
+                seg = slice(pg * bs, min((pg + 1) * bs, lens[b]))
+                n = seg.stop - seg.start
+                kp[phys, :n] = k[b, :, seg].transpose(0, 1)
+                vp[phys, :n] = v[b, :, seg].transpose(0, 1)
+                ikp[phys, :n] = ik[b, seg]
+            o += npg[b]
+        kd, vd, ikd = kp.to(DEV), vp.to(DEV), ikp.to(DEV)
+        kw.update(block_table=table.to(DEV), page_size=bs)
+        nblk = max(npg)
+    else:
+        kd, vd, ikd = k.to(DEV), v.to(DEV), ik.to(DEV)
+    st = pipeline.init_decode_state(ikd, hc.to(DEV), bs, nblk, **kw)
+    idx_scale = 128.0 / math.sqrt(128)
+    out, (ti, bi, va), z = pipeline.decode_step(
+        st, q.to(DEV), kd, vd, iq.to(DEV), ikd, hc.to(DEV), bs, lb, idx_scale, 1e-4, 1.0, K,
+        topm, 1 / math.sqrt(128), return_routing=True, fused=fused, return_scores=True, **kw)
+    out, ti, bi, va, z, kbar = out.cpu(), ti.cpu().long(), bi.cpu(), va.cpu(), z.cpu(), \
+        st.kbar.cpu()
+    Kp = ti.shape[-1]
+    for b, L in enumerate(lens):
+        kb_r, cv = O.kbar_headcls(ik[b:b + 1, :L], hc, bs)
+        nb = kb_r.shape[1]
+        torch.testing.assert_close(kbar[b:b + 1, :nb], kb_r, atol=1e-5, rtol=1e-5)
+        z_r = O.block_scores_headcls(iq[b:b + 1, None], kb_r, cv, torch.tensor([[L - 1]]), bs,
+                                     lb)
+        zb = z[b:b + 1, None, :nb]
+        sent = z_r < -5e8
+        assert torch.equal(zb < -5e8, sent), f"sequence {b}: sentinel pattern"
+        torch.testing.assert_close(zb[~sent], z_r[~sent], atol=2e-5, rtol=2e-5)
+        t_r, b_r, v_r = O.infer_route_select(zb, None, idx_scale, 1e-4, 1.0, K, topm)
+        kp_ = t_r.shape[-1]
+        assert torch.equal(ti[b:b + 1, :, :kp_], t_r), f"sequence {b}: routed ids"
+        assert torch.equal(va[b:b + 1, :, :kp_], v_r), f"sequence {b}: validity"
+        torch.testing.assert_close(bi[b:b + 1, :, :kp_], b_r, atol=2e-5, rtol=1e-5)
+        assert bool((ti[b, :, kp_:Kp] == -1).all())
+        ref = O.decode_attend(q[b:b + 1, :, None].float(), k[b:b + 1, :, :L], v[b:b + 1, :, :L],
+                              t_r, b_r, v_r, torch.tensor([[L - 1]]), bs, lw, 1 / math.sqrt(128))
+        _close(out[b:b + 1], ref[:, :, 0], f"decode bs 32 sequence {b} ({L} tokens)")
