@@ -45,6 +45,12 @@ SIGNATURES = {
                               _p, _l, _i, _i, _f, _f, _f, _i, _i, _i, _p, _p, _p, _p, _l,
                               _p, _l, _l, _p, _l, _l, _l, _l, _p, _l, _l, _l, _l,
                               _p, _i, _l, _l, _p, _l, _l, _i, _i, _i, _i, _i, _f, _p, _l, _p]),
+    "dash_decode_step_noalloc": (_i, [_p, _l, _p, _l, _l, _l, _p, _l, _i, _p, _p, _i, _p, _i, _p,
+                                      _l, _i, _p, _l, _i, _i, _f, _f, _f, _i, _i, _i, _p, _p, _p,
+                                      _p, _l, _p, _l, _l, _p, _l, _l, _l, _l, _p, _l, _l, _l,
+                                      _l, _p, _i, _l, _l, _p, _l, _l, _i, _i, _i, _i, _i, _f,
+                                      _p]),
+    "dash_decode_step_scratch_bytes": (_l, []),
 }
 
 _LIB = None

@@ -9,6 +9,8 @@ extern "C" const char* dash_status_string(int status) {
     case dash::kErrUnsupported: return "unsupported shape or parameter";
     case dash::kErrInvalid: return "invalid argument";
     case dash::kErrWorkspace: return "workspace too small";
+    case dash::kErrScratch:
+      return "sizes exceed the fixed 64 MiB scratch of the allocation-free entry point";
     default: break;
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);

@@ -29,6 +29,7 @@ enum Status : int {
   kErrUnsupported = -2,   // a shape or parameter the library does not implement
   kErrInvalid = -3,       // inconsistent arguments (null pointer, negative size...)
   kErrWorkspace = -4,     // caller-provided workspace too small
+  kErrScratch = -5,       // beyond the fixed scratch of the allocation-free entry point
 };
 
 __device__ __forceinline__ float bf2f(bf16 x) { return (float)x; }

@@ -11,6 +11,9 @@
 //                      (modeling_deepseekv2.py:309-333, dash_attention.py:615-662)
 
 #include "dash_common.h"
+
+#include <atomic>
+#include <mutex>
 #include "dash_decode_unit.h"
 
 namespace dash {
@@ -1559,6 +1562,79 @@ extern "C" int dash_decode_step(
   hipLaunchKernelGGL(decode_step_merge_kernel, dim3(H, B), dim3(64), 0, (hipStream_t)stream, a,
                      npw);
   return launch_status();
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode step: the window and routed-block partials live in a
+// fixed device array of this library instead of a caller workspace.  Each GPU
+// holds its own copy; its address is looked up once per device (with that device
+// current) on the first call there.  The partial slots a step reads are all
+// written by the same step, so nothing needs clearing between calls; calls that
+// overlap on one GPU share the array and race.
+// ---------------------------------------------------------------------------
+namespace dash {
+constexpr int64_t kStepScratchBytes = 64ll << 20;
+static __device__ __align__(256) float scratch[kStepScratchBytes / sizeof(float)];
+constexpr int kMaxScratchDevices = 64;
+static std::atomic<float*> g_scratch_ptr[kMaxScratchDevices];
+static std::mutex g_scratch_mu;
+
+// The array's device address on the current device (hipGetSymbolAddress the first
+// time); returns a status.
+static int scratch_on_current_device(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return kErrUnsupported;
+  float* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      void* addr = nullptr;
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return (int)e;
+      if (!addr) return kErrInvalid;
+      p = (float*)addr;
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return kOk;
+}
+}  // namespace dash
+
+extern "C" int64_t dash_decode_step_scratch_bytes(void) { return dash::kStepScratchBytes; }
+
+extern "C" int dash_decode_step_noalloc(
+    const float* idx_q, int64_t iq_sb, const float* idx_k, int64_t ik_sb, int64_t ik_st,
+    int64_t ik_sp, const int32_t* block_table, int64_t table_stride, int page_size,
+    const int32_t* seq_lens, const int32_t* q_pos, int S, const float* head_cls,
+    int refresh_tail, float* kbar, int64_t kb_sb, int nblk_cap, const uint8_t* cand,
+    int64_t cand_stride, int d, int local_blocks, float idx_scale, float floor_p, float sigma,
+    int K, int topm, int Kout, int32_t* idx, float* bias, uint8_t* valid, float* z,
+    int64_t z_stride,
+    const void* q, int64_t q_sb, int64_t q_sh,
+    const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t k_sp,
+    const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t v_sp,
+    void* out, int out_bf16, int64_t o_sb, int64_t o_sh, float* lse, int64_t lse_sb,
+    int64_t lse_sh, int B, int H, int D, int block_size, int local_window, float scale,
+    void* stream) {
+  using namespace dash;
+  int64_t need = 0;
+  const int ws = dash_decode_step_workspace_size(B, H, D, block_size, local_window, &need);
+  if (ws != kOk) return ws;
+  if (need > kStepScratchBytes) return kErrScratch;
+  float* ptr = nullptr;
+  const int sst = scratch_on_current_device(&ptr);
+  if (sst != kOk) return sst;
+  return dash_decode_step(idx_q, iq_sb, idx_k, ik_sb, ik_st, ik_sp, block_table, table_stride,
+                          page_size, seq_lens, q_pos, S, head_cls, refresh_tail, kbar, kb_sb,
+                          nblk_cap, cand, cand_stride, d, local_blocks, idx_scale, floor_p, sigma,
+                          K, topm, Kout, idx, bias, valid, z, z_stride, q, q_sb, q_sh, k, k_sb,
+                          k_sh, k_st, k_sp, v, v_sb, v_sh, v_st, v_sp, out, out_bf16, o_sb, o_sh,
+                          lse, lse_sb, lse_sh, B, H, D, block_size, local_window, scale, ptr,
+                          kStepScratchBytes, stream);
 }
 
 // ---------------------------------------------------------------------------

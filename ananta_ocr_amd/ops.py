@@ -407,12 +407,15 @@ def decode_route(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, i
 def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks,
                       idx_scale, floor, sigma, K, topm, scale, seq_lens=None, block_table=None,
                       page_size=None, cand=None, width=None, out_dtype=torch.float32,
-                      return_lse=False, q_pos=None, workspace=None, return_scores=False):
+                      return_lse=False, q_pos=None, workspace=None, return_scores=False,
+                      no_alloc=False):
     """decode_route followed by attn_decode of its routing, in two launches: the window
     part of the attention runs beside the router.  Same arguments and results as those
     two calls (q [B,H,D] or [B,H,1,D]; out [B,H,D]); returns (out, (idx, bias, valid))
     with idx/bias/valid [B,1,K'] (valid uint8), or (out, lse, routing) with return_lse;
-    return_scores appends the block scores z [B, nblk_cap] the router computed."""
+    return_scores appends the block scores z [B, nblk_cap] the router computed.
+    no_alloc: call dash_decode_step_noalloc, whose partials live in the library's fixed
+    per-GPU scratch array (no workspace; the outputs are still allocated here)."""
     _need_gpu(q, k, v, idx_q, idx_k, kbar_cache)
     lib = _lib.load()
     squeeze = q.dim() == 4
@@ -458,6 +461,21 @@ def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, l
     c2 = None if cand is None else _u8(cand.reshape(B, -1))
     hc = head_cls.float().contiguous()
     lw = int(local_blocks) * int(block_size)
+    qp = None if q_pos is None else _i32(q_pos.reshape(B))
+    if no_alloc:
+        st_ = lib.dash_decode_step_noalloc(
+            _ptr(idx_q), idx_q.stride(0), _ptr(idx_k), isb, ist, isp, _ptr(bt), bt_stride,
+            int(page_size or 0), _ptr(lens), _ptr(qp), S, _ptr(hc), 1, _ptr(kbar_cache),
+            kbar_cache.stride(0), nblk_cap, _ptr(c2), 0 if c2 is None else c2.stride(0), d,
+            int(local_blocks), float(idx_scale), float(floor), float(sigma), int(K), int(topm),
+            Kw, _ptr(idx), _ptr(bias), _ptr(valid), _ptr(z), z.stride(0),
+            _ptr(q), q.stride(0), q.stride(1),
+            _ptr(k), k_sb, k_sh, k_st, k_sp, _ptr(v), v_sb, v_sh, v_st, v_sp,
+            _ptr(out), int(out_dtype == torch.bfloat16), out.stride(0), out.stride(1),
+            _ptr(lse), 0 if lse is None else lse.stride(0), 1,
+            B, H, D, int(block_size), lw, float(scale), _stream())
+        _lib.check(st_, "dash_decode_step_noalloc")
+        return _step_result(out, lse, idx, bias, valid, z, squeeze, return_lse, return_scores)
     ws_bytes = ctypes.c_int64(0)
     _lib.check(lib.dash_decode_step_workspace_size(B, H, D, int(block_size), lw, ws_bytes),
                "workspace")
@@ -467,7 +485,6 @@ def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, l
         ws = workspace
         if ws.numel() * ws.element_size() < ws_bytes.value:
             raise ValueError("decode step workspace too small")
-    qp = None if q_pos is None else _i32(q_pos.reshape(B))
     st_ = lib.dash_decode_step(
         _ptr(idx_q), idx_q.stride(0), _ptr(idx_k), isb, ist, isp, _ptr(bt), bt_stride,
         int(page_size or 0), _ptr(lens), _ptr(qp), S, _ptr(hc), 1, _ptr(kbar_cache),
@@ -482,6 +499,10 @@ def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, l
         B, H, D, int(block_size), lw, float(scale), _ptr(ws), ws.numel() * ws.element_size(),
         _stream())
     _lib.check(st_, "dash_decode_step")
+    return _step_result(out, lse, idx, bias, valid, z, squeeze, return_lse, return_scores)
+
+
+def _step_result(out, lse, idx, bias, valid, z, squeeze, return_lse, return_scores):
     if squeeze:
         out = out[:, :, None]
     routing = (idx[:, None], bias[:, None], valid[:, None])

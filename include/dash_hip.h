@@ -10,8 +10,8 @@
  *     contiguous; bf16 tensors need 16-byte aligned rows.
  *   - `stream` is a hipStream_t; all work is enqueued on it, nothing synchronises.
  *   - Return value: 0 ok, -2 unsupported shape/parameter (the Python layer raises
- *     NotImplementedError), -3 invalid argument, -4 workspace too small, >0 a
- *     hipError_t from the launch.
+ *     NotImplementedError), -3 invalid argument, -4 workspace too small, -5 sizes beyond
+ *     the fixed scratch of the allocation-free entry point, >0 a hipError_t.
  *   - Sequence layouts: contiguous ([B, S, ...] with a batch stride), varlen
  *     (`cu_seqlens` [B+1] prefix sums over a packed token axis; every sequence has
  *     its own block grid starting at its first token) or paged (`block_table`
@@ -251,6 +251,38 @@ int dash_decode_step(const float* idx_q, int64_t iq_sb, const float* idx_k, int6
                      float* lse, int64_t lse_sb, int64_t lse_sh,
                      int B, int H, int D, int block_size, int local_window, float scale,
                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Allocation-free decode step.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops).
+ * Same arguments and results as dash_decode_step without the workspace: the window and
+ * routed-block partials live in a fixed 64 MiB device array of this library
+ * (dash_decode_step_scratch_bytes()), one per GPU, held until the process ends.  Sizes
+ * whose dash_decode_step_workspace_size exceeds it return -5.  Calls that overlap on one
+ * GPU share that array and race; nothing in it needs clearing between calls.
+ */
+int dash_decode_step_noalloc(const float* idx_q, int64_t iq_sb, const float* idx_k,
+                             int64_t ik_sb, int64_t ik_st, int64_t ik_sp,
+                             const int32_t* block_table, int64_t table_stride, int page_size,
+                             const int32_t* seq_lens, const int32_t* q_pos, int S,
+                             const float* head_cls, int refresh_tail, float* kbar,
+                             int64_t kb_sb, int nblk_cap, const uint8_t* cand,
+                             int64_t cand_stride, int d, int local_blocks, float idx_scale,
+                             float floor_p, float sigma, int K, int topm, int Kout,
+                             int32_t* idx, float* bias, uint8_t* valid, float* z,
+                             int64_t z_stride,
+                             const void* q, int64_t q_sb, int64_t q_sh,
+                             const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                             int64_t k_sp,
+                             const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                             int64_t v_sp,
+                             void* out, int out_bf16, int64_t o_sb, int64_t o_sh,
+                             float* lse, int64_t lse_sb, int64_t lse_sh,
+                             int B, int H, int D, int block_size, int local_window, float scale,
+                             void* stream);
+
+/* Bytes of the fixed scratch array dash_decode_step_noalloc uses (per GPU). */
+int64_t dash_decode_step_scratch_bytes(void);
 
 #ifdef __cplusplus
 }
