@@ -41,6 +41,14 @@ def _u8(t):
     return t.to(torch.uint8).contiguous()
 
 
+def _max_len(cu, max_seqlen):
+    """Longest document of cu_seqlens: the caller's value, else read from the device
+    (one synchronisation; graph capture needs the caller's value)."""
+    if max_seqlen is not None:
+        return int(max_seqlen)
+    return int((cu[1:] - cu[:-1]).max().item()) if cu.numel() > 1 else 0
+
+
 def _rows(x):
     """bf16 [.., D] tensor whose feature axis is contiguous with 16-byte rows."""
     if x.stride(-1) != 1 or any(s % 8 for s in x.stride()[:-1]) or x.data_ptr() % 16:
@@ -49,9 +57,10 @@ def _rows(x):
 
 
 def kbar(idx_k, head_cls, block_size, cu_seqlens=None, seq_lens=None, nblk_cap=None,
-         tail_only=False, out=None, block_table=None, page_size=None):
+         tail_only=False, out=None, block_table=None, page_size=None, max_seqlen=None):
     """Stage-0 block summaries.  idx_k fp32 [B,S,d] (or [1,T,d] with cu_seqlens, or
-    paged [pages, page_size, d] with block_table).  Returns [B, nblk_cap, d] fp32."""
+    paged [pages, page_size, d] with block_table).  Returns [B, nblk_cap, d] fp32.
+    max_seqlen: the longest cu_seqlens document (read from the device when omitted)."""
     _need_gpu(idx_k, head_cls)
     lib = _lib.load()
     idx_k = idx_k.float()
@@ -61,7 +70,7 @@ def kbar(idx_k, head_cls, block_size, cu_seqlens=None, seq_lens=None, nblk_cap=N
     if cu_seqlens is not None:
         cu = _i32(cu_seqlens)
         B = cu.numel() - 1
-        S = int((cu[1:] - cu[:-1]).max().item()) if B > 0 else 0
+        S = _max_len(cu, max_seqlen)
         sb, st, sp = 0, idx_k.stride(-2), 0
     elif block_table is not None:
         cu = None
@@ -94,7 +103,7 @@ def kbar(idx_k, head_cls, block_size, cu_seqlens=None, seq_lens=None, nblk_cap=N
 
 
 def block_scores(idx_q, kb, block_size, local_blocks, q_pos=None, cu_seqlens=None,
-                 seq_lens=None, S=None):
+                 seq_lens=None, S=None, max_seqlen=None):
     """Block scores z for query rows idx_q fp32 [B,Lq,d] (or [1,T,d] + cu_seqlens)
     against k_bar [B,nblk,d].  Returns [B,Lq,nblk] (or [T,nblk]) fp32."""
     _need_gpu(idx_q, kb)
@@ -110,7 +119,7 @@ def block_scores(idx_q, kb, block_size, local_blocks, q_pos=None, cu_seqlens=Non
     if cu_seqlens is not None:
         cu = _i32(cu_seqlens)
         T = idx_q.shape[-2]
-        Lq = int((cu[1:] - cu[:-1]).max().item()) if B > 0 else 0
+        Lq = _max_len(cu, max_seqlen)
         z = torch.empty(T, zs, dtype=torch.float32, device=idx_q.device)[:, :nblk]
         sb, st = 0, idx_q.stride(-2)
         Sk = Lq if S is None else S
@@ -259,9 +268,7 @@ def attn_prefill(q, k, v, idx, bias, valid, block_size, local_window, scale,
         if B != 1:
             raise ValueError("varlen prefill takes q of shape [1, H, T, D]")
         nb = cu.numel() - 1
-        if max_seqlen is None:
-            max_seqlen = int((cu[1:] - cu[:-1]).max().item()) if nb > 0 else 0
-        Smax = int(max_seqlen)
+        Smax = _max_len(cu, max_seqlen)
         rows = S
     else:
         Smax = S

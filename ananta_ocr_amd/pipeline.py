@@ -17,12 +17,15 @@ from . import ops
 def prefill(q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks, idx_scale, floor,
             sigma, K, topm, scale=None, cu_seqlens=None, max_seqlen=None, block_cand=None,
             return_routing=False):
-    """q/k/v bf16 [B,H,S,D] (or [1,H,T,D] + cu_seqlens), idx_q/idx_k fp32 [B,S,d]."""
+    """q/k/v bf16 [B,H,S,D] (or [1,H,T,D] + cu_seqlens), idx_q/idx_k fp32 [B,S,d].
+    With cu_seqlens, max_seqlen (the longest document) keeps the pass free of host
+    synchronisations, so that it can be captured in a HIP graph."""
     D = q.shape[-1]
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    kb = ops.kbar(idx_k, head_cls, block_size, cu_seqlens=cu_seqlens)
-    z = ops.block_scores(idx_q, kb, block_size, local_blocks, cu_seqlens=cu_seqlens)
+    kb = ops.kbar(idx_k, head_cls, block_size, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen)
+    z = ops.block_scores(idx_q, kb, block_size, local_blocks, cu_seqlens=cu_seqlens,
+                         max_seqlen=max_seqlen)
     if cu_seqlens is not None:
         lens = (cu_seqlens[1:] - cu_seqlens[:-1]).to(torch.int32)
         nblk_doc = (lens + block_size - 1) // block_size
@@ -33,7 +36,7 @@ def prefill(q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks, idx_scale
     else:
         idx, bias, valid = ops.route(z, block_cand, idx_scale, floor, sigma, K, topm)
     out = ops.attn_prefill(q, k, v, idx, bias, valid, block_size, local_blocks * block_size,
-                           scale, cu_seqlens=cu_seqlens)
+                           scale, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen)
     if return_routing:
         return out, (idx, bias, valid.bool())
     return out

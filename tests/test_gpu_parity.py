@@ -766,3 +766,56 @@ def test_decode_checkpoint_config_matches_oracle(paged, fused):
         ref = O.decode_attend(q[b:b + 1, :, None].float(), k[b:b + 1, :, :L], v[b:b + 1, :, :L],
                               t_r, b_r, v_r, torch.tensor([[L - 1]]), bs, lw, 1 / math.sqrt(128))
         _close(out[b:b + 1], ref[:, :, 0], f"decode bs 32 sequence {b} ({L} tokens)")
+
+
+def test_packed_prefill_graph_replays_match_eager():
+    """A packed (cu_seqlens) prefill pass (k_bar, scores, routing, attention) given
+    max_seqlen makes no host synchronisation, so it is captured in a HIP graph; every
+    replay (with eager work and synchronisations between replays, and after new
+    inputs are written into the captured buffers) equals the eager pass bit for bit."""
+    from ananta_ocr_amd import pipeline
+    cfg = W.Prefill("graph_packed", 1, 0, 64, 512, 8, seed=21, doc_pages=[3, 1, 7, 2])
+    d = W.make_prefill(cfg, device=DEV)
+    cu, cl = d["cu_seqlens"], d["cu_list"]
+    maxlen = max(b - a for a, b in zip(cl[:-1], cl[1:]))
+    hc = torch.zeros(128, device=DEV)
+    args = (hc, cfg.bs, cfg.lw // cfg.bs, W.IDX_SCALE * 50, W.FLOOR, W.SIGMA, cfg.cap, cfg.cap,
+            1 / math.sqrt(128))
+    ins = [d["q"], d["k"], d["v"], d["idx_q"], d["idx_k"]]
+
+    def run():
+        return pipeline.prefill(*ins, *args, cu_seqlens=cu, max_seqlen=maxlen)
+
+    eager = run().clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            run()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = run()
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        again = run()                                  # eager work in between
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager)
+    d2 = W.make_prefill(W.Prefill("graph_packed2", 1, 0, 64, 512, 8, seed=22,
+                                  doc_pages=[3, 1, 7, 2]), device=DEV)
+    for dst, key in zip(ins, ["q", "k", "v", "idx_q", "idx_k"]):
+        dst.copy_(d2[key])
+    ref2 = run().clone()
+    assert not torch.equal(ref2, eager)
+    for i in range(2):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref2), f"replay with new inputs {i}"
+    # and the pass against the oracle on the new inputs, document by document
+    ref = O.prefill_varlen(d2["q"].cpu(), d2["k"].cpu(), d2["v"].cpu(), d2["idx_q"].cpu(),
+                           d2["idx_k"].cpu(), cu.cpu(), torch.zeros(128), cfg.bs,
+                           cfg.lw // cfg.bs, W.IDX_SCALE * 50, W.FLOOR, W.SIGMA, cfg.cap,
+                           cfg.cap, 1 / math.sqrt(128))[0]
+    _close(out, ref, "captured packed prefill")
