@@ -51,6 +51,14 @@ SIGNATURES = {
                                       _l, _p, _i, _l, _l, _p, _l, _l, _i, _i, _i, _i, _i, _f,
                                       _p]),
     "dash_decode_step_scratch_bytes": (_l, []),
+    "dash_page_ids": (_i, [_p, _l, _i, _i, _l, _l, _i, _i, _p, _p, _p, _p, _p, _l, _p]),
+    "dash_pages_workspace_size": (_i, [_i, _i, ctypes.POINTER(_l)]),
+    "dash_block_pages": (_i, [_p, _l, _i, _i, _i, _i, _p, _p, _p, _p]),
+    "dash_block_cand": (_i, [_p, _l, _i, _p, _l, _i, _p, _l, _i, _p, _p, _p, _i, _i, _i, _i,
+                             _p, _l, _l, _p]),
+    "dash_decode_page_state": (_i, [_p, _l, _i, _i, _l, _l, _i, _i, _i, _p, _p, _p, _p, _p, _l,
+                                    _p]),
+    "dash_decode_allow": (_i, [_p, _l, _i, _l, _p, _p, _i, _p, _p, _i, _p, _l, _p]),
 }
 
 _LIB = None

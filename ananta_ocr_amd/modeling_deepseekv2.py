@@ -27,7 +27,7 @@ import math
 
 import torch
 
-from . import ops
+from . import ops, pages
 from .dash_attention import DashAttention, apply_rotary
 
 _INFER = {"on": False}
@@ -40,11 +40,12 @@ def configure_dash_inference(decoder, on, topm=16, page_scope_prefill=True, stat
     (indexed by the router's slot among the sparse layers, :256-266)."""
     if not on:
         if state is not None:
+            pages.PAGE_SCOPE["prefill"] = state["page_scope_prefill"]
             for mod, stage0 in state["stage0"]:
                 mod.stage0 = stage0
         _INFER["on"] = False
         return None
-    state = {"stage0": [], "page_scope_prefill": bool(page_scope_prefill)}
+    state = {"stage0": [], "page_scope_prefill": pages.PAGE_SCOPE["prefill"]}
     cfg = getattr(decoder, "config", None)
     sp = (getattr(cfg, "sparse_attention_config", None) or {}) if cfg is not None else {}
     stage0 = str(sp.get("dash_stage0") or "indexer").lower()
@@ -63,6 +64,7 @@ def configure_dash_inference(decoder, on, topm=16, page_scope_prefill=True, stat
                                     K=int(budget), topm=int(topm))
         state["stage0"].append((router, router.stage0))
         router.stage0 = stage0
+    pages.PAGE_SCOPE["prefill"] = bool(page_scope_prefill)
     _INFER["on"] = True
     return state
 

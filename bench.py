@@ -392,6 +392,58 @@ def paged_entry(cfg, res, counters):
             "cached_tokens_per_layer": int(res["lengths"].sum()), "roofline": roof}
 
 
+# ------------------------------------------------------------------ page-aware candidates
+
+PAGES_NAME = "page_candidates_s27300_100pages"
+
+
+def ocr_prompt_ids(pages_n=100, per_page=W.PAGE_TOKENS, seed=6):
+    """Token ids [1, L] of a 100-page OCR prompt: BOS, per page a <PAGE> marker and 273
+    image tokens, an instruction, then the response: per page a marker and text.  Ids:
+    1 BOS, 5 image, 9 marker, 7 text."""
+    g = torch.Generator().manual_seed(seed)
+    ids = [1]
+    for _ in range(pages_n):
+        ids += [9] + [5] * per_page
+    ids += [7] * 8
+    for _ in range(pages_n):
+        ids += [9] + [7] * int(torch.randint(20, 60, (1,), generator=g))
+    return torch.tensor([ids], dtype=torch.int64)
+
+
+def bench_pages(steps):
+    """Prefill candidates of a 100-page prompt (page ids, block pages, [S, nblk] rows) and
+    the decode allow row of its batch of 8 copies."""
+    from ananta_ocr_amd import pages
+    ids = ocr_prompt_ids().to("cuda")
+    S = ids.shape[1]
+    bs = 64
+    nblk = (S + bs - 1) // bs
+    pos = torch.arange(S, device="cuda", dtype=torch.int32)[None]
+    out = torch.empty(1, S, nblk, dtype=torch.bool, device="cuda")
+
+    def prefill(i=0):
+        img, ipi, qpi, _ = pages.page_ids(ids, 5, 9, S, W.PAGE_TOKENS, True)
+        pages.block_cand(pos, nblk, bs, img, ipi, qpi, out=out)
+
+    prefill()
+    t_pre = time_kernel(prefill, max(steps, 10))
+    ids8 = ids.expand(8, -1).contiguous()
+    st = pages.DecodePageState(ids8, 5, 9, bs)
+    new = torch.full((8,), 7, dtype=torch.int64, device="cuda")
+    arow = torch.empty(8, nblk + 1, dtype=torch.bool, device="cuda")
+    t_dec = time_kernel(lambda i: st.allow(new, S + 1, out=arow), max(steps, 20))
+    nbytes = S * 8 * 3 + S * (1 + 4 + 4) * 2 + S * nblk     # ids reads, page ids, rows
+    gbs = nbytes / t_pre / 1e9
+    return {"workload": PAGES_NAME, "value": round(t_pre * 1e6, 2), "unit": "us per prefill",
+            "tokens": S, "blocks": nblk,
+            "decode_allow_us": round(t_dec * 1e6, 2),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                         "kernel": "page_ids + block_pages + block_cand",
+                         "bytes_per_launch": nbytes, "avg_launch_us": round(t_pre * 1e6, 2)}}
+
+
 # ------------------------------------------------------------------ CPU baselines
 
 def _median_time(run, reps):
@@ -697,6 +749,8 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     only = set(filter(None, args.only.split(",")))
     todo = [c for c in ALL if not only or c.name in only]
+    if only and not todo and PAGES_NAME not in only:
+        sys.exit(f"bench.py: unknown workload(s) {sorted(only)}")
     counters, cnote = read_counters()
     res, entries = {}, {}
     for cfg in todo:
@@ -724,10 +778,35 @@ def main():
             else:
                 cb = cpu_decode_baseline(r, cfg)
             entries[cfg.name]["cpu_baseline"] = cb
+    if not only or PAGES_NAME in only:
+        entries[PAGES_NAME] = bench_pages(args.steps)
+        if not args.no_cpu:
+            from oracle import dash_oracle as O
+            ids = ocr_prompt_ids()
+            S = ids.shape[1]
+            nblk = (S + 63) // 64
+
+            def cpu_pages():
+                itm, ipi, qpi = O.page_aware_ids(ids, 5, 9, S, W.PAGE_TOKENS, True)
+                for c0 in range(0, S, 2048):             # the reference's query chunks
+                    c1 = min(c0 + 2048, S)
+                    O.kl_candidate_mask(torch.arange(c0, c1)[None], nblk, itm, 1, c1 - c0, 64,
+                                        ipi, qpi)
+
+            t = _median_time(cpu_pages, 3)
+            entries[PAGES_NAME]["cpu_baseline"] = _cpu_fields(
+                t * 1e6, "us per prefill", "oracle page ids and candidate rows of the same "
+                "100-page prompt in 2,048-query chunks; median of 3 after 1 warm-up")
     head = entries.get(W.PREFILL_27300.name)
     if head is None:                      # a partial run: the first workload timed
-        head = entries[todo[0].name]
-    hcfg = next(c for c in ALL if c.name == head["workload"])
+        head = next(iter(entries.values()))
+    hcfg = next((c for c in ALL if c.name == head["workload"]), None)
+    if hcfg is not None:
+        hconf = {"workload": hcfg.name, "B": hcfg.B, "seq_len": hcfg.S, "heads": W.H,
+                 "head_dim": W.D, "block": hcfg.bs, "window": hcfg.lw,
+                 "routed_cap": hcfg.cap, "parallelism": "single-gpu"}
+    else:
+        hconf = {"workload": head["workload"], "parallelism": "single-gpu"}
     line = {
         "metric": METRIC,
         "value": head["value"],
@@ -741,14 +820,12 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": hcfg.name, "B": hcfg.B, "seq_len": hcfg.S, "heads": W.H,
-                   "head_dim": W.D, "block": hcfg.bs, "window": hcfg.lw,
-                   "routed_cap": hcfg.cap, "parallelism": "single-gpu"},
+        "config": hconf,
         "roofline": head["roofline"],
     }
     if "cpu_baseline" in head:
         line["cpu_baseline"] = head["cpu_baseline"]
-    line["workloads"] = {k: v for k, v in entries.items() if k != hcfg.name}
+    line["workloads"] = {k: v for k, v in entries.items() if k != head["workload"]}
     if cnote:
         line["counters_note"] = cnote
     print(json.dumps(line), flush=True)

@@ -253,6 +253,74 @@ int dash_decode_step(const float* idx_q, int64_t iq_sb, const float* idx_k, int6
                      void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Page ids of prompt rows: replaces _build_page_aware_ids (_sparse_base_impl.py:2189-2259).
+ *   ids          int64 token ids [B, L] (row stride ids_sb)
+ *   image_mask   u8 [B, L]: token == image_token_id
+ *   image_page_ids int32 [B, L]: page of each image token (-1 elsewhere): <PAGE> markers
+ *                seen so far - 1 when the prompt has a marker before its last image token,
+ *                else (image tokens before it) / per_page_tokens
+ *   query_page_ids int32 [B, L]: the page a query at that position belongs to (-1: none;
+ *                inside the prompt only with page_scope_prefill)
+ *   enabled      int32 [B, 2] or NULL: (row has an image token, row has a query page)
+ *   workspace    dash_pages_workspace_size(B, L) bytes, 16-byte aligned (chunk summaries)
+ * Two launches: per-chunk marker and image counts, then every chunk from its prefix.
+ */
+int dash_page_ids(const int64_t* ids, int64_t ids_sb, int B, int L, int64_t image_token_id,
+                  int64_t page_token_id, int per_page_tokens, int page_scope_prefill,
+                  uint8_t* image_mask, int32_t* image_page_ids, int32_t* query_page_ids,
+                  int32_t* enabled, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes of dash_page_ids and dash_decode_page_state for B rows of L tokens. */
+int dash_pages_workspace_size(int B, int L, int64_t* bytes);
+
+/*
+ * Image pages of every key block: bmin/bmax int32 [B, nblk] (-1 with no image token) and
+ * bits u64 [B, nblk] (bit k: page bmin + k has an image token in the block), from
+ * image_page_ids [B, L] (row stride ipi_sb).  Feeds dash_block_cand.
+ */
+int dash_block_pages(const int32_t* image_page_ids, int64_t ipi_sb, int B, int L,
+                     int block_size, int nblk, int32_t* bmin, int32_t* bmax, uint64_t* bits,
+                     void* stream);
+
+/*
+ * Per-query routing candidates [B, Lq, nblk] u8 (strides cand_sb, cand_st): replaces
+ * _build_kl_candidate_mask (_sparse_base_impl.py:2457-2484) as _dash_block_cand calls it
+ * (modeling_deepseekv2.py:96-110).  mode 0: blocks holding an image token of the query's
+ * page (query_page_ids [B, Lqp] at pos [B, Lq], clamped; pos NULL: 0..Lq-1); mode 1:
+ * blocks holding any image token; mode 2: every block.  A row with no candidate allows
+ * every block (the reference's per-query fallback).  nblk <= 2048.
+ */
+int dash_block_cand(const int32_t* query_page_ids, int64_t qpi_sb, int Lqp, const int32_t* pos,
+                    int64_t pos_sb, int Lq, const int32_t* image_page_ids, int64_t ipi_sb,
+                    int Lk, const int32_t* bmin, const int32_t* bmax, const uint64_t* bits,
+                    int nblk, int mode, int B, int block_size, uint8_t* cand, int64_t cand_sb,
+                    int64_t cand_st, void* stream);
+
+/*
+ * Decode page state of prompt rows: the prefill branch of _uocr_dash_decode_allow
+ * (modeling_anantaocr.py:465-479).  bmin/bmax int32 [B, nblk] (the smallest/largest image
+ * page of each block, -1 with none; nblk * block_size >= L), prompt_pages int32 [B]
+ * (markers up to the last image token), markers int32 [B] (markers in the row).
+ * block_size <= 1024; workspace: dash_pages_workspace_size(B, L) bytes, 16-byte aligned.
+ */
+int dash_decode_page_state(const int64_t* ids, int64_t ids_sb, int B, int L,
+                           int64_t image_token_id, int64_t page_token_id, int per_page_tokens,
+                           int block_size, int nblk, int32_t* bmin, int32_t* bmax,
+                           int32_t* prompt_pages, int32_t* markers, void* workspace,
+                           int64_t workspace_bytes, void* stream);
+
+/*
+ * Decode allow row: the decode branch of _uocr_dash_decode_allow (modeling_anantaocr.py:
+ * 480-496).  new_ids int64 [B] (stride new_stride) is the step's token; markers is
+ * updated in place.  allow u8 [B, nblk] (row stride allow_sb): blocks with
+ * bmin <= page <= bmax for the query's page, or every block when it has none.
+ */
+int dash_decode_allow(const int64_t* new_ids, int64_t new_stride, int B, int64_t page_token_id,
+                      const int32_t* bmin, const int32_t* bmax, int nblk_state,
+                      const int32_t* prompt_pages, int32_t* markers, int nblk, uint8_t* allow,
+                      int64_t allow_sb, void* stream);
+
+/*
  * Allocation-free decode step.  No counterpart in the reference: it is for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving loops).
  * Same arguments and results as dash_decode_step without the workspace: the window and

@@ -21,6 +21,9 @@ for the path (citations are ``file:line`` in the reference repository):
 * decode attention            -- modeling_deepseekv2.py:424-451
 * packed varlen (cu_seqlens)  -- block-diagonal: each document is run on its own
                                  block grid (the per-request semantics of the serving path)
+* page-aware candidates       -- _sparse_base_impl.py:2189-2259 (page ids), :2363-2380 (flat
+                                 image mask), :2436-2484 (candidate mask); decode allow row
+                                 modeling_anantaocr.py:450-496
 
 Deliberate, documented deviation: ``torch.topk`` leaves the order of tied values
 unspecified (the CPU kernel returns ties in an arbitrary order).  The oracle
@@ -34,6 +37,8 @@ Parity pinning (what each function is checked against, in tests/):
   dense_attend     -> brute-force float64 enumeration of the explicit key sets,
                       sliding-window / causal SDPA special cases
   decode_attend    -> the same enumeration at one query; equality with prefill rows
+  page candidates  -> known-answer prompts written out by hand, and a token-by-token
+                      walk of the prompt (tests/bruteforce.py) on random prompts
 """
 
 import math
@@ -395,3 +400,136 @@ def decode_pipeline(q, k_all, v_all, idx_q, idx_k, head_cls, block_size, local_b
     out = decode_attend(q, k_all, v_all, topi, bias, valid, q_pos, block_size,
                         local_blocks * block_size, scale)
     return out, topi, bias, valid
+
+
+# ----------------------------------------------------------------------------
+# page-aware candidate domain (the OCR prompt's pages)
+# ----------------------------------------------------------------------------
+
+def _pad_ids(source_input_ids, key_length):
+    ids = source_input_ids[..., :key_length].long()
+    if ids.shape[-1] < key_length:
+        ids = F.pad(ids, (0, key_length - ids.shape[-1]), value=-1)
+    return ids
+
+
+def page_aware_ids(source_input_ids, img_id, page_id, key_length, per_page=273,
+                   page_scope_prefill=False):
+    """(image_token_mask, image_token_page_ids, query_token_page_ids) [B, key_length],
+    or (None, None, None): _sparse_base_impl.py:2189-2259 (diagnostic prints left out)."""
+    if source_input_ids is None or img_id is None or page_id is None:
+        return None, None, None
+    if source_input_ids.ndim != 2:
+        return None, None, None
+    token_ids = _pad_ids(source_input_ids, key_length)
+    image_token_mask = token_ids == img_id
+    page_starts = token_ids == page_id
+    cum_pages = torch.cumsum(page_starts.long(), dim=-1)
+    seq = token_ids.shape[-1]
+    ar = torch.arange(seq)
+    last_img = (image_token_mask.long() * (ar + 1)).max(dim=-1).values - 1
+    prompt_pages = cum_pages.gather(1, last_img.clamp(min=0)[:, None])
+    prompt_pages = prompt_pages * (last_img >= 0)[:, None].long()
+    marker_mode = prompt_pages > 0
+    per_page = max(1, int(per_page))
+    img_running = torch.cumsum(image_token_mask.long(), dim=-1) - 1
+    image_token_page_ids = torch.where(marker_mode, cum_pages - 1, img_running // per_page)
+    image_token_page_ids = image_token_page_ids.masked_fill(~image_token_mask, -1)
+    raw_page = cum_pages - 1
+    resp_page = raw_page - torch.where(marker_mode, prompt_pages, torch.zeros_like(prompt_pages))
+    in_prefill = ar[None, :] <= last_img[:, None]
+    query_token_page_ids = torch.where(in_prefill, raw_page, resp_page)
+    if not page_scope_prefill:
+        query_token_page_ids = query_token_page_ids.masked_fill(in_prefill, -1)
+    query_token_page_ids = query_token_page_ids.masked_fill(query_token_page_ids < 0, -1)
+    if image_token_mask.sum() == 0 or (query_token_page_ids >= 0).sum() == 0:
+        return None, None, None
+    return image_token_mask, image_token_page_ids, query_token_page_ids
+
+
+def flat_image_token_mask(source_input_ids, img_id, key_length):
+    """_sparse_base_impl.py:2363-2380."""
+    if source_input_ids is None or img_id is None or source_input_ids.ndim != 2:
+        return None
+    mask = _pad_ids(source_input_ids, key_length) == img_id
+    if mask.sum() == 0:
+        return None
+    return mask
+
+
+def kl_candidate_mask(pos_chunk, num_key_blocks, image_token_mask, batch, cq, block_size,
+                      image_token_page_ids=None, query_token_page_ids=None,
+                      image_bucket_constraint=True):
+    """[B, 1, cq, nblk] bool: _sparse_base_impl.py:2457-2484 with the page-aware block
+    mask of :2436-2455 and the image-block mask of :2173-2183."""
+    bs = int(block_size)
+    nblk = int(num_key_blocks)
+    if image_bucket_constraint and image_token_page_ids is not None \
+            and query_token_page_ids is not None:
+        k_len = image_token_page_ids.shape[-1]
+        pos_clamped = pos_chunk.long().clamp(0, query_token_page_ids.shape[-1] - 1)
+        query_pages = query_token_page_ids.gather(1, pos_clamped)
+        pad = nblk * bs - k_len
+        if pad > 0:
+            img_page_padded = F.pad(image_token_page_ids.float(), (0, pad), value=-1).long()
+        elif pad < 0:
+            img_page_padded = image_token_page_ids[..., :nblk * bs]
+        else:
+            img_page_padded = image_token_page_ids
+        img_page_blocks = img_page_padded.view(batch, nblk, bs)
+        qp = query_pages[:, :, None, None]
+        kp = img_page_blocks[:, None, :, :]
+        same_page = (qp >= 0) & (qp == kp)
+        candidate = same_page.any(dim=-1).unsqueeze(1)
+    elif image_token_mask is not None:
+        B, Sk = image_token_mask.shape
+        pad = nblk * bs - Sk
+        m = image_token_mask.bool()
+        if pad > 0:
+            m = F.pad(m, (0, pad), value=False)
+        elif pad < 0:
+            m = m[..., :nblk * bs]
+        img_blk = m.view(B, nblk, bs).any(dim=-1)
+        candidate = img_blk[:, None, None, :].expand(batch, 1, cq, nblk).contiguous()
+    else:
+        candidate = torch.ones(batch, 1, cq, nblk, dtype=torch.bool)
+    has_candidate = candidate.any(dim=-1, keepdim=True)
+    return torch.where(has_candidate, candidate, torch.ones_like(candidate))
+
+
+def decode_page_state(input_ids, img_id, pg_id, block_size, per_page=273):
+    """Prefill branch of _uocr_dash_decode_allow (modeling_anantaocr.py:465-479)."""
+    bs = int(block_size)
+    ids = input_ids.long()
+    B, L = ids.shape
+    img = ids == img_id
+    cum = torch.cumsum((ids == pg_id).long(), dim=-1)
+    run = torch.cumsum(img.long(), dim=-1)
+    per_page = max(1, int(per_page))
+    page = torch.where(cum > 0, cum - 1, (run - 1) // per_page)
+    page = torch.where(img, page, torch.full_like(page, -1))
+    pp = torch.where(img, cum, torch.zeros_like(cum)).cummax(dim=-1).values[:, -1]
+    nblk = -(-L // bs)
+    pg = F.pad(page, (0, nblk * bs - L), value=-1).view(B, nblk, bs)
+    bmax = pg.amax(dim=-1)
+    bmin = torch.where(pg >= 0, pg, torch.full_like(pg, 1 << 30)).amin(dim=-1)
+    bmin = torch.where(bmax >= 0, bmin, torch.full_like(bmin, -1))
+    return {"bmin": bmin, "bmax": bmax, "pp": pp, "mcum": cum[:, -1].clone()}
+
+
+def decode_allow(state, input_ids, pg_id, total_len, block_size):
+    """Decode branch of _uocr_dash_decode_allow (modeling_anantaocr.py:480-496); updates
+    state["mcum"].  input_ids [B, 1]; total_len = cached tokens + 1."""
+    ids = input_ids.long()
+    B = ids.shape[0]
+    state["mcum"] = state["mcum"] + (ids[:, -1] == pg_id).long()
+    qp = state["mcum"] - 1 - state["pp"]
+    qp = torch.where(qp >= 0, qp, torch.full_like(qp, -1))[:, None]
+    nblk = -(-int(total_len) // int(block_size))
+    bmin, bmax = state["bmin"], state["bmax"]
+    same = (bmin >= 0) & (bmin <= qp) & (bmax >= qp) & (qp >= 0)
+    open_row = (qp[:, 0] < 0) | ~same.any(dim=-1)
+    allow = torch.zeros(B, nblk, dtype=torch.bool)
+    n0 = min(nblk, same.shape[-1])
+    allow[:, :n0] = same[:, :n0]
+    return allow | open_row[:, None]

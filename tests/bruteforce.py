@@ -112,3 +112,86 @@ def attend_brute(q, k, v, topi, bias, valid, block_size, local_window, scale, ro
             for h in range(H):
                 out[(b, h, t)] = attend_row(q[b, h, t], k[b, h], v[b, h], keys, scale)
     return out
+
+
+# ---------------------------------------------------------------- OCR pages
+
+def walk_pages(ids, img_id, page_id, per_page, page_scope_prefill):
+    """Token-by-token page assignment of one prompt row, from the definitions: an image
+    token belongs to the page of the last <PAGE> marker before it when the prompt has a
+    marker before its last image token, else to (its index among image tokens) //
+    per_page; a query token belongs to the page of the last marker before it, counted
+    from the first marker after the prompt's last image (response pages restart at 0)
+    when the prompt is in marker mode, and has no page inside the prompt unless
+    page_scope_prefill.  Returns (image flags, image pages, query pages), lists."""
+    L = len(ids)
+    last = max([t for t in range(L) if ids[t] == img_id], default=-1)
+    prompt_markers = sum(1 for t in range(last + 1) if ids[t] == page_id)
+    marker_mode = prompt_markers > 0
+    markers = nimg = 0
+    flags, ipages, qpages = [], [], []
+    for t in range(L):
+        if ids[t] == page_id:
+            markers += 1
+        if ids[t] == img_id:
+            ipages.append(markers - 1 if marker_mode else nimg // per_page)
+            nimg += 1
+            flags.append(True)
+        else:
+            ipages.append(-1)
+            flags.append(False)
+        if t <= last:
+            q = markers - 1 if page_scope_prefill else -1
+        else:
+            q = markers - 1 - (prompt_markers if marker_mode else 0)
+        qpages.append(q if q >= 0 else -1)
+    return flags, ipages, qpages
+
+
+def candidates_row(qp, ipages, nblk, bs):
+    """Candidate blocks of a query of page qp: blocks with an image token of page qp,
+    or every block when there is none."""
+    L = len(ipages)
+    row = [qp >= 0 and any(ipages[j] == qp for j in range(c * bs, min(c * bs + bs, L)))
+           for c in range(nblk)]
+    return row if any(row) else [True] * nblk
+
+
+def walk_decode_pages(ids, img_id, page_id, per_page, bs):
+    """Decode page state of one prompt row: each image token's page (the last marker
+    before it - 1 once a marker was seen, else its index among image tokens // per_page),
+    per key block the smallest and largest such page (-1 without image tokens), the
+    markers up to the last image token and all markers."""
+    L = len(ids)
+    markers = nimg = 0
+    pages = []
+    pp = 0
+    for t in range(L):
+        if ids[t] == page_id:
+            markers += 1
+        if ids[t] == img_id:
+            pages.append(markers - 1 if markers > 0 else nimg // per_page)
+            nimg += 1
+            pp = markers
+        else:
+            pages.append(-1)
+    nblk = (L + bs - 1) // bs
+    bmin, bmax = [], []
+    for c in range(nblk):
+        ps = [p for p in pages[c * bs:(c + 1) * bs] if p >= 0]
+        bmin.append(min(ps) if ps else -1)
+        bmax.append(max(ps) if ps else -1)
+    return bmin, bmax, pp, markers
+
+
+def decode_allow_row(bmin, bmax, pp, markers, new_is_marker, nblk):
+    """Allow row of one decode step: the query's page is (markers after this token) - 1 -
+    pp; blocks whose [bmin, bmax] holds it; every block when none does or there is no
+    page.  Returns (row, updated markers)."""
+    m = markers + (1 if new_is_marker else 0)
+    qp = m - 1 - pp
+    same = [qp >= 0 and c < len(bmin) and bmin[c] >= 0 and bmin[c] <= qp <= bmax[c]
+            for c in range(nblk)]
+    if qp < 0 or not any(same):
+        return [True] * nblk, m
+    return same, m
