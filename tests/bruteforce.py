@@ -64,6 +64,33 @@ def route_row(z_row, cand_row, idx_scale, floor, sigma, K, topm):
     return idx, valid, bias
 
 
+def train_route_row(z_row, cand_row, idx_scale, floor, sigma, K):
+    """Training routing of one query row from the definition: the 1.5-entmax prior over
+    every block (bisection on its threshold, float64), the K highest candidate priors
+    (non-candidates ranked below every candidate), the centred log-prior bias over the
+    candidates among them, clamped to +-1e4.  Returns (idx, valid, bias)."""
+    nblk = len(z_row)
+    remote = [float(z) > -5.0e8 for z in z_row]
+    cand = list(remote) if cand_row is None else [r and bool(c) for r, c in zip(remote, cand_row)]
+    if not any(cand):
+        cand = list(remote)
+    x = []
+    for i in range(nblk):
+        v = np.float32(z_row[i]) * np.float32(idx_scale) if cand[i] else np.float32(-1.0e4)
+        x.append(float(v) if np.isfinite(v) else -1.0e4)
+    prior = entmax15_bisect(x)
+    masked = [float(prior[i]) if cand[i] else -1.0 for i in range(nblk)]
+    Kp = max(1, min(K, nblk))
+    idx = rank_desc(masked)[:Kp]
+    valid = [masked[i] >= 0.0 for i in idx]
+    logp = [math.log(max(masked[i], floor)) if valid[j] else math.log(floor)
+            for j, i in enumerate(idx)]
+    cnt = max(1, sum(valid))
+    mu = sum(lp for lp, va in zip(logp, valid) if va) / cnt
+    bias = [max(-1e4, min(1e4, (lp - mu) / sigma)) if va else 0.0 for lp, va in zip(logp, valid)]
+    return idx, valid, bias
+
+
 def key_sets(t, S, topi_row, bias_row, valid_row, block_size, local_window, kmin=0):
     """Explicit key set of query t: dict key -> additive bias.
 

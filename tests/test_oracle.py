@@ -137,6 +137,24 @@ def test_route_no_remote_rows_are_invalid():
     assert (bi == 0).all()
 
 
+@pytest.mark.parametrize("seed,scale,with_cand,K", [(21, 11.3, False, 5), (22, 0.7, True, 8),
+                                                    (23, 40.0, True, 12), (24, 11.3, True, 30)])
+def test_train_route_matches_definition(seed, scale, with_cand, K):
+    """Ids, validity and bias of the training router against the from-definition row
+    (full-width entmax by bisection): wide and narrow support, candidate masks, and
+    K above the number of candidates (the remaining slots are non-candidates)."""
+    z, cand = _route_case(seed, 1, 40, 37, 0.5, with_cand)
+    ti, bi, va = O.train_route_select(z, cand, scale, 1e-4, 1.0, K)
+    for t in range(40):
+        idx, valid, bias = bf.train_route_row(z[0, t].numpy(), None if cand is None else
+                                              cand[0, t].numpy(), scale, 1e-4, 1.0, K)
+        assert va[0, t].tolist() == valid, t
+        nv = sum(valid)
+        assert ti[0, t, :nv].tolist() == idx[:nv], t
+        torch.testing.assert_close(bi[0, t].double(), torch.tensor(bias, dtype=torch.float64),
+                                   atol=2e-4, rtol=1e-4)
+
+
 def test_train_route_selects_top_prior():
     z, cand = _route_case(13, 1, 50, 13, 0.5, True)
     ti, bi, va = O.train_route_select(z, cand, 11.3, 1e-4, 1.0, 5)
