@@ -1277,6 +1277,30 @@ inline PlanLayout plan_layout(int B, int H, int S_max, int64_t rows, int K, int 
 
 }  // namespace dash
 
+#include "dash_prefill_bwd.h"
+
+namespace dash {
+// Workspace of the backward: the plan (as the forward's, every routed pair
+// block-major), fp32 bias-gradient and dQ partials per (head, pair position), delta.
+struct BwdLayout {
+  PlanLayout P;
+  int64_t pdb, pdq, delta, total;
+};
+
+inline BwdLayout bwd_layout(int B, int H, int S_max, int64_t rows, int K, int D, int nblk_cap,
+                            int bs) {
+  BwdLayout L;
+  L.P = plan_layout(B, H, S_max, rows, K, D, nblk_cap, bs);
+  int64_t o = L.P.plse;                    // the forward's partials are not needed
+  const int64_t nsub = (bs + 63) / 64;     // 64-key stages per block
+  L.pdb = o; o = align256(o + L.P.ppos * H * nsub * 4);
+  L.pdq = o; o = align256(o + L.P.ppos * H * nsub * (int64_t)D * 4);
+  L.delta = o; o = align256(o + rows * H * 4);
+  L.total = o;
+  return L;
+}
+}  // namespace dash
+
 // ---------------------------------------------------------------------------
 // C entry points
 // ---------------------------------------------------------------------------
@@ -1384,6 +1408,115 @@ extern "C" int dash_attn_prefill(
     hipLaunchKernelGGL(prefill_sparse_kernel<128>, dim3(L.chunk_cap * H * B), dim3(256), 0, st, a);
   }
   hipLaunchKernelGGL((prefill_tile_kernel<128, kTileIT, kTileOcc>), dim3(ntiles * H * B), dim3(256), 0, st, a);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? kOk : (int)e;
+}
+
+extern "C" int dash_attn_prefill_backward_workspace_size(int B, int H, int S_max,
+                                                         int64_t total_rows, int K, int D,
+                                                         int block_size, int64_t* bytes) {
+  using namespace dash;
+  if (!bytes || B < 0 || H <= 0 || S_max < 0 || total_rows < 0 || K < 0 || block_size <= 0)
+    return kErrInvalid;
+  const int nblk_cap = (S_max + block_size - 1) / block_size;
+  *bytes = bwd_layout(B, H, S_max, total_rows, K, D, nblk_cap, block_size).total;
+  return kOk;
+}
+
+extern "C" int dash_attn_prefill_backward(
+    const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+    const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    const void* o, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    const void* dout, int64_t do_sb, int64_t do_sh, int64_t do_st,
+    const float* lse, int64_t lse_row, int64_t lse_sh,
+    const int32_t* idx, const uint8_t* valid, const float* bias, int K,
+    const int32_t* cu_seqlens, const int32_t* kmin,
+    int B, int H, int S, int D, int block_size, int local_window, float scale,
+    void* dq, int64_t dq_sb, int64_t dq_sh, int64_t dq_st,
+    void* dk, int64_t dk_sb, int64_t dk_sh, int64_t dk_st,
+    void* dv, int64_t dv_sb, int64_t dv_sh, int64_t dv_st,
+    float* dbias, int64_t total_rows, void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace dash;
+  if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv) return kErrInvalid;
+  if (B < 0 || H <= 0 || S < 0 || total_rows < 0) return kErrInvalid;
+  if (K > 0 && (!idx || !bias)) return kErrInvalid;
+  if (D != 128) return kErrUnsupported;
+  if (block_size <= 0 || block_size % 32 != 0 || block_size > 256) return kErrUnsupported;
+  if (K < 0 || K > kPfMaxK) return kErrUnsupported;
+  if (local_window < 1) return kErrInvalid;
+  if (B == 0 || S == 0) return kOk;
+  const int nblk_cap = (S + block_size - 1) / block_size;
+  if (nblk_cap > kPfMaxBlocks) return kErrUnsupported;
+  const int64_t strides[] = {q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st,
+                             do_sb, do_sh, do_st, dq_sb, dq_sh, dq_st, dk_sb, dk_sh, dk_st,
+                             dv_sb, dv_sh, dv_st};
+  for (int64_t s : strides)
+    if (s % 8 != 0) return kErrUnsupported;
+  const void* ptrs[] = {q, k, v, o, dout, dq, dk, dv};
+  for (const void* ptr : ptrs)
+    if ((uintptr_t)ptr % 16 != 0) return kErrUnsupported;
+  const BwdLayout L = bwd_layout(B, H, S, total_rows, K, D, nblk_cap, block_size);
+  if (!workspace || workspace_bytes < L.total || (uintptr_t)workspace % 256 != 0)
+    return kErrWorkspace;
+  char* w = (char*)workspace;
+  BwdArgs a = {};
+  PrefillArgs& p = a.p;
+  p.q = (const bf16*)q; p.k = (const bf16*)k; p.v = (const bf16*)v;
+  p.q_sb = q_sb; p.q_sh = q_sh; p.q_st = q_st;
+  p.k_sb = k_sb; p.k_sh = k_sh; p.k_st = k_st;
+  p.v_sb = v_sb; p.v_sh = v_sh; p.v_st = v_st;
+  p.idx = idx; p.valid = valid; p.bias = bias; p.K = K;
+  p.cu = cu_seqlens; p.kmin = kmin;
+  p.S = S; p.H = H; p.bs = block_size; p.lw = local_window; p.nblk_cap = nblk_cap;
+  p.scale_log2e = scale * 1.4426950408889634f;
+  p.ntiles = (S + kPfTQ - 1) / kPfTQ;
+  p.B = B;
+  a.o = (const bf16*)o; a.o_sb = o_sb; a.o_sh = o_sh; a.o_st = o_st;
+  a.dout = (const bf16*)dout; a.do_sb = do_sb; a.do_sh = do_sh; a.do_st = do_st;
+  a.lse = lse; a.lse_row = lse_row; a.lse_sh = lse_sh;
+  a.dq = (bf16*)dq; a.dq_sb = dq_sb; a.dq_sh = dq_sh; a.dq_st = dq_st;
+  a.dk = (bf16*)dk; a.dk_sb = dk_sb; a.dk_sh = dk_sh; a.dk_st = dk_st;
+  a.dv = (bf16*)dv; a.dv_sb = dv_sb; a.dv_sh = dv_sh; a.dv_st = dv_st;
+  a.dbias = dbias;
+  a.scale = scale;
+  a.nsub = (block_size + kBwIT - 1) / kBwIT;
+  a.nstage = (int)(((int64_t)nblk_cap * block_size + kBwIT - 1) / kBwIT);
+  a.delta = (float*)(w + L.delta);
+  a.part_db = (float*)(w + L.pdb);
+  a.part_dq = (float*)(w + L.pdq);
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t nitems = total_rows * H;
+  if (nitems > 0)
+    hipLaunchKernelGGL(bwd_delta_kernel, dim3((unsigned)((nitems * 16 + 255) / 256)), dim3(256), 0, st,
+                       a, total_rows);
+  if (K > 0) {
+    p.kind = (uint8_t*)(w + L.P.kind);
+    p.dense_threshold = kPfTQ + 1;         // no dense blocks: every routed pair block-major
+    p.blk_count = (int32_t*)(w + L.P.count);
+    p.tile_base = (int32_t*)(w + L.P.tbase);
+    p.ntiles_cap = L.P.ntiles_cap;
+    p.blk_chunk = (int32_t*)(w + L.P.bch);
+    p.num_chunks = (int32_t*)(w + L.P.nchunks);
+    p.chunk_pref = (int32_t*)(w + L.P.cpref);
+    p.done = (int32_t*)(w + L.P.done);
+    p.err = (int32_t*)(w + L.P.err);
+    p.chunk_rec = (int32_t*)(w + L.P.rec);
+    p.chunk_cap = L.P.chunk_cap;
+    p.spos = (int32_t*)(w + L.P.spos);
+    p.ppos = L.P.ppos;
+    const int ncount = (int)((L.P.err - L.P.count) / 4) + 1;
+    hipLaunchKernelGGL(prefill_clear_kernel, dim3((ncount + 255) / 256), dim3(256), 0, st,
+                       p.blk_count, ncount);
+    hipLaunchKernelGGL(prefill_plan_kernel, dim3(p.ntiles, B), dim3(kPfTQ), 0, st, p);
+    hipLaunchKernelGGL(prefill_scan_kernel, dim3(B), dim3(1024), 0, st, p);
+    hipLaunchKernelGGL(prefill_scatter_kernel, dim3(p.ntiles, B), dim3(kPfTQ), 0, st, p);
+  }
+  hipLaunchKernelGGL(bwd_kv_kernel, dim3(a.nstage * H * B), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(bwd_q_kernel, dim3(p.ntiles * H * B), dim3(256), 0, st, a);
+  if (dbias && K > 0 && total_rows > 0)
+    hipLaunchKernelGGL(bwd_dbias_kernel, dim3((unsigned)((total_rows * K + 255) / 256)), dim3(256), 0,
+                       st, a, total_rows * K);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? kOk : (int)e;
 }

@@ -295,6 +295,92 @@ def attn_prefill(q, k, v, idx, bias, valid, block_size, local_window, scale,
     return (o, lse) if return_lse else o
 
 
+def attn_prefill_backward(q, k, v, o, lse, dout, idx, bias, valid, block_size, local_window,
+                          scale, cu_seqlens=None, kmin=None, max_seqlen=None, need_dbias=True):
+    """Gradients of attn_prefill: (dq, dk, dv) bf16 shaped like q, k, v and the routed
+    slots' bias gradient dbias fp32 shaped like bias (or None).  o and lse [B,S,H] (or
+    [1,T,H]) are the forward's outputs (attn_prefill(..., return_lse=True))."""
+    _need_gpu(q, k, v, o, lse, dout)
+    lib = _lib.load()
+    q, k, v = _rows(q), _rows(k.to(q.dtype)), _rows(v.to(q.dtype))
+    o, dout = _rows(o), _rows(dout.to(q.dtype))
+    B, H, S, D = q.shape
+    lse = lse.float().contiguous()
+    K = 0 if idx is None else idx.shape[-1]
+    idx_c = None if idx is None else _i32(idx)
+    bias_c = None if bias is None else bias.float().contiguous()
+    valid_c = _u8(valid)
+    cu = _i32(cu_seqlens)
+    nb = B
+    if cu is not None:
+        nb = cu.numel() - 1
+        Smax = _max_len(cu, max_seqlen)
+        rows = S
+    else:
+        Smax = S
+        rows = B * S
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    dbias = None
+    if need_dbias and K > 0:
+        dbias = torch.empty(idx.shape, dtype=torch.float32, device=q.device)
+    nbytes = ctypes.c_int64(0)
+    _lib.check(lib.dash_attn_prefill_backward_workspace_size(nb, H, Smax, rows, K, D,
+                                                             int(block_size), nbytes),
+               "workspace")
+    ws = cached_workspace("prefill_bwd", nbytes.value, q.device)
+    km = _i32(kmin)
+    st_ = lib.dash_attn_prefill_backward(
+        _ptr(q), q.stride(0), q.stride(1), q.stride(2),
+        _ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        _ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        _ptr(o), o.stride(0), o.stride(1), o.stride(2),
+        _ptr(dout), dout.stride(0), dout.stride(1), dout.stride(2),
+        _ptr(lse), H, 1,
+        _ptr(idx_c), _ptr(valid_c), _ptr(bias_c), K, _ptr(cu), _ptr(km),
+        nb, H, Smax, D, int(block_size), int(local_window), float(scale),
+        _ptr(dq), dq.stride(0), dq.stride(1), dq.stride(2),
+        _ptr(dk), dk.stride(0), dk.stride(1), dk.stride(2),
+        _ptr(dv), dv.stride(0), dv.stride(1), dv.stride(2),
+        _ptr(dbias), rows, _ptr(ws), ws.numel(), _stream())
+    _lib.check(st_, "dash_attn_prefill_backward")
+    return dq, dk, dv, dbias
+
+
+class _DashAttnFn(torch.autograd.Function):
+    """attn_prefill with gradients to q, k, v and the routed slots' bias (the role of
+    _E2EGatherAttnFn, sparse_gather_e2e_triton.py:288-339)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, bias, idx, valid, block_size, local_window, scale, cu_seqlens,
+                kmin, max_seqlen):
+        out, lse = attn_prefill(q, k, v, idx, bias, valid, block_size, local_window, scale,
+                                cu_seqlens=cu_seqlens, kmin=kmin, return_lse=True,
+                                max_seqlen=max_seqlen)
+        ctx.save_for_backward(q, k, v, out, lse, idx, bias, valid, cu_seqlens, kmin)
+        ctx.cfg = (block_size, local_window, scale, max_seqlen)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse, idx, bias, valid, cu, kmin = ctx.saved_tensors
+        block_size, local_window, scale, max_seqlen = ctx.cfg
+        dq, dk, dv, dbias = attn_prefill_backward(
+            q, k, v, out, lse, dout, idx, bias, valid, block_size, local_window, scale,
+            cu_seqlens=cu, kmin=kmin, max_seqlen=max_seqlen,
+            need_dbias=bias is not None and ctx.needs_input_grad[3])
+        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dbias, None, None, None, None,
+                None, None, None, None)
+
+
+def attn_prefill_autograd(q, k, v, idx, bias, valid, block_size, local_window, scale,
+                          cu_seqlens=None, kmin=None, max_seqlen=None):
+    """attn_prefill recorded for autograd (bf16 q/k/v; the bias gradient is fp32)."""
+    return _DashAttnFn.apply(q, k, v, bias, idx, valid, block_size, local_window, scale,
+                             cu_seqlens, kmin, max_seqlen)
+
+
 def default_nsplit(nunits):
     """One unit (key block) per wavefront, at most 64 partials per (b, h)."""
     return int(max(1, min(64, nunits)))

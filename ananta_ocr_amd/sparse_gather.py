@@ -9,9 +9,10 @@ arguments, shapes and "return None on an unsupported input" behaviour:
 * ``triton_block_max_score``      -- sparse_gather_triton.py:431-467
 
 The names are kept so existing call sites import them unchanged; the work runs
-in ``libdash_hip.so`` (dash_attn_prefill, dash_block_max_score).  Forward only:
-tensors that require grad raise NotImplementedError (the backward kernels are
-not part of this library).
+in ``libdash_hip.so`` (dash_attn_prefill, dash_block_max_score).  The fused entry
+point records autograd when its inputs require grad (the backward runs in
+dash_attn_prefill_backward); ``triton_gather_attention`` (no bias) is forward only
+and raises NotImplementedError for tensors that require grad.
 """
 
 import torch
@@ -44,13 +45,17 @@ def gather_attention_e2e(query_states, key_states, value_states, block_indices,
     ar = torch.arange(T, device=position_ids.device)
     if not bool((position_ids == ar).all()):
         return None
-    _no_grad_check(query_states, key_states, value_states, blk_bias_slots)
     if key_states.shape[1] != HQ:
         rep = HQ // key_states.shape[1]
         key_states = key_states.repeat_interleave(rep, dim=1)
         value_states = value_states.repeat_interleave(rep, dim=1)
     lw = block_size if local_window is None else max(1, int(local_window))
     sel = block_indices[:, 0]
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in
+                                       (query_states, key_states, value_states, blk_bias_slots)):
+        # gradients to q, k, v and the bias slots (_E2EGatherAttnFn, :288-339)
+        return ops.attn_prefill_autograd(query_states, key_states, value_states, sel,
+                                         blk_bias_slots, None, block_size, lw, scale)
     return ops.attn_prefill(query_states, key_states, value_states, sel, blk_bias_slots, None,
                             block_size, lw, scale)
 

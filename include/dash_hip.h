@@ -148,6 +148,38 @@ int dash_attn_prefill(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
 int dash_attn_prefill_workspace_size(int B, int H, int S_max, int64_t total_rows, int K, int D,
                                      int block_size, int64_t* bytes);
 
+/* Workspace bytes of dash_attn_prefill_backward. */
+int dash_attn_prefill_backward_workspace_size(int B, int H, int S_max, int64_t total_rows, int K,
+                                              int D, int block_size, int64_t* bytes);
+
+/*
+ * Backward of dash_attn_prefill: dq, dk, dv (bf16, the layouts and strides of q, k, v)
+ * and dbias fp32 [total_rows, K] (the gradient of every routed slot's bias: summed over
+ * heads and the block's visible keys for the first valid slot of a block, 0 for the other
+ * slots; NULL: not computed).  Replaces the Triton backward of the fused gather attention
+ * (_E2EGatherAttnFn.backward, sparse_gather_e2e_triton.py:311-339, with its dq/d_bias
+ * kernel :118-190 and dk/dv kernel :193-262).  o and lse (natural log, lse[row * lse_row
+ * + h * lse_sh]) are the forward's outputs; dout the gradient of o.  Same routing, varlen
+ * and kmin arguments as the forward; block_size in {32, 64, ..., 256}, K <= 16, D == 128.
+ * workspace: dash_attn_prefill_backward_workspace_size bytes, 256-byte aligned, any
+ * contents.  Calls sharing a workspace must not overlap.
+ */
+int dash_attn_prefill_backward(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                               const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                               const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                               const void* o, int64_t o_sb, int64_t o_sh, int64_t o_st,
+                               const void* dout, int64_t do_sb, int64_t do_sh, int64_t do_st,
+                               const float* lse, int64_t lse_row, int64_t lse_sh,
+                               const int32_t* idx, const uint8_t* valid, const float* bias,
+                               int K, const int32_t* cu_seqlens, const int32_t* kmin,
+                               int B, int H, int S, int D, int block_size, int local_window,
+                               float scale,
+                               void* dq, int64_t dq_sb, int64_t dq_sh, int64_t dq_st,
+                               void* dk, int64_t dk_sb, int64_t dk_sh, int64_t dk_st,
+                               void* dv, int64_t dv_sb, int64_t dv_sh, int64_t dv_st,
+                               float* dbias, int64_t total_rows, void* workspace,
+                               int64_t workspace_bytes, void* stream);
+
 /*
  * Byte offset, inside a dash_attn_prefill workspace of these sizes, of the plan's int32
  * error word: 0 after a call whose pair counts fit the workspace; nonzero if a chunk
