@@ -27,6 +27,10 @@ SIGNATURES = {
     "dash_router_qk_norm": (_i, [_p, _i, _l, _l, _i, _i, _p, _p, _f, _p, _p, _i, _l, _l, _p, _p,
                                  _p]),
     "dash_route": (_i, [_p, _l, _i, _i, _p, _p, _l, _f, _f, _f, _i, _i, _i, _p, _p, _p, _p]),
+    "dash_train_route": (_i, [_p, _l, _i, _i, _p, _p, _l, _f, _f, _f, _i, _i, _p, _p, _p, _p,
+                              _p, _p]),
+    "dash_train_route_backward": (_i, [_p, _l, _i, _i, _p, _p, _l, _f, _f, _f, _i, _p, _p, _p,
+                                       _p, _p, _p, _l, _p]),
     "dash_attn_prefill": (_i, [_p, _l, _l, _l, _p, _l, _l, _l, _p, _l, _l, _l, _p, _l, _l, _l,
                                _p, _l, _l, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _f,
                                _i, _l, _p, _l, _p]),

@@ -20,6 +20,7 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4;
 constexpr float kScoreNeg = -1.0e9f;
 constexpr float kEntmaxNeg = -1.0e4f;
 constexpr float kActClamp = 1.0e4f;
+constexpr float kGradClamp = 1.0e4f;   // gradient sanitizer bound (dash_attention.py:603)
 
 constexpr int kWave = 64;
 

@@ -852,6 +852,288 @@ __global__ __launch_bounds__(kRtWaves * kWave) void route_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Training routing (dash_attention.py:906-960): one wavefront per score row.
+//   x = cand ? z idx_scale : -1e4 (non-finite -> -1e4), over the row's nblk blocks;
+//   prior = 1.5-entmax(x) over the whole row (dash_attention.py:638-647):
+//     X = (x - max)/2, prior = max(X - tau, 0)^2 with sum(prior) = 1; tau by
+//     bisection in double, then exactly from the support's sums (the sort-threshold
+//     closed form at the support size);
+//   the K' = max(1, min(K, nblk)) largest of the masked prior (non-candidates at -1),
+//     ties to the lower block id; valid = candidate;
+//   bias = valid ? clamp((log(max(p, floor)) - mean over valid) / sigma, +-1e4) : 0.
+// The row maximum and tau are kept for the backward, which recomputes the prior.
+// ---------------------------------------------------------------------------
+constexpr int kTrWaves = 4;
+constexpr int kTrMaxK = 64;
+
+struct TrainRow {
+  int nb;
+  float xmax;
+};
+
+// x of the row's columns c = lane + 64 i (entries past nb: -inf) and candidate flags.
+template <int NPL>
+__device__ __forceinline__ TrainRow train_row_inputs(const float* z, int64_t z_stride, int row,
+                                                     int nblk, const int32_t* row_nblk,
+                                                     const uint8_t* cand_in, int64_t cand_stride,
+                                                     float idx_scale, float (&x)[NPL],
+                                                     bool (&cd)[NPL]) {
+  const int lane = wave_lane();
+  TrainRow r;
+  r.nb = row_nblk ? max(0, min(row_nblk[row], nblk)) : nblk;
+  float zv[NPL];
+  uint8_t cb[NPL];
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int c = min(lane + kWave * i, nblk - 1);
+    zv[i] = z[(int64_t)row * z_stride + c];
+    cb[i] = cand_in ? cand_in[(int64_t)row * cand_stride + c] : 1;
+  }
+  bool any_cand = false;
+  if (cand_in) {
+#pragma unroll
+    for (int i = 0; i < NPL; ++i)
+      any_cand |= (lane + kWave * i < r.nb) && zv[i] > kScoreNeg * 0.5f && cb[i] != 0;
+  }
+  const bool use_cand = cand_in && __any(any_cand);
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int c = lane + kWave * i;
+    const bool remote = c < r.nb && zv[i] > kScoreNeg * 0.5f;
+    cd[i] = use_cand ? (remote && cb[i] != 0) : remote;
+    float xv = cd[i] ? zv[i] * idx_scale : kEntmaxNeg;
+    if (!(fabsf(xv) <= 3.402823466e38f)) xv = kEntmaxNeg;
+    x[i] = c < r.nb ? xv : -INFINITY;
+    mx = fmaxf(mx, x[i]);
+  }
+  r.xmax = wave_max(mx);
+  return r;
+}
+
+// tau of the 1.5-entmax of X = (x - xmax)/2 over the live entries (max X = 0).
+template <int NPL>
+__device__ __forceinline__ float train_tau(const float (&x)[NPL], float xmax) {
+#pragma clang fp contract(off)
+  float X[NPL];
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) X[i] = __fdiv_rn(__fsub_rn(x[i], xmax), 2.0f);   // -inf stays
+  double lo = -1.0, hi = 0.0;               // f(-1) >= 1 (the maximum contributes 1), f(0) = 0
+  for (int it = 0; it < 48; ++it) {
+    const double mid = 0.5 * (lo + hi);
+    double f = 0.0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const double d = (double)X[i] - mid;
+      if (d > 0.0) f += d * d;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) f += __shfl_xor(f, m, kWave);
+    if (f >= 1.0) lo = mid; else hi = mid;
+  }
+  const double t0 = 0.5 * (lo + hi);
+  double n = 0.0, s1 = 0.0, s2 = 0.0;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i)
+    if ((double)X[i] > t0) { n += 1.0; s1 += X[i]; s2 += (double)X[i] * X[i]; }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    n += __shfl_xor(n, m, kWave);
+    s1 += __shfl_xor(s1, m, kWave);
+    s2 += __shfl_xor(s2, m, kWave);
+  }
+  const double mean = s1 / n, msq = s2 / n;
+  const double delta = (1.0 - n * (msq - mean * mean)) / n;
+  return (float)(mean - sqrt(delta > 0.0 ? delta : 0.0));
+}
+
+__device__ __forceinline__ float train_prior(float x, float xmax, float tau) {
+#pragma clang fp contract(off)
+  const float X = __fdiv_rn(__fsub_rn(x, xmax), 2.0f);
+  const float t = __fsub_rn(X, tau);
+  return t > 0.f ? __fmul_rn(t, t) : 0.f;
+}
+
+template <int NPL>
+__global__ __launch_bounds__(kTrWaves * kWave) void train_route_kernel(
+    const float* __restrict__ z, int64_t z_stride, int rows, int nblk,
+    const int32_t* __restrict__ row_nblk, const uint8_t* __restrict__ cand_in,
+    int64_t cand_stride, float idx_scale, float floor_p, float inv_sigma, int K, int Kout,
+    int32_t* __restrict__ idx_out, float* __restrict__ bias_out, uint8_t* __restrict__ valid_out,
+    float* __restrict__ topv_out, float2* __restrict__ stat_out) {
+  __shared__ uint64_t s_sel[kTrWaves][kTrMaxK];
+  const int lane = wave_lane(), wv = threadIdx.x / kWave;
+  const int row = blockIdx.x * kTrWaves + wv;
+  if (row >= rows) return;
+  float x[NPL];
+  bool cd[NPL];
+  const TrainRow tr = train_row_inputs<NPL>(z, z_stride, row, nblk, row_nblk, cand_in, cand_stride,
+                                            idx_scale, x, cd);
+  int32_t* io = idx_out + (int64_t)row * Kout;
+  float* bo = bias_out + (int64_t)row * Kout;
+  if (tr.nb == 0) {
+    for (int m = lane; m < Kout; m += kWave) {
+      io[m] = -1; bo[m] = 0.f;
+      if (valid_out) valid_out[(int64_t)row * Kout + m] = 0;
+      if (topv_out) topv_out[(int64_t)row * Kout + m] = -1.f;
+    }
+    if (lane == 0 && stat_out) stat_out[row] = make_float2(0.f, 0.f);
+    return;
+  }
+  const float tau = train_tau<NPL>(x, tr.xmax);
+  // masked prior keys: candidates by prior, non-candidates at -1, absent entries 0
+  uint32_t hkey[NPL];
+  uint32_t kmx = 0;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int c = lane + kWave * i;
+    const float sp = cd[i] ? train_prior(x[i], tr.xmax, tau) : -1.f;
+    hkey[i] = c < tr.nb ? ord_key(sp) : 0u;
+    kmx = max(kmx, hkey[i]);
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) kmx = max(kmx, (uint32_t)__shfl_xor((int)kmx, m, kWave));
+  const int Kp = max(1, min(min(K, kTrMaxK), tr.nb));
+  const uint32_t T = kth_key<NPL>(hkey, Kp, ord_key(-1.f), kmx);
+  int n_gt = 0;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) n_gt += __popcll(__ballot(hkey[i] > T));
+  const int need_eq = Kp - n_gt;
+  int taken = 0, eq_seen = 0;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const bool eq = hkey[i] == T;
+    const uint64_t meq = __ballot(eq);
+    const bool take = hkey[i] > T || (eq && eq_seen + lane_prefix(meq) < need_eq);
+    const uint64_t mt = __ballot(take);
+    const int c = lane + kWave * i;
+    if (take)
+      s_sel[wv][taken + lane_prefix(mt)] =
+          ((uint64_t)hkey[i] << 32) | ((uint32_t)(0xffff - c) << 1) | (cd[i] ? 1u : 0u);
+    taken += __popcll(mt);
+    eq_seen += __popcll(meq);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // rank of lane m's entry among the Kp selected: its output slot
+  const uint64_t key = lane < Kp ? s_sel[wv][lane] : 0ull;
+  int rank = 0;
+  for (int j = 0; j < Kp; ++j) rank += s_sel[wv][j] > key ? 1 : 0;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (lane < Kp) s_sel[wv][rank] = key;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // lane m holds slot m
+  const uint64_t ks = lane < Kp ? s_sel[wv][lane] : 0ull;
+  const float v = lane < Kp ? ord_key_inv((uint32_t)(ks >> 32)) : -1.f;
+  const int c = 0xffff - (int)(((uint32_t)ks >> 1) & 0xffff);
+  const bool va = lane < Kp && (ks & 1ull) != 0;
+  const float logp = logf(fmaxf(v, floor_p));
+  // mean log-prior of the valid slots, summed in slot order
+  const uint64_t vm = __ballot(va);
+  float musum = 0.f;
+  int cnt = 0;
+  for (int j = 0; j < Kp; ++j)
+    if ((vm >> j) & 1ull) {
+      musum += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(logp), j));
+      ++cnt;
+    }
+  const float mu = musum / (float)max(cnt, 1);
+  for (int m = lane; m < Kout; m += kWave) {
+    const bool in = m < Kp;
+    const bool mv = in && va;                  // m == lane when in (Kp <= 64)
+    io[m] = in ? c : -1;
+    bo[m] = mv ? fminf(fmaxf((logp - mu) * inv_sigma, -kActClamp), kActClamp) : 0.f;
+    if (valid_out) valid_out[(int64_t)row * Kout + m] = mv ? 1 : 0;
+    if (topv_out) topv_out[(int64_t)row * Kout + m] = in ? v : -1.f;
+  }
+  if (lane == 0 && stat_out) stat_out[row] = make_float2(tr.xmax, tau);
+}
+
+// Backward of train_route_kernel for one row: the bias gradient of the valid slots
+// through the centred log-prior (d logp_j = (g_j - mean over valid g)/sigma, g the
+// bias gradient where the clamp passes it; d p_j = d logp_j / p_j where p_j >= floor),
+// scattered to the prior's columns; the 1.5-entmax backward (dash_attention.py:650-658:
+// dX = dY sqrt(Y) - q sqrt(Y), q = sum(dY sqrt(Y)) / sum(sqrt(Y))) on the recomputed
+// prior; dz = dX idx_scale on candidates, 0 elsewhere.
+template <int NPL>
+__global__ __launch_bounds__(kTrWaves * kWave) void train_route_bwd_kernel(
+    const float* __restrict__ z, int64_t z_stride, int rows, int nblk,
+    const int32_t* __restrict__ row_nblk, const uint8_t* __restrict__ cand_in,
+    int64_t cand_stride, float idx_scale, float floor_p, float inv_sigma, int Kout,
+    const int32_t* __restrict__ idx, const uint8_t* __restrict__ valid,
+    const float* __restrict__ topv, const float2* __restrict__ stat,
+    const float* __restrict__ dbias, float* __restrict__ dz, int64_t dz_stride) {
+  __shared__ float s_dy[kTrWaves][64 * NPL];
+  const int lane = wave_lane(), wv = threadIdx.x / kWave;
+  const int row = blockIdx.x * kTrWaves + wv;
+  if (row >= rows) return;
+  float x[NPL];
+  bool cd[NPL];
+  const TrainRow tr = train_row_inputs<NPL>(z, z_stride, row, nblk, row_nblk, cand_in, cand_stride,
+                                            idx_scale, x, cd);
+  float* dzr = dz + (int64_t)row * dz_stride;
+  const float2 st = stat[row];
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) s_dy[wv][lane + kWave * i] = 0.f;
+  // slot gradients, lane m = slot m (Kout <= 64)
+  const int64_t so = (int64_t)row * Kout;
+  const bool in = lane < Kout;
+  const int ci = in ? idx[so + lane] : -1;
+  const bool va = in && valid[so + lane] != 0 && ci >= 0 && ci < tr.nb;
+  const float v = in ? topv[so + lane] : 0.f;
+  const float logp = logf(fmaxf(v, floor_p));
+  const uint64_t vm = __ballot(va);
+  float musum = 0.f;
+  int cnt = 0;
+  for (int j = 0; j < Kout && j < kWave; ++j)
+    if ((vm >> j) & 1ull) {
+      musum += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(logp), j));
+      ++cnt;
+    }
+  const float mu = musum / (float)max(cnt, 1);
+  const float bv = (logp - mu) * inv_sigma;
+  const float g = (va && bv >= -kActClamp && bv <= kActClamp) ? dbias[so + lane] : 0.f;
+  const float gsum = wave_sum(g);
+  const float dlogp = va ? (g - gsum / (float)max(cnt, 1)) * inv_sigma : 0.f;
+  // the prior's gradient passes _sanitize_grad (dash_attention.py:607-613, hooked at :1046):
+  // non-finite -> 0, clamped to +-1e4
+  float dv = (va && v >= floor_p) ? dlogp / v : 0.f;
+  dv = (fabsf(dv) <= 3.402823466e38f) ? fminf(fmaxf(dv, -kGradClamp), kGradClamp) : 0.f;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (va) s_dy[wv][ci] = dv;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // entmax backward on the recomputed prior
+  float gp[NPL], dx[NPL];
+  float sg = 0.f, sdx = 0.f;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int c = lane + kWave * i;
+    const float y = c < tr.nb ? train_prior(x[i], st.x, st.y) : 0.f;
+    gp[i] = sqrtf(y);
+    dx[i] = (c < tr.nb ? s_dy[wv][c] : 0.f) * gp[i];
+    sg += gp[i];
+    sdx += dx[i];
+  }
+  sg = wave_sum(sg);
+  sdx = wave_sum(sdx);
+  const float qv = sdx / fmaxf(sg, 1e-12f);
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int c = lane + kWave * i;
+    if (c < nblk) dzr[c] = (c < tr.nb && cd[i]) ? (dx[i] - qv * gp[i]) * idx_scale : 0.f;
+  }
+}
+
 }  // namespace dash
 
 // ---------------------------------------------------------------------------
@@ -965,6 +1247,71 @@ extern "C" int dash_route(const float* z, int64_t z_stride, int rows, int nblk_c
   else if (npl <= 16) DASH_ROUTE(16);
   else DASH_ROUTE(32);
 #undef DASH_ROUTE
+  return launch_status();
+}
+
+extern "C" int dash_train_route(const float* z, int64_t z_stride, int rows, int nblk_cols,
+                                const int32_t* row_nblk, const uint8_t* cand, int64_t cand_stride,
+                                float idx_scale, float floor_p, float sigma, int K, int Kout,
+                                int32_t* idx, float* bias, uint8_t* valid, float* topv,
+                                float* stat, void* stream) {
+  using namespace dash;
+  if (!z || !idx || !bias || !topv || !stat || rows < 0 || nblk_cols < 0) return kErrInvalid;
+  if (z_stride < nblk_cols || (cand && cand_stride < nblk_cols)) return kErrInvalid;
+  if (K < 1 || Kout < 1 || Kout < std::min(K, std::max(nblk_cols, 1))) return kErrInvalid;
+  if (K > kTrMaxK || Kout > kTrMaxK) return kErrUnsupported;
+  if (nblk_cols > 64 * 32) return kErrUnsupported;
+  if (rows == 0) return kOk;
+  if (nblk_cols == 0) return kErrInvalid;
+  const float inv_sigma = (float)(1.0 / (double)sigma);
+  dim3 grid((rows + kTrWaves - 1) / kTrWaves);
+  hipStream_t st = (hipStream_t)stream;
+  const int npl = (nblk_cols + 63) / 64;
+#define DASH_TROUTE(N)                                                                           \
+  hipLaunchKernelGGL(train_route_kernel<N>, grid, dim3(kTrWaves * kWave), 0, st, z, z_stride, rows, \
+                     nblk_cols, row_nblk, cand, cand_stride, idx_scale, floor_p, inv_sigma, K, Kout, \
+                     idx, bias, valid, topv, (float2*)stat)
+  if (npl <= 1) DASH_TROUTE(1);
+  else if (npl <= 2) DASH_TROUTE(2);
+  else if (npl <= 4) DASH_TROUTE(4);
+  else if (npl <= 8) DASH_TROUTE(8);
+  else if (npl <= 16) DASH_TROUTE(16);
+  else DASH_TROUTE(32);
+#undef DASH_TROUTE
+  return launch_status();
+}
+
+extern "C" int dash_train_route_backward(const float* z, int64_t z_stride, int rows, int nblk_cols,
+                                         const int32_t* row_nblk, const uint8_t* cand,
+                                         int64_t cand_stride, float idx_scale, float floor_p,
+                                         float sigma, int Kout, const int32_t* idx,
+                                         const uint8_t* valid, const float* topv,
+                                         const float* stat, const float* dbias, float* dz,
+                                         int64_t dz_stride, void* stream) {
+  using namespace dash;
+  if (!z || !idx || !valid || !topv || !stat || !dbias || !dz || rows < 0 || nblk_cols < 0)
+    return kErrInvalid;
+  if (z_stride < nblk_cols || dz_stride < nblk_cols || (cand && cand_stride < nblk_cols))
+    return kErrInvalid;
+  if (Kout < 1 || Kout > kTrMaxK) return kErrUnsupported;
+  if (nblk_cols > 64 * 32) return kErrUnsupported;
+  if (rows == 0) return kOk;
+  if (nblk_cols == 0) return kErrInvalid;
+  const float inv_sigma = (float)(1.0 / (double)sigma);
+  dim3 grid((rows + kTrWaves - 1) / kTrWaves);
+  hipStream_t st = (hipStream_t)stream;
+  const int npl = (nblk_cols + 63) / 64;
+#define DASH_TRBWD(N)                                                                            \
+  hipLaunchKernelGGL(train_route_bwd_kernel<N>, grid, dim3(kTrWaves * kWave), 0, st, z, z_stride,  \
+                     rows, nblk_cols, row_nblk, cand, cand_stride, idx_scale, floor_p, inv_sigma,  \
+                     Kout, idx, valid, topv, (const float2*)stat, dbias, dz, dz_stride)
+  if (npl <= 1) DASH_TRBWD(1);
+  else if (npl <= 2) DASH_TRBWD(2);
+  else if (npl <= 4) DASH_TRBWD(4);
+  else if (npl <= 8) DASH_TRBWD(8);
+  else if (npl <= 16) DASH_TRBWD(16);
+  else DASH_TRBWD(32);
+#undef DASH_TRBWD
   return launch_status();
 }
 

@@ -221,6 +221,97 @@ def route(z, cand, idx_scale, floor, sigma, K, topm, row_nblk=None, width=None):
     return idx.view(*lead, Kp), bias.view(*lead, Kp), valid.view(*lead, Kp).view(torch.bool)
 
 
+TRAIN_MAX_K = 64
+
+
+def _train_route_inputs(z, cand, row_nblk):
+    nblk = z.shape[-1]
+    z2 = z.detach().reshape(-1, nblk).float()
+    if z2.stride(-1) != 1:
+        z2 = z2.contiguous()
+    c2 = None if cand is None else _u8(cand.reshape(-1, nblk))
+    return z2, c2, _i32(row_nblk)
+
+
+def train_route_raw(z, cand, idx_scale, floor, sigma, K, row_nblk=None):
+    """Training routing of every row of z [..., nblk] fp32 (no autograd).
+    Returns (idx int32, bias fp32, valid bool, topv fp32, stat fp32 [rows, 2]) with
+    K' = max(1, min(K, nblk)) slots."""
+    _need_gpu(z)
+    if int(K) > TRAIN_MAX_K:
+        raise NotImplementedError(f"training routing supports K <= {TRAIN_MAX_K}, got {K}")
+    lib = _lib.load()
+    lead = z.shape[:-1]
+    nblk = z.shape[-1]
+    z2, c2, rn = _train_route_inputs(z, cand, row_nblk)
+    rows = z2.shape[0]
+    Kp = max(1, min(int(K), nblk))
+    idx = torch.empty(rows, Kp, dtype=torch.int32, device=z.device)
+    bias = torch.empty(rows, Kp, dtype=torch.float32, device=z.device)
+    valid = torch.empty(rows, Kp, dtype=torch.uint8, device=z.device)
+    topv = torch.empty(rows, Kp, dtype=torch.float32, device=z.device)
+    stat = torch.empty(rows, 2, dtype=torch.float32, device=z.device)
+    st_ = lib.dash_train_route(_ptr(z2), z2.stride(0), rows, nblk, _ptr(rn), _ptr(c2),
+                               0 if c2 is None else c2.stride(0), float(idx_scale), float(floor),
+                               float(sigma), int(K), Kp, _ptr(idx), _ptr(bias), _ptr(valid),
+                               _ptr(topv), _ptr(stat), _stream())
+    _lib.check(st_, "dash_train_route")
+    return (idx.view(*lead, Kp), bias.view(*lead, Kp), valid.view(*lead, Kp).view(torch.bool),
+            topv.view(*lead, Kp), stat)
+
+
+def train_route_backward(z, cand, idx_scale, floor, sigma, idx, valid, topv, stat, dbias,
+                         row_nblk=None):
+    """dz [..., nblk] fp32 for the bias gradient dbias [..., K'] of train_route_raw."""
+    _need_gpu(z, dbias)
+    lib = _lib.load()
+    nblk = z.shape[-1]
+    z2, c2, rn = _train_route_inputs(z, cand, row_nblk)
+    rows = z2.shape[0]
+    Kp = idx.shape[-1]
+    idx2 = _i32(idx.reshape(rows, Kp))
+    val2 = _u8(valid.reshape(rows, Kp))
+    tv2 = topv.reshape(rows, Kp).float().contiguous()
+    db2 = dbias.reshape(rows, Kp).float().contiguous()
+    dz = torch.empty(rows, nblk, dtype=torch.float32, device=z.device)
+    st_ = lib.dash_train_route_backward(
+        _ptr(z2), z2.stride(0), rows, nblk, _ptr(rn), _ptr(c2),
+        0 if c2 is None else c2.stride(0), float(idx_scale), float(floor), float(sigma), Kp,
+        _ptr(idx2), _ptr(val2), _ptr(tv2), _ptr(stat), _ptr(db2), _ptr(dz), dz.stride(0),
+        _stream())
+    _lib.check(st_, "dash_train_route_backward")
+    return dz.view(z.shape)
+
+
+class _TrainRouteFn(torch.autograd.Function):
+    """_route + _select_and_bias (dash_attention.py:906-960) with the bias
+    differentiable in the block scores; topi and valid carry no gradient."""
+
+    @staticmethod
+    def forward(ctx, z, cand, idx_scale, floor, sigma, K, row_nblk):
+        idx, bias, valid, topv, stat = train_route_raw(z, cand, idx_scale, floor, sigma, K,
+                                                       row_nblk)
+        ctx.save_for_backward(z, cand, row_nblk, idx, valid, topv, stat)
+        ctx.cfg = (idx_scale, floor, sigma)
+        ctx.mark_non_differentiable(idx, valid)
+        return idx, bias, valid
+
+    @staticmethod
+    def backward(ctx, didx, dbias, dvalid):
+        z, cand, row_nblk, idx, valid, topv, stat = ctx.saved_tensors
+        idx_scale, floor, sigma = ctx.cfg
+        if dbias is None:
+            return (None,) * 7
+        dz = train_route_backward(z, cand, idx_scale, floor, sigma, idx, valid, topv, stat,
+                                  dbias, row_nblk)
+        return dz.to(z.dtype), None, None, None, None, None, None
+
+
+def train_route(z, cand, idx_scale, floor, sigma, K, row_nblk=None):
+    """Training routing with autograd: (idx int32 [..., K'], bias fp32, valid bool)."""
+    return _TrainRouteFn.apply(z, cand, idx_scale, floor, sigma, K, row_nblk)
+
+
 DENSE_THRESHOLD = 32   # of the 128 queries of a tile; below it a routed block goes sparse
 
 _WORKSPACES = {}

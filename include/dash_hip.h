@@ -117,6 +117,39 @@ int dash_route(const float* z, int64_t z_stride, int rows, int nblk_cols,
                int32_t* idx, float* bias, uint8_t* valid, void* stream);
 
 /*
+ * Training routing of every score row (dash_attention.py:906-960, _route then
+ * _select_and_bias): candidates as dash_route; x = cand ? z*idx_scale : -1e4
+ * (non-finite -> -1e4); prior = 1.5-entmax(x) over the row's first nb columns
+ * (nb = row_nblk[r] or nblk_cols); the K' = max(1, min(K, nb)) largest of
+ * (cand ? prior : -1), ties to the lower block id; valid = candidate; bias =
+ * valid ? clamp((log(max(prior,floor)) - mean_valid)/sigma, +-1e4) : 0.
+ * K <= 64, Kout <= 64, Kout >= K', nblk_cols <= 2048.
+ *   idx/bias/valid/topv [rows, Kout]: slots >= K' get idx -1, bias 0, valid 0, topv -1.
+ *   topv is the masked prior of each slot (-1 for a non-candidate).
+ *   stat fp32 [rows, 2]: the row maximum of x and the entmax threshold, which
+ *   dash_train_route_backward uses to recompute the prior.
+ */
+int dash_train_route(const float* z, int64_t z_stride, int rows, int nblk_cols,
+                     const int32_t* row_nblk, const uint8_t* cand, int64_t cand_stride,
+                     float idx_scale, float floor_p, float sigma, int K, int Kout, int32_t* idx,
+                     float* bias, uint8_t* valid, float* topv, float* stat, void* stream);
+
+/*
+ * Gradient of dash_train_route's bias with respect to z, as autograd differentiates
+ * _route/_select_and_bias (dash_attention.py:906-960) through the clamp, the
+ * centred log of the clamped prior and _Entmax15.backward (dash_attention.py:650-658).
+ * Takes the same z/row_nblk/cand/scalars as the forward call and its idx, valid,
+ * topv and stat outputs; dbias fp32 [rows, Kout]; writes dz fp32 [rows, dz_stride]
+ * for every column < nblk_cols (0 outside the candidates).
+ */
+int dash_train_route_backward(const float* z, int64_t z_stride, int rows, int nblk_cols,
+                              const int32_t* row_nblk, const uint8_t* cand, int64_t cand_stride,
+                              float idx_scale, float floor_p, float sigma, int Kout,
+                              const int32_t* idx, const uint8_t* valid, const float* topv,
+                              const float* stat, const float* dbias, float* dz, int64_t dz_stride,
+                              void* stream);
+
+/*
  * Prefill block-sparse attention (q_len == k_len), bf16 in/out, fp32 accumulation:
  * window keys [max(t-LW+1, kmin[t]), t] with bias 0 and the keys kmin[t] <= j < t-LW+1
  * of the routed blocks idx[t, :] (skipped where idx < 0 or valid == 0) with bias[t, slot].

@@ -34,6 +34,9 @@ Parity pinning (what each function is checked against, in tests/):
   kbar/scores      -> brute-force float64 loops, closed form (mean pooling)
   entmax15         -> closed forms, invariants, independent float64 bisection
   route            -> brute-force stable ranking, torch.topk as sets
+  training route   -> a from-definition row (full-width entmax by bisection); its
+                      autograd gradient -> float64 finite differences (gradcheck) and the
+                      closed-form entmax Jacobian of dash_attention.py:650-658
   dense_attend     -> brute-force float64 enumeration of the explicit key sets,
                       sliding-window / causal SDPA special cases
   decode_attend    -> the same enumeration at one query; equality with prefill rows
@@ -49,6 +52,7 @@ import torch.nn.functional as F
 SCORE_NEG = -1.0e9     # dash_attention.py:602
 MASK_NEG = -1.0e9      # dash_attention.py:601
 ACT_CLAMP = 1.0e4      # dash_attention.py:604
+GRAD_CLAMP = 1.0e4     # dash_attention.py:603
 ENTMAX_NEG = -1.0e4    # modeling_deepseekv2.py:56
 
 
@@ -182,6 +186,11 @@ def _entmax_threshold_and_support(X, dim=-1):
     return tau_star, support_size
 
 
+def sanitize_grad(g):
+    """The gradient hook of dash_attention.py:607-613: non-finite -> 0, clamp +-1e4."""
+    return torch.nan_to_num(g, nan=0.0, posinf=0.0, neginf=0.0).clamp(-GRAD_CLAMP, GRAD_CLAMP)
+
+
 def entmax15(X, dim=-1):
     """1.5-entmax forward (dash_attention.py:638-662): ``X=(X-max)/2``,
     ``p = clamp(X - tau*, 0)^2``."""
@@ -237,10 +246,15 @@ def infer_route_select(block_scores, block_cand, idx_scale, floor, sigma, K, top
 def train_route_select(block_scores, block_cand, idx_scale, floor, sigma, K):
     """Training-mode routing: full-width entmax prior (dash_attention.py:906-930)
     then top-K of the masked prior with the centred log-prior bias
-    (dash_attention.py:932-960).  Ties in the prior are broken by lower block id."""
+    (dash_attention.py:932-960).  Ties in the prior are broken by lower block id.
+
+    Differentiable in ``block_scores`` by autograd through the sort-based forward,
+    with the prior's gradient hook of dash_attention.py:1045-1046."""
     block_scores = block_scores.float()
     x, cand = route_inputs(block_scores, block_cand, idx_scale)
     prior = entmax15(x, dim=-1)
+    if prior.requires_grad:
+        prior.register_hook(sanitize_grad)
     nblk = x.shape[-1]
     Kp = max(1, min(int(K), nblk))
     sel_prior = prior.masked_fill(~cand, -1.0)

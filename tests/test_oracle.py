@@ -165,6 +165,50 @@ def test_train_route_selects_top_prior():
         assert ti[0, t].tolist() == bf.rank_desc(pr)[:5]
 
 
+def test_entmax15_gradient_is_the_closed_form_jacobian():
+    """Autograd through the sort-based forward equals float64 finite differences
+    (gradcheck) and the closed-form backward of dash_attention.py:650-658,
+    dX = dY*sqrt(Y) - sqrt(Y) * sum(dY*sqrt(Y)) / sum(sqrt(Y))."""
+    g = _rng(31)
+    X = (torch.randn(6, 19, generator=g, dtype=torch.float64) * 1.5).requires_grad_()
+    assert torch.autograd.gradcheck(lambda t: O.entmax15(t, dim=-1), (X,), eps=1e-7, atol=1e-6)
+    Y = O.entmax15(X, dim=-1)
+    assert ((Y > 0).sum(-1) < 19).all() and ((Y > 0).sum(-1) > 1).all()   # partial support
+    dY = torch.randn(6, 19, generator=g, dtype=torch.float64)
+    (gx,) = torch.autograd.grad(Y, X, dY)
+    gp = Y.detach().sqrt()
+    closed = dY * gp - gp * (dY * gp).sum(-1, keepdim=True) / gp.sum(-1, keepdim=True)
+    torch.testing.assert_close(gx, closed, atol=1e-12, rtol=1e-10)
+
+
+@pytest.mark.parametrize("with_cand", [False, True])
+def test_train_route_gradient_central_differences(with_cand):
+    """d(sum(w * bias))/dz of the training router by autograd against central
+    differences of the forward (selection fixed: a small step keeps the top-K set)."""
+    z, cand = _route_case(41, 1, 24, 19, 0.5, with_cand)
+    remote = z > O.SCORE_NEG * 0.5
+    w = torch.randn(1, 24, 5, generator=_rng(42))
+
+    def f(zz):
+        _, b, _ = O.train_route_select(zz, cand, 3.0, 1e-2, 1.0, 5)
+        return (w * b).sum()
+
+    zg = z.clone().requires_grad_()
+    f(zg).backward()
+    grad = zg.grad
+    d = torch.randn(z.shape, generator=_rng(43)) * remote
+    eps = 1e-3
+    num = (f(z + eps * d) - f(z - eps * d)).item() / (2 * eps)
+    ana = (grad * d).sum().item()
+    assert abs(num - ana) <= 2e-2 * max(abs(ana), 1.0), (num, ana)
+    assert (grad[~remote] == 0).all()
+
+
+def test_sanitize_grad_bounds_and_zeroes_nonfinite():
+    g = torch.tensor([float("nan"), float("inf"), -float("inf"), 3e4, -2e5, 7.0])
+    assert O.sanitize_grad(g).tolist() == [0.0, 0.0, 0.0, 1e4, -1e4, 7.0]
+
+
 # ---------------------------------------------------------------- stage 0
 
 def test_kbar_zero_headcls_is_block_mean():
