@@ -32,7 +32,9 @@
 namespace dash {
 
 constexpr int kPfTQ = 128;        // queries per tile work-group
-constexpr int kPfMaxK = 16;       // routed slots per query
+constexpr int kPfMaxK = 16;       // routed slots per query processed as one group
+constexpr int kPfMaxSlots = 64;   // routed slots per query (groups of kPfMaxK; above
+                                  // kPfMaxK every routed pair goes block-major)
 constexpr int kPfMaxBlocks = 2048;
 // Keys per tile-kernel item (a double-buffered LDS stage) and the work-groups per
 // CU that the stage size and the register budget allow.
@@ -133,12 +135,13 @@ __device__ __forceinline__ bool slot_usable(const PrefillArgs& a, int c, int64_t
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4v lds_short4;
 
-// Load the K <= 16 routed slots of one row: ids, validity and bias, with
-// vector loads where the row is 16-byte aligned.
-__device__ __forceinline__ void load_row_slots(const PrefillArgs& a, int64_t row, int32_t (&c)[kPfMaxK],
-                                               uint32_t& vmask) {
-  const int64_t p0 = row * a.K;
-  if (a.K == kPfMaxK) {
+// Load the routed slots g0 .. g0+15 of one row (K <= 64): ids and validity, with
+// vector loads where the slots are 16-byte aligned; slots past K get id -1.
+__device__ __forceinline__ void load_row_slots(const PrefillArgs& a, int64_t row, int g0,
+                                               int32_t (&c)[kPfMaxK], uint32_t& vmask) {
+  const int64_t p0 = row * a.K + g0;
+  const int ng = min(kPfMaxK, a.K - g0);
+  if (a.K % kPfMaxK == 0) {
     const int4* ip = (const int4*)(a.idx + p0);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -147,20 +150,27 @@ __device__ __forceinline__ void load_row_slots(const PrefillArgs& a, int64_t row
     }
   } else {
 #pragma unroll
-    for (int s = 0; s < kPfMaxK; ++s) c[s] = s < a.K ? a.idx[p0 + s] : -1;
+    for (int s = 0; s < kPfMaxK; ++s) c[s] = s < ng ? a.idx[p0 + s] : -1;
   }
   vmask = 0;
   if (a.valid) {
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s)
-      if (s < a.K && a.valid[p0 + s]) vmask |= 1u << s;
+      if (s < ng && a.valid[p0 + s]) vmask |= 1u << s;
   } else {
-    vmask = (a.K >= 32) ? 0xffffffffu : ((1u << a.K) - 1u);
+    vmask = (1u << ng) - 1u;
   }
 }
 
+// Plan: per 128-query tile, the queries selecting each routed block; a block
+// chosen by at least dense_threshold of them is "dense" (kind 1, processed by the
+// tile kernel), otherwise its pairs are "sparse" (kind 2) and reserve a range of
+// the block's pair list.  Duplicate and unusable slots get kind 0 (first slot of a
+// block wins).  Slots are handled in groups of 16: registers within a group, the
+// ids kept by earlier groups in LDS.
 __global__ __launch_bounds__(kPfTQ) void prefill_plan_kernel(PrefillArgs a) {
   __shared__ int32_t sCnt[kPfMaxBlocks];
+  __shared__ int16_t sKept[kPfMaxSlots - kPfMaxK][kPfTQ];   // earlier groups' kept ids
   const int b = blockIdx.y, tid = threadIdx.x;
   const int len = seq_len(a, b);
   const int t0 = blockIdx.x * kPfTQ;
@@ -170,21 +180,32 @@ __global__ __launch_bounds__(kPfTQ) void prefill_plan_kernel(PrefillArgs a) {
   __syncthreads();
   const int t = t0 + tid;
   const int64_t row = row0(a, b) + t;
-  int32_t c[kPfMaxK];
-  uint32_t vmask = 0, keep_mask = 0;
+  uint64_t keep_all = 0;
   if (t < len) {
-    load_row_slots(a, row, c, vmask);
     const int km = a.kmin ? a.kmin[row] : 0;
     const int ls = t - a.lw + 1;
+    int nprev = 0;
+    for (int g0 = 0; g0 < a.K; g0 += kPfMaxK) {
+      int32_t c[kPfMaxK];
+      uint32_t vmask, keep_mask = 0;
+      load_row_slots(a, row, g0, c, vmask);
 #pragma unroll
-    for (int s = 0; s < kPfMaxK; ++s) {
-      bool ok = s < a.K && ((vmask >> s) & 1u) && c[s] >= 0 && c[s] < nblk &&
-                c[s] * a.bs < ls && (c[s] + 1) * a.bs > km;
+      for (int s = 0; s < kPfMaxK; ++s) {
+        bool ok = ((vmask >> s) & 1u) && c[s] >= 0 && c[s] < nblk && c[s] * a.bs < ls &&
+                  (c[s] + 1) * a.bs > km;
 #pragma unroll
-      for (int u = 0; u < s; ++u) ok = ok && !(((keep_mask >> u) & 1u) && c[u] == c[s]);
-      if (ok) {
-        keep_mask |= 1u << s;
-        atomicAdd(&sCnt[c[s]], 1);
+        for (int u = 0; u < s; ++u) ok = ok && !(((keep_mask >> u) & 1u) && c[u] == c[s]);
+        for (int u = 0; ok && u < nprev; ++u) ok = sKept[u][tid] != c[s];
+        if (ok) {
+          keep_mask |= 1u << s;
+          atomicAdd(&sCnt[c[s]], 1);
+        }
+      }
+      keep_all |= (uint64_t)keep_mask << g0;
+      if (g0 + kPfMaxK < a.K) {
+#pragma unroll
+        for (int s = 0; s < kPfMaxK; ++s)
+          if ((keep_mask >> s) & 1u) sKept[nprev++][tid] = (int16_t)c[s];
       }
     }
   }
@@ -198,15 +219,15 @@ __global__ __launch_bounds__(kPfTQ) void prefill_plan_kernel(PrefillArgs a) {
       tb[cc] = atomicAdd(&a.blk_count[(int64_t)b * a.nblk_cap + cc], n);
   }
   if (t < len) {
-    uint8_t kd[kPfMaxK];
-#pragma unroll
-    for (int s = 0; s < kPfMaxK; ++s) {
-      kd[s] = 0;
-      if ((keep_mask >> s) & 1u) kd[s] = sCnt[c[s]] >= a.dense_threshold ? 1 : 2;
+    for (int g0 = 0; g0 < a.K; g0 += kPfMaxK) {
+      const int ng = min(kPfMaxK, a.K - g0);
+      for (int s = 0; s < ng; ++s) {
+        uint8_t kd = 0;
+        if ((keep_all >> (g0 + s)) & 1ull)
+          kd = sCnt[a.idx[row * a.K + g0 + s]] >= a.dense_threshold ? 1 : 2;
+        a.kind[row * a.K + g0 + s] = kd;
+      }
     }
-#pragma unroll
-    for (int s = 0; s < kPfMaxK; ++s)
-      if (s < a.K) a.kind[row * a.K + s] = kd[s];
   }
 }
 
@@ -329,29 +350,33 @@ __global__ __launch_bounds__(kPfTQ) void prefill_scatter_kernel(PrefillArgs a) {
   const int32_t* bch = a.blk_chunk + (int64_t)b * a.nblk_cap;
   int32_t* rec = a.chunk_rec + (int64_t)b * a.chunk_cap * kRec;
   const int64_t pos0 = (int64_t)a.chunk_pref[b] * kPfCH;   // first pair position of the sequence
-  int32_t c[kPfMaxK];
-  uint32_t vmask;
-  load_row_slots(a, row, c, vmask);
-  int pos[kPfMaxK];
-  bool sp[kPfMaxK];
+  for (int g0 = 0; g0 < a.K; g0 += kPfMaxK) {
+    int32_t c[kPfMaxK];
+    uint32_t vmask;
+    load_row_slots(a, row, g0, c, vmask);
+    const int ng = min(kPfMaxK, a.K - g0);
+    int pos[kPfMaxK];
+    bool sp[kPfMaxK];
 #pragma unroll
-  for (int s = 0; s < kPfMaxK; ++s) {
-    sp[s] = s < a.K && a.kind[row * a.K + s] == 2;
-    pos[s] = sp[s] ? atomicAdd(&sFill[c[s]], 1) : 0;
-  }
-#pragma unroll
-  for (int s = 0; s < kPfMaxK; ++s)
-    if (sp[s]) {
-      const int q = tb[c[s]] + pos[s];               // position in the block's pair list
-      int64_t rc, pp;
-      if (scatter_target(a.chunk_cap, a.ppos, pos0, bch[c[s]], q, &rc, &pp)) {
-        rec[rc * kRec + kRecHead + q % kPfCH] = (int32_t)(row * a.K + s - base);
-        a.spos[row * a.K + s] = (int32_t)pp;
-      } else {                                       // never with consistent counts
-        atomicOr(a.err, 2);
-        a.spos[row * a.K + s] = -1;                  // the tile kernel skips the slot
-      }
+    for (int s = 0; s < kPfMaxK; ++s) {
+      sp[s] = s < ng && a.kind[row * a.K + g0 + s] == 2;
+      pos[s] = sp[s] ? atomicAdd(&sFill[c[s]], 1) : 0;
     }
+#pragma unroll
+    for (int s = 0; s < kPfMaxK; ++s)
+      if (sp[s]) {
+        const int64_t slot = row * a.K + g0 + s;
+        const int q = tb[c[s]] + pos[s];               // position in the block's pair list
+        int64_t rc, pp;
+        if (scatter_target(a.chunk_cap, a.ppos, pos0, bch[c[s]], q, &rc, &pp)) {
+          rec[rc * kRec + kRecHead + q % kPfCH] = (int32_t)(slot - base);
+          a.spos[slot] = (int32_t)pp;
+        } else {                                       // never with consistent counts
+          atomicOr(a.err, 2);
+          a.spos[slot] = -1;                           // the tile kernel skips the slot
+        }
+      }
+  }
 }
 
 
@@ -605,6 +630,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
     const int t = t0 + tid;
     int cnt = 0;
     auto insert = [&](int c, float bv) {
+      if (cnt >= kPfMaxK) return;        // dense lists hold 16 blocks (K > 16 plans none)
       int u = cnt;
       while (u > 0 && sIdx[tid][u - 1] > c) {
         sIdx[tid][u] = sIdx[tid][u - 1];
@@ -936,12 +962,14 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
   // All kinds, pair positions and log-sum-exps are loaded first and the
   // reference moves once to their maximum; partial rows are lane-contiguous and
   // read with 16-byte loads.
-  if (pa.kind) {
-    const int64_t p0 = (r0 + tqc) * pa.K;
+  // Slots are merged in groups of 16.
+  for (int g0 = 0; pa.kind && g0 < pa.K; g0 += kPfMaxK) {
+    const int64_t p0 = (r0 + tqc) * pa.K + g0;
+    const int ng = min(kPfMaxK, pa.K - g0);
     float l2[kPfMaxK];
     int32_t sp[kPfMaxK];                   // positions (read for sparse slots only)
     uint32_t smask = 0;
-    if (pa.K == kPfMaxK) {
+    if (pa.K % kPfMaxK == 0) {
       const uint4 kv = *(const uint4*)(pa.kind + p0);
 #pragma unroll
       for (int g = 0; g < kPfMaxK / 4; ++g) {
@@ -955,7 +983,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
     } else {
 #pragma unroll
       for (int s = 0; s < kPfMaxK; ++s) sp[s] = 0;
-      for (int s = 0; s < pa.K; ++s)
+      for (int s = 0; s < ng; ++s)
         if (qvalid && pa.kind[p0 + s] == 2) {
           smask |= 1u << s;
           sp[s] = pa.spos[p0 + s];
@@ -1349,7 +1377,13 @@ extern "C" int dash_attn_prefill(
   if (K > 0 && (!idx || !bias)) return kErrInvalid;
   if (D != 128) return kErrUnsupported;
   if (block_size <= 0 || block_size % 32 != 0 || block_size > 256) return kErrUnsupported;
-  if (K < 0 || K > kPfMaxK) return kErrUnsupported;
+  if (K < 0 || K > kPfMaxSlots) return kErrUnsupported;
+  // above 16 slots every routed pair goes through the block-major sparse kernel
+  if (K > kPfMaxK) {
+    if (block_size > kPfIT) return kErrUnsupported;
+    if (dense_threshold <= 0) return kErrWorkspace;
+    dense_threshold = kPfTQ + 1;
+  }
   if (local_window < 1) return kErrInvalid;
   if (B == 0 || S == 0) return kOk;
   const int nblk_cap = (S + block_size - 1) / block_size;
@@ -1443,7 +1477,7 @@ extern "C" int dash_attn_prefill_backward(
   if (K > 0 && (!idx || !bias)) return kErrInvalid;
   if (D != 128) return kErrUnsupported;
   if (block_size <= 0 || block_size % 32 != 0 || block_size > 256) return kErrUnsupported;
-  if (K < 0 || K > kPfMaxK) return kErrUnsupported;
+  if (K < 0 || K > kPfMaxSlots) return kErrUnsupported;
   if (local_window < 1) return kErrInvalid;
   if (B == 0 || S == 0) return kOk;
   const int nblk_cap = (S + block_size - 1) / block_size;

@@ -2,20 +2,25 @@
 
 ``DashAttention`` keeps the constructor (``config.sparse_attention_config`` keys)
 and the ``forward`` signature of the reference module (dash_attention.py:703-1071)
-so that the DeepSeek-V2 decoder can use it unchanged.  The router's index
-projections (two 1280->d linears, Gemma RMSNorm, optional RoPE) stay in PyTorch
-(dash_attention.py:680-700, :801-852); stage 0 (block summaries and scores),
-routing and the block-sparse attention run in ``libdash_hip.so``.
+so that the DeepSeek-V2 decoder can use it unchanged.
 
-Routing is the inference form (modeling_deepseekv2.py:309-333): top-M by score,
-1.5-entmax over the M, first K blocks, centred log-prior bias.  ``_infer_params``
-holds {idx_scale, floor, sigma, K, topm} exactly as configure_dash_inference sets
-them (modeling_deepseekv2.py:299-301); it defaults to the config's values.
-Forward only: no autograd (the reference's backward kernels are not part of this
-library), no additive attention_mask, GPU tensors only.
+``forward`` is the reference's training forward (dash_attention.py:1008-1071):
+stage-0 block scores from the router's index projections (indexer block-max or
+head_cls summaries, in PyTorch so that autograd reaches the projections, norms and
+head_cls), then the training router in ``libdash_hip.so`` (full-width 1.5-entmax
+prior, top-k of the masked prior with k from the global schedule, centred
+log-prior bias; dash_train_route with its backward), then the fused block-sparse
+attention in ``libdash_hip.so`` with gradients to q, k, v and the bias
+(dash_attn_prefill and dash_attn_prefill_backward).
+
+The inference form (modeling_deepseekv2.py:309-333: top-M by score, entmax over
+the M, first K) is ``route``; ``_infer_params`` holds {idx_scale, floor, sigma, K,
+topm} exactly as configure_dash_inference sets them (modeling_deepseekv2.py:299-301).
+An additive attention_mask is not supported (NotImplementedError); GPU tensors only.
 """
 
 import math
+import os
 
 import torch
 import torch.nn as nn
@@ -23,6 +28,85 @@ import torch.nn as nn
 from . import ops
 
 ACT_CLAMP = 1.0e4
+GRAD_CLAMP = 1.0e4
+SCORE_NEG = -1.0e9
+
+
+def _sanitize_grad(g):
+    """Gradient hook: non-finite -> 0, clamp +-1e4 (dash_attention.py:607-613)."""
+    if g is None:
+        return None
+    return torch.nan_to_num(g, nan=0.0, posinf=0.0, neginf=0.0).clamp(-GRAD_CLAMP, GRAD_CLAMP)
+
+
+def _env_int(name, default):
+    v = os.environ.get(name)
+    return default if v is None or v == "" else int(v)
+
+
+class KSchedule:
+    """The global routed-block budget k of training (dash_attention.py:272-341):
+    geometric from DASH_K_START (64) to DASH_K_END (12) over DASH_K_ANNEAL_STEPS
+    (1000) steps, rounded and clamped to the endpoints.  The clock is the optimizer
+    step of an attached trainer state (``attach``, or the first live HF TrainerState
+    found on the reference's probe schedule), else the count of training forwards of
+    the first registered layer.  A forward replayed inside backward (activation
+    checkpointing) does not move it."""
+
+    PROBE_AT = (1, 4, 16, 64, 256)
+
+    def __init__(self):
+        self.k_start = _env_int("DASH_K_START", 64)
+        self.k_end = _env_int("DASH_K_END", 12)
+        self.steps = max(1, _env_int("DASH_K_ANNEAL_STEPS", 1000))
+        self.k = self.k_start
+        self.micro = 0
+        self.step = 0
+        self.state = None
+        self.leader = None
+        self.registered = 0
+
+    def register(self):
+        sid = self.registered
+        self.registered += 1
+        if self.leader is None:
+            self.leader = sid
+        return sid
+
+    def attach(self, trainer_state):
+        """Use trainer_state.global_step as the clock."""
+        self.state = trainer_state
+
+    def k_for(self, step):
+        frac = min(1.0, max(0.0, step / float(self.steps)))
+        k = self.k_start * (self.k_end / float(self.k_start)) ** frac
+        lo, hi = sorted((self.k_start, self.k_end))
+        return max(lo, min(hi, int(round(k))))
+
+    @staticmethod
+    def _find_trainer_state():
+        import gc
+        for o in gc.get_objects():
+            try:
+                if type(o).__name__ == "TrainerState" and int(getattr(o, "max_steps", 0) or 0) > 0:
+                    return o
+            except Exception:
+                continue
+        return None
+
+    def advance(self, sid, training):
+        if not training or sid != self.leader:
+            return
+        if torch._C._current_graph_task_id() != -1:
+            return
+        self.micro += 1
+        if self.state is None and self.micro in self.PROBE_AT:
+            self.state = self._find_trainer_state()
+        self.step = int(self.state.global_step) if self.state is not None else self.micro
+        self.k = self.k_for(self.step)
+
+
+K_SCHEDULE = KSchedule()
 
 
 class GemmaRMSNorm(nn.Module):
@@ -79,13 +163,14 @@ class DashAttention(nn.Module):
         self.k_proj = nn.Linear(config.hidden_size, self.index_dim, bias=False)
         self.q_norm = GemmaRMSNorm(self.index_dim, eps=eps)
         self.k_norm = GemmaRMSNorm(self.index_dim, eps=eps)
-        self.stage0 = str(sp.get("dash_stage0", "indexer")).lower()
+        self.stage0 = str(os.environ.get("DASH_STAGE0") or sp.get("dash_stage0", "indexer")).lower()
         self.head_cls = nn.Parameter(torch.zeros(self.index_dim))
         self._scale = 1.0 / math.sqrt(self.head_dim)
         self._idx_scale = self.scaling_factor / math.sqrt(self.index_dim)
         budget = sp.get("dash_topk_blocks") or sp.get("dash_image_fallback_remote") or 12
         self._infer_params = dict(idx_scale=self._idx_scale, floor=self._prior_floor,
                                   sigma=self.sigma, K=int(budget), topm=16)
+        self._ks_id = K_SCHEDULE.register()
 
     # ---------------------------------------------------------------- router
     def router_qk(self, hidden_states, position_embeddings=None):
@@ -166,19 +251,124 @@ class DashAttention(nn.Module):
                                self._scale)
         return out.to(q.dtype)
 
+    # ---------------------------------------------------------------- training stage 0
+    def _index_qk_train(self, hidden_states, position_embeddings):
+        """idx_q/idx_k [B,S,d] fp32 with autograd to the projections and norms, and
+        the gradient sanitizer on both (dash_attention.py:808-821)."""
+        B, S, _ = hidden_states.shape
+        d = self.index_dim
+        hs = torch.nan_to_num(hidden_states, nan=0.0, posinf=0.0, neginf=0.0)
+        iq = self.q_norm(self.q_proj(hs).view(B, S, 1, d)).transpose(1, 2)
+        ik = self.k_norm(self.k_proj(hs).view(B, S, 1, d)).transpose(1, 2)
+        if position_embeddings is not None:
+            cos, sin = position_embeddings
+            iq, ik = apply_rotary(iq, ik, cos[..., :d], sin[..., :d])
+        iq = torch.nan_to_num(iq[:, 0].float(), nan=0.0, posinf=0.0, neginf=0.0)
+        ik = torch.nan_to_num(ik[:, 0].float(), nan=0.0, posinf=0.0, neginf=0.0)
+        for t in (iq, ik):
+            if t.requires_grad:
+                t.register_hook(_sanitize_grad)
+        return iq, ik
+
+    def _block_scores_train(self, iq, ik, position_ids, nblk):
+        """Indexer scores (dash_attention.py:801-835): for query t and block c the max
+        over the block's keys j with j <= pos_t - LW of clamp(iq_t . ik_j, +-1e4),
+        -1e9 where the block has no such key; chunks of q_chunk queries."""
+        B, S, d = ik.shape
+        bs = self.block_size
+        pad = nblk * bs - S
+        kpos = torch.arange(S, device=ik.device)
+        rows = []
+        for c0 in range(0, S, self.q_chunk):
+            c1 = min(c0 + self.q_chunk, S)
+            sc = torch.matmul(iq[:, c0:c1], ik.transpose(-1, -2)).clamp(-ACT_CLAMP, ACT_CLAMP)
+            reach = position_ids[:, c0:c1, None] - self.local_window      # last remote key
+            sc = sc.masked_fill(kpos[None, None, :] > reach, SCORE_NEG)
+            if pad > 0:
+                sc = torch.nn.functional.pad(sc, (0, pad), value=SCORE_NEG)
+            elif pad < 0:
+                sc = sc[..., :nblk * bs]
+            rows.append(sc.view(B, c1 - c0, nblk, bs).amax(dim=-1))
+        return torch.cat(rows, dim=1)
+
+    def _block_scores_headcls_train(self, iq, ik, position_ids, nblk):
+        """head_cls scores (dash_attention.py:837-904): per block the softmax over its
+        real keys of clamp(ik_j . head_cls / sqrt(d), +-1e4) pools k_bar (the mean when
+        head_cls = 0); z = clamp(iq_t . k_bar_c / sqrt(d), +-1e4) for blocks c <=
+        pos_t // bs - LB holding a real key, else -1e9."""
+        B, S, d = ik.shape
+        bs = self.block_size
+        inv = 1.0 / math.sqrt(d)
+        npad = nblk * bs - S
+        real = torch.ones(B, S, dtype=torch.bool, device=ik.device)
+        if npad >= 0:
+            kk = torch.nn.functional.pad(ik, (0, 0, 0, npad))
+            real = torch.nn.functional.pad(real, (0, npad), value=False)
+        else:
+            kk, real = ik[:, :nblk * bs], real[:, :nblk * bs]
+        kk = kk.view(B, nblk, bs, d)
+        real = real.view(B, nblk, bs)
+        logits = ((kk * self.head_cls.to(kk.dtype)).sum(-1) * inv).clamp(-ACT_CLAMP, ACT_CLAMP)
+        lowest = torch.finfo(logits.dtype).min
+        top = torch.where(real, logits, logits.new_full((), lowest)).amax(-1, keepdim=True)
+        top = torch.where(real.any(-1, keepdim=True), top, torch.zeros_like(top))
+        e = torch.exp(logits - top) * real.to(logits.dtype)
+        w = e / e.sum(-1, keepdim=True).clamp_min(1e-6)
+        kbar = torch.nan_to_num((w.unsqueeze(-1) * kk).sum(2), nan=0.0, posinf=0.0, neginf=0.0)
+        has_key = real.any(-1)
+        blk = torch.arange(nblk, device=ik.device)
+        rows = []
+        for c0 in range(0, S, self.q_chunk):
+            c1 = min(c0 + self.q_chunk, S)
+            z = torch.matmul(iq[:, c0:c1], kbar.transpose(-1, -2))
+            if z.requires_grad:
+                z.register_hook(_sanitize_grad)
+            z = (z * inv).clamp(-ACT_CLAMP, ACT_CLAMP)
+            qblk = position_ids[:, c0:c1] // bs
+            keep = (blk[None, None, :] <= qblk[:, :, None] - self.local_blocks) & has_key[:, None, :]
+            rows.append(z.masked_fill(~keep, SCORE_NEG))
+        return torch.cat(rows, dim=1)
+
     # ---------------------------------------------------------------- forward
     def forward(self, hidden_states, q, k, v, position_embeddings=None, position_ids=None,
                 attention_mask=None, image_block_mask=None, block_cand=None, page_ids=None):
         """hidden_states [B,S,hidden]; q,k,v [B,H,S,D] (RoPE'd, GQA-expanded).
         Returns [B,H,S,D] in q.dtype (dash_attention.py:1008-1071).
 
-        The reference's forward routes with its training router: 1.5-entmax over
-        every block of the row (dash_attention.py:906-930) and the top k of the masked
-        prior under a global k schedule (:932-960).  This module implements the
-        inference router only (modeling_deepseekv2.py:403-421, reached through
-        ``modeling_deepseekv2._infer_prefill_attend``), so ``forward`` raises
-        NotImplementedError instead of silently routing another way."""
-        raise NotImplementedError(
-            "DashAttention.forward routes with the training router (full-width entmax, "
-            "k schedule), which the HIP path does not implement; enable inference routing "
-            "(configure_dash_inference) and call _infer_prefill_attend")
+        Stage-0 scores (indexer, or head_cls when the config's dash_stage0 says so),
+        the training router with k = the schedule's current budget (advanced once per
+        training forward), and the fused attention over token positions; gradients
+        reach q, k, v, the router's projections, norms and head_cls.  block_cand
+        [B,S,nblk] takes precedence over image_block_mask [B,nblk] (used when
+        dash_image_only); page_ids are diagnostics in the reference and are ignored.
+        The reference's per-layer temperature loop (DASH_SPARSITY_SCHED, off by
+        default) is not implemented: idx_scale and the prior floor are the config's."""
+        if attention_mask is not None:
+            raise NotImplementedError("additive attention_mask is not supported by the HIP path")
+        B, H, S, D = q.shape
+        nblk = (S + self.block_size - 1) // self.block_size
+        if position_ids is None:
+            position_ids = torch.arange(S, device=q.device)[None].expand(B, -1)
+        K_SCHEDULE.advance(self._ks_id, self.training)
+
+        iq, ik = self._index_qk_train(hidden_states, position_embeddings)
+        if self.stage0 == "head_cls":
+            z = self._block_scores_headcls_train(iq, ik, position_ids, nblk)
+        else:
+            z = self._block_scores_train(iq, ik, position_ids, nblk)
+        if z.requires_grad:
+            z.register_hook(_sanitize_grad)
+        cand = block_cand
+        if cand is None and self.image_only and image_block_mask is not None:
+            cand = image_block_mask[:, None, :].expand(B, S, nblk)
+        K = max(1, min(int(K_SCHEDULE.k), nblk))
+        topi, blk_bias, valid = ops.train_route(z, cand, self._idx_scale, self._prior_floor,
+                                                self.sigma, K)
+        if k.shape[1] != H:
+            rep = H // k.shape[1]
+            k = k.repeat_interleave(rep, dim=1)
+            v = v.repeat_interleave(rep, dim=1)
+        bf = torch.bfloat16
+        out = ops.attn_prefill_autograd(q.to(bf), k.to(bf), v.to(bf), topi, blk_bias, valid,
+                                        self.block_size, self.local_window, self._scale)
+        return out.to(q.dtype)

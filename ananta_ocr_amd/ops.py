@@ -365,6 +365,8 @@ def attn_prefill(q, k, v, idx, bias, valid, block_size, local_window, scale,
         Smax = S
         rows = B * S
     thr = DENSE_THRESHOLD if dense_threshold is None else int(dense_threshold)
+    if K > 16:
+        thr = max(thr, 129)          # more than 16 slots: every routed pair block-major
     ws, ws_n = None, 0
     if thr > 0 and K > 0 and block_size <= 64 and rows > 0:
         nbytes = ctypes.c_int64(0)

@@ -158,7 +158,8 @@ int dash_train_route_backward(const float* z, int64_t z_stride, int rows, int nb
  * packing segment start, triton_gather_attention (sparse_gather_triton.py:29-104,
  * :343-392).  q/k/v/o [B, H, S, D] by strides (or varlen via cu_seqlens, S = the longest
  * sequence); lse (optional) fp32 at lse[token_row*lse_row + h*lse_sh].  D == 128,
- * block_size in {32, 64, ..., 256}, K <= 16.
+ * block_size in {32, 64, ..., 256}, K <= 64.  K > 16 needs block_size <= 64 and a
+ * workspace (dense_threshold > 0): every routed pair then takes the sparse path.
  * dense_threshold > 0 (block_size <= 64): routed blocks selected by fewer than
  * dense_threshold of the 128 queries of a tile go through the block-major sparse path,
  * which needs `workspace` (dash_attn_prefill_workspace_size bytes, 256-byte aligned, any
@@ -193,7 +194,7 @@ int dash_attn_prefill_backward_workspace_size(int B, int H, int S_max, int64_t t
  * (_E2EGatherAttnFn.backward, sparse_gather_e2e_triton.py:311-339, with its dq/d_bias
  * kernel :118-190 and dk/dv kernel :193-262).  o and lse (natural log, lse[row * lse_row
  * + h * lse_sh]) are the forward's outputs; dout the gradient of o.  Same routing, varlen
- * and kmin arguments as the forward; block_size in {32, 64, ..., 256}, K <= 16, D == 128.
+ * and kmin arguments as the forward; block_size in {32, 64, ..., 256}, K <= 64, D == 128.
  * workspace: dash_attn_prefill_backward_workspace_size bytes, 256-byte aligned, any
  * contents.  Calls sharing a workspace must not overlap.
  */

@@ -72,6 +72,8 @@ def _case(seed, B, H, S, bs, lw, K, dup=True):
     (2, 2, 1000, 32, 128, 12),          # the shipped checkpoint's block 32, window 128, K 12
     (1, 3, 1300, 64, 512, 16),
     (1, 2, 333, 128, 200, 4),           # window not a block multiple, 128-key blocks
+    (1, 2, 1200, 32, 128, 64),          # the training schedule's first k
+    (1, 2, 900, 64, 256, 20),           # two slot groups, the last one partial
 ])
 def test_backward_matches_torch_autograd(B, H, S, bs, lw, K):
     q, k, v, topi, bias, valid, dout = _case(10 + S + bs, B, H, S, bs, lw, K)

@@ -185,7 +185,8 @@ def test_forward_triton_and_dense_match_reference_semantics():
         with pytest.raises(NotImplementedError):
             router._forward_dense(*a, S, nblk, torch.zeros(1, 1, S, S, device=DEV))
         with pytest.raises(NotImplementedError):
-            router(torch.zeros(B, S, 256, device=DEV), *a[:3])
+            router(torch.zeros(B, S, 256, device=DEV), *a[:3],
+                   attention_mask=torch.zeros(1, 1, S, S, device=DEV))
 
 
 def test_decode_position_before_cache_end():

@@ -98,8 +98,8 @@ def test_dash_attention_candidate_mask_and_errors():
     with pytest.raises(NotImplementedError):
         MD._infer_prefill_attend(layer, mod, hs, q, k, v, None, pos, None,
                                  torch.zeros(1, 1, S, S, device=DEV), None)
-    with pytest.raises(NotImplementedError):          # the training router is not provided
-        mod(hs, q, k, v)
+    with pytest.raises(NotImplementedError):          # no additive mask in the training forward
+        mod(hs, q, k, v, attention_mask=torch.zeros(1, 1, S, S, device=DEV))
 
 
 def test_gather_attention_e2e_matches_oracle_and_returns_none():

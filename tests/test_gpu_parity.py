@@ -203,6 +203,21 @@ def _attn_inputs(seed, B, H, S, bs, lw, K, qscale=1.0, dup=False):
     (1, 2, 3000, 64, 256, 16, 2.0),   # many remote blocks per tile
 ])
 def test_prefill_attention_matches_oracle(B, H, S, bs, lw, K, qs, thr):
+    _prefill_check(B, H, S, bs, lw, K, qs, thr)
+
+
+@pytest.mark.parametrize("B,H,S,bs,lw,K,qs", [
+    (1, 2, 2000, 32, 128, 64, 2.0),   # the training schedule's first k, block 32
+    (2, 2, 1500, 64, 256, 33, 2.0),   # three slot groups, the last one partial
+    (1, 3, 900, 64, 128, 24, 1.0),
+])
+def test_prefill_attention_more_than_16_slots(B, H, S, bs, lw, K, qs):
+    """K > 16: every routed pair goes block-major whatever the threshold asks."""
+    for thr in (24, 129):
+        _prefill_check(B, H, S, bs, lw, K, qs, thr)
+
+
+def _prefill_check(B, H, S, bs, lw, K, qs, thr):
     q, k, v, idx, bias, valid = _attn_inputs(300 + S, B, H, S, bs, lw, K, qscale=qs)
     scale = 1 / math.sqrt(128)
     ref = O.dense_attend(q, k, v, idx, bias, valid, bs, lw, scale)
