@@ -20,8 +20,8 @@ template <int D>
 __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeArgs a) {
   static_assert(D == 128, "head_dim 128");
   __shared__ int sTmp[kWave];
-  __shared__ int sRC[kDcMaxK];
-  __shared__ float sRB[kDcMaxK];
+  __shared__ int sRC[kDcMaxSlots];
+  __shared__ float sRB[kDcMaxSlots];
 
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x;
@@ -83,7 +83,7 @@ extern "C" int dash_attn_decode(
   if (!q || !k || !v || !out || B < 0 || H <= 0) return kErrInvalid;
   if (K > 0 && (!idx || !bias)) return kErrInvalid;
   if (D != 128) return kErrUnsupported;
-  if (K < 0 || K > kDcMaxK) return kErrUnsupported;
+  if (K < 0 || K > kDcMaxSlots) return kErrUnsupported;
   if (block_size <= 0 || (block_size % 64 != 0 && block_size != 32)) return kErrUnsupported;
   if (local_window < 1) return kErrInvalid;
   if (block_table && (page_size <= 0 || page_size % block_size != 0)) return kErrUnsupported;

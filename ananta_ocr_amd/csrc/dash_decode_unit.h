@@ -12,7 +12,8 @@
 
 namespace dash {
 
-constexpr int kDcMaxK = 16;
+constexpr int kDcMaxK = 16;       // routed slots of the fused decode step
+constexpr int kDcMaxSlots = 64;   // routed slots of dash_attn_decode (one per lane)
 constexpr int kDcMaxSplit = 64;
 
 struct DecodeArgs {

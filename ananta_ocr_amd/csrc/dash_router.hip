@@ -960,8 +960,8 @@ __global__ __launch_bounds__(kTrWaves * kWave) void train_route_kernel(
     const float* __restrict__ z, int64_t z_stride, int rows, int nblk,
     const int32_t* __restrict__ row_nblk, const uint8_t* __restrict__ cand_in,
     int64_t cand_stride, float idx_scale, float floor_p, float inv_sigma, int K, int Kout,
-    int32_t* __restrict__ idx_out, float* __restrict__ bias_out, uint8_t* __restrict__ valid_out,
-    float* __restrict__ topv_out, float2* __restrict__ stat_out) {
+    int by_x, int topm, int32_t* __restrict__ idx_out, float* __restrict__ bias_out,
+    uint8_t* __restrict__ valid_out, float* __restrict__ topv_out, float2* __restrict__ stat_out) {
   __shared__ uint64_t s_sel[kTrWaves][kTrMaxK];
   const int lane = wave_lane(), wv = threadIdx.x / kWave;
   const int row = blockIdx.x * kTrWaves + wv;
@@ -981,21 +981,51 @@ __global__ __launch_bounds__(kTrWaves * kWave) void train_route_kernel(
     if (lane == 0 && stat_out) stat_out[row] = make_float2(0.f, 0.f);
     return;
   }
-  const float tau = train_tau<NPL>(x, tr.xmax);
-  // masked prior keys: candidates by prior, non-candidates at -1, absent entries 0
   uint32_t hkey[NPL];
   uint32_t kmx = 0;
+  int Mp = tr.nb;
+  if (by_x) {
+    // inference: entries ranked by x (ties to the lower id); the entmax runs over
+    // the top M' = max(1, min(topm, nb)) of them (all nb when topm <= 0)
 #pragma unroll
-  for (int i = 0; i < NPL; ++i) {
-    const int c = lane + kWave * i;
-    const float sp = cd[i] ? train_prior(x[i], tr.xmax, tau) : -1.f;
-    hkey[i] = c < tr.nb ? ord_key(sp) : 0u;
-    kmx = max(kmx, hkey[i]);
+    for (int i = 0; i < NPL; ++i) {
+      hkey[i] = lane + kWave * i < tr.nb ? ord_key(x[i]) : 0u;
+      kmx = max(kmx, hkey[i]);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) kmx = max(kmx, (uint32_t)__shfl_xor((int)kmx, m, kWave));
+    if (topm > 0 && topm < tr.nb) {
+      Mp = topm;
+      const uint32_t TM = kth_key<NPL>(hkey, Mp, 1u, kmx);
+      int gt = 0;
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) gt += __popcll(__ballot(hkey[i] > TM));
+      int eq_seen = 0;
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) {
+        const bool eq = hkey[i] == TM;
+        const uint64_t meq = __ballot(eq);
+        const bool in = hkey[i] > TM || (eq && eq_seen + lane_prefix(meq) < Mp - gt);
+        if (!in) x[i] = -INFINITY;               // outside the top M': not in the entmax
+        eq_seen += __popcll(meq);
+      }
+    }
   }
+  const float tau = train_tau<NPL>(x, tr.xmax);
+  if (!by_x) {
+    // training: candidates by masked prior, non-candidates at -1, absent entries 0
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) kmx = max(kmx, (uint32_t)__shfl_xor((int)kmx, m, kWave));
-  const int Kp = max(1, min(min(K, kTrMaxK), tr.nb));
-  const uint32_t T = kth_key<NPL>(hkey, Kp, ord_key(-1.f), kmx);
+    for (int i = 0; i < NPL; ++i) {
+      const int c = lane + kWave * i;
+      const float sp = cd[i] ? train_prior(x[i], tr.xmax, tau) : -1.f;
+      hkey[i] = c < tr.nb ? ord_key(sp) : 0u;
+      kmx = max(kmx, hkey[i]);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) kmx = max(kmx, (uint32_t)__shfl_xor((int)kmx, m, kWave));
+  }
+  const int Kp = max(1, min(min(K, kTrMaxK), Mp));
+  const uint32_t T = kth_key<NPL>(hkey, Kp, by_x ? 1u : ord_key(-1.f), kmx);
   int n_gt = 0;
 #pragma unroll
   for (int i = 0; i < NPL; ++i) n_gt += __popcll(__ballot(hkey[i] > T));
@@ -1030,7 +1060,11 @@ __global__ __launch_bounds__(kTrWaves * kWave) void train_route_kernel(
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   // lane m holds slot m
   const uint64_t ks = lane < Kp ? s_sel[wv][lane] : 0ull;
-  const float v = lane < Kp ? ord_key_inv((uint32_t)(ks >> 32)) : -1.f;
+  float v = -1.f;
+  if (lane < Kp) {
+    v = ord_key_inv((uint32_t)(ks >> 32));
+    if (by_x) v = train_prior(v, tr.xmax, tau);       // the key held x: its prior
+  }
   const int c = 0xffff - (int)(((uint32_t)ks >> 1) & 0xffff);
   const bool va = lane < Kp && (ks & 1ull) != 0;
   const float logp = logf(fmaxf(v, floor_p));
@@ -1048,7 +1082,8 @@ __global__ __launch_bounds__(kTrWaves * kWave) void train_route_kernel(
     const bool in = m < Kp;
     const bool mv = in && va;                  // m == lane when in (Kp <= 64)
     io[m] = in ? c : -1;
-    bo[m] = mv ? fminf(fmaxf((logp - mu) * inv_sigma, -kActClamp), kActClamp) : 0.f;
+    const float bv = (logp - mu) * inv_sigma;
+    bo[m] = mv ? (by_x ? bv : fminf(fmaxf(bv, -kActClamp), kActClamp)) : 0.f;
     if (valid_out) valid_out[(int64_t)row * Kout + m] = mv ? 1 : 0;
     if (topv_out) topv_out[(int64_t)row * Kout + m] = in ? v : -1.f;
   }
@@ -1226,7 +1261,33 @@ extern "C" int dash_route(const float* z, int64_t z_stride, int rows, int nblk_c
                           void* stream) {
   using namespace dash;
   if (!z || !idx || !bias || rows < 0 || nblk_cols < 0) return kErrInvalid;
-  if (topm < 1 || topm > kMaxM) return kErrUnsupported;
+  if (topm < 1 || topm > kMaxM) {
+    // wider entmax (topm > 16, or the whole row for topm <= 0): one row per wavefront
+    if (K < 1 || Kout < 1) return kErrInvalid;
+    const int Mw = topm > 0 ? std::min(topm, std::max(nblk_cols, 1)) : std::max(nblk_cols, 1);
+    if (Kout < std::min(K, Mw)) return kErrInvalid;
+    if (K > kTrMaxK || Kout > kTrMaxK) return kErrUnsupported;
+    if (z_stride < nblk_cols || (cand && cand_stride < nblk_cols)) return kErrInvalid;
+    if (nblk_cols > 64 * 32) return kErrUnsupported;
+    if (rows == 0) return kOk;
+    if (nblk_cols == 0) return kErrInvalid;
+    const float inv_s = (float)(1.0 / (double)sigma);
+    dim3 g((rows + kTrWaves - 1) / kTrWaves);
+    hipStream_t s0 = (hipStream_t)stream;
+    const int np = (nblk_cols + 63) / 64;
+#define DASH_WROUTE(N)                                                                            \
+  hipLaunchKernelGGL(train_route_kernel<N>, g, dim3(kTrWaves * kWave), 0, s0, z, z_stride, rows,    \
+                     nblk_cols, row_nblk, cand, cand_stride, idx_scale, floor_p, inv_s, K, Kout, 1, \
+                     topm, idx, bias, valid, (float*)nullptr, (float2*)nullptr)
+    if (np <= 1) DASH_WROUTE(1);
+    else if (np <= 2) DASH_WROUTE(2);
+    else if (np <= 4) DASH_WROUTE(4);
+    else if (np <= 8) DASH_WROUTE(8);
+    else if (np <= 16) DASH_WROUTE(16);
+    else DASH_WROUTE(32);
+#undef DASH_WROUTE
+    return launch_status();
+  }
   if (K < 1 || Kout < 1) return kErrInvalid;
   if (Kout < std::min(K, std::min(topm, std::max(nblk_cols, 1)))) return kErrInvalid;
   if (nblk_cols > 64 * 32) return kErrUnsupported;
@@ -1270,7 +1331,7 @@ extern "C" int dash_train_route(const float* z, int64_t z_stride, int rows, int 
 #define DASH_TROUTE(N)                                                                           \
   hipLaunchKernelGGL(train_route_kernel<N>, grid, dim3(kTrWaves * kWave), 0, st, z, z_stride, rows, \
                      nblk_cols, row_nblk, cand, cand_stride, idx_scale, floor_p, inv_sigma, K, Kout, \
-                     idx, bias, valid, topv, (float2*)stat)
+                     0, 0, idx, bias, valid, topv, (float2*)stat)
   if (npl <= 1) DASH_TROUTE(1);
   else if (npl <= 2) DASH_TROUTE(2);
   else if (npl <= 4) DASH_TROUTE(4);

@@ -548,6 +548,11 @@ def decode_route(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, i
     Returns idx int32 [B,1,K'], bias fp32, valid (bool, or valid_dtype) and with
     return_scores the scores [B,nblk_cap]."""
     _need_gpu(idx_q, idx_k, kbar_cache)
+    if _wide_topm(topm):
+        return _decode_route_wide(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks,
+                                  idx_scale, floor, sigma, K, topm, seq_lens, block_table,
+                                  page_size, cand, refresh_tail, width, return_scores,
+                                  valid_dtype, q_pos)
     lib = _lib.load()
     if idx_q.dim() == 3:
         idx_q = idx_q[:, 0]
@@ -590,6 +595,44 @@ def decode_route(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, i
     return res + (z,) if return_scores else res
 
 
+def _wide_topm(topm):
+    """Entmax widths the fused decode router does not take (the whole row, or above
+    16): those rows are routed by dash_route's one-row-per-wavefront kernel."""
+    return int(topm) < 1 or int(topm) > 16
+
+
+def _decode_route_wide(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, idx_scale,
+                       floor, sigma, K, topm, seq_lens, block_table, page_size, cand,
+                       refresh_tail, width, return_scores, valid_dtype, q_pos):
+    """decode_route for a wide entmax: the decode router refreshes the tail summary
+    and writes the scores (its own one-slot routing is discarded), then dash_route
+    routes each sequence's row over its ceil(len / block_size) blocks."""
+    _, _, _, z = decode_route(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks,
+                              idx_scale, floor, sigma, 1, 1, seq_lens=seq_lens,
+                              block_table=block_table, page_size=page_size, cand=cand,
+                              refresh_tail=refresh_tail, width=1, return_scores=True,
+                              q_pos=q_pos)
+    B, nblk_cap = z.shape
+    S = block_table.shape[1] * page_size if block_table is not None else idx_k.shape[1]
+    if seq_lens is not None:
+        lens = seq_lens.reshape(B).to(device=z.device, dtype=torch.int64).clamp(0, S)
+    else:
+        lens = torch.full((B,), S, dtype=torch.int64, device=z.device)
+    nb = ((lens + block_size - 1) // block_size).clamp(max=nblk_cap).to(torch.int32)
+    c2 = None
+    if cand is not None:
+        c2 = cand.reshape(B, -1)
+        if c2.shape[1] < nblk_cap:
+            c2 = torch.nn.functional.pad(c2.to(torch.uint8), (0, nblk_cap - c2.shape[1]))
+        c2 = c2[:, :nblk_cap]
+    M = nblk_cap if int(topm) < 1 else min(int(topm), nblk_cap)
+    Kw = max(1, min(int(K), M)) if width is None else int(width)
+    idx, bias, valid = route(z, c2, idx_scale, floor, sigma, K, topm, row_nblk=nb, width=Kw)
+    vd = valid[:, None] if valid_dtype == torch.bool else valid[:, None].to(valid_dtype)
+    res = (idx[:, None], bias[:, None], vd)
+    return res + (z,) if return_scores else res
+
+
 def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks,
                       idx_scale, floor, sigma, K, topm, scale, seq_lens=None, block_table=None,
                       page_size=None, cand=None, width=None, out_dtype=torch.float32,
@@ -601,8 +644,27 @@ def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, l
     with idx/bias/valid [B,1,K'] (valid uint8), or (out, lse, routing) with return_lse;
     return_scores appends the block scores z [B, nblk_cap] the router computed.
     no_alloc: call dash_decode_step_noalloc, whose partials live in the library's fixed
-    per-GPU scratch array (no workspace; the outputs are still allocated here)."""
+    per-GPU scratch array (no workspace; the outputs are still allocated here).
+    A wide entmax (topm <= 0 or > 16) routes through _decode_route_wide and attends
+    with attn_decode (three launches instead of two)."""
     _need_gpu(q, k, v, idx_q, idx_k, kbar_cache)
+    if _wide_topm(topm):
+        if no_alloc:
+            raise NotImplementedError("the allocation-free step takes topm in 1..16")
+        idx, bias, valid, z = _decode_route_wide(
+            idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, idx_scale, floor,
+            sigma, K, topm, seq_lens, block_table, page_size, cand, True, width, True,
+            torch.uint8, q_pos)
+        squeeze = q.dim() == 4
+        qq = q[:, :, 0] if squeeze else q
+        lw = int(local_blocks) * int(block_size)
+        res = attn_decode(qq, k, v, idx[:, 0], bias[:, 0], valid[:, 0], block_size, lw, scale,
+                          seq_lens=seq_lens, q_pos=None if q_pos is None else q_pos.reshape(-1),
+                          block_table=block_table, page_size=page_size, out_dtype=out_dtype,
+                          return_lse=True)
+        out, lse = res
+        return _step_result(out, lse if return_lse else None, idx[:, 0], bias[:, 0], valid[:, 0],
+                            z, squeeze, return_lse, return_scores)
     lib = _lib.load()
     squeeze = q.dim() == 4
     if squeeze:

@@ -30,7 +30,7 @@ def prefill(q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks, idx_scale
         lens = (cu_seqlens[1:] - cu_seqlens[:-1]).to(torch.int32)
         nblk_doc = (lens + block_size - 1) // block_size
         row_nblk = torch.repeat_interleave(nblk_doc, lens.long(), output_size=z.shape[0])
-        width = max(1, min(int(K), int(topm)))
+        width = max(1, min(int(K), int(topm))) if int(topm) > 0 else max(1, int(K))
         idx, bias, valid = ops.route(z, block_cand, idx_scale, floor, sigma, K, topm,
                                      row_nblk=row_nblk, width=width)
     else:
@@ -69,11 +69,11 @@ def decode_step(state, q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks
     D = q.shape[-1]
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    width = None if seq_lens is None else max(1, min(int(K), int(topm)))
+    slots = max(1, min(int(K), int(topm))) if int(topm) > 0 else max(1, int(K))
+    width = None if seq_lens is None else slots
     if fused is None:
         npw = (local_blocks * block_size + block_size - 1 + 31) // 32
-        fused = nsplit is None and D == 128 and min(int(K), int(topm)) <= 16 and \
-            npw + max(1, min(int(K), int(topm))) <= 64
+        fused = nsplit is None and D == 128 and slots <= 16 and npw + slots <= 64
     if fused:
         out, (idx, bias, valid), z = ops.decode_step_fused(
             q, k, v, idx_q, idx_k, head_cls, state.kbar, block_size, local_blocks, idx_scale,

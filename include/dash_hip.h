@@ -105,7 +105,10 @@ int dash_router_qk_norm(const void* proj, int proj_bf16, int64_t proj_row, int64
  * 1.5-entmax prior over the M values, first K' = max(1,min(K,M)) slots, bias =
  * valid ? (log(max(prior,floor)) - mean_valid)/sigma : 0.
  * Replaces _infer_route_select (modeling_deepseekv2.py:309-333) with entmax15
- * (dash_attention.py:615-662).  1 <= topm <= 16, nblk_cols <= 2048.
+ * (dash_attention.py:615-662).  nblk_cols <= 2048.  topm in 1..16: one kernel whose
+ * entmax matches the serial sort-based computation bit for bit.  topm <= 0 (entmax
+ * over the whole row, as modeling_deepseekv2.py:323 allows) or topm > 16: one row per
+ * wavefront, the threshold by bisection in double then exact on the support; K <= 64.
  *   z         fp32 [rows, z_stride]; row_nblk optional per-row block count
  *   cand      optional uint8 [rows, cand_stride]
  *   idx/bias/valid  [rows, Kout]; slots >= K' get idx -1, bias 0, valid 0.
@@ -271,7 +274,7 @@ int dash_attn_decode_workspace_size(int B, int H, int D, int nsplit, int64_t* by
  * _dash_decode_forward (:454-500).  Cache: contiguous [B, H, S, D] (k_sb, k_sh, k_st) or
  * paged [pages, page_size, H, D] (k_sp, k_st, k_sh + block_table).  Split-K over nsplit
  * (<= 64) wavefronts per (b, h), then a merge kernel.  out [B, H, D] fp32 (out_bf16 = 0)
- * or bf16, lse optional.  D == 128, block_size 32 or a multiple of 64, K <= 16.
+ * or bf16, lse optional.  D == 128, block_size 32 or a multiple of 64, K <= 64.
  * workspace: dash_attn_decode_workspace_size bytes (the split partials), 16-byte aligned.
  */
 int dash_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,

@@ -783,6 +783,72 @@ def test_decode_checkpoint_config_matches_oracle(paged, fused):
         _close(out[b:b + 1], ref[:, :, 0], f"decode bs 32 sequence {b} ({L} tokens)")
 
 
+@pytest.mark.parametrize("nblk,scale,K,topm,quant,with_cand", [
+    (427, 0.5, 16, 0, None, False),     # entmax over the whole row (topm <= 0)
+    (100, 3.0, 12, 40, None, True),     # topm above 16
+    (2048, 0.2, 64, 0, None, False),    # widest row, 64 slots
+    (300, 1.0, 24, 64, 4.0, True),      # exact ties in x
+    (43, 1e-4, 8, -1, None, False),
+])
+def test_route_wide_entmax_matches_oracle(nblk, scale, K, topm, quant, with_cand):
+    """dash_route with topm <= 0 or > 16 (modeling_deepseekv2.py:323): ids and validity
+    bit for bit (they depend on the ranking of x only), bias within 2e-3 (the oracle's
+    threshold comes from float32 cumulative sums, the kernel's from float64)."""
+    S = 600 if nblk < 1000 else 80
+    bs, lb = (4, 2) if nblk < 1000 else (1, 1 - nblk + S)
+    z = _scores(S, nblk, bs, lb, 700 + nblk + K, scale, quant=quant, nan_frac=0.005)
+    cand = None
+    if with_cand:
+        cand = torch.rand(1, S, nblk, generator=_gen(701)) < 0.4
+        cand[:, ::6] = False
+    ti_r, bi_r, va_r = O.infer_route_select(z, cand, W.IDX_SCALE, W.FLOOR, W.SIGMA, K, topm)
+    ti, bi, va = ops.route(z.to(DEV), None if cand is None else cand.to(DEV), W.IDX_SCALE,
+                           W.FLOOR, W.SIGMA, K, topm)
+    ti, bi, va = ti.cpu().long(), bi.cpu(), va.cpu()
+    assert ti.shape == ti_r.shape
+    assert torch.equal(ti, ti_r), f"routed ids differ at {(ti != ti_r).nonzero()[:5].tolist()}"
+    assert torch.equal(va, va_r)
+    torch.testing.assert_close(bi, bi_r, atol=2e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("topm,K", [(0, 24), (40, 20)])
+def test_decode_wide_entmax_matches_oracle(topm, K):
+    """Decode with a wide entmax: routing on the GPU's own scores equals the oracle's
+    (ids and validity exactly), attention within the output tolerance."""
+    from ananta_ocr_amd import pipeline
+    bs, lb, H, d = 64, 4, 2, 128
+    lens = [3000, 700, 1, 2222]
+    B, S = len(lens), max(lens)
+    g = _gen(990 + topm)
+    k = (torch.randn(B, H, S, 128, generator=g) / math.sqrt(128)).bfloat16()
+    v = torch.randn(B, H, S, 128, generator=g).bfloat16()
+    q = (torch.randn(B, H, 128, generator=g) * 2).bfloat16()
+    ik = torch.randn(B, S, d, generator=g)
+    iq = torch.randn(B, d, generator=g)
+    hc = torch.randn(d, generator=g) * 0.3
+    lens_t = torch.tensor(lens, dtype=torch.int32).to(DEV)
+    nblk = (S + bs - 1) // bs
+    st = pipeline.init_decode_state(ik.to(DEV), hc.to(DEV), bs, nblk, seq_lens=lens_t)
+    idx_scale = 4.0 / math.sqrt(128)
+    out, (ti, bi, va), z = pipeline.decode_step(
+        st, q.to(DEV), k.to(DEV), v.to(DEV), iq.to(DEV), ik.to(DEV), hc.to(DEV), bs, lb,
+        idx_scale, 1e-4, 1.0, K, topm, 1 / math.sqrt(128), return_routing=True, fused=True,
+        return_scores=True, seq_lens=lens_t)
+    out, ti, bi, va, z = out.cpu(), ti.cpu().long(), bi.cpu(), va.cpu().bool(), z.cpu()
+    for b, L in enumerate(lens):
+        nb = (L + bs - 1) // bs
+        zb = z[b:b + 1, None, :nb]
+        t_r, b_r, v_r = O.infer_route_select(zb, None, idx_scale, 1e-4, 1.0, K, topm)
+        kp_ = t_r.shape[-1]
+        assert torch.equal(ti[b:b + 1, :, :kp_], t_r), f"sequence {b}: routed ids"
+        assert torch.equal(va[b:b + 1, :, :kp_], v_r), f"sequence {b}: validity"
+        torch.testing.assert_close(bi[b:b + 1, :, :kp_], b_r, atol=2e-3, rtol=1e-3)
+        ref = O.decode_attend(q[b:b + 1, :, None].float(), k[b:b + 1, :, :L], v[b:b + 1, :, :L],
+                              t_r, b_r, v_r, torch.tensor([[L - 1]]), bs, lb * bs,
+                              1 / math.sqrt(128))
+        _close(out[b:b + 1], ref[:, :, 0], f"decode wide entmax sequence {b}")
+
+
 def test_packed_prefill_graph_replays_match_eager():
     """A packed (cu_seqlens) prefill pass (k_bar, scores, routing, attention) given
     max_seqlen makes no host synchronisation, so it is captured in a HIP graph; every
