@@ -11,18 +11,13 @@ arguments, shapes and "return None on an unsupported input" behaviour:
 The names are kept so existing call sites import them unchanged; the work runs
 in ``libdash_hip.so`` (dash_attn_prefill, dash_block_max_score).  The fused entry
 point records autograd when its inputs require grad (the backward runs in
-dash_attn_prefill_backward); ``triton_gather_attention`` (no bias) is forward only
-and raises NotImplementedError for tensors that require grad.
+dash_attn_prefill_backward), and so does ``triton_gather_attention`` (no bias;
+gradients to q, k and v).
 """
 
 import torch
 
 from . import ops
-
-
-def _no_grad_check(*ts):
-    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts):
-        raise NotImplementedError("DASH HIP gather attention is forward-only (no backward)")
 
 
 def gather_attention_e2e(query_states, key_states, value_states, block_indices,
@@ -64,9 +59,9 @@ def gather_attention(query_states, key_states, value_states, block_indices, posi
                      attention_mask, block_size, scale, local_window=None):
     """[B,HQ,T,D] block-sparse attention without bias; packed rows (position_ids
     restarting at 0) keep every query inside its segment [t - position_ids[t], t].
-    Returns None where the reference does (mask, prefix cache, index heads that do
-    not divide the heads); several index heads are not supported by this library and
-    raise NotImplementedError."""
+    block_indices [B,HI,T,S]: query head h uses index head h // (HQ / HI).  Returns
+    None where the reference does (mask, prefix cache, index heads that do not divide
+    the heads).  Records autograd (q, k, v) when its inputs require grad."""
     if attention_mask is not None:
         return None
     B, HQ, T, D = query_states.shape
@@ -78,9 +73,6 @@ def gather_attention(query_states, key_states, value_states, block_indices, posi
         return None
     if position_ids is None or position_ids.dim() != 2 or position_ids.shape[-1] != T:
         return None
-    if HI != 1:
-        raise NotImplementedError("one shared index head only")
-    _no_grad_check(query_states, key_states, value_states)
     if Hkv != HQ:
         key_states = key_states.repeat_interleave(HQ // Hkv, dim=1)
         value_states = value_states.repeat_interleave(HQ // Hkv, dim=1)
@@ -89,11 +81,22 @@ def gather_attention(query_states, key_states, value_states, block_indices, posi
     if B != 1 and bool((seg != 0).any()):
         raise NotImplementedError("packed rows are supported with batch 1")
     lw = block_size if local_window is None else max(1, int(local_window))
-    sel = block_indices[:, 0]
-    zero_bias = torch.zeros(sel.shape, dtype=torch.float32, device=sel.device)
     kmin = None if not bool((seg != 0).any()) else seg.reshape(-1)
-    return ops.attn_prefill(query_states, key_states, value_states, sel, zero_bias, None,
-                            block_size, lw, scale, kmin=kmin)
+    grad = torch.is_grad_enabled() and any(t.requires_grad for t in
+                                           (query_states, key_states, value_states))
+    # query head h reads index head h // (HQ / HI) (sparse_gather_triton.py:47)
+    G = HQ // HI
+    outs = []
+    for g in range(HI):
+        hs = slice(g * G, (g + 1) * G)
+        sel = block_indices[:, g]
+        zero_bias = torch.zeros(sel.shape, dtype=torch.float32, device=sel.device)
+        args = (query_states[:, hs], key_states[:, hs], value_states[:, hs], sel, zero_bias,
+                None, block_size, lw, scale)
+        # the unbiased backward of _TritonGatherAttnFn (sparse_gather_triton.py:107-244)
+        outs.append(ops.attn_prefill_autograd(*args, kmin=kmin) if grad else
+                    ops.attn_prefill(*args, kmin=kmin))
+    return outs[0] if HI == 1 else torch.cat(outs, dim=1)
 
 
 def block_max_score(q, k, pos, seg, block_size, num_key_blocks, local_window=None):

@@ -143,6 +143,42 @@ def test_gather_attention_packed_segments():
     _close(out, ref, "gather packed")
 
 
+def test_gather_attention_index_heads_packed_with_gradients():
+    """Several index heads (query head h reads index head h // (HQ / HI), with GQA kv
+    heads), packed segments, and gradients to q, k, v against autograd through the
+    oracle (the unbiased backward of _TritonGatherAttnFn)."""
+    g = torch.Generator().manual_seed(6)
+    HQ, Hkv, HI, bs, lw, K = 4, 2, 2, 32, 96, 5
+    lens = [260, 333, 90]
+    T = sum(lens)
+    pos = torch.cat([torch.arange(L) for L in lens])[None]
+    q = (torch.randn(1, HQ, T, 128, generator=g) * 0.5).bfloat16()
+    k = (torch.randn(1, Hkv, T, 128, generator=g) * 0.5).bfloat16()
+    v = torch.randn(1, Hkv, T, 128, generator=g).bfloat16()
+    dout = torch.randn(1, HQ, T, 128, generator=g).bfloat16()
+    nblk = (T + bs - 1) // bs
+    sel = torch.randint(-1, nblk, (1, HI, T, K), generator=g, dtype=torch.int32)
+    qg, kg, vg = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    out = SG.triton_gather_attention(qg, kg, vg, sel.to(DEV), pos.to(DEV), None, bs, 0.1, lw)
+    out.backward(dout.to(DEV))
+    qr, kr, vr = (t.float().requires_grad_() for t in (q, k, v))
+    ke, ve = kr.repeat_interleave(HQ // Hkv, 1), vr.repeat_interleave(HQ // Hkv, 1)
+    kmin = torch.arange(T)[None] - pos
+    G = HQ // HI
+    refs = []
+    for hi in range(HI):
+        hs = slice(hi * G, (hi + 1) * G)
+        refs.append(O.dense_attend(qr[:, hs], ke[:, hs], ve[:, hs], sel[:, hi].long(),
+                                   torch.zeros(1, T, K), sel[:, hi] >= 0, bs, lw, 0.1, kmin=kmin))
+    ref = torch.cat(refs, 1)
+    ref.backward(dout.float())
+    _close(out.detach(), ref.detach(), "gather index heads")
+    for got, want, what in ((qg.grad, qr.grad, "dq"), (kg.grad, kr.grad, "dk"),
+                            (vg.grad, vr.grad, "dv")):
+        err = (got.float().cpu() - want).abs().max().item()
+        assert err <= 3e-2 * want.abs().max().item() + 1e-6, f"{what}: {err:.3e}"
+
+
 def test_decode_attend_helper_matches_oracle():
     g = torch.Generator().manual_seed(5)
     B, H, S, bs, lw, K = 2, 2, 2000, 64, 512, 6
