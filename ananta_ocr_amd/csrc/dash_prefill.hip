@@ -166,11 +166,11 @@ __device__ __forceinline__ void load_row_slots(const PrefillArgs& a, int64_t row
 // chosen by at least dense_threshold of them is "dense" (kind 1, processed by the
 // tile kernel), otherwise its pairs are "sparse" (kind 2) and reserve a range of
 // the block's pair list.  Duplicate and unusable slots get kind 0 (first slot of a
-// block wins).  Slots are handled in groups of 16: registers within a group, the
-// ids kept by earlier groups in LDS.
+// block wins).  Slots are handled in groups of 16 in registers; every slot's id
+// (0 where not kept) goes to LDS for the dedup of later groups and the kinds.
 __global__ __launch_bounds__(kPfTQ) void prefill_plan_kernel(PrefillArgs a) {
   __shared__ int32_t sCnt[kPfMaxBlocks];
-  __shared__ int16_t sKept[kPfMaxSlots - kPfMaxK][kPfTQ];   // earlier groups' kept ids
+  __shared__ int16_t sId[kPfMaxSlots][kPfTQ];      // every slot's block id, per row
   const int b = blockIdx.y, tid = threadIdx.x;
   const int len = seq_len(a, b);
   const int t0 = blockIdx.x * kPfTQ;
@@ -184,7 +184,6 @@ __global__ __launch_bounds__(kPfTQ) void prefill_plan_kernel(PrefillArgs a) {
   if (t < len) {
     const int km = a.kmin ? a.kmin[row] : 0;
     const int ls = t - a.lw + 1;
-    int nprev = 0;
     for (int g0 = 0; g0 < a.K; g0 += kPfMaxK) {
       int32_t c[kPfMaxK];
       uint32_t vmask, keep_mask = 0;
@@ -195,18 +194,15 @@ __global__ __launch_bounds__(kPfTQ) void prefill_plan_kernel(PrefillArgs a) {
                   (c[s] + 1) * a.bs > km;
 #pragma unroll
         for (int u = 0; u < s; ++u) ok = ok && !(((keep_mask >> u) & 1u) && c[u] == c[s]);
-        for (int u = 0; ok && u < nprev; ++u) ok = sKept[u][tid] != c[s];
+        for (int u = 0; ok && u < g0; ++u)
+          ok = !(((keep_all >> u) & 1ull) && sId[u][tid] == c[s]);
         if (ok) {
           keep_mask |= 1u << s;
           atomicAdd(&sCnt[c[s]], 1);
         }
+        if (g0 + s < kPfMaxSlots) sId[g0 + s][tid] = (int16_t)(ok ? c[s] : 0);
       }
       keep_all |= (uint64_t)keep_mask << g0;
-      if (g0 + kPfMaxK < a.K) {
-#pragma unroll
-        for (int s = 0; s < kPfMaxK; ++s)
-          if ((keep_mask >> s) & 1u) sKept[nprev++][tid] = (int16_t)c[s];
-      }
     }
   }
   __syncthreads();
@@ -219,14 +215,19 @@ __global__ __launch_bounds__(kPfTQ) void prefill_plan_kernel(PrefillArgs a) {
       tb[cc] = atomicAdd(&a.blk_count[(int64_t)b * a.nblk_cap + cc], n);
   }
   if (t < len) {
-    for (int g0 = 0; g0 < a.K; g0 += kPfMaxK) {
-      const int ng = min(kPfMaxK, a.K - g0);
-      for (int s = 0; s < ng; ++s) {
-        uint8_t kd = 0;
-        if ((keep_all >> (g0 + s)) & 1ull)
-          kd = sCnt[a.idx[row * a.K + g0 + s]] >= a.dense_threshold ? 1 : 2;
-        a.kind[row * a.K + g0 + s] = kd;
+    auto kind_of = [&](int s) -> uint32_t {
+      if (!((keep_all >> s) & 1ull)) return 0u;
+      return sCnt[sId[s][tid]] >= a.dense_threshold ? 1u : 2u;
+    };
+    if (a.K % kPfMaxK == 0) {               // 16 kinds per 16-byte store
+      for (int g0 = 0; g0 < a.K; g0 += kPfMaxK) {
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int s = 0; s < kPfMaxK; ++s) w[s >> 2] |= kind_of(g0 + s) << (8 * (s & 3));
+        *(uint4*)(a.kind + row * a.K + g0) = make_uint4(w[0], w[1], w[2], w[3]);
       }
+    } else {
+      for (int s = 0; s < a.K; ++s) a.kind[row * a.K + s] = (uint8_t)kind_of(s);
     }
   }
 }
@@ -1240,7 +1241,9 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
     // two pieces of 16 rows, so that every store instruction writes 1 KB
     // contiguously (whole 128-byte lines) instead of 16 bytes of 64 different
     // rows.  Rows of lanes past the chunk's pair count are written too: their
-    // positions belong to this chunk and are never read.
+    // positions belong to this chunk and are never read.  In LDS, 16-byte chunk c
+    // of row r sits at slot c ^ r: the 16 rows a write instruction covers (one
+    // chunk each) then fall on distinct banks instead of all on the same four.
     const int64_t pw = part_row(a, (int64_t)(pb + ch) * kPfCH + wv * 32 + 128 * j, h);
 #pragma unroll
     for (int piece = 0; piece < 2; ++piece) {
@@ -1252,14 +1255,18 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
             bf16x8 w;
 #pragma unroll
             for (int e2 = 0; e2 < 8; ++e2) w[e2] = (bf16)(acc_o[dt][g * 4 + e2] * inv);
-            *(bf16x8*)(st + (n & 15) * D + part_index(hl, dt, g, 0)) = w;
+            const int cidx = part_index(hl, dt, g, 0) / 8;
+            *(bf16x8*)(st + (n & 15) * D + ((cidx ^ (n & 15)) * 8)) = w;
           }
       }
       wave_lds_sync();                     // other lanes' rows are read below
       char* const dst = (char*)(a.part_o + (pw + 16 * piece) * D);
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
-        *(bf16x8*)(dst + k * 1024 + lane * 16) = *(const bf16x8*)((const char*)st + k * 1024 + lane * 16);
+      for (int k = 0; k < 4; ++k) {
+        const int rr = 4 * k + (lane >> 4), cidx = lane & 15;
+        *(bf16x8*)(dst + k * 1024 + lane * 16) =
+            *(const bf16x8*)((const char*)st + rr * (D * 2) + ((cidx ^ rr) * 16));
+      }
       wave_lds_sync();                     // and overwritten by the next piece
     }
     if (active && hl == 0) a.part_lse[pw + n] = l_tot > 0.f ? mloc + log2f(l_tot) : -INFINITY;
