@@ -12,6 +12,9 @@ product kernels and the CPU oracle timed on a bounded sample on this host:
   * decode step, B = 8 x 27,300 cached tokens (window 1,024, cap 16)
   * 16-document packed prefill (cu_seqlens, window 512, cap 8)
   * 12-layer paged decode step, B = 32 sequences of 2,730..27,300 tokens
+  * training step at 27,300 tokens (training routing, attention forward and backward,
+    routing backward; k = 16)
+  * page-aware candidate masks of a 100-page OCR prompt (prefill rows, decode row)
 
 HBM traffic and executed MFMA work per launch come from hardware-counter runs
 (rocprofv3 --pmc over ``bench.py --counter-probe WORKLOAD``), summarised by
@@ -392,6 +395,110 @@ def paged_entry(cfg, res, counters):
             "cached_tokens_per_layer": int(res["lengths"].sum()), "roofline": roof}
 
 
+# ------------------------------------------------------------------ training step
+
+TRAIN_NAME = "train_s27300_lw1024_k16"
+
+
+def bench_train(steps, warmup):
+    """One training step of the routed attention at 27,300 tokens (block 64, window
+    1,024, k = 16): training routing of the block scores, fused attention forward,
+    its backward (dq, dk, dv, bias gradient) and the routing backward to the scores.
+    Stage-0 scores come from the inference kernels (their autograd runs in PyTorch in
+    DashAttention and is not timed)."""
+    cfg = W.PREFILL_27300
+    log(f"[bench] training step {TRAIN_NAME}: generating inputs")
+    d = W.make_prefill(cfg, device="cuda")
+    hc = torch.zeros(W.D, device="cuda")
+    lb = cfg.lw // cfg.bs
+    scale = 1.0 / math.sqrt(W.D)
+    kb = ops.kbar(d["idx_k"], hc, cfg.bs)
+    z = ops.block_scores(d["idx_q"], kb, cfg.bs, lb)
+    q, k, v = d["q"], d["k"], d["v"]
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    dout = torch.randn(q.shape, device="cuda", generator=gen).bfloat16()
+    K = cfg.cap
+
+    def fwd_bwd(i=0):
+        idx, bias, valid, topv, stat = ops.train_route_raw(z, None, W.IDX_SCALE, W.FLOOR,
+                                                           W.SIGMA, K)
+        out, lse = ops.attn_prefill(q, k, v, idx, bias, valid, cfg.bs, cfg.lw, scale,
+                                    return_lse=True)
+        dq, dk, dv, db = ops.attn_prefill_backward(q, k, v, out, lse, dout, idx, bias, valid,
+                                                   cfg.bs, cfg.lw, scale)
+        ops.train_route_backward(z, None, W.IDX_SCALE, W.FLOOR, W.SIGMA, idx, valid, topv, stat,
+                                 db)
+
+    idx, bias, valid, topv, stat = ops.train_route_raw(z, None, W.IDX_SCALE, W.FLOOR, W.SIGMA, K)
+    torch.cuda.synchronize()
+    pairs = prefill_pairs(idx[0], valid[0], d["S"], cfg.bs, cfg.lw)
+    fwd_flops = 4.0 * W.D * W.H * pairs
+    bwd_flops = 2.5 * fwd_flops            # S recomputed, dP, dV, dK, dQ: five products
+    t_step = time_steps(fwd_bwd, steps, warmup)
+    out, lse = ops.attn_prefill(q, k, v, idx, bias, valid, cfg.bs, cfg.lw, scale, return_lse=True)
+
+    def bwd(i):
+        ops.attn_prefill_backward(q, k, v, out, lse, dout, idx, bias, valid, cfg.bs, cfg.lw,
+                                  scale)
+
+    t_bwd = time_kernel(bwd, max(steps, 5))
+    t_route = time_kernel(lambda i: ops.train_route_raw(z, None, W.IDX_SCALE, W.FLOOR, W.SIGMA,
+                                                        K), max(steps, 5))
+    tf = bwd_flops / t_bwd / 1e12
+    log(f"[bench] training step: {t_step * 1e3:.3f} ms, attention backward {t_bwd * 1e3:.3f} ms")
+    return dict(cfg=cfg, data=d, z=z, K=K, pairs=pairs, t_step=t_step, t_bwd=t_bwd,
+                t_route=t_route,
+                entry={"workload": TRAIN_NAME,
+                       "value": round((fwd_flops + bwd_flops) / t_step / 1e12, 2),
+                       "unit": "TFLOP/s", "ms_per_step": round(t_step * 1e3, 4),
+                       "step": "training routing + attention forward + attention backward + "
+                               "routing backward, one sequence of 27,300 tokens, k = 16",
+                       "train_route_forward_us": round(t_route * 1e6, 2),
+                       "roofline": {"bound": "mfma", "achieved": round(tf, 2),
+                                    "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                                    "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                                    "kernel": "attention backward (delta, plan, dK/dV, dQ, "
+                                              "bias gradient)",
+                                    "flop_per_launch": bwd_flops,
+                                    "avg_launch_ms": round(t_bwd * 1e3, 4)}})
+
+
+def cpu_train_baseline(res, rows=512, reps=3):
+    """The oracle's training path on this host, differentiated by torch autograd: the
+    training routing and dense attention for the last `rows` query rows, forward and
+    backward."""
+    from oracle import dash_oracle as O
+    cfg, d = res["cfg"], res["data"]
+    S = d["S"]
+    r0 = S - rows
+    scale = 1.0 / math.sqrt(W.D)
+    q, k, v = d["q"].float().cpu(), d["k"].float().cpu(), d["v"].float().cpu()
+    z = res["z"][:, r0:].cpu()
+
+    def run():
+        zz = z.clone().requires_grad_()
+        qq, kk, vv = (t.clone().requires_grad_() for t in (q, k, v))
+        ti, bi, va = O.train_route_select(zz, None, W.IDX_SCALE, W.FLOOR, W.SIGMA, res["K"])
+        full = torch.zeros(1, S, ti.shape[-1], dtype=torch.long)
+        fv = torch.zeros(1, S, ti.shape[-1], dtype=torch.bool)
+        full[:, r0:], fv[:, r0:] = ti, va
+        fb = torch.cat([torch.zeros(1, r0, ti.shape[-1]), bi], dim=1)
+        out = O.dense_attend(qq, kk, vv, full, fb, fv, cfg.bs, cfg.lw, scale, rows=(r0, S))
+        out.sum().backward()
+        return ti, va
+
+    t = _median_time(run, reps)
+    ti, va = run()
+    pairs = prefill_pairs(torch.cat([torch.zeros(r0, ti.shape[-1], dtype=torch.long), ti[0]]),
+                          torch.cat([torch.zeros(r0, ti.shape[-1], dtype=torch.bool), va[0]]),
+                          S, cfg.bs, cfg.lw)
+    pairs -= sum(min(t_ + 1, cfg.lw) for t_ in range(r0))
+    sample = (f"oracle fp32 training routing + dense attention, forward and autograd backward, "
+              f"on the last {rows} of {S} query rows; median of {reps} after 1 warm-up; "
+              f"{t:.2f} s per sample")
+    return _cpu_fields(14.0 * W.D * W.H * pairs / t / 1e12, "TFLOP/s", sample)
+
+
 # ------------------------------------------------------------------ page-aware candidates
 
 PAGES_NAME = "page_candidates_s27300_100pages"
@@ -749,7 +856,7 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     only = set(filter(None, args.only.split(",")))
     todo = [c for c in ALL if not only or c.name in only]
-    if only and not todo and PAGES_NAME not in only:
+    if only and not todo and not ({PAGES_NAME, TRAIN_NAME} & only):
         sys.exit(f"bench.py: unknown workload(s) {sorted(only)}")
     counters, cnote = read_counters()
     res, entries = {}, {}
@@ -778,6 +885,11 @@ def main():
             else:
                 cb = cpu_decode_baseline(r, cfg)
             entries[cfg.name]["cpu_baseline"] = cb
+    if not only or TRAIN_NAME in only:
+        tr = bench_train(max(3, args.steps // 2), 1)
+        entries[TRAIN_NAME] = tr["entry"]
+        if not args.no_cpu:
+            entries[TRAIN_NAME]["cpu_baseline"] = cpu_train_baseline(tr)
     if not only or PAGES_NAME in only:
         entries[PAGES_NAME] = bench_pages(args.steps)
         if not args.no_cpu:
