@@ -463,6 +463,19 @@ def bench_train(steps, warmup):
                                     "avg_launch_ms": round(t_bwd * 1e3, 4)}})
 
 
+def train_entry(res, counters):
+    e = res["entry"]
+    roof = e["roofline"]
+    tr = counters.get((TRAIN_NAME, "hbm_bytes"))
+    if tr is not None:
+        roof["traffic"] = int(tr)
+    ex = counters.get((TRAIN_NAME, "mfma_flop"))
+    if ex is not None:
+        roof["executed_flop_per_launch"] = ex
+        roof["executed_frac"] = round(ex / res["t_bwd"] / 1e12 / PEAK_BF16_TFLOPS, 4)
+    return e
+
+
 def cpu_train_baseline(res, rows=512, reps=3):
     """The oracle's training path on this host, differentiated by torch autograd: the
     training routing and dense attention for the last `rows` query rows, forward and
@@ -693,8 +706,24 @@ def counter_probe(name):
     scale = 1.0 / math.sqrt(W.D)
     cfgs = {c.name: c for c in (W.PREFILL_2730, W.PREFILL_27300, W.PACKED_16DOC, W.DECODE_B8,
                                 W.PAGED_12L)}
+    cfgs[TRAIN_NAME] = TRAIN_NAME
     cfg = cfgs[name]
-    if isinstance(cfg, W.Prefill):
+    if cfg == TRAIN_NAME:
+        c27 = W.PREFILL_27300
+        d = W.make_prefill(c27, device=dev)
+        kb = ops.kbar(d["idx_k"], hc, c27.bs)
+        z = ops.block_scores(d["idx_q"], kb, c27.bs, c27.lw // c27.bs)
+        idx, bias, valid, _, _ = ops.train_route_raw(z, None, W.IDX_SCALE, W.FLOOR, W.SIGMA,
+                                                     c27.cap)
+        out, lse = ops.attn_prefill(d["q"], d["k"], d["v"], idx, bias, valid, c27.bs, c27.lw,
+                                    scale, return_lse=True)
+        gen = torch.Generator(device=dev).manual_seed(11)
+        dout = torch.randn(d["q"].shape, device=dev, generator=gen).bfloat16()
+
+        def launch():
+            ops.attn_prefill_backward(d["q"], d["k"], d["v"], out, lse, dout, idx, bias, valid,
+                                      c27.bs, c27.lw, scale)
+    elif isinstance(cfg, W.Prefill):
         d = W.make_prefill(cfg, device=dev)
         cu, ml = d.get("cu_seqlens"), _maxlen(d)
         _, (idx, bias, valid) = pipeline.prefill(d["q"], d["k"], d["v"], d["idx_q"], d["idx_k"],
@@ -748,6 +777,9 @@ PROBE_KERNELS = {
     "prefill": ["prefill_clear_kernel", "prefill_plan_kernel", "prefill_scan_kernel",
                 "prefill_scatter_kernel", "prefill_sparse_kernel", "prefill_tile_kernel"],
     "decode": ["decode_route_window_kernel", "decode_routed_kernel", "decode_step_merge_kernel"],
+    "train": ["bwd_delta_kernel", "prefill_clear_kernel", "prefill_plan_kernel",
+              "prefill_scan_kernel", "prefill_scatter_kernel", "bwd_kv_kernel", "bwd_q_kernel",
+              "bwd_dbias_kernel"],
 }
 
 
@@ -772,12 +804,13 @@ def summarize_counters(dirs):
             key = (int(r["Dispatch_Id"]), r["Kernel_Name"], r["Counter_Name"])
             per[key] = per.get(key, 0.0) + float(r["Counter_Value"])
         counters = sorted({k[2] for k in per})
-        wl = next((c.name for c in (W.PREFILL_2730, W.PREFILL_27300, W.PACKED_16DOC,
-                                    W.DECODE_B8, W.PAGED_12L) if c.name in dr), None)
+        names = [c.name for c in (W.PREFILL_2730, W.PREFILL_27300, W.PACKED_16DOC, W.DECODE_B8,
+                                  W.PAGED_12L)] + [TRAIN_NAME]
+        wl = next((nm for nm in names if nm in dr), None)
         if wl is None:
             log(f"{dr}: directory names no workload")
             continue
-        kind = "decode" if "decode" in wl else "prefill"
+        kind = "train" if wl == TRAIN_NAME else "decode" if "decode" in wl else "prefill"
         disp = sorted({(k[0], k[1]) for k in per})
         copy = [x for x in disp if "copyBuffer" in x[1]
                 and per.get((x[0], x[1], counters[0]), 0.0) > 1024]
@@ -887,7 +920,7 @@ def main():
             entries[cfg.name]["cpu_baseline"] = cb
     if not only or TRAIN_NAME in only:
         tr = bench_train(max(3, args.steps // 2), 1)
-        entries[TRAIN_NAME] = tr["entry"]
+        entries[TRAIN_NAME] = train_entry(tr, counters)
         if not args.no_cpu:
             entries[TRAIN_NAME]["cpu_baseline"] = cpu_train_baseline(tr)
     if not only or PAGES_NAME in only:
