@@ -45,6 +45,7 @@ SIGNATURES = {
     "dash_attn_prefill_error_offset": (_i, [_i, _i, _i, _l, _i, _i, _i, ctypes.POINTER(_l)]),
     "dash_prefill_plan_target": (_i, [_l, _l, _l, _l, _l, ctypes.POINTER(_l), ctypes.POINTER(_l)]),
     "dash_decode_route": (_i, [_p, _l, _p, _l, _l, _l, _p, _l, _i, _p, _p, _i, _p, _i, _p, _l, _i,
+                               _p, _l, _p,
                                _p, _l, _i, _i, _i, _i, _f, _f, _f, _i, _i, _i, _p, _p, _p, _p,
                                _l, _p]),
     "dash_attn_decode_workspace_size": (_i, [_i, _i, _i, _i, ctypes.POINTER(_l)]),
@@ -53,15 +54,18 @@ SIGNATURES = {
                               _i, _i, _i, _f, _i, _p, _l, _p]),
     "dash_decode_step_workspace_size": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_l)]),
     "dash_decode_step": (_i, [_p, _l, _p, _l, _l, _l, _p, _l, _i, _p, _p, _i, _p, _i, _p, _l, _i,
+                              _p, _l, _p,
                               _p, _l, _i, _i, _f, _f, _f, _i, _i, _i, _p, _p, _p, _p, _l,
                               _p, _l, _l, _p, _l, _l, _l, _l, _p, _l, _l, _l, _l,
                               _p, _i, _l, _l, _p, _l, _l, _i, _i, _i, _i, _i, _f, _p, _l, _p]),
     "dash_decode_step_noalloc": (_i, [_p, _l, _p, _l, _l, _l, _p, _l, _i, _p, _p, _i, _p, _i, _p,
-                                      _l, _i, _p, _l, _i, _i, _f, _f, _f, _i, _i, _i, _p, _p, _p,
+                                      _l, _i, _p, _l, _p,
+                                      _p, _l, _i, _i, _f, _f, _f, _i, _i, _i, _p, _p, _p,
                                       _p, _l, _p, _l, _l, _p, _l, _l, _l, _l, _p, _l, _l, _l,
                                       _l, _p, _i, _l, _l, _p, _l, _l, _i, _i, _i, _i, _i, _f,
                                       _p]),
     "dash_decode_step_scratch_bytes": (_l, []),
+    "dash_decode_win_bounds": (_i, [_p, _l, _i, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p]),
     "dash_page_ids": (_i, [_p, _l, _i, _i, _l, _l, _i, _i, _p, _p, _p, _p, _p, _l, _p]),
     "dash_pages_workspace_size": (_i, [_i, _i, ctypes.POINTER(_l)]),
     "dash_block_pages": (_i, [_p, _l, _i, _i, _i, _i, _p, _p, _p, _p]),

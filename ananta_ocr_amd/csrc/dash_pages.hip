@@ -406,6 +406,56 @@ __global__ __launch_bounds__(256) void decode_allow_kernel(
   if (tid == 0) markers[b] = m;
 }
 
+
+// ---------------------------------------------------------------------------
+// Window bounds of decode rows (the serving router's _win_bounds_kernel,
+// whl:sglang/srt/layers/attention/unlimited_dash_ops/route_triton.py:466-505, for
+// one decode query per sequence): the span [lo, hi) of the blocks that are allowed
+// and remote (c <= q_blk - local_blocks, c * bs < len); with none, the live remote
+// width [0, ceil(len / bs)) (or [0, 0) when no block is remote); fit = the span is at
+// most `tile` blocks wide.  One work-group of 256 threads per sequence.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void win_bounds_kernel(const uint8_t* __restrict__ allow,
+                                                         int64_t allow_sb, int allow_w,
+                                                         const int32_t* __restrict__ lens,
+                                                         const int32_t* __restrict__ q_pos, int S,
+                                                         int nblk_cap, int bs, int local_blocks,
+                                                         int tile, int32_t* __restrict__ bounds,
+                                                         uint8_t* __restrict__ fit) {
+  __shared__ int s_lo[256 / kWave], s_hi[256 / kWave];
+  const int b = blockIdx.x, tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
+  const int len = lens ? min(max(lens[b], 0), S) : S;
+  const int qp = q_pos ? min(q_pos[b], len - 1) : len - 1;
+  const int q_blk = qp >= 0 ? qp / bs : -1;
+  const int lim = q_blk - local_blocks;
+  const int w = min(nblk_cap, allow_w);
+  int lo = nblk_cap, hi = -1;
+  for (int c = tid; c < w; c += 256) {
+    const bool keep = allow[(int64_t)b * allow_sb + c] != 0 && c <= lim && (int64_t)c * bs < len;
+    if (keep) { lo = min(lo, c); hi = max(hi, c); }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    lo = min(lo, __shfl_xor(lo, m, kWave));
+    hi = max(hi, __shfl_xor(hi, m, kWave));
+  }
+  if (lane == 0) { s_lo[wv] = lo; s_hi[wv] = hi; }
+  __syncthreads();
+  if (tid == 0) {
+    for (int i = 1; i < 256 / kWave; ++i) { lo = min(lo, s_lo[i]); hi = max(hi, s_hi[i]); }
+    lo = min(lo, s_lo[0]); hi = max(hi, s_hi[0]);
+    const bool any_r = hi >= 0;
+    const int n_blk = (len + bs - 1) / bs;
+    const int w_seq = min(nblk_cap, max(n_blk, 1));
+    const bool no_remote = len <= 0 || lim < 0;
+    const int lo_v = any_r ? lo : 0;
+    const int hi_v = any_r ? hi + 1 : (no_remote ? 0 : w_seq);
+    bounds[2 * b] = lo_v;
+    bounds[2 * b + 1] = hi_v;
+    if (fit) fit[b] = (hi_v - lo_v) <= tile ? 1 : 0;
+  }
+}
+
 }  // namespace dash
 
 namespace {
@@ -538,5 +588,21 @@ extern "C" int dash_decode_allow(const int64_t* new_ids, int64_t new_stride, int
   hipLaunchKernelGGL(decode_allow_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream, new_ids,
                      new_stride, page_token_id, bmin, bmax, nblk_state, prompt_pages, markers,
                      nblk, allow, allow_sb);
+  return pages_status();
+}
+
+extern "C" int dash_decode_win_bounds(const uint8_t* allow, int64_t allow_sb, int allow_w,
+                                      const int32_t* seq_lens, const int32_t* q_pos, int B, int S,
+                                      int nblk_cap, int block_size, int local_blocks, int tile,
+                                      int32_t* bounds, uint8_t* fit, void* stream) {
+  using namespace dash;
+  if (B < 0 || S < 0 || nblk_cap < 0 || allow_w < 0 || block_size <= 0 || local_blocks < 0)
+    return kErrInvalid;
+  if (B == 0) return kOk;
+  if (!allow || !bounds) return kErrInvalid;
+  if (allow_sb < allow_w) return kErrInvalid;
+  hipLaunchKernelGGL(win_bounds_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream, allow, allow_sb,
+                     allow_w, seq_lens, q_pos, S, nblk_cap, block_size, local_blocks, tile, bounds,
+                     fit);
   return pages_status();
 }

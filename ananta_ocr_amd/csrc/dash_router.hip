@@ -1393,6 +1393,12 @@ struct DecodeRouteArgs {
   const float* head_cls; int refresh_tail;
   int skip_tail;                     // the scores read no k_bar row past the last remote block
   float* kbar; int64_t kb_sb; int nblk_cap;
+  // k_bar page pool: the row of block c of sequence b is kb_table[b * kb_ts + c]
+  // (pages of one block each); null: row b * kb_sb / d + c
+  const int32_t* kb_table; int64_t kb_ts;
+  // window bounds [B, 2]: only blocks lo <= c < hi are scored (the others score as
+  // not remote); null: every block
+  const int32_t* bounds;
   const uint8_t* cand; int64_t cand_stride;
   int d, bs, local_blocks;
   float inv_sqrt_d, idx_scale, floor_p, inv_sigma;
@@ -1400,6 +1406,11 @@ struct DecodeRouteArgs {
   int32_t* idx; float* bias; uint8_t* valid;
   float* z; int64_t z_stride;
 };
+
+__device__ __forceinline__ float* kbar_row(const DecodeRouteArgs& a, int b, int c) {
+  return a.kb_table ? a.kbar + (int64_t)a.kb_table[(int64_t)b * a.kb_ts + c] * a.d
+                    : a.kbar + (int64_t)b * a.kb_sb + (int64_t)c * a.d;
+}
 
 // 1.5-entmax of the sorted top M, the log-prior bias and the output slots of one
 // decode row, by one wavefront with lane m holding entry m (each lane forms its own
@@ -1508,7 +1519,15 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
   // that the tail row being rewritten elsewhere is never read (rows past the last
   // remote block read that block again, and a sequence with no remote block reads
   // head_cls, d floats, instead; those scores are masked).
-  const int c_clamp = a.skip_tail ? max(lim, 0) : nblk - 1;
+  int c_clamp = a.skip_tail ? max(lim, 0) : nblk - 1;
+  // window bounds: scores outside [blo, bhi) are not computed (their rows are not read)
+  int blo = 0, bhi = nblk;
+  if (a.bounds && mode != kTailOnly) {
+    blo = min(max(a.bounds[2 * b], 0), nblk);
+    bhi = min(max(a.bounds[2 * b + 1], blo), nblk);
+  }
+  const int c_lo = min(blo, c_clamp);
+  c_clamp = max(min(c_clamp, bhi - 1), c_lo);
   // d = 128 and up to 512 blocks: every block's k_bar row is loaded now, 16 lanes
   // per row, so that the loads are in flight during the tail refresh
   const bool fast_scores = mode != kTailOnly && a.d == 128 && nblk <= 8 * (kDrThreads / 16);
@@ -1518,8 +1537,8 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
     if (!fast_scores) return;
 #pragma unroll
     for (int r = r0; r < r1; ++r) {
-      const int c = min(slot16 + r * (kDrThreads / 16), c_clamp);
-      const float* kr = (a.skip_tail && lim < 0) ? a.head_cls : a.kbar + (int64_t)b * a.kb_sb + (int64_t)c * 128;
+      const int c = max(min(slot16 + r * (kDrThreads / 16), c_clamp), c_lo);
+      const float* kr = (a.skip_tail && lim < 0) ? a.head_cls : kbar_row(a, b, c);
       kp[r][0] = *(const float4*)(kr + l16 * 4);
       kp[r][1] = *(const float4*)(kr + 64 + l16 * 4);
     }
@@ -1578,7 +1597,7 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
         for (int g = 0; g < 8; ++g) t += s_part[g][tid];
         if (!(fabsf(t) <= 3.402823466e38f)) t = 0.f;
         s_tail[i] = t;
-        a.kbar[(int64_t)b * a.kb_sb + (int64_t)ct * a.d + i] = t;
+        kbar_row(a, b, ct)[i] = t;
       }
       __syncthreads();
     }
@@ -1601,7 +1620,7 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
       for (int m = 8; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
       if (l16 == 0 && c < nblk) {
         float zz = kScoreNeg;
-        if (c <= lim) zz = fminf(fmaxf(v * a.inv_sqrt_d, -kActClamp), kActClamp);
+        if (c <= lim && c >= blo && c < bhi) zz = fminf(fmaxf(v * a.inv_sqrt_d, -kActClamp), kActClamp);
         s_x[c] = zz;
         a.z[(int64_t)b * a.z_stride + c] = zz;
       }
@@ -1618,8 +1637,8 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
         float4 kv[8];
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
-          const int c = min(cb + row0 + r * (kDrThreads / 32), c_clamp);
-          kv[r] = *(const float4*)(((a.skip_tail && lim < 0) ? a.head_cls : a.kbar + (int64_t)b * a.kb_sb + (int64_t)c * a.d) + i);
+          const int c = max(min(cb + row0 + r * (kDrThreads / 32), c_clamp), c_lo);
+          kv[r] = *(const float4*)(((a.skip_tail && lim < 0) ? a.head_cls : kbar_row(a, b, c)) + i);
         }
         const float4 qv = *(const float4*)(s_q + i);
         const float4 tv = *(const float4*)(s_tail + i);
@@ -1638,7 +1657,7 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
         const int c = cb + row0 + r * (kDrThreads / 32);
         if (l32 == 0 && c < nblk) {
           float zz = kScoreNeg;
-          if (c <= lim) zz = fminf(fmaxf(v * a.inv_sqrt_d, -kActClamp), kActClamp);
+          if (c <= lim && c >= blo && c < bhi) zz = fminf(fmaxf(v * a.inv_sqrt_d, -kActClamp), kActClamp);
           s_x[c] = zz;
           a.z[(int64_t)b * a.z_stride + c] = zz;
         }
@@ -1831,7 +1850,8 @@ static int decode_route_args(const float* idx_q, int64_t iq_sb, const float* idx
                                  const int32_t* block_table, int64_t table_stride,
                                  int page_size, const int32_t* seq_lens, const int32_t* q_pos,
                                  int S, const float* head_cls, int refresh_tail, float* kbar,
-                                 int64_t kb_sb, int nblk_cap, const uint8_t* cand,
+                                 int64_t kb_sb, int nblk_cap, const int32_t* kb_table,
+                                 int64_t kb_ts, const int32_t* bounds, const uint8_t* cand,
                                  int64_t cand_stride, int B, int d, int block_size,
                                  int local_blocks, float idx_scale, float floor_p, float sigma,
                                  int K, int topm, int Kout, int32_t* idx, float* bias,
@@ -1846,6 +1866,7 @@ static int decode_route_args(const float* idx_q, int64_t iq_sb, const float* idx
   // cache and the score rows must hold ceil(S / block_size) blocks
   if (S < 0 || ((int64_t)S + block_size - 1) / block_size > nblk_cap) return kErrInvalid;
   if (d % 16 != 0 || kb_sb % 4 != 0 || (uintptr_t)kbar % 16 != 0) return kErrUnsupported;
+  if (kb_table && kb_ts < nblk_cap) return kErrInvalid;
   if (ik_st % 4 != 0 || ik_sp % 4 != 0 || ik_sb % 4 != 0 || (uintptr_t)idx_k % 16 != 0 ||
       (uintptr_t)head_cls % 16 != 0)
     return kErrUnsupported;
@@ -1855,6 +1876,7 @@ static int decode_route_args(const float* idx_q, int64_t iq_sb, const float* idx
   a.lens = seq_lens; a.q_pos = q_pos; a.S = S;
   a.head_cls = head_cls; a.refresh_tail = refresh_tail; a.skip_tail = 0;
   a.kbar = kbar; a.kb_sb = kb_sb; a.nblk_cap = nblk_cap;
+  a.kb_table = kb_table; a.kb_ts = kb_ts; a.bounds = bounds;
   a.cand = cand; a.cand_stride = cand_stride;
   a.d = d; a.bs = block_size; a.local_blocks = local_blocks;
   a.inv_sqrt_d = (float)(1.0 / sqrt((double)d));
@@ -1871,7 +1893,8 @@ extern "C" int dash_decode_route(const float* idx_q, int64_t iq_sb, const float*
                                  const int32_t* block_table, int64_t table_stride,
                                  int page_size, const int32_t* seq_lens, const int32_t* q_pos,
                                  int S, const float* head_cls, int refresh_tail, float* kbar,
-                                 int64_t kb_sb, int nblk_cap, const uint8_t* cand,
+                                 int64_t kb_sb, int nblk_cap, const int32_t* kb_table,
+                                 int64_t kb_ts, const int32_t* bounds, const uint8_t* cand,
                                  int64_t cand_stride, int B, int d, int block_size,
                                  int local_blocks, float idx_scale, float floor_p, float sigma,
                                  int K, int topm, int Kout, int32_t* idx, float* bias,
@@ -1880,7 +1903,8 @@ extern "C" int dash_decode_route(const float* idx_q, int64_t iq_sb, const float*
   DecodeRouteArgs a;
   const int st = decode_route_args(idx_q, iq_sb, idx_k, ik_sb, ik_st, ik_sp, block_table, table_stride,
                                    page_size, seq_lens, q_pos, S, head_cls, refresh_tail, kbar, kb_sb,
-                                   nblk_cap, cand, cand_stride, B, d, block_size, local_blocks,
+                                   nblk_cap, kb_table, kb_ts, bounds, cand, cand_stride, B, d,
+                                   block_size, local_blocks,
                                    idx_scale, floor_p, sigma, K, topm, Kout, idx, bias, valid, z,
                                    z_stride, a);
   if (st != kOk || B == 0) return st;
@@ -1907,7 +1931,8 @@ extern "C" int dash_decode_step(
     int64_t ik_sp, const int32_t* block_table, int64_t table_stride, int page_size,
     const int32_t* seq_lens, const int32_t* q_pos, int S, const float* head_cls,
     int refresh_tail, float* kbar,
-    int64_t kb_sb, int nblk_cap, const uint8_t* cand, int64_t cand_stride, int d,
+    int64_t kb_sb, int nblk_cap, const int32_t* kb_table, int64_t kb_ts, const int32_t* bounds,
+    const uint8_t* cand, int64_t cand_stride, int d,
     int local_blocks, float idx_scale, float floor_p, float sigma, int K, int topm, int Kout,
     int32_t* idx, float* bias, uint8_t* valid, float* z, int64_t z_stride,
     const void* q, int64_t q_sb, int64_t q_sh,
@@ -1920,7 +1945,8 @@ extern "C" int dash_decode_step(
   DecodeRouteArgs ra;
   const int rs = decode_route_args(idx_q, iq_sb, idx_k, ik_sb, ik_st, ik_sp, block_table,
                                    table_stride, page_size, seq_lens, q_pos, S, head_cls, refresh_tail,
-                                   kbar, kb_sb, nblk_cap, cand, cand_stride, B, d, block_size,
+                                   kbar, kb_sb, nblk_cap, kb_table, kb_ts, bounds, cand,
+                                   cand_stride, B, d, block_size,
                                    local_blocks, idx_scale, floor_p, sigma, K, topm, Kout, idx, bias,
                                    valid, z, z_stride, ra);
   if (rs != kOk) return rs;
@@ -2018,7 +2044,8 @@ extern "C" int dash_decode_step_noalloc(
     const float* idx_q, int64_t iq_sb, const float* idx_k, int64_t ik_sb, int64_t ik_st,
     int64_t ik_sp, const int32_t* block_table, int64_t table_stride, int page_size,
     const int32_t* seq_lens, const int32_t* q_pos, int S, const float* head_cls,
-    int refresh_tail, float* kbar, int64_t kb_sb, int nblk_cap, const uint8_t* cand,
+    int refresh_tail, float* kbar, int64_t kb_sb, int nblk_cap, const int32_t* kb_table,
+    int64_t kb_ts, const int32_t* bounds, const uint8_t* cand,
     int64_t cand_stride, int d, int local_blocks, float idx_scale, float floor_p, float sigma,
     int K, int topm, int Kout, int32_t* idx, float* bias, uint8_t* valid, float* z,
     int64_t z_stride,
@@ -2038,7 +2065,8 @@ extern "C" int dash_decode_step_noalloc(
   if (sst != kOk) return sst;
   return dash_decode_step(idx_q, iq_sb, idx_k, ik_sb, ik_st, ik_sp, block_table, table_stride,
                           page_size, seq_lens, q_pos, S, head_cls, refresh_tail, kbar, kb_sb,
-                          nblk_cap, cand, cand_stride, d, local_blocks, idx_scale, floor_p, sigma,
+                          nblk_cap, kb_table, kb_ts, bounds, cand, cand_stride, d, local_blocks,
+                          idx_scale, floor_p, sigma,
                           K, topm, Kout, idx, bias, valid, z, z_stride, q, q_sb, q_sh, k, k_sb,
                           k_sh, k_st, k_sp, v, v_sb, v_sh, v_st, v_sp, out, out_bf16, o_sb, o_sh,
                           lse, lse_sb, lse_sh, B, H, D, block_size, local_window, scale, ptr,

@@ -537,22 +537,35 @@ def attn_decode(q, k, v, idx, bias, valid, block_size, local_window, scale, seq_
     return (out, lse) if return_lse else out
 
 
+def _kbar_layout(kbar_cache, kbar_table, bounds):
+    """(nblk_cap, kb_sb, table int32 or None, kb_ts, bounds int32 or None) of a k_bar
+    cache: per sequence [B, nblk_cap, d], or a page pool [pages, d] addressed through
+    kbar_table [B, >= nblk_cap] (one page per block)."""
+    bnd = None if bounds is None else _i32(bounds.reshape(-1, 2))
+    if kbar_table is None:
+        return kbar_cache.shape[1], kbar_cache.stride(0), None, 0, bnd
+    kbt = _i32(kbar_table)
+    return kbt.shape[1], 0, kbt, kbt.stride(0), bnd
+
+
 def decode_route(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, idx_scale,
                  floor, sigma, K, topm, seq_lens=None, block_table=None, page_size=None,
                  cand=None, refresh_tail=True, width=None, return_scores=False,
-                 valid_dtype=torch.bool, q_pos=None):
+                 valid_dtype=torch.bool, q_pos=None, kbar_table=None, bounds=None):
     """Decode routing for one query per sequence (at q_pos [B], default the last cached
     token; positions past it are taken as it): refreshes the
     tail block of `kbar_cache` [B, nblk_cap, d] in place, scores and routes.
     idx_q [B,d] or [B,1,d]; idx_k contiguous [B,S,d] or paged [pages, page_size, d].
     Returns idx int32 [B,1,K'], bias fp32, valid (bool, or valid_dtype) and with
-    return_scores the scores [B,nblk_cap]."""
+    return_scores the scores [B,nblk_cap].
+    kbar_table: kbar_cache is a page pool [pages, d] whose row for block c of sequence b is
+    kbar_table[b, c]; bounds [B, 2] (win_bounds): only those blocks are scored."""
     _need_gpu(idx_q, idx_k, kbar_cache)
     if _wide_topm(topm):
         return _decode_route_wide(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks,
                                   idx_scale, floor, sigma, K, topm, seq_lens, block_table,
                                   page_size, cand, refresh_tail, width, return_scores,
-                                  valid_dtype, q_pos)
+                                  valid_dtype, q_pos, kbar_table, bounds)
     lib = _lib.load()
     if idx_q.dim() == 3:
         idx_q = idx_q[:, 0]
@@ -561,7 +574,7 @@ def decode_route(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, i
     if idx_k.stride(-1) != 1:
         idx_k = idx_k.contiguous()
     B, d = idx_q.shape
-    nblk_cap = kbar_cache.shape[1]
+    nblk_cap, kb_sb, kbt, kb_ts, bnd = _kbar_layout(kbar_cache, kbar_table, bounds)
     if block_table is not None:
         bt = _i32(block_table)
         S = bt.shape[1] * page_size
@@ -585,7 +598,8 @@ def decode_route(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, i
         _ptr(idx_q), idx_q.stride(0), _ptr(idx_k), sb, st, sp, _ptr(bt),
         0 if bt is None else bt.stride(0), int(page_size or 0), _ptr(lens), _ptr(qp), S,
         _ptr(hc),
-        int(bool(refresh_tail)), _ptr(kbar_cache), kbar_cache.stride(0), nblk_cap, _ptr(c2),
+        int(bool(refresh_tail)), _ptr(kbar_cache), kb_sb, nblk_cap, _ptr(kbt), kb_ts, _ptr(bnd),
+        _ptr(c2),
         0 if c2 is None else c2.stride(0), B, d, int(block_size), int(local_blocks),
         float(idx_scale), float(floor), float(sigma), int(K), int(topm), Kw, _ptr(idx),
         _ptr(bias), _ptr(valid), _ptr(z), z.stride(0), _stream())
@@ -603,7 +617,8 @@ def _wide_topm(topm):
 
 def _decode_route_wide(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, idx_scale,
                        floor, sigma, K, topm, seq_lens, block_table, page_size, cand,
-                       refresh_tail, width, return_scores, valid_dtype, q_pos):
+                       refresh_tail, width, return_scores, valid_dtype, q_pos, kbar_table=None,
+                       bounds=None):
     """decode_route for a wide entmax: the decode router refreshes the tail summary
     and writes the scores (its own one-slot routing is discarded), then dash_route
     routes each sequence's row over its ceil(len / block_size) blocks."""
@@ -611,7 +626,7 @@ def _decode_route_wide(idx_q, idx_k, head_cls, kbar_cache, block_size, local_blo
                               idx_scale, floor, sigma, 1, 1, seq_lens=seq_lens,
                               block_table=block_table, page_size=page_size, cand=cand,
                               refresh_tail=refresh_tail, width=1, return_scores=True,
-                              q_pos=q_pos)
+                              q_pos=q_pos, kbar_table=kbar_table, bounds=bounds)
     B, nblk_cap = z.shape
     S = block_table.shape[1] * page_size if block_table is not None else idx_k.shape[1]
     if seq_lens is not None:
@@ -637,7 +652,7 @@ def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, l
                       idx_scale, floor, sigma, K, topm, scale, seq_lens=None, block_table=None,
                       page_size=None, cand=None, width=None, out_dtype=torch.float32,
                       return_lse=False, q_pos=None, workspace=None, return_scores=False,
-                      no_alloc=False):
+                      no_alloc=False, kbar_table=None, bounds=None):
     """decode_route followed by attn_decode of its routing, in two launches: the window
     part of the attention runs beside the router.  Same arguments and results as those
     two calls (q [B,H,D] or [B,H,1,D]; out [B,H,D]); returns (out, (idx, bias, valid))
@@ -654,7 +669,7 @@ def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, l
         idx, bias, valid, z = _decode_route_wide(
             idx_q, idx_k, head_cls, kbar_cache, block_size, local_blocks, idx_scale, floor,
             sigma, K, topm, seq_lens, block_table, page_size, cand, True, width, True,
-            torch.uint8, q_pos)
+            torch.uint8, q_pos, kbar_table, bounds)
         squeeze = q.dim() == 4
         qq = q[:, :, 0] if squeeze else q
         lw = int(local_blocks) * int(block_size)
@@ -680,7 +695,7 @@ def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, l
         idx_k = idx_k.contiguous()
     B, H, D = q.shape
     d = idx_q.shape[1]
-    nblk_cap = kbar_cache.shape[1]
+    nblk_cap, kb_sb, kbt, kb_ts, bnd = _kbar_layout(kbar_cache, kbar_table, bounds)
     if block_table is not None:
         bt = _i32(block_table)
         S = bt.shape[1] * page_size
@@ -714,7 +729,8 @@ def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, l
         st_ = lib.dash_decode_step_noalloc(
             _ptr(idx_q), idx_q.stride(0), _ptr(idx_k), isb, ist, isp, _ptr(bt), bt_stride,
             int(page_size or 0), _ptr(lens), _ptr(qp), S, _ptr(hc), 1, _ptr(kbar_cache),
-            kbar_cache.stride(0), nblk_cap, _ptr(c2), 0 if c2 is None else c2.stride(0), d,
+            kb_sb, nblk_cap, _ptr(kbt), kb_ts, _ptr(bnd), _ptr(c2),
+            0 if c2 is None else c2.stride(0), d,
             int(local_blocks), float(idx_scale), float(floor), float(sigma), int(K), int(topm),
             Kw, _ptr(idx), _ptr(bias), _ptr(valid), _ptr(z), z.stride(0),
             _ptr(q), q.stride(0), q.stride(1),
@@ -736,8 +752,8 @@ def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, l
     st_ = lib.dash_decode_step(
         _ptr(idx_q), idx_q.stride(0), _ptr(idx_k), isb, ist, isp, _ptr(bt), bt_stride,
         int(page_size or 0), _ptr(lens), _ptr(qp), S, _ptr(hc), 1, _ptr(kbar_cache),
-        kbar_cache.stride(0),
-        nblk_cap, _ptr(c2), 0 if c2 is None else c2.stride(0), d, int(local_blocks),
+        kb_sb, nblk_cap, _ptr(kbt), kb_ts, _ptr(bnd), _ptr(c2),
+        0 if c2 is None else c2.stride(0), d, int(local_blocks),
         float(idx_scale), float(floor), float(sigma), int(K), int(topm), Kw, _ptr(idx),
         _ptr(bias), _ptr(valid), _ptr(z), z.stride(0),
         _ptr(q), q.stride(0), q.stride(1),

@@ -248,3 +248,35 @@ def _uocr_dash_decode_allow(indexer, input_ids, cache):
     if st is None:
         return None
     return st.allow(input_ids, int(cache.get_seq_length()) + L)
+
+
+def win_bounds_decode(allow, seq_lens, max_block, block_size, local_blocks, tile=128,
+                      q_pos=None, out=None):
+    """Window bounds of decode rows, as the serving router computes them
+    (win_bounds_decode, whl:sglang/srt/layers/attention/unlimited_dash_ops/
+    route_triton.py:466-526, one decode query per sequence): the span [lo, hi) of the
+    allowed remote blocks of each row, the live remote width when none is allowed, and
+    whether the span fits `tile` blocks.  allow [B, W] bool/u8 (the decode allow rows);
+    returns (bounds int32 [B, 2], fit bool [B]); `out` = (bounds, fit) to write in place
+    (fixed buffers for graph capture)."""
+    _need_gpu(allow, seq_lens)
+    lib = _lib.load()
+    a = allow.view(torch.uint8) if allow.dtype == torch.bool else allow
+    if a.dtype != torch.uint8:
+        a = a.to(torch.uint8)
+    if a.stride(-1) != 1:
+        a = a.contiguous()
+    B = a.shape[0]
+    if out is None:
+        bounds = torch.empty(B, 2, dtype=torch.int32, device=a.device)
+        fit = torch.empty(B, dtype=torch.uint8, device=a.device)
+    else:
+        bounds, fit = out
+    lens = seq_lens.to(device=a.device, dtype=torch.int32).contiguous()
+    qp = None if q_pos is None else q_pos.to(device=a.device, dtype=torch.int32).contiguous()
+    S = int(max_block) * int(block_size)
+    st = lib.dash_decode_win_bounds(_ptr(a), a.stride(0), a.shape[1], _ptr(lens), _ptr(qp), B, S,
+                                    int(max_block), int(block_size), int(local_blocks), int(tile),
+                                    _ptr(bounds), _ptr(fit), _stream())
+    _lib.check(st, "dash_decode_win_bounds")
+    return bounds, fit.view(torch.bool) if fit.dtype == torch.uint8 else fit

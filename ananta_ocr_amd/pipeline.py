@@ -45,8 +45,50 @@ def prefill(q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks, idx_scale
 class DecodeState:
     """Per-layer decode state: the k_bar cache [B, nblk_cap, d] of the index keys."""
 
+    paged = False
+
     def __init__(self, kbar):
         self.kbar = kbar
+
+
+class KBarPageCache:
+    """Per-layer k_bar page pool: one fp32 summary per physical KV page [num_pages, d]
+    (one page is one routing block), the serving path's KBarCache
+    (whl:sglang/srt/layers/attention/unlimited_dash_ops/dash_stage0.py:106-148).  The
+    summaries stay with their pages, so sequences can join, leave or be reordered in the
+    batch without moving them; the decode router reads the pool through the block table
+    and rewrites the tail page's row in place."""
+
+    paged = True
+
+    def __init__(self, num_pages, dim, device):
+        self.kbar = torch.zeros(num_pages, dim, dtype=torch.float32, device=device)
+
+    def put(self, pages, k_bar):
+        """Write the summaries k_bar [n, d] of the given physical pages [n]."""
+        self.kbar[pages.reshape(-1).long()] = k_bar.reshape(-1, self.kbar.shape[1]).float()
+
+    def put_sequences(self, idx_k, head_cls, block_size, block_table, seq_lens):
+        """Summaries of every page the sequences use (after their prefill): idx_k is the
+        paged index-key cache [pages, block_size, d], block_table [B, P], seq_lens [B]."""
+        nblk = block_table.shape[1]
+        kb = ops.kbar(idx_k, head_cls, block_size, seq_lens=seq_lens, nblk_cap=nblk,
+                      block_table=block_table, page_size=block_size)
+        nb = (seq_lens.to(torch.int64) + block_size - 1) // block_size
+        used = torch.arange(nblk, device=kb.device)[None, :] < nb[:, None]
+        self.kbar[block_table.to(torch.int64)[used]] = kb[used]
+
+    def refresh_tail(self, idx_k, head_cls, block_size, block_table, seq_lens, tail_pages=1):
+        """Recompute the last tail_pages summaries of every sequence
+        (dash_stage0.py:121-148) -- the decode router already refreshes the last one."""
+        nblk = block_table.shape[1]
+        kb = ops.kbar(idx_k, head_cls, block_size, seq_lens=seq_lens, nblk_cap=nblk,
+                      block_table=block_table, page_size=block_size,
+                      tail_only=tail_pages == 1)
+        nb = (seq_lens.to(torch.int64) + block_size - 1) // block_size
+        c = torch.arange(nblk, device=kb.device)[None, :]
+        sel = (c < nb[:, None]) & (c >= nb[:, None] - int(tail_pages))
+        self.kbar[block_table.to(torch.int64)[sel]] = kb[sel]
 
 
 def init_decode_state(idx_k, head_cls, block_size, nblk_cap, seq_lens=None, block_table=None,
@@ -59,13 +101,23 @@ def init_decode_state(idx_k, head_cls, block_size, nblk_cap, seq_lens=None, bloc
 def decode_step(state, q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks, idx_scale,
                 floor, sigma, K, topm, scale=None, seq_lens=None, block_table=None,
                 page_size=None, out_dtype=torch.float32, nsplit=None, block_cand=None,
-                return_routing=False, fused=None, return_scores=False):
+                return_routing=False, fused=None, return_scores=False, bounds=None):
     """One decode step for the query at the last cached token of each sequence.
     The newest token is already in k/v and idx_k; its block's summary is refreshed
     inside the fused decode router.  fused (default: whenever nsplit is not given and
     the shapes allow it) runs the window part of the attention beside the router
     (ops.decode_step_fused); otherwise decode_route then attn_decode.  return_scores
-    (with return_routing) also returns the block scores [B, nblk_cap] of the router."""
+    (with return_routing) also returns the block scores [B, nblk_cap] of the router.
+    state: a DecodeState (k_bar per sequence) or a KBarPageCache (k_bar per page, read
+    through block_table; page_size must equal block_size).  bounds [B, 2]
+    (pages.win_bounds_decode of the candidate rows): only those blocks are scored."""
+    kbx = {}
+    if state.paged:
+        if block_table is None or page_size != block_size:
+            raise NotImplementedError("a k_bar page pool needs pages of one block")
+        kbx["kbar_table"] = block_table
+    if bounds is not None:
+        kbx["bounds"] = bounds
     D = q.shape[-1]
     if scale is None:
         scale = 1.0 / math.sqrt(D)
@@ -79,7 +131,7 @@ def decode_step(state, q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks
             q, k, v, idx_q, idx_k, head_cls, state.kbar, block_size, local_blocks, idx_scale,
             floor, sigma, K, topm, scale, seq_lens=seq_lens, block_table=block_table,
             page_size=page_size, cand=block_cand, width=width, out_dtype=out_dtype,
-            return_scores=True)
+            return_scores=True, **kbx)
         if return_routing:
             res = (out, (idx, bias, valid.bool()))
             return res + (z,) if return_scores else res
@@ -88,7 +140,7 @@ def decode_step(state, q, k, v, idx_q, idx_k, head_cls, block_size, local_blocks
                                            local_blocks, idx_scale, floor, sigma, K, topm,
                                            seq_lens=seq_lens, block_table=block_table,
                                            page_size=page_size, cand=block_cand, width=width,
-                                           valid_dtype=torch.uint8, return_scores=True)
+                                           valid_dtype=torch.uint8, return_scores=True, **kbx)
     out = ops.attn_decode(q, k, v, idx[:, 0], bias[:, 0], valid[:, 0], block_size,
                           local_blocks * block_size, scale, seq_lens=seq_lens,
                           block_table=block_table, page_size=page_size, out_dtype=out_dtype,

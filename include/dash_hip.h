@@ -246,7 +246,15 @@ int dash_prefill_plan_target(int64_t chunk_cap, int64_t ppos, int64_t pos0, int6
  * _dash_decode_forward (modeling_deepseekv2.py:481-496: _block_scores_infer over the whole
  * index-key cache + _infer_route_select), keeping the summaries of complete blocks cached.
  *   idx_q    fp32 [B, d] rows (iq_sb); idx_k index-key cache addressed like dash_kbar
- *   kbar     [B, nblk_cap, d] fp32 cache (updated in place at the tail block)
+ *   kbar     [B, nblk_cap, d] fp32 cache (updated in place at the tail block), or with
+ *            kb_table a page pool [pages, d]: the row of block c of sequence b is
+ *            kb_table[b * kb_ts + c] (one page per block; the serving path's KBarCache,
+ *            whl:sglang/srt/layers/attention/unlimited_dash_ops/dash_stage0.py:106-148),
+ *            kb_ts >= nblk_cap
+ *   bounds   optional int32 [B, 2] (lo, hi) from dash_decode_win_bounds: only blocks
+ *            lo <= c < hi are scored, the others score as not remote (their k_bar rows are
+ *            not read).  With bounds computed from the same candidate rows the routing is
+ *            identical to the unbounded one; z outside the span reads -1e9.
  *   z        [B, z_stride] fp32 scores (written, for inspection)
  *   One 1024-thread work-group per sequence; with refresh_tail and local_blocks >= 1 a
  *   second one per sequence refreshes the tail block beside the routing (the tail block
@@ -258,7 +266,8 @@ int dash_decode_route(const float* idx_q, int64_t iq_sb, const float* idx_k,
                       const int32_t* block_table, int64_t table_stride, int page_size,
                       const int32_t* seq_lens, const int32_t* q_pos, int S,
                       const float* head_cls, int refresh_tail,
-                      float* kbar, int64_t kb_sb, int nblk_cap, const uint8_t* cand,
+                      float* kbar, int64_t kb_sb, int nblk_cap, const int32_t* kb_table,
+                      int64_t kb_ts, const int32_t* bounds, const uint8_t* cand,
                       int64_t cand_stride, int B, int d, int block_size, int local_blocks,
                       float idx_scale, float floor_p, float sigma, int K, int topm, int Kout,
                       int32_t* idx, float* bias, uint8_t* valid, float* z, int64_t z_stride,
@@ -309,7 +318,8 @@ int dash_decode_step(const float* idx_q, int64_t iq_sb, const float* idx_k, int6
                      int64_t table_stride, int page_size, const int32_t* seq_lens,
                      const int32_t* q_pos, int S,
                      const float* head_cls, int refresh_tail, float* kbar, int64_t kb_sb,
-                     int nblk_cap, const uint8_t* cand, int64_t cand_stride, int d,
+                     int nblk_cap, const int32_t* kb_table, int64_t kb_ts, const int32_t* bounds,
+                     const uint8_t* cand, int64_t cand_stride, int d,
                      int local_blocks, float idx_scale, float floor_p, float sigma, int K,
                      int topm, int Kout, int32_t* idx, float* bias, uint8_t* valid, float* z,
                      int64_t z_stride,
@@ -390,6 +400,21 @@ int dash_decode_allow(const int64_t* new_ids, int64_t new_stride, int B, int64_t
                       int64_t allow_sb, void* stream);
 
 /*
+ * Window bounds of decode rows, as the serving router computes them
+ * (_win_bounds_kernel, whl:sglang/srt/layers/attention/unlimited_dash_ops/
+ * route_triton.py:466-505, one decode query per sequence): for the query at q_pos[b]
+ * (NULL: len - 1), the span [lo, hi) of blocks c < min(nblk_cap, allow_w) with
+ * allow[b, c] != 0, c <= q_pos / block_size - local_blocks and c * block_size < len;
+ * with none, [0, min(nblk_cap, max(ceil(len / block_size), 1))), or [0, 0) when no
+ * block is remote.  bounds int32 [B, 2]; fit (optional) u8 [B] = (hi - lo <= tile).
+ * Replaces win_bounds_decode (route_triton.py:508-526).
+ */
+int dash_decode_win_bounds(const uint8_t* allow, int64_t allow_sb, int allow_w,
+                           const int32_t* seq_lens, const int32_t* q_pos, int B, int S,
+                           int nblk_cap, int block_size, int local_blocks, int tile,
+                           int32_t* bounds, uint8_t* fit, void* stream);
+
+/*
  * Allocation-free decode step.  No counterpart in the reference: it is for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving loops).
  * Same arguments and results as dash_decode_step without the workspace: the window and
@@ -403,7 +428,8 @@ int dash_decode_step_noalloc(const float* idx_q, int64_t iq_sb, const float* idx
                              const int32_t* block_table, int64_t table_stride, int page_size,
                              const int32_t* seq_lens, const int32_t* q_pos, int S,
                              const float* head_cls, int refresh_tail, float* kbar,
-                             int64_t kb_sb, int nblk_cap, const uint8_t* cand,
+                             int64_t kb_sb, int nblk_cap, const int32_t* kb_table,
+                             int64_t kb_ts, const int32_t* bounds, const uint8_t* cand,
                              int64_t cand_stride, int d, int local_blocks, float idx_scale,
                              float floor_p, float sigma, int K, int topm, int Kout,
                              int32_t* idx, float* bias, uint8_t* valid, float* z,

@@ -24,6 +24,7 @@ for the path (citations are ``file:line`` in the reference repository):
 * page-aware candidates       -- _sparse_base_impl.py:2189-2259 (page ids), :2363-2380 (flat
                                  image mask), :2436-2484 (candidate mask); decode allow row
                                  modeling_anantaocr.py:450-496
+* decode window bounds        -- the vendored serving router's route_triton.py:466-505
 
 Deliberate, documented deviation: ``torch.topk`` leaves the order of tied values
 unspecified (the CPU kernel returns ties in an arbitrary order).  The oracle
@@ -42,6 +43,8 @@ Parity pinning (what each function is checked against, in tests/):
   decode_attend    -> the same enumeration at one query; equality with prefill rows
   page candidates  -> known-answer prompts written out by hand, and a token-by-token
                       walk of the prompt (tests/bruteforce.py) on random prompts
+  window bounds    -> known-answer rows written out by hand, and a per-row loop from the
+                      definition (tests/bruteforce.py:win_bounds_row)
 """
 
 import math
@@ -547,3 +550,28 @@ def decode_allow(state, input_ids, pg_id, total_len, block_size):
     n0 = min(nblk, same.shape[-1])
     allow[:, :n0] = same[:, :n0]
     return allow | open_row[:, None]
+
+
+def decode_win_bounds(allow, seq_lens, max_block, block_size, local_blocks, tile, q_pos=None):
+    """Window bounds of decode rows (the serving router's _win_bounds_kernel,
+    whl:sglang/srt/layers/attention/unlimited_dash_ops/route_triton.py:466-505, sglang
+    0.5.20.dev13+g75b9b06b02, one decode query per sequence).  allow [B, WQ] bool;
+    returns (lo, hi, fit) int64/int64/bool [B]."""
+    B, WQ = allow.shape
+    seq = seq_lens.long()
+    qp = seq - 1 if q_pos is None else torch.minimum(q_pos.long(), seq - 1)
+    q_blk = torch.div(qp, block_size, rounding_mode="floor")
+    W = int(max_block)
+    off = torch.arange(min(W, WQ))
+    keep = allow[:, :off.numel()].bool() & (off[None, :] <= (q_blk[:, None] - local_blocks)) \
+        & (off[None, :] * block_size < seq[:, None])
+    big = torch.full_like(off, W)
+    lo = torch.where(keep, off[None, :], big[None, :]).min(dim=-1).values
+    hi = torch.where(keep, off[None, :], torch.full_like(big, -1)[None, :]).max(dim=-1).values
+    any_r = hi >= 0
+    n_blk = torch.div(seq + block_size - 1, block_size, rounding_mode="floor")
+    w_seq = torch.clamp(n_blk, min=1).clamp(max=W)
+    no_remote = (seq <= 0) | ((q_blk - local_blocks) < 0)
+    lo_v = torch.where(any_r, lo, torch.zeros_like(lo))
+    hi_v = torch.where(any_r, hi + 1, torch.where(no_remote, torch.zeros_like(hi), w_seq))
+    return lo_v, hi_v, (hi_v - lo_v) <= tile

@@ -222,3 +222,19 @@ def decode_allow_row(bmin, bmax, pp, markers, new_is_marker, nblk):
     if qp < 0 or not any(same):
         return [True] * nblk, m
     return same, m
+
+
+def win_bounds_row(allow, seq, max_block, bs, lb, tile):
+    """(lo, hi, fit) of one decode row from the definition: the allowed blocks that are
+    remote for the query at seq - 1 and hold a live key; with none, the live width (or
+    nothing when the query has no remote block)."""
+    q_blk = (seq - 1) // bs if seq > 0 else -1
+    live = [c for c in range(min(max_block, len(allow)))
+            if allow[c] and c <= q_blk - lb and c * bs < seq]
+    if live:
+        lo, hi = min(live), max(live) + 1
+    elif seq <= 0 or q_blk - lb < 0:
+        lo, hi = 0, 0
+    else:
+        lo, hi = 0, min(max_block, max((seq + bs - 1) // bs, 1))
+    return lo, hi, hi - lo <= tile

@@ -126,3 +126,34 @@ def test_decode_allow_matches_token_walk(seed):
             row, marks[b] = BF.decode_allow_row(walks[b][0], walks[b][1], walks[b][2], marks[b],
                                                 new[b] == PG, nblk)
             assert a[b].tolist() == row, (seed, step, b)
+
+
+def test_win_bounds_known_answers():
+    """Block 4, one local block: the query at 29 sits in block 7, so blocks <= 6 are
+    remote.  Rows: allowed {2, 5} -> [2, 6); allowed only beyond the remote range ->
+    the live width [0, 8); a query in block 0 -> nothing; allowed {6} with a tile of
+    0 blocks -> does not fit."""
+    allow = torch.zeros(4, 10, dtype=torch.bool)
+    allow[0, [2, 5]] = True
+    allow[1, [7, 9]] = True
+    allow[2, [0]] = True
+    allow[3, [6]] = True
+    seq = torch.tensor([30, 30, 3, 30])
+    lo, hi, fit = O.decode_win_bounds(allow, seq, 10, 4, 1, 2)
+    assert lo.tolist() == [2, 0, 0, 6]
+    assert hi.tolist() == [6, 8, 0, 7]
+    assert fit.tolist() == [False, False, True, True]
+    lo, hi, fit = O.decode_win_bounds(allow, seq, 10, 4, 1, 0)
+    assert fit.tolist() == [False, False, True, False]
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_win_bounds_match_definition(seed):
+    g = torch.Generator().manual_seed(seed)
+    B, W, bs, lb = 64, 40, 8, 2
+    allow = torch.rand(B, W + 3, generator=g) < torch.rand(B, 1, generator=g) * 0.3
+    seq = torch.randint(0, W * bs + 1, (B,), generator=g)
+    lo, hi, fit = O.decode_win_bounds(allow, seq, W, bs, lb, 6)
+    for b in range(B):
+        assert (int(lo[b]), int(hi[b]), bool(fit[b])) == \
+            BF.win_bounds_row(allow[b].tolist(), int(seq[b]), W, bs, lb, 6), b

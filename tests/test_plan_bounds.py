@@ -116,7 +116,8 @@ def test_error_word_inside_cleared_counters():
 def _decode_route_status(lib, S, nblk_cap, bs=64, B=2, d=128):
     fake = ctypes.c_void_p(1 << 20)            # aligned, never dereferenced
     return lib.dash_decode_route(fake, d, fake, S * d, d, 0, None, 0, 0, None, None, S, fake, 1,
-                                 fake, nblk_cap * d, nblk_cap, None, 0, B, d, bs, 2,
+                                 fake, nblk_cap * d, nblk_cap, None, 0, None, None, 0, B, d, bs,
+                                 2,
                                  1.0, 1e-4, 1.0, 4, 4, 4, fake, fake, fake, fake, nblk_cap,
                                  None)
 

@@ -65,7 +65,8 @@ def test_noalloc_refuses_sizes_beyond_its_scratch():
     fake = ctypes.c_void_p(1 << 20)
     st = lib.dash_decode_step_noalloc(
         fake, 128, fake, 0, 128, 0, None, 0, 0, None, None, 1000, fake, 1, fake, 16 * 128,
-        16, None, 0, 128, 16, 1.0, 1e-4, 1.0, 16, 16, 16, fake, fake, fake, fake, 16,
+        16, None, 0, None, None, 0, 128, 16, 1.0, 1e-4, 1.0, 16, 16, 16, fake, fake, fake, fake,
+        16,
         fake, H * D, D, fake, 0, 0, 0, 0, fake, 0, 0, 0, 0, fake, 0, H * D, D, None, 0, 0,
         B, H, D, bs, lw, 0.1, None)
     assert st == -5
