@@ -26,6 +26,9 @@ SIGNATURES = {
                                   _i, _i, _p, _l, _l, _p]),
     "dash_router_qk_norm": (_i, [_p, _i, _l, _l, _i, _i, _p, _p, _f, _p, _p, _i, _l, _l, _p, _p,
                                  _p]),
+    "dash_router_front": (_i, [_p, _l, _l, _i, _i, _i, _p, _p, _p, _p, _p, _f, _p, _p, _i, _l, _l,
+                               _p, _i, _f, _p, _l, _p, _l, _p, _l, _i, _p]),
+    "dash_router_front_pack_weights": (_i, [_p, _p, _i, _p, _p]),
     "dash_route": (_i, [_p, _l, _i, _i, _p, _p, _l, _f, _f, _f, _i, _i, _i, _p, _p, _p, _p]),
     "dash_train_route": (_i, [_p, _l, _i, _i, _p, _p, _l, _f, _f, _f, _i, _i, _p, _p, _p, _p,
                               _p, _p]),

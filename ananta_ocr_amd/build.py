@@ -8,7 +8,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libdash_hip.so")
 SOURCES = ["dash_capi.hip", "dash_router.hip", "dash_prefill.hip", "dash_decode.hip",
-           "dash_pages.hip"]
+           "dash_pages.hip", "dash_front.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -628,6 +628,99 @@ __device__ __forceinline__ float ord_key_inv(uint32_t h) {
   return __uint_as_float((h & 0x80000000u) ? (h & 0x7fffffffu) : ~h);
 }
 
+// Phase 2 of the inference routing for one row per 16-lane group (lane m = entry
+// m): the row's M <= 16 selected keys sel[0..M) (any order; sorted in place) are
+// ranked, then 1.5-entmax with entry m on lane m (each lane forms its prefix sums
+// in the serial order, so the result is the serial one bit for bit), first K,
+// centred log-prior bias; writes idx / bias / valid row `row` (Kout slots).  Every
+// lane of the wavefront calls it (wavefront barriers inside).
+__device__ __forceinline__ void route_finish(uint64_t* sel, int M, bool row_ok, int64_t row,
+                                             float floor_p, float inv_sigma, int K, int Kout,
+                                             int32_t* __restrict__ idx_out,
+                                             float* __restrict__ bias_out,
+                                             uint8_t* __restrict__ valid_out) {
+#pragma clang fp contract(off)
+  const int lane = wave_lane();
+  const int m = lane & 15, gbase = lane & ~15;
+  const uint64_t key = m < M ? sel[m] : 0ull;
+  int rank = 0;
+#pragma unroll
+  for (int j = 0; j < kMaxM; ++j) {
+    const uint64_t kj = row_ok ? sel[j] : 0ull;
+    rank += (j < M && kj > key) ? 1 : 0;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (m < M) sel[rank] = key;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const uint64_t ks = m < M ? sel[m] : 0ull;           // entry m of the descending order
+  const uint32_t kh = (uint32_t)(ks >> 32), kl = (uint32_t)ks;
+  const float xv = m < M ? ord_key_inv(kh) : 0.f;
+  const int sel_id = 0xffff - (int)((kl >> 1) & 0xffff);
+  const bool sel_c = (kl & 1u) != 0;
+  const float x0 = __shfl(xv, gbase, kWave);
+  const float X = __fdiv_rn(__fsub_rn(xv, x0), 2.0f);
+  double cs = 0.0, cs2 = 0.0;
+#pragma unroll
+  for (int j = 0; j < kMaxM; ++j) {
+    const float Xj = __shfl(X, gbase + j, kWave);
+    if (j <= m) {
+      cs += (double)Xj;
+      cs2 += (double)__fmul_rn(Xj, Xj);
+    }
+  }
+  const int Me = max(M, 1);                  // entmax over at least one entry
+  float tau = 0.f;
+  bool sup = false;
+  if (m < Me) {
+    const float rho = (float)(m + 1);
+    const float mean = __fdiv_rn((float)cs, rho);
+    const float mean_sq = __fdiv_rn((float)cs2, rho);
+    const float ss = __fmul_rn(rho, __fsub_rn(mean_sq, __fmul_rn(mean, mean)));
+    const float delta = __fdiv_rn(__fsub_rn(1.0f, ss), rho);
+    const float delta_nz = delta > 0.f ? delta : 0.f;
+    tau = __fsub_rn(mean, __fsqrt_rn(delta_nz));
+    sup = tau <= X;
+  }
+  const uint32_t grp = (uint32_t)(__ballot(sup) >> gbase) & 0xffffu;
+  const int support = max(__popc(grp), 1);
+  const float tau_star = __shfl(tau, gbase + support - 1, kWave);
+  const float tt = __fsub_rn(X, tau_star);
+  const float cc = tt > 0.f ? tt : 0.f;
+  const float prior = m < M ? __fmul_rn(cc, cc) : 0.f;
+  const float logp = logf(fmaxf(prior, floor_p));
+  const int Kp = max(1, min(K, M));
+  // mean log-prior of the kept candidate slots, summed in slot order
+  const uint32_t keep = (uint32_t)(__ballot(m < Kp && m < M && sel_c) >> gbase) & 0xffffu;
+  float musum = 0.f;
+  int cnt = 0;
+#pragma unroll
+  for (int j = 0; j < kMaxM; ++j) {
+    const float lj = __shfl(logp, gbase + j, kWave);
+    if ((keep >> j) & 1u) { musum += lj; ++cnt; }
+  }
+  const float mu = musum / (float)max(cnt, 1);
+  if (!row_ok) return;
+  int32_t* io = idx_out + row * Kout;
+  float* bo = bias_out + row * Kout;
+  uint8_t* vo = valid_out ? valid_out + row * Kout : nullptr;
+  if (m < Kout) {
+    const bool in = m < Kp && m < M;
+    const bool va = in && sel_c;
+    io[m] = in ? sel_id : -1;
+    bo[m] = va ? (logp - mu) * inv_sigma : 0.f;
+    if (vo) vo[m] = va ? 1 : 0;
+  }
+  for (int mm = kMaxM + m; mm < Kout; mm += kMaxM) {
+    io[mm] = -1;
+    bo[mm] = 0.f;
+    if (vo) vo[mm] = 0;
+  }
+}
+
 template <int NPL>
 __global__ __launch_bounds__(kRtWaves * kWave) void route_kernel(
     const float* __restrict__ z, int64_t z_stride, int rows, int nblk_cols,
@@ -761,94 +854,13 @@ __global__ __launch_bounds__(kRtWaves * kWave) void route_kernel(
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- phase 2: each wavefront finishes its own rows, 16 lanes per row (lane
-  // group gi = row rr, lane m = entry m): rank sort, then 1.5-entmax with entry m
-  // on lane m (each lane forms its prefix sums in the serial order, so the result
-  // is the serial one bit for bit), first K, centred log-prior bias ----
+  // ---- phase 2: each wavefront finishes its own rows, 16 lanes per row ----
   {
-#pragma clang fp contract(off)
-  const int gi = lane >> 4, m = lane & 15, gbase = lane & ~15;
-  const bool row_ok = gi < nrow;
-  const int sr = wv * kRtRowsPerWave + gi;
-  const int row = row0 + gi;
-  const int M = row_ok ? s_M[sr] : 0;
-  const uint64_t key = m < M ? s_sel[sr][m] : 0ull;
-  int rank = 0;
-#pragma unroll
-  for (int j = 0; j < kMaxM; ++j) {
-    const uint64_t kj = row_ok ? s_sel[sr][j] : 0ull;
-    rank += (j < M && kj > key) ? 1 : 0;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (m < M) s_sel[sr][rank] = key;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const uint64_t ks = m < M ? s_sel[sr][m] : 0ull;     // entry m of the descending order
-  const uint32_t kh = (uint32_t)(ks >> 32), kl = (uint32_t)ks;
-  const float xv = m < M ? ord_key_inv(kh) : 0.f;
-  const int sel_id = 0xffff - (int)((kl >> 1) & 0xffff);
-  const bool sel_c = (kl & 1u) != 0;
-  const float x0 = __shfl(xv, gbase, kWave);
-  const float X = __fdiv_rn(__fsub_rn(xv, x0), 2.0f);
-  double cs = 0.0, cs2 = 0.0;
-#pragma unroll
-  for (int j = 0; j < kMaxM; ++j) {
-    const float Xj = __shfl(X, gbase + j, kWave);
-    if (j <= m) {
-      cs += (double)Xj;
-      cs2 += (double)__fmul_rn(Xj, Xj);
-    }
-  }
-  const int Me = max(M, 1);                  // entmax over at least one entry
-  float tau = 0.f;
-  bool sup = false;
-  if (m < Me) {
-    const float rho = (float)(m + 1);
-    const float mean = __fdiv_rn((float)cs, rho);
-    const float mean_sq = __fdiv_rn((float)cs2, rho);
-    const float ss = __fmul_rn(rho, __fsub_rn(mean_sq, __fmul_rn(mean, mean)));
-    const float delta = __fdiv_rn(__fsub_rn(1.0f, ss), rho);
-    const float delta_nz = delta > 0.f ? delta : 0.f;
-    tau = __fsub_rn(mean, __fsqrt_rn(delta_nz));
-    sup = tau <= X;
-  }
-  const uint32_t grp = (uint32_t)(__ballot(sup) >> gbase) & 0xffffu;
-  const int support = max(__popc(grp), 1);
-  const float tau_star = __shfl(tau, gbase + support - 1, kWave);
-  const float tt = __fsub_rn(X, tau_star);
-  const float cc = tt > 0.f ? tt : 0.f;
-  const float prior = m < M ? __fmul_rn(cc, cc) : 0.f;
-  const float logp = logf(fmaxf(prior, floor_p));
-  const int Kp = max(1, min(K, M));
-  // mean log-prior of the kept candidate slots, summed in slot order
-  const uint32_t keep = (uint32_t)(__ballot(m < Kp && m < M && sel_c) >> gbase) & 0xffffu;
-  float musum = 0.f;
-  int cnt = 0;
-#pragma unroll
-  for (int j = 0; j < kMaxM; ++j) {
-    const float lj = __shfl(logp, gbase + j, kWave);
-    if ((keep >> j) & 1u) { musum += lj; ++cnt; }
-  }
-  const float mu = musum / (float)max(cnt, 1);
-  if (!row_ok) return;
-  int32_t* io = idx_out + (int64_t)row * Kout;
-  float* bo = bias_out + (int64_t)row * Kout;
-  uint8_t* vo = valid_out ? valid_out + (int64_t)row * Kout : nullptr;
-  if (m < Kout) {
-    const bool in = m < Kp && m < M;
-    const bool va = in && sel_c;
-    io[m] = in ? sel_id : -1;
-    bo[m] = va ? (logp - mu) * inv_sigma : 0.f;
-    if (vo) vo[m] = va ? 1 : 0;
-  }
-  for (int mm = kMaxM + m; mm < Kout; mm += kMaxM) {
-    io[mm] = -1;
-    bo[mm] = 0.f;
-    if (vo) vo[mm] = 0;
-  }
+    const int gi = lane >> 4;
+    const bool row_ok = gi < nrow;
+    const int sr = wv * kRtRowsPerWave + gi;
+    route_finish(s_sel[sr], row_ok ? s_M[sr] : 0, row_ok, row0 + gi, floor_p, inv_sigma, K, Kout,
+                 idx_out, bias_out, valid_out);
   }
 }
 

@@ -173,10 +173,52 @@ class DashAttention(nn.Module):
         self._ks_id = K_SCHEDULE.register()
 
     # ---------------------------------------------------------------- router
+    # fewest token rows for the fused front end: its work-groups own 64 rows and run
+    # the whole hidden width, which loses to the library GEMM for decode-sized batches
+    FRONT_MIN_ROWS = 1024
+
+    def _front_ok(self, hidden_states):
+        return (self.index_dim == 128 and self.q_norm.eps == self.k_norm.eps
+                and hidden_states.shape[0] * hidden_states.shape[1] >= self.FRONT_MIN_ROWS
+                and ops.router_front_supported(hidden_states, self.q_proj.weight,
+                                               self.k_proj.weight))
+
+    def _front_weights(self):
+        """The projection weights in the fused front end's operand order, repacked when
+        the weights change."""
+        wq, wk = self.q_proj.weight, self.k_proj.weight
+        key = (wq.data_ptr(), wk.data_ptr(), wq._version, wk._version)
+        cached = getattr(self, "_front_pack", None)
+        if cached is None or cached[0] != key:
+            cached = (key, ops.router_front_pack(wq.detach(), wk.detach()))
+            self._front_pack = cached
+        return cached[1]
+
+    def router_front(self, hidden_states, position_embeddings=None, with_kbar=False,
+                     idx_k_out=None, kbar_out=None, nblk_cap=None):
+        """(idx_q, idx_k, k_bar or None) from bf16 hidden states in one launch: the
+        projections, norms, RoPE and guards of router_qk and, with with_kbar (stage 0
+        head_cls, blocks of 32 or 64), the block summaries of block_scores."""
+        cos = sin = None
+        if position_embeddings is not None:
+            cos, sin = position_embeddings
+        kb = with_kbar and self.stage0 == "head_cls"
+        return ops.router_front(hidden_states, self.q_proj.weight.detach(),
+                                self.k_proj.weight.detach(), self.q_norm.weight.detach(),
+                                self.k_norm.weight.detach(), self.q_norm.eps, cos, sin,
+                                head_cls=self.head_cls.detach() if kb else None,
+                                block_size=self.block_size if kb else None,
+                                idx_k_out=idx_k_out, kbar_out=kbar_out if kb else None,
+                                nblk_cap=nblk_cap if kb else None,
+                                w_pack=self._front_weights())
+
     def router_qk(self, hidden_states, position_embeddings=None):
         """idx_q/idx_k [B,S,d] fp32 (modeling_deepseekv2.py:336-348)."""
         B, S, _ = hidden_states.shape
         d = self.index_dim
+        if hidden_states.is_cuda and self._front_ok(hidden_states):
+            iq, ik, _ = self.router_front(hidden_states, position_embeddings)
+            return iq, ik
         hs = torch.nan_to_num(hidden_states, nan=0.0, posinf=0.0, neginf=0.0)
         if d == 128 and hs.is_cuda and self.q_norm.eps == self.k_norm.eps:
             # one GEMM for both projections, then the fused norm / RoPE / guards

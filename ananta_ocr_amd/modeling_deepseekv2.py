@@ -113,8 +113,7 @@ class DashDecodeCache:
         B, S, d = idx_k.shape
         self.bs = router.block_size
         self.head_cls = router.head_cls.detach().float()
-        cap = max(S + (spare if spare is not None else max(S, 1024)), 1)
-        cap = (cap + self.bs - 1) // self.bs * self.bs
+        cap = self.capacity(S, self.bs, spare)
         self._buf = torch.zeros(B, cap, d, dtype=torch.float32, device=idx_k.device)
         self._buf[:, :S] = idx_k
         self.S = S
@@ -122,6 +121,31 @@ class DashDecodeCache:
         if router.stage0 == "head_cls":
             self.kbar = ops.kbar(self._buf[:, :S], self.head_cls, self.bs,
                                  nblk_cap=cap // self.bs)
+
+    @staticmethod
+    def capacity(S, bs, spare=None):
+        cap = max(S + (spare if spare is not None else max(S, 1024)), 1)
+        return (cap + bs - 1) // bs * bs
+
+    @classmethod
+    def buffers(cls, B, S, d, bs, device, head_cls_stage):
+        """Zeroed index-key buffer [B, cap, d] and summaries [B, cap // bs, d] (or None)
+        for a prefill of S tokens to write into (then ``from_buffers``)."""
+        cap = cls.capacity(S, bs)
+        buf = torch.zeros(B, cap, d, dtype=torch.float32, device=device)
+        kb = torch.zeros(B, cap // bs, d, dtype=torch.float32, device=device) \
+            if head_cls_stage else None
+        return buf, kb
+
+    @classmethod
+    def from_buffers(cls, router, buf, kbar, S):
+        """The cache over buffers a prefill wrote: index keys in buf[:, :S] and, for stage
+        0 head_cls, the summaries of its blocks in kbar."""
+        dc = cls.__new__(cls)
+        dc.bs = router.block_size
+        dc.head_cls = router.head_cls.detach().float()
+        dc._buf, dc.kbar, dc.S = buf, kbar, S
+        return dc
 
     @property
     def idx_k(self):
@@ -167,15 +191,33 @@ def _infer_prefill_attend(self, router, hidden_states, q, k, v, idx_pe, pos_ids,
     B, H, S, D = q.shape
     nblk = (S + router.block_size - 1) // router.block_size
     p = router._infer_params
-    idx_q, idx_k = _router_qk(router, hidden_states, idx_pe)
     kb = None
+    head_cls = router.stage0 == "head_cls"
+    if hidden_states.is_cuda and router._front_ok(hidden_states) and \
+            (not head_cls or router.block_size in (32, 64)):
+        # one launch: projections, norms, RoPE, guards and the block summaries, the index
+        # keys and summaries written straight into the decode cache's buffers
+        buf = kbuf = None
+        if past_kv is not None:
+            buf, kbuf = DashDecodeCache.buffers(B, S, router.index_dim, router.block_size,
+                                                q.device, head_cls)
+        idx_q, idx_k, kb = router.router_front(hidden_states, idx_pe, with_kbar=head_cls,
+                                               idx_k_out=buf, kbar_out=kbuf,
+                                               nblk_cap=None if kbuf is None else kbuf.shape[1])
+        if kb is not None:
+            kb = kb[:, :nblk]
+        if past_kv is not None:
+            dc = DashDecodeCache.from_buffers(router, buf, kbuf, S)
+    else:
+        idx_q, idx_k = _router_qk(router, hidden_states, idx_pe)
+        dc = DashDecodeCache(router, idx_k) if past_kv is not None else None
+        if dc is not None:
+            kb = dc.kbar                    # the block summaries the scores use
     if past_kv is not None:
         if not hasattr(past_kv, "_dash_idx_k"):
             past_kv._dash_idx_k = {}
-        dc = DashDecodeCache(router, idx_k)
         _decode_caches(past_kv)[self.layer_idx] = dc
         past_kv._dash_idx_k[self.layer_idx] = dc.idx_k
-        kb = dc.kbar                    # the block summaries the scores use
     sc = router.block_scores(idx_q, idx_k, q_pos=pos_ids.to(torch.int32), nblk=nblk, kbar=kb)
     topi, bias, valid = _infer_route_select(sc, block_cand, p)
     if router.use_triton and q.is_cuda and attn_mask is None:

@@ -193,6 +193,86 @@ def router_qk_norm(proj, wq, wk, eps, cos=None, sin=None):
     return iq, ik
 
 
+def router_front_supported(hs, w_q, w_k, block_size=None):
+    """Whether dash_router_front takes these inputs (bf16 hidden states and weights
+    [128, hidden], hidden % 64 == 0; block 32 or 64 for the k_bar / scores)."""
+    return (hs.is_cuda and hs.dtype == torch.bfloat16 and w_q.dtype == torch.bfloat16
+            and w_k.dtype == torch.bfloat16 and w_q.shape == (128, hs.shape[-1])
+            and w_k.shape == w_q.shape and hs.shape[-1] % 64 == 0
+            and (block_size is None or block_size in (32, 64)))
+
+
+def router_front_pack(w_q, w_k):
+    """The q_proj / k_proj weights bf16 [128, hidden] in the fused front end's operand
+    order (dash_router_front_pack_weights); recompute when the weights change."""
+    _need_gpu(w_q, w_k)
+    lib = _lib.load()
+    w_q, w_k = w_q.contiguous(), w_k.contiguous()
+    out = torch.empty(w_q.numel() * 2, dtype=torch.bfloat16, device=w_q.device)
+    _lib.check(lib.dash_router_front_pack_weights(_ptr(w_q), _ptr(w_k), w_q.shape[1], _ptr(out),
+                                                  _stream()), "dash_router_front_pack_weights")
+    return out
+
+
+def router_front(hs, w_q, w_k, nq, nk, eps, cos=None, sin=None, head_cls=None, block_size=None,
+                 want_q=True, idx_k_out=None, kbar_out=None, nblk_cap=None, w_pack=None):
+    """Fused router front end (one launch) for bf16 hidden states hs [B,S,hidden]:
+    projections by w_q / w_k bf16 [128,hidden], Gemma RMSNorm (weights nq / nk [128]),
+    RoPE (cos/sin [B or 1,S,>=128] or None) and guards (modeling_deepseekv2.py:336-348);
+    with head_cls the block summaries k_bar [B,nblk_cap,128] (:362-379).
+    idx_k_out / kbar_out: [B,>=S,128] / [B,>=nblk_cap,128] fp32 views to write into (rows
+    contiguous).  w_pack: router_front_pack(w_q, w_k), packed here when omitted.
+    Returns (idx_q or None, idx_k, kbar or None)."""
+    _need_gpu(hs, w_q, w_k, nq, nk)
+    lib = _lib.load()
+    B, S, hid = hs.shape
+    if not router_front_supported(hs, w_q, w_k, block_size if head_cls is not None else None):
+        raise NotImplementedError("dash_router_front: bf16 inputs, hidden % 64 == 0, block 32/64")
+    hs = _rows(hs)
+    w_q, w_k = w_q.contiguous(), w_k.contiguous()
+    if w_pack is None:
+        w_pack = router_front_pack(w_q, w_k)
+    wq = nq.float().contiguous()
+    wk = nk.float().contiguous()
+    dev = hs.device
+
+    def _out(t, rows):
+        if t is None:
+            return torch.empty(B, rows, 128, dtype=torch.float32, device=dev)
+        if t.shape[0] != B or t.shape[1] < rows or t.stride(2) != 1 or t.stride(1) != 128:
+            raise ValueError("output views need rows of 128 contiguous fp32")
+        return t
+
+    iq = torch.empty(B, S, 128, dtype=torch.float32, device=dev) if want_q else None
+    ik = _out(idx_k_out, S)
+    kb = None
+    bs = cap = 0
+    if head_cls is not None:
+        bs = int(block_size)
+        cap = int(nblk_cap) if nblk_cap is not None else (S + bs - 1) // bs
+        kb = _out(kbar_out, cap)
+        head_cls = head_cls.float().contiguous()
+    cs_bf16, cs_sb, cs_st = 0, 0, 0
+    if cos is not None:
+        if cos.shape[-1] < 128 or cos.shape[-2] != S or cos.shape[0] not in (1, B) \
+                or cos.shape != sin.shape:
+            raise ValueError("cos/sin must be [B or 1, S, >=128]")
+        dt = torch.bfloat16 if (cos.dtype == torch.bfloat16 and sin.dtype == torch.bfloat16) \
+            else torch.float32
+        cos, sin = cos[..., :128].to(dt), sin[..., :128].to(dt)
+        if cos.stride(-1) != 1 or cos.stride() != sin.stride():
+            cos, sin = cos.contiguous(), sin.contiguous()
+        cs_bf16 = int(dt == torch.bfloat16)
+        cs_sb = 0 if cos.shape[0] == 1 else cos.stride(0)
+        cs_st = cos.stride(1)
+    st_ = lib.dash_router_front(
+        _ptr(hs), hs.stride(0), hs.stride(1), B, S, hid, _ptr(w_pack), _ptr(w_q), _ptr(w_k),
+        _ptr(wq), _ptr(wk), float(eps), _ptr(cos), _ptr(sin), cs_bf16, cs_sb, cs_st,
+        _ptr(head_cls), bs, 1.0 / math.sqrt(128), _ptr(iq), 0 if iq is None else iq.stride(0),
+        _ptr(ik), ik.stride(0), _ptr(kb), 0 if kb is None else kb.stride(0), cap, _stream())
+    _lib.check(st_, "dash_router_front")
+    return iq, (ik if idx_k_out is None else ik[:, :S]), kb
+
 def route(z, cand, idx_scale, floor, sigma, K, topm, row_nblk=None, width=None):
     """Inference routing of every row of z [..., nblk] fp32.
     Returns (idx int32 [..., K'], bias fp32, valid bool) with K' = max(1, min(K, M'))."""

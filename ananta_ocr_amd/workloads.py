@@ -146,3 +146,29 @@ def paged_layout(cfg):
         table[b, :n] = perm[o:o + n].to(torch.int32)
         o += n
     return lengths.to(torch.int32), table
+
+
+# Router front end: the index projections of the checkpoint's shape (hidden 1280,
+# index dim 128, bf16), its block size 32 and stage 0 head_cls, over 27,300 tokens.
+FRONT_NAME = "router_front_s27300_h1280_bs32"
+FRONT_S, FRONT_HIDDEN, FRONT_BS = 27300, 1280, 32
+
+
+def make_front(S=FRONT_S, hidden=FRONT_HIDDEN, seed=8, device="cpu"):
+    """Synthetic router inputs: hidden states randn bf16 [1, S, hidden], q/k projection
+    weights randn/sqrt(hidden) bf16 [128, hidden], Gemma norm weights randn*0.1,
+    head_cls randn*0.5, and the 1-D RoPE (cos, sin) bf16 [1, S, 128] of positions 0..S-1
+    (theta 5e5, the config's sparse_rope_theta)."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    hs = torch.randn(1, S, hidden, generator=g).bfloat16()
+    wq = (torch.randn(D, hidden, generator=g) / math.sqrt(hidden)).bfloat16()
+    wk = (torch.randn(D, hidden, generator=g) / math.sqrt(hidden)).bfloat16()
+    nq = torch.randn(D, generator=g) * 0.1
+    nk = torch.randn(D, generator=g) * 0.1
+    hc = torch.randn(D, generator=g) * 0.5
+    inv = 1.0 / 5.0e5 ** (torch.arange(0, D, 2).float() / D)
+    ang = torch.arange(S).float()[:, None] * inv[None]
+    emb = torch.cat([ang, ang], -1)[None]
+    out = dict(hs=hs, wq=wq, wk=wk, nq=nq, nk=nk, hc=hc, cos=emb.cos().bfloat16(),
+               sin=emb.sin().bfloat16())
+    return {k: v.to(device) for k, v in out.items()}

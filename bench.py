@@ -15,6 +15,8 @@ product kernels and the CPU oracle timed on a bounded sample on this host:
   * training step at 27,300 tokens (training routing, attention forward and backward,
     routing backward; k = 16)
   * page-aware candidate masks of a 100-page OCR prompt (prefill rows, decode row)
+  * the fused router front end at 27,300 tokens, hidden 1,280, block 32 (index
+    projections, norms, RoPE, block summaries in one launch)
 
 HBM traffic and executed MFMA work per launch come from hardware-counter runs
 (rocprofv3 --pmc over ``bench.py --counter-probe WORKLOAD``), summarised by
@@ -564,6 +566,78 @@ def bench_pages(steps):
                          "bytes_per_launch": nbytes, "avg_launch_us": round(t_pre * 1e6, 2)}}
 
 
+FRONT_NAME = W.FRONT_NAME
+
+
+def front_bytes(S, hidden, bs):
+    """Algorithmic HBM bytes of one fused front-end call: hidden states and weights read,
+    bf16 cos/sin read, idx_q / idx_k and the block summaries written."""
+    nblk = (S + bs - 1) // bs
+    return S * hidden * 2 + 2 * W.D * hidden * 2 + 2 * S * W.D * 2 + 2 * S * W.D * 4 + \
+        nblk * W.D * 4
+
+
+def bench_front(steps):
+    """The fused router front end (projections, norms, RoPE, guards, block summaries in
+    one launch) against the unfused sequence it replaces (nan_to_num, one library GEMM
+    for both projections, the norm / RoPE kernel, the block-summary kernel)."""
+    d = W.make_front(device="cuda")
+    S, hid, bs = W.FRONT_S, W.FRONT_HIDDEN, W.FRONT_BS
+    wpack = ops.router_front_pack(d["wq"], d["wk"])
+    wcat = torch.cat([d["wq"], d["wk"]], 0)
+
+    def fused(i=0):
+        ops.router_front(d["hs"], d["wq"], d["wk"], d["nq"], d["nk"], 1e-6, d["cos"], d["sin"],
+                         head_cls=d["hc"], block_size=bs, w_pack=wpack)
+
+    def unfused(i=0):
+        h = torch.nan_to_num(d["hs"], nan=0.0, posinf=0.0, neginf=0.0)
+        proj = torch.nn.functional.linear(h, wcat)
+        iq, ik = ops.router_qk_norm(proj, d["nq"], d["nk"], 1e-6, d["cos"], d["sin"])
+        ops.kbar(ik, d["hc"], bs)
+
+    t = time_kernel(fused, max(steps, 10))
+    t_un = time_kernel(unfused, max(steps, 10))
+    nbytes = front_bytes(S, hid, bs)
+    gbs = nbytes / t / 1e9
+    flop = 2.0 * S * hid * 2 * W.D
+    return {"workload": FRONT_NAME, "value": round(t * 1e6, 2), "unit": "us per call",
+            "tokens": S, "hidden": hid, "block": bs,
+            "unfused_us": round(t_un * 1e6, 2),
+            "mfma_tflops": round(flop / t / 1e12, 1),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                         "kernel": "router_front_kernel", "bytes_per_launch": nbytes,
+                         "avg_launch_us": round(t * 1e6, 2)}}
+
+
+def front_entry(res, counters):
+    tr = counters.get((FRONT_NAME, "hbm_bytes"))
+    if tr is not None:
+        res["roofline"]["traffic"] = int(tr)
+    return res
+
+
+def cpu_front_baseline(rows=2048, reps=3):
+    """The oracle's router_qk (float64 projections rounded to bf16, then the norm and RoPE
+    of the reference in fp32/bf16) and k_bar pooling for the last `rows` tokens, scaled to
+    the whole sequence (the work is linear in the tokens)."""
+    from oracle import dash_oracle as O
+    d = W.make_front()
+    S, bs = W.FRONT_S, W.FRONT_BS
+    sl = slice(S - rows, S)
+
+    def run():
+        iq, ik = O.router_qk(d["hs"][:, sl], d["wq"], d["wk"], d["nq"], d["nk"], 1e-6,
+                             d["cos"][:, sl], d["sin"][:, sl])
+        O.kbar_headcls(ik, d["hc"], bs)
+
+    t = _median_time(run, reps) * S / rows
+    return _cpu_fields(round(t * 1e6, 1), "us per call",
+                       f"oracle router_qk + kbar_headcls on the last {rows} of {S} tokens, "
+                       f"scaled by {S / rows:.2f}; median of {reps} after 1 warm-up")
+
+
 # ------------------------------------------------------------------ CPU baselines
 
 def _median_time(run, reps):
@@ -707,8 +781,16 @@ def counter_probe(name):
     cfgs = {c.name: c for c in (W.PREFILL_2730, W.PREFILL_27300, W.PACKED_16DOC, W.DECODE_B8,
                                 W.PAGED_12L)}
     cfgs[TRAIN_NAME] = TRAIN_NAME
+    cfgs[FRONT_NAME] = FRONT_NAME
     cfg = cfgs[name]
-    if cfg == TRAIN_NAME:
+    if cfg == FRONT_NAME:
+        d = W.make_front(device=dev)
+        wpack = ops.router_front_pack(d["wq"], d["wk"])
+
+        def launch():
+            ops.router_front(d["hs"], d["wq"], d["wk"], d["nq"], d["nk"], 1e-6, d["cos"],
+                             d["sin"], head_cls=d["hc"], block_size=W.FRONT_BS, w_pack=wpack)
+    elif cfg == TRAIN_NAME:
         c27 = W.PREFILL_27300
         d = W.make_prefill(c27, device=dev)
         kb = ops.kbar(d["idx_k"], hc, c27.bs)
@@ -777,6 +859,7 @@ PROBE_KERNELS = {
     "prefill": ["prefill_clear_kernel", "prefill_plan_kernel", "prefill_scan_kernel",
                 "prefill_scatter_kernel", "prefill_sparse_kernel", "prefill_tile_kernel"],
     "decode": ["decode_route_window_kernel", "decode_routed_kernel", "decode_step_merge_kernel"],
+    "front": ["router_front_kernel"],
     "train": ["bwd_delta_kernel", "prefill_clear_kernel", "prefill_plan_kernel",
               "prefill_scan_kernel", "prefill_scatter_kernel", "bwd_kv_kernel", "bwd_q_kernel",
               "bwd_dbias_kernel"],
@@ -805,12 +888,13 @@ def summarize_counters(dirs):
             per[key] = per.get(key, 0.0) + float(r["Counter_Value"])
         counters = sorted({k[2] for k in per})
         names = [c.name for c in (W.PREFILL_2730, W.PREFILL_27300, W.PACKED_16DOC, W.DECODE_B8,
-                                  W.PAGED_12L)] + [TRAIN_NAME]
+                                  W.PAGED_12L)] + [TRAIN_NAME, FRONT_NAME]
         wl = next((nm for nm in names if nm in dr), None)
         if wl is None:
             log(f"{dr}: directory names no workload")
             continue
-        kind = "train" if wl == TRAIN_NAME else "decode" if "decode" in wl else "prefill"
+        kind = "train" if wl == TRAIN_NAME else "front" if wl == FRONT_NAME else \
+            "decode" if "decode" in wl else "prefill"
         disp = sorted({(k[0], k[1]) for k in per})
         copy = [x for x in disp if "copyBuffer" in x[1]
                 and per.get((x[0], x[1], counters[0]), 0.0) > 1024]
@@ -889,7 +973,7 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     only = set(filter(None, args.only.split(",")))
     todo = [c for c in ALL if not only or c.name in only]
-    if only and not todo and not ({PAGES_NAME, TRAIN_NAME} & only):
+    if only and not todo and not ({PAGES_NAME, TRAIN_NAME, FRONT_NAME} & only):
         sys.exit(f"bench.py: unknown workload(s) {sorted(only)}")
     counters, cnote = read_counters()
     res, entries = {}, {}
@@ -942,6 +1026,10 @@ def main():
             entries[PAGES_NAME]["cpu_baseline"] = _cpu_fields(
                 t * 1e6, "us per prefill", "oracle page ids and candidate rows of the same "
                 "100-page prompt in 2,048-query chunks; median of 3 after 1 warm-up")
+    if not only or FRONT_NAME in only:
+        entries[FRONT_NAME] = front_entry(bench_front(args.steps), counters)
+        if not args.no_cpu:
+            entries[FRONT_NAME]["cpu_baseline"] = cpu_front_baseline()
     head = entries.get(W.PREFILL_27300.name)
     if head is None:                      # a partial run: the first workload timed
         head = next(iter(entries.values()))

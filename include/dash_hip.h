@@ -100,6 +100,32 @@ int dash_router_qk_norm(const void* proj, int proj_bf16, int64_t proj_row, int64
                         float* idx_q, float* idx_k, void* stream);
 
 /*
+ * Fused router front end for bf16 hidden states, one launch: nan_to_num of the
+ * hidden states, the index q/k projections (w_q / w_k bf16 [128, hidden], and the same
+ * weights packed by dash_router_front_pack_weights into w_pack [256 * hidden]; fp32
+ * accumulation, rounded to bf16 as the bf16 linear layer), Gemma RMSNorm with
+ * (1 + weight), RoPE (cos/sin [.., S, >=128] bf16 or fp32, or none) and the finiteness
+ * guards -- replaces _router_qk (modeling_deepseekv2.py:336-348) with _RMSNorm.forward
+ * (dash_attention.py:680-700).  idx_q / idx_k fp32 [B, S, 128] (row stride 128, batch
+ * strides iq_sb / ik_sb) are written when non-null.  With head_cls (stage 0
+ * "head_cls", block_size 32 or 64) it also writes the block summaries kbar
+ * [B, nblk_cap, 128] (the pooling of _block_scores_infer, modeling_deepseekv2.py:
+ * 362-379) from the index keys still on chip.  hidden % 64 == 0; 16-byte aligned
+ * hidden rows and weights.
+ */
+int dash_router_front(const void* hs, int64_t hs_sb, int64_t hs_st, int B, int S, int hidden,
+                      const void* w_pack, const void* w_q, const void* w_k,
+                      const float* wq_norm, const float* wk_norm, float eps, const void* cos,
+                      const void* sin, int cs_bf16, int64_t cs_sb, int64_t cs_st,
+                      const float* head_cls, int block_size, float inv_sqrt_d, float* idx_q,
+                      int64_t iq_sb, float* idx_k, int64_t ik_sb, float* kbar, int64_t kb_sb,
+                      int nblk_cap, void* stream);
+/* The q_proj / k_proj weights (bf16 [128, hidden] each, row-major) in the operand order
+ * of dash_router_front: w_pack bf16 [256 * hidden]; repack when the weights change. */
+int dash_router_front_pack_weights(const void* w_q, const void* w_k, int hidden, void* w_pack,
+                                   void* stream);
+
+/*
  * Inference routing of every score row: candidates (remote, optionally AND cand,
  * falling back to remote), x = z*idx_scale, top-M by (value desc, block id asc),
  * 1.5-entmax prior over the M values, first K' = max(1,min(K,M)) slots, bias =

@@ -7,6 +7,8 @@ The shipped package (``ananta_ocr_amd``) never imports it and has no CPU path.
 It restates, op for op in fp32 on the CPU, the reference's PyTorch algorithm
 for the path (citations are ``file:line`` in the reference repository):
 
+* router front end (index projections, Gemma RMSNorm, RoPE, guards)
+                              -- modeling_deepseekv2.py:336-348, dash_attention.py:684-693
 * stage-0 block summaries ``k_bar`` (head_cls softmax pooling; mean pooling when
   ``head_cls == 0``)          -- dash_attention.py:851-888, modeling_deepseekv2.py:362-377
 * head_cls block scores       -- dash_attention.py:890-904, modeling_deepseekv2.py:378-386
@@ -32,6 +34,8 @@ selects with a *stable* descending sort, so ties go to the lower block id.  Test
 compare the oracle with ``torch.topk`` as sets wherever ties straddle the cut.
 
 Parity pinning (what each function is checked against, in tests/):
+  router_qk        -> torch's rms_norm (in-range rows), closed forms (constant rows,
+                      cos = 1 / sin = 0 identity, cos = 0 / sin = 1 rotate_half), guards
   kbar/scores      -> brute-force float64 loops, closed form (mean pooling)
   entmax15         -> closed forms, invariants, independent float64 bisection
   route            -> brute-force stable ranking, torch.topk as sets
@@ -57,6 +61,46 @@ MASK_NEG = -1.0e9      # dash_attention.py:601
 ACT_CLAMP = 1.0e4      # dash_attention.py:604
 GRAD_CLAMP = 1.0e4     # dash_attention.py:603
 ENTMAX_NEG = -1.0e4    # modeling_deepseekv2.py:56
+
+
+# ----------------------------------------------------------------------------
+# router front end: index q/k projections, Gemma RMSNorm, RoPE
+# ----------------------------------------------------------------------------
+
+def gemma_rmsnorm(x, weight, eps):
+    """_RMSNorm.forward (dash_attention.py:684-693): fp32 with nan_to_num, x*rsqrt(mean
+    x^2 + eps), clamp, scale by (1 + weight), clamp, back to the input dtype."""
+    x32 = torch.nan_to_num(x.float(), nan=0.0, posinf=0.0, neginf=0.0)
+    x32 = x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + eps)
+    x32 = x32.clamp(-ACT_CLAMP, ACT_CLAMP)
+    return (x32 * (1.0 + weight.float())).clamp(-ACT_CLAMP, ACT_CLAMP).to(x.dtype)
+
+
+def rotate_half_rope(x, cos, sin):
+    """q * cos + rotate_half(q) * sin (the llama apply_rotary_pos_emb the router calls,
+    modeling_deepseekv2.py:345), each op in torch's promoted dtype; cos/sin broadcast
+    over x's leading dims."""
+    x1, x2 = x.chunk(2, dim=-1)
+    return x * cos + torch.cat((-x2, x1), dim=-1) * sin
+
+
+def router_qk(hidden_states, w_q, w_k, norm_q, norm_k, eps, cos=None, sin=None):
+    """_router_qk (modeling_deepseekv2.py:336-348): idx_q, idx_k fp32 [B,S,d].
+
+    The projections are the exact products (float64) rounded once to the hidden
+    states' dtype, which is what a linear layer in that dtype returns up to its
+    accumulation order.  cos/sin [B or 1, S, >= d]."""
+    hs = torch.nan_to_num(hidden_states, nan=0.0, posinf=0.0, neginf=0.0)
+    d = w_q.shape[0]
+    out = []
+    for w, nw in ((w_q, norm_q), (w_k, norm_k)):
+        p = (hs.double() @ w.double().t()).to(hs.dtype)
+        y = gemma_rmsnorm(p, nw, eps)
+        if cos is not None:
+            # torch type promotion: bf16 rows with fp32 cos/sin rotate in fp32
+            y = rotate_half_rope(y, cos[..., :d], sin[..., :d])
+        out.append(torch.nan_to_num(y.float(), nan=0.0, posinf=0.0, neginf=0.0))
+    return out[0], out[1]
 
 
 # ----------------------------------------------------------------------------

@@ -209,6 +209,57 @@ def test_sanitize_grad_bounds_and_zeroes_nonfinite():
     assert O.sanitize_grad(g).tolist() == [0.0, 0.0, 0.0, 1e4, -1e4, 7.0]
 
 
+# ---------------------------------------------------------------- router front end
+
+def test_gemma_rmsnorm_is_rms_norm_with_one_plus_weight():
+    x = torch.randn(5, 9, 128, generator=_rng(30)) * 3
+    w = torch.randn(128, generator=_rng(31)) * 0.3
+    ref = F.rms_norm(x.double(), (128,), weight=1.0 + w.double(), eps=1e-6)
+    torch.testing.assert_close(O.gemma_rmsnorm(x, w, 1e-6).double(), ref, atol=2e-6, rtol=2e-6)
+
+
+def test_gemma_rmsnorm_constant_rows_clamps_and_guards():
+    w = torch.linspace(-0.5, 0.5, 128)
+    x = torch.full((3, 128), 2.5)
+    x[1] = -7.0
+    x[2, :] = float("nan")                                  # nan -> 0 -> the zero row
+    y = O.gemma_rmsnorm(x, w, 1e-6)                          # c / sqrt(c^2 + eps) = 1 - O(1e-7)
+    torch.testing.assert_close(y[0], 1.0 + w, atol=1e-6, rtol=0)
+    torch.testing.assert_close(y[1], -(1.0 + w), atol=1e-6, rtol=0)
+    assert (y[2] == 0).all()
+    big = torch.zeros(1, 128)
+    big[0, 0] = 1.0                                          # one hot: sqrt(128) before clamp
+    y = O.gemma_rmsnorm(big, torch.full((128,), 1e4), 1e-6)  # (1 + w) * sqrt(128) > 1e4
+    assert y[0, 0].item() == 1e4 and (y[0, 1:] == 0).all()
+
+
+def test_rope_identity_and_rotate_half():
+    x = torch.randn(2, 7, 128, generator=_rng(32))
+    one, zero = torch.ones(1, 7, 128), torch.zeros(1, 7, 128)
+    assert torch.equal(O.rotate_half_rope(x, one, zero), x)
+    rot = O.rotate_half_rope(x, zero, one)
+    assert torch.equal(rot[..., :64], -x[..., 64:]) and torch.equal(rot[..., 64:], x[..., :64])
+
+
+def test_router_qk_projection_and_guards():
+    g = _rng(33)
+    hs = torch.randn(2, 11, 256, generator=g)
+    hs[0, 3, 5] = float("inf")                              # nan_to_num before the projection
+    wq, wk = torch.randn(128, 256, generator=g) * 0.1, torch.randn(128, 256, generator=g) * 0.1
+    nq, nk = torch.randn(128, generator=g) * 0.2, torch.randn(128, generator=g) * 0.2
+    ang = torch.arange(11)[:, None] * (1e4 ** (-torch.arange(0, 128, 2) / 128))[None]
+    emb = torch.cat([ang, ang], -1)[None]
+    iq, ik = O.router_qk(hs, wq, wk, nq, nk, 1e-6, emb.cos(), emb.sin())
+    clean = torch.nan_to_num(hs, posinf=0.0)
+    for got, w, nw in ((iq, wq, nq), (ik, wk, nk)):
+        p = (clean.double() @ w.double().t())
+        y = F.rms_norm(p, (128,), weight=1.0 + nw.double(), eps=1e-6)
+        y1, y2 = y[..., :64], y[..., 64:]
+        ref = torch.cat([y1 * emb.cos()[..., :64] - y2 * emb.sin()[..., :64],
+                         y2 * emb.cos()[..., 64:] + y1 * emb.sin()[..., 64:]], -1)
+        torch.testing.assert_close(got.double(), ref, atol=1e-5, rtol=1e-5)
+
+
 # ---------------------------------------------------------------- stage 0
 
 def test_kbar_zero_headcls_is_block_mean():
