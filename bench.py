@@ -596,6 +596,10 @@ def bench_front(steps):
         iq, ik = ops.router_qk_norm(proj, d["nq"], d["nk"], 1e-6, d["cos"], d["sin"])
         ops.kbar(ik, d["hc"], bs)
 
+    for _ in range(3):                    # first calls (library GEMM set-up) off the clock
+        fused()
+        unfused()
+    torch.cuda.synchronize()
     t = time_kernel(fused, max(steps, 10))
     t_un = time_kernel(unfused, max(steps, 10))
     nbytes = front_bytes(S, hid, bs)
