@@ -7,7 +7,7 @@
 // One work-group of four wavefronts per 64 token rows of one sequence.  Wavefront
 // w computes side w / 2 (0: q, 1: k) for index dims 32 (w % 2) + [0, 32) and
 // 64 + 32 (w % 2) + [0, 32): the two halves that RoPE's rotate_half pairs, so the
-// rotation needs no exchange.  The hidden states stream through a three-stage LDS
+// rotation needs no exchange.  The hidden states stream through a four-stage LDS
 // ring filled by direct loads; the weights come pre-packed in the MFMA operand
 // order, so that every weight load of a wavefront is one contiguous 1 KB read.  The
 // projection stays in the MFMA accumulators through the norm, RoPE and k_bar
@@ -105,16 +105,33 @@ __device__ __forceinline__ int fr_aslot(int r, int p) { return r * 8 + (p ^ ((r 
 template <int N>
 __device__ __forceinline__ void fr_wait_vm() {
   // vmcnt(N): this wavefront has at most N vector-memory operations outstanding
-  static_assert(N >= 0 && N < 16, "vmcnt field");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xf << 8));
+  // (vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt left at their maxima)
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// Waits until at most n vector-memory operations are outstanding, for the counts
+// the projection loop can produce (each one an immediate).
+__device__ __forceinline__ void fr_wait_vm_n(int n) {
+  switch (n) {
+    case 0: fr_wait_vm<0>(); break;
+    case 2: fr_wait_vm<2>(); break;
+    case 4: fr_wait_vm<4>(); break;
+    case 8: fr_wait_vm<8>(); break;
+    case 10: fr_wait_vm<10>(); break;
+    case 12: fr_wait_vm<12>(); break;
+    case 16: fr_wait_vm<16>(); break;
+    case 18: fr_wait_vm<18>(); break;
+    default: fr_wait_vm<20>(); break;
+  }
 }
 
 __global__ __launch_bounds__(256, 2) void router_front_kernel(FrontArgs a) {
 #pragma clang fp contract(off)
   __shared__ FrontSmem sm;
-  // the hidden-state ring: three stages, each its own LDS object, so that reads of
+  // the hidden-state ring: four stages, each its own LDS object, so that reads of
   // one stage do not wait for the direct loads into another
-  __shared__ uint4 sH0[kFrStage], sH1[kFrStage], sH2[kFrStage];
+  __shared__ uint4 sH0[kFrStage], sH1[kFrStage], sH2[kFrStage], sH3[kFrStage];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int side = wv >> 1, part = wv & 1;
   const int m32 = lane & 31, half = lane >> 5;
@@ -160,7 +177,7 @@ __global__ __launch_bounds__(256, 2) void router_front_kernel(FrontArgs a) {
                                        (__attribute__((address_space(3))) void*)(stage + u * 256 + wv * 64),
                                        16, 0, 0);
   };
-  uint4 wA[4][2], wB[4][2];
+  uint4 wA[4][2], wB[4][2], wC[4][2];
   auto load_w = [&](uint4 (&dst)[4][2], int c) {
     const bf16* src = wp + (int64_t)c * 4 * 8 * 512;
 #pragma unroll
@@ -189,37 +206,51 @@ __global__ __launch_bounds__(256, 2) void router_front_kernel(FrontArgs a) {
       acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc[1][1], 0, 0, 0);
     }
   };
+  // Vector-memory operations of this wavefront issued after the stage of chunk c:
+  // the prologue issues W(0), W(1) (8 each), then the stages of chunks 0, 1, 2 (2
+  // each); step k issues W(k+2) and then the stage of chunk k+3, when they exist.
+  auto ops_after_stage = [&](int c) {
+    int n = 0;
+    if (c <= 2)
+      n += 2 * max(0, min(2, nch - 1) - c);
+    for (int k = max(0, c - 2); k < c; ++k) n += (k + 2 < nch ? 8 : 0) + (k + 3 < nch ? 2 : 0);
+    return n;
+  };
   // Step c: chunk c's stage has landed (each wavefront waits for its own direct
-  // loads, then the barrier), the weights of chunk c+1 and the stage of chunk c+2
-  // are requested, chunk c is multiplied.  Queue order per step: weights (8), then
-  // the stage (2), so chunk c's stage is followed by 8 + 2 operations when c+1 < nch.
+  // loads, then the barrier), the weights of chunk c+2 and the stage of chunk c+3
+  // are requested, chunk c is multiplied.
   auto step = [&](int c, auto hs_tag, auto w_tag) {
     constexpr int HS = decltype(hs_tag)::value, WS = decltype(w_tag)::value;
-    uint4* const cur = HS == 0 ? sH0 : (HS == 1 ? sH1 : sH2);
-    uint4* const nxt = HS == 0 ? sH2 : (HS == 1 ? sH0 : sH1);     // stage of chunk c+2
-    if (c == 0) {
-      if (nch > 1) fr_wait_vm<2>(); else fr_wait_vm<0>();
-    } else {
-      if (c + 1 < nch) fr_wait_vm<10>(); else fr_wait_vm<8>();
-    }
+    uint4* const cur = HS == 0 ? sH0 : (HS == 1 ? sH1 : (HS == 2 ? sH2 : sH3));
+    uint4* const nxt = HS == 0 ? sH3 : (HS == 1 ? sH0 : (HS == 2 ? sH1 : sH2));   // chunk c+3
+    fr_wait_vm_n(ops_after_stage(c));
     __syncthreads();
-    if (c + 1 < nch) load_w(WS == 0 ? wB : wA, c + 1);
-    if (c + 2 < nch) dma_h(nxt, c + 2);
-    compute(WS == 0 ? wA : wB, cur);
+    if (c + 2 < nch) load_w(WS == 0 ? wC : (WS == 1 ? wA : wB), c + 2);
+    if (c + 3 < nch) dma_h(nxt, c + 3);
+    compute(WS == 0 ? wA : (WS == 1 ? wB : wC), cur);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
   load_w(wA, 0);
+  if (nch > 1) load_w(wB, 1);
   dma_h(sH0, 0);
   if (nch > 1) dma_h(sH1, 1);
-  for (int c = 0; c < nch; c += 6) {
+  if (nch > 2) dma_h(sH2, 2);
+  for (int c = 0; c < nch; c += 12) {
     step(c, I0{}, I0{});
     if (c + 1 < nch) step(c + 1, I1{}, I1{});
-    if (c + 2 < nch) step(c + 2, I2{}, I0{});
-    if (c + 3 < nch) step(c + 3, I0{}, I1{});
-    if (c + 4 < nch) step(c + 4, I1{}, I0{});
-    if (c + 5 < nch) step(c + 5, I2{}, I1{});
+    if (c + 2 < nch) step(c + 2, I2{}, I2{});
+    if (c + 3 < nch) step(c + 3, I3{}, I0{});
+    if (c + 4 < nch) step(c + 4, I0{}, I1{});
+    if (c + 5 < nch) step(c + 5, I1{}, I2{});
+    if (c + 6 < nch) step(c + 6, I2{}, I0{});
+    if (c + 7 < nch) step(c + 7, I3{}, I1{});
+    if (c + 8 < nch) step(c + 8, I0{}, I2{});
+    if (c + 9 < nch) step(c + 9, I1{}, I0{});
+    if (c + 10 < nch) step(c + 10, I2{}, I1{});
+    if (c + 11 < nch) step(c + 11, I3{}, I2{});
   }
 
   // ---------------------------------------------------------------- non-finite rows
