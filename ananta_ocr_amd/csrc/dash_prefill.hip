@@ -1494,6 +1494,8 @@ extern "C" int dash_attn_prefill_backward(
                              dv_sb, dv_sh, dv_st};
   for (int64_t s : strides)
     if (s % 8 != 0) return kErrUnsupported;
+  // the key-major kernel forms the row offsets of Q and dO as 32 x 32-bit products
+  if (q_st < 0 || q_st > INT32_MAX || do_st < 0 || do_st > INT32_MAX) return kErrUnsupported;
   const void* ptrs[] = {q, k, v, o, dout, dq, dk, dv};
   for (const void* ptr : ptrs)
     if ((uintptr_t)ptr % 16 != 0) return kErrUnsupported;
