@@ -411,6 +411,21 @@ def cached_workspace(key, nbytes, device):
     return buf
 
 
+def release_workspaces(device=None):
+    """Drops the cached workspaces (of one device, or of every device) so that their
+    memory returns to torch's allocator; the next call that needs one allocates it
+    again.  Safe between calls on one stream (torch hands freed memory out again in
+    stream order); with work that used a workspace still running on another stream,
+    synchronise first."""
+    for k in [k for k in _WORKSPACES if device is None or k[1] == str(torch.device(device))]:
+        del _WORKSPACES[k]
+
+
+def cached_workspace_bytes():
+    """Total bytes of the cached workspaces."""
+    return sum(b.numel() for b in _WORKSPACES.values())
+
+
 def attn_prefill(q, k, v, idx, bias, valid, block_size, local_window, scale,
                  cu_seqlens=None, kmin=None, return_lse=False, dense_threshold=None,
                  max_seqlen=None):

@@ -41,3 +41,17 @@ def test_library_loads_and_exports_every_symbol():
         assert hasattr(lib, name), name
     assert lib.dash_abi_version() == 1
     assert lib.dash_status_string(-2) == b"unsupported shape or parameter"
+
+
+def test_cached_workspace_grows_and_is_released():
+    """The host-side workspace cache: reused when large enough, replaced by a larger
+    buffer, and dropped by release_workspaces (host memory here; the same code path
+    serves device buffers)."""
+    from ananta_ocr_amd import ops
+    ops.release_workspaces()
+    a = ops.cached_workspace("t", 1000, "cpu")
+    assert a.numel() >= 1000 and ops.cached_workspace("t", 500, "cpu") is a
+    b = ops.cached_workspace("t", 10 * a.numel(), "cpu")
+    assert b.numel() >= 10 * a.numel() and ops.cached_workspace_bytes() == b.numel()
+    ops.release_workspaces("cpu")
+    assert ops.cached_workspace_bytes() == 0
