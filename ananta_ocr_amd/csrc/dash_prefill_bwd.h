@@ -16,9 +16,10 @@
 //     stage's K and V stay in LDS while 64 queries at a time stream through it --
 //     first the window band (every query whose window reaches the stage), then
 //     the routed pairs of the stage's blocks, gathered.  Per 32-query chunk and
-//     32-key half (one wavefront): S = Q K^T and dP = dO V^T on the matrix cores
-//     (lane = key), P and dS in registers, dV^T += dO^T P and dK^T += Q^T dS with
-//     the transposed operands read by ds_read_tr16_b64 from the staged rows.  dK
+//     32-key half, two wavefronts (one per half of the head dims): S = Q K^T in
+//     one, dP = dO V^T in the other, on the matrix cores (lane = key), exchanged
+//     through LDS so that both hold P and dS; each adds its dims of dV^T += dO^T P
+//     and dK^T += Q^T dS, the transposed operands read by ds_read_tr16_b64.  dK
 //     and dV are complete when the work-group ends (no atomics).  For routed
 //     pairs it also writes dQ^T = K^T dS^T (dS through LDS, read transposed) and
 //     the row sums of dS as fp32 partials per (head, pair).  The steps are
@@ -159,23 +160,6 @@ __device__ __forceinline__ void stage_rows(bf16* sX, int wv, int lane, RowPtr ro
   }
 }
 
-// Loads the query rows of a 64-row step into a k_slot-swizzled stage: wavefront
-// wv, lane l fills slot l % 16 of rows 16 u + r0 (r0 = 4 wv + l / 16, u < 4) from
-// the row numbers rw (component u for row 16 u + r0) -- stage_rows with the four row
-// numbers of a lane read at once.  Row numbers are >= 0 and the row stride is below
-// 2^32 elements (one 32 x 32 -> 64-bit multiply per row).
-__device__ __forceinline__ void stage_rows4(bf16* sX, int wv, int lane, const bf16* xb, int64_t x_st,
-                                            int4 rw) {
-  const int r0 = 4 * wv + (lane >> 4), slot = lane & 15;
-  const int rr[4] = {rw.x, rw.y, rw.z, rw.w};
-#pragma unroll
-  for (int u = 0; u < 4; ++u)
-    __builtin_amdgcn_global_load_lds((const void*)(xb + (uint64_t)(uint32_t)rr[u] * (uint32_t)x_st +
-                                                   (slot ^ (r0 & 15)) * 8),
-                                     (__attribute__((address_space(3))) void*)(sX + (4 * u + wv) * 4 * 128),
-                                     16, 0, 0);
-}
-
 // Lane byte offsets of tr_frag_k's reads for row base qbase (a multiple of 16): the
 // reads of k-step ks (rows qbase + 16 ks ..), dim tile dt are at 4096 ks + (lo ^ 64 dt)
 // and 4096 ks + (hi ^ 64 dt) of the stage (the row's swizzle is the same for every
@@ -225,26 +209,66 @@ struct KvMetaLoad {
   int km;
 };
 
-__global__ __launch_bounds__(256, 1) void bwd_kv_kernel(BwdArgs a) {
+// Loads rows of a 64-row, k_slot-swizzled stage by 8 wavefronts: wavefront wv,
+// lane l fills slot l % 16 of rows 32 u + r0 (r0 = 4 wv + l / 16, u < 2) from the
+// row pointer rowp(r).
+template <typename RowPtr>
+__device__ __forceinline__ void stage_rows8(bf16* sX, int wv, int lane, RowPtr rowp) {
+  const int r0 = 4 * wv + (lane >> 4), slot = lane & 15;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int r = 32 * u + r0;
+    __builtin_amdgcn_global_load_lds((const void*)(rowp(r) + (slot ^ (r0 & 15)) * 8),
+                                     (__attribute__((address_space(3))) void*)(sX + (32 * u + 4 * wv) * 128),
+                                     16, 0, 0);
+  }
+}
+// The same with the lane's two row numbers given (rw.x: row r0, rw.y: row 32 + r0);
+// row numbers are >= 0 and the row stride is below 2^32 elements.
+__device__ __forceinline__ void stage_rows8r(bf16* sX, int wv, int lane, const bf16* xb, int64_t x_st,
+                                             int2 rw) {
+  const int r0 = 4 * wv + (lane >> 4), slot = lane & 15;
+  const int rr[2] = {rw.x, rw.y};
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+    __builtin_amdgcn_global_load_lds((const void*)(xb + (uint64_t)(uint32_t)rr[u] * (uint32_t)x_st +
+                                                   (slot ^ (r0 & 15)) * 8),
+                                     (__attribute__((address_space(3))) void*)(sX + (32 * u + 4 * wv) * 128),
+                                     16, 0, 0);
+}
+
+// Key-major kernel, eight wavefronts: wavefront (kh, qc, dh) = (wv % 2, wv / 2 % 2,
+// wv / 4) owns keys 32 kh .. + 31 of the stage, queries 32 qc .. + 31 of a step and
+// head dims 64 dh .. + 63 of dK and dV, so that two wavefronts fit on a SIMD.  Per
+// step the dh = 0 wavefront of a (kh, qc) pair computes S and P, the dh = 1 one dP;
+// they exchange P and dP (fp32) through LDS and both form dS; each then adds its
+// dims' share of dV^T += dO^T P and dK^T += Q^T dS.  Routed steps: dQ^T = K^T dS^T
+// for the step's 64 queries x 128 dims, one 32 x 32 tile per wavefront (dims
+// 32 (2 dh + kh) ..), and the bias-gradient row sums.
+// Software pipeline over the steps: step s computes on the query rows in buffer
+// s % 2 with the per-query values in sM[s % 2]; meanwhile the rows of step s + 1
+// load into the other buffer (row numbers from sRow[(s + 1) % 2]), and wavefront 0
+// loads the values of step s + 1 and the pair ids of step s + 2, which it stores
+// after the products (sM[(s + 1) % 2], sRow[s % 2]).  A routed step's dQ^T partials
+// wait in LDS and are stored at the start of the next step, so that the wait that
+// ends a step does not wait for stores just issued.  One wait and one barrier end
+// each step.
+__global__ __launch_bounds__(512, 1) void bwd_kv_kernel(BwdArgs a) {
   constexpr int D = 128;
-  // The stage's K and V, and two buffers of query rows (Q and dO), each a
-  // separately named array so that the reads of one never wait for the loads into
-  // another; the end of the kernel reuses the four query-row buffers to add the
-  // two query groups' dK and dV.
   __shared__ __attribute__((aligned(16))) bf16 sK[kBwIT * D];
   __shared__ __attribute__((aligned(16))) bf16 sV[kBwIT * D];
   __shared__ __attribute__((aligned(16))) bf16 sQ0[kBwIT * D];
   __shared__ __attribute__((aligned(16))) bf16 sQ1[kBwIT * D];
   __shared__ __attribute__((aligned(16))) bf16 sO0[kBwIT * D];   // dO rows
   __shared__ __attribute__((aligned(16))) bf16 sO1[kBwIT * D];
-  // dS [key][query] per query group, rows of 32 queries padded to 72 bytes
-  __shared__ __attribute__((aligned(16))) bf16 sDS[2][kBwIT][36];
+  __shared__ __attribute__((aligned(16))) bf16 sDS[2][kBwIT][36];  // dS [qc][key][query]
   __shared__ __attribute__((aligned(16))) KvMeta sM[2];
-  // row numbers of a step for the loads: query slot q at [q % 16][q / 16], so that
-  // a lane reads the four rows it loads at once
-  __shared__ __attribute__((aligned(16))) int sRow[2][16][4];
+  // row numbers of a step for the loads: query slot q at [q % 32][q / 32]
+  __shared__ __attribute__((aligned(16))) int sRow[2][32][2];
   __shared__ float sDb[2][kBwIT];
-  __shared__ __attribute__((aligned(16))) float sSt[4][32 * 64];   // dQ^T staging per wavefront
+  // per wavefront 4 KB: the P / dP exchange inside a step, and the dQ^T staging of
+  // a routed step until the start of the next
+  __shared__ __attribute__((aligned(16))) float sX[8][1024];
 
   const PrefillArgs& p = a.p;
   const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
@@ -252,12 +276,10 @@ __global__ __launch_bounds__(256, 1) void bwd_kv_kernel(BwdArgs a) {
   const int h = bh % p.H, b = bh / p.H;
   const int len = seq_len(p, b);
   const int j0 = stage * kBwIT;
-  // stages past the sequence exit, except those of a block that starts inside it
-  // (blocks of more than 64 keys): they write that block's zero partials
   if (j0 / p.bs * p.bs >= len) return;
-  const int sub = (j0 % p.bs) / kBwIT;     // this stage within its block (0 for blocks <= 64)
+  const int sub = (j0 % p.bs) / kBwIT;
   const int tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
-  const int kh = wv & 1, qc = wv >> 1, hl = lane >> 5, n = lane & 31;
+  const int kh = wv & 1, qc = (wv >> 1) & 1, dh = wv >> 2, hl = lane >> 5, n = lane & 31;
   const int64_t r0 = row0(p, b);
   const float c2 = a.scale * 1.4426950408889634f;
   const float log2e = 1.4426950408889634f;
@@ -266,12 +288,9 @@ __global__ __launch_bounds__(256, 1) void bwd_kv_kernel(BwdArgs a) {
   const bf16* vb = seq_base(p.v, p.cu, b, p.v_sb, p.v_st) + (int64_t)h * p.v_sh;
   const bf16* qb = seq_base(p.q, p.cu, b, p.q_sb, p.q_st) + (int64_t)h * p.q_sh;
   const bf16* ob = seq_base(a.dout, p.cu, b, a.do_sb, a.do_st) + (int64_t)h * a.do_sh;
-  stage_rows(sK, wv, lane, [&](int r) { return kb + (int64_t)min(j0 + r, len - 1) * p.k_st; });
-  stage_rows(sV, wv, lane, [&](int r) { return vb + (int64_t)min(j0 + r, len - 1) * p.v_st; });
+  stage_rows8(sK, wv, lane, [&](int r) { return kb + (int64_t)min(j0 + r, len - 1) * p.k_st; });
+  stage_rows8(sV, wv, lane, [&](int r) { return vb + (int64_t)min(j0 + r, len - 1) * p.v_st; });
 
-  // The steps: the window band (queries j0 + 64 w .. + 63 up to t_end, every
-  // query whose window reaches the stage), then the routed pairs of the stage's
-  // blocks (one, or two for 32-key blocks), 64 at a time.
   const int LW = p.lw, bs = p.bs;
   const int t_end = min(j0 + kBwIT - 1 + LW - 1, len - 1);
   const int n_win = t_end >= j0 ? (t_end - j0) / kBwIT + 1 : 0;
@@ -289,8 +308,6 @@ __global__ __launch_bounds__(256, 1) void bwd_kv_kernel(BwdArgs a) {
   const int rs0 = (np0 + kBwIT - 1) / kBwIT;
   const int n_steps = n_win + rs0 + (np1 + kBwIT - 1) / kBwIT;
 
-  // Query slot tid (< 64) of step u.  Routed steps: the pair id from the chunk
-  // records (-1: no pair), loaded first; then the row's values.
   auto pair_of = [&](int u) -> int {
     const int v = u - n_win;
     const bool second = v >= rs0;
@@ -339,66 +356,57 @@ __global__ __launch_bounds__(256, 1) void bwd_kv_kernel(BwdArgs a) {
     M.pos[tid] = m.ok ? m.pos : -1;
   };
 
-  floatx16 acc_dk[4], acc_dv[4];
+  floatx16 acc_dk[2], acc_dv[2];           // dims 64 dh + 32 t ..
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) { acc_dk[dt][r] = 0.f; acc_dv[dt][r] = 0.f; }
+    for (int r = 0; r < 16; ++r) { acc_dk[t][r] = 0.f; acc_dv[t][r] = 0.f; }
 
-  const uint32_t kl0 = k_lane_off(n, hl);  // k_frag_at offsets (rows 32 qc + n, 32 kh + n)
+  const uint32_t kl0 = k_lane_off(n, hl);
   const TrOff tq0 = tr_lane_off(32 * qc, lane), tk0 = tr_lane_off(0, lane);
-  const int key = j0 + 32 * kh + n;        // this lane's key
-  const int kst = 32 * kh;                 // this wavefront's keys in the stage
-  const int qst = 32 * qc;                 // this wavefront's queries in the step
+  const int key = j0 + 32 * kh + n;
+  const int kst = 32 * kh, qst = 32 * qc;
+  const int dtq = 2 * dh + kh;             // this wavefront's dQ dim tile
+  float* const xs = sX[wv];                // own exchange / staging area
+  const float* const xp = sX[wv ^ 4];      // the partner's (other dim half)
 
-  // Software pipeline over the steps.  Step s computes on the query rows in
-  // buffer s % 2 with the values in sM[s % 2]; meanwhile it loads the rows of step
-  // s + 1 into the other buffer (their row numbers are in sRow[(s + 1) % 2]), and
-  // wavefront 0 loads the values of step s + 1 and the pair ids of step s + 2,
-  // which it stores after the products (sM[(s + 1) % 2], sRow[s % 2]).  One wait
-  // and one barrier end each step.
-  int pid_next = -1;                       // pair id of step s + 1 (query slot tid)
+  int pid_next = -1;
   if (n_steps > 0) {
     if (wv == 0) {
       const int pid0 = n_win > 0 ? -1 : pair_of(0);
       pid_next = n_steps > 1 && n_win <= 1 ? pair_of(1) : -1;
       meta_store(0, meta_load(0, pid0), sM[0]);
-      sRow[0][tid & 15][tid >> 4] = row_of(0, pid0);
-      if (n_steps > 1) sRow[1][tid & 15][tid >> 4] = row_of(1, pid_next);
+      sRow[0][tid & 31][tid >> 5] = row_of(0, pid0);
+      if (n_steps > 1) sRow[1][tid & 31][tid >> 5] = row_of(1, pid_next);
     }
     __syncthreads();
-    const int4 rw = *(const int4*)&sRow[0][4 * wv + (lane >> 4)][0];
-    stage_rows4(sQ0, wv, lane, qb, p.q_st, rw);
-    stage_rows4(sO0, wv, lane, ob, a.do_st, rw);
+    const int2 rw = *(const int2*)&sRow[0][4 * wv + (lane >> 4)][0];
+    stage_rows8r(sQ0, wv, lane, qb, p.q_st, rw);
+    stage_rows8r(sO0, wv, lane, ob, a.do_st, rw);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  // dQ^T and bias-gradient partials of a routed step, stored at the start of the
-  // next step, so that the wait that ends a step does not wait for stores just
-  // issued.  The wavefront's dQ^T tiles (its 32 queries x dims 64 kh .. + 63) wait
-  // in its LDS staging area, query row r at 64 floats with 16-byte chunk c in slot
-  // c ^ (r % 16); the store writes each pair's 256 bytes whole (16 lanes per row).
+  // dQ^T partials of a routed step wait in the wavefront's area (query row r at 32
+  // floats, 16-byte chunk c in slot c ^ (r % 8)) and are stored at the start of the
+  // next step, 8 lanes per 128-byte row piece.
   bool pend = false;
-  int64_t pend_pi = -1;                    // bias-gradient partial of query column n
+  int64_t pend_pi = -1;
   float pend_db = 0.f;
   auto store_pending = [&](int par) {
     if (pend) {
-      const int rb = 8 * (lane >> 4), c = lane & 15;   // rows rb .. rb + 7, chunk c
-      const int4 pa = *(const int4*)&sM[par].pos[qst + rb];
-      const int4 pb = *(const int4*)&sM[par].pos[qst + rb + 4];
-      const int pos8[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
-      const float* st = sSt[wv];
+      const int c = lane & 7;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int r = rb + i;
-        const float4 v = *(const float4*)(st + r * 64 + ((c ^ (r & 15)) << 2));
-        if (pos8[i] >= 0) {
-          const int64_t pi = ((int64_t)h * p.ppos + pos8[i]) * a.nsub + sub;
-          *(float4*)(a.part_dq + pi * D + 64 * kh + 4 * c) = v;
+      for (int i = 0; i < 4; ++i) {
+        const int r = 8 * i + (lane >> 3);
+        const int pos = sM[par].pos[qst + r];
+        const float4 v = *(const float4*)(xs + r * 32 + ((c ^ (r & 7)) << 2));
+        if (pos >= 0) {
+          const int64_t pi = ((int64_t)h * p.ppos + pos) * a.nsub + sub;
+          *(float4*)(a.part_dq + pi * D + 32 * dtq + 4 * c) = v;
         }
       }
-      if (kh == 0 && hl == 0 && pend_pi >= 0) a.part_db[pend_pi] = pend_db;
+      if (kh == 0 && dh == 0 && hl == 0 && pend_pi >= 0) a.part_db[pend_pi] = pend_db;
     }
     pend = false;
   };
@@ -413,12 +421,10 @@ __global__ __launch_bounds__(256, 1) void bwd_kv_kernel(BwdArgs a) {
     const bool routed = s >= n_win;
     store_pending(P ^ 1);
     if (s + 1 < n_steps) {
-      const int4 rw = *(const int4*)&sRow[P ^ 1][4 * wv + (lane >> 4)][0];
-      stage_rows4(sQn, wv, lane, qb, p.q_st, rw);
-      stage_rows4(sOn, wv, lane, ob, a.do_st, rw);
+      const int2 rw = *(const int2*)&sRow[P ^ 1][4 * wv + (lane >> 4)][0];
+      stage_rows8r(sQn, wv, lane, qb, p.q_st, rw);
+      stage_rows8r(sOn, wv, lane, ob, a.do_st, rw);
     }
-    // Lane offsets pass through an empty asm each step, so that the compiler
-    // derives the per-read LDS addresses here instead of keeping them all live.
     uint32_t kl = kl0;
     TrOff tq = tq0, tk = tk0;
     asm volatile("" : "+v"(kl), "+v"(tq.lo), "+v"(tq.hi), "+v"(tk.lo), "+v"(tk.hi));
@@ -429,105 +435,143 @@ __global__ __launch_bounds__(256, 1) void bwd_kv_kernel(BwdArgs a) {
       if (s + 2 < n_steps && s + 2 >= n_win) pid2 = pair_of(s + 2);
     }
 
-    floatx16 sc, dp;
+    // S (dh = 0) or dP (dh = 1) of the (kh, qc) tile, lane = key, rows = queries
+    // 8 g + 4 hl + j of the chunk
+    floatx16 x;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) { sc[r] = 0.f; dp[r] = 0.f; }
+    for (int r = 0; r < 16; ++r) x[r] = 0.f;
+    // The operand reads of four products are issued together, fenced from the
+    // products by scheduling barriers, so that one LDS latency serves four products
+    // (left to itself the scheduler reads just before each product).
+    // (a branch per dim half, so that each names its LDS arrays statically: reads
+    // through a pointer chosen at run time would wait for the row loads in flight)
+    auto sdp = [&](const bf16* sA, const bf16* sB) {
+      bf16x8 fa[4], fb[4];
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) {
-      sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag_at(sQ, kl, qc, kk), k_frag_at(sK, kl, kh, kk),
-                                                   sc, 0, 0, 0);
-      dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag_at(sO, kl, qc, kk), k_frag_at(sV, kl, kh, kk),
-                                                   dp, 0, 0, 0);
+      for (int kk = 0; kk < 4; ++kk) { fa[kk] = k_frag_at(sA, kl, qc, kk); fb[kk] = k_frag_at(sB, kl, kh, kk); }
+      __builtin_amdgcn_sched_barrier(0);
+      bf16x8 ga[4], gb[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        ga[kk] = k_frag_at(sA, kl, qc, kk + 4);
+        gb[kk] = k_frag_at(sB, kl, kh, kk + 4);
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) x = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk], fb[kk], x, 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) x = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ga[kk], gb[kk], x, 0, 0, 0);
+    };
+    if (dh == 0)
+      sdp(sQ, sK);
+    else
+      sdp(sO, sV);
+    float pr[16], ds[16];
+    if (dh == 0) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int q0 = qst + 8 * g + 4 * hl;
+        const float4 l2 = *(const float4*)&M.l2[q0];
+        const float4 b2 = *(const float4*)&M.b2[q0];
+        const int4 lo = *(const int4*)&M.lo[q0];
+        const int4 hi = *(const int4*)&M.hi[q0];
+        const float l2a[4] = {l2.x, l2.y, l2.z, l2.w};
+        const float b2a[4] = {b2.x, b2.y, b2.z, b2.w};
+        const int loa[4] = {lo.x, lo.y, lo.z, lo.w};
+        const int hia[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e = fast_exp2(fmaf(x[4 * g + j], c2, b2a[j] - l2a[j]));
+          const bool vis = (key >= loa[j]) & (key <= hia[j]);
+          pr[4 * g + j] = vis ? e : 0.f;
+        }
+      }
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        *(float4*)(xs + (r4 * 64 + lane) * 4) = make_float4(pr[4 * r4], pr[4 * r4 + 1], pr[4 * r4 + 2],
+                                                            pr[4 * r4 + 3]);
+    } else {
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        *(float4*)(xs + (r4 * 64 + lane) * 4) = make_float4(x[4 * r4], x[4 * r4 + 1], x[4 * r4 + 2],
+                                                            x[4 * r4 + 3]);
     }
-    // operand reads two k-steps ahead of the products
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+    lds_barrier();
+    // the partner's half: dP for dh = 0, P for dh = 1; then dS = P (dP - delta)
+    float other[16];
 #pragma unroll
-    for (int kk = 0; kk < D / 16 - 2; ++kk) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const float4 v = *(const float4*)(xp + (r4 * 64 + lane) * 4);
+      other[4 * r4] = v.x; other[4 * r4 + 1] = v.y; other[4 * r4 + 2] = v.z; other[4 * r4 + 3] = v.w;
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-    // P and dS, lane = key, rows = queries 8 g + 4 hl + j of this wavefront's chunk
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const int q0 = qst + 8 * g + 4 * hl;
-      const float4 l2 = *(const float4*)&M.l2[q0];
-      const float4 de = *(const float4*)&M.del[q0];
-      const float4 b2 = *(const float4*)&M.b2[q0];
-      const int4 lo = *(const int4*)&M.lo[q0];
-      const int4 hi = *(const int4*)&M.hi[q0];
-      const float l2a[4] = {l2.x, l2.y, l2.z, l2.w};
+      const float4 de = *(const float4*)&M.del[qst + 8 * g + 4 * hl];
       const float dea[4] = {de.x, de.y, de.z, de.w};
-      const float b2a[4] = {b2.x, b2.y, b2.z, b2.w};
-      const int loa[4] = {lo.x, lo.y, lo.z, lo.w};
-      const int hia[4] = {hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = 4 * g + j;
-        // branch-free, so that the products and the softmax stay one scheduling region
-        const float e = fast_exp2(fmaf(sc[r], c2, b2a[j] - l2a[j]));
-        const bool vis = (key >= loa[j]) & (key <= hia[j]);
-        const float pr = vis ? e : 0.f;
-        sc[r] = pr;                                  // sc now holds P
-        dp[r] = pr * (dp[r] - dea[j]);               // dp now holds dS
+        const float pv = dh == 0 ? pr[r] : other[r];
+        const float dpv = dh == 0 ? other[r] : x[r];
+        pr[r] = pv;
+        ds[r] = pv * (dpv - dea[j]);
       }
     }
-    // dV^T += dO^T P and dK^T += Q^T dS over this wavefront's 32 queries
+    // this wavefront's dims of dV^T += dO^T P and dK^T += Q^T dS (operand reads
+    // issued together, as above)
+    floatx16 pf, df;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const bf16x8 pb = acc_bop(sc, ks);
-      const bf16x8 db = acc_bop(dp, ks);
+    for (int r = 0; r < 16; ++r) { pf[r] = pr[r]; df[r] = ds[r]; }
+    {
+      bf16x8 fo[2][2], fq[2][2];
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        acc_dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag_at(sO, tq, ks, dt), pb, acc_dv[dt],
-                                                             0, 0, 0);
-        acc_dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag_at(sQ, tq, ks, dt), db, acc_dk[dt],
-                                                             0, 0, 0);
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          fo[ks][t] = tr_frag_at(sO, tq, ks, 2 * dh + t);
+          fq[ks][t] = tr_frag_at(sQ, tq, ks, 2 * dh + t);
+        }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const bf16x8 pb = acc_bop(pf, ks);
+        const bf16x8 db = acc_bop(df, ks);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          acc_dv[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fo[ks][t], pb, acc_dv[t], 0, 0, 0);
+          acc_dk[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fq[ks][t], db, acc_dk[t], 0, 0, 0);
+        }
       }
     }
-    // operand reads four products ahead
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-    for (int i = 0; i < 12; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     if (routed) {
-      // dS through LDS: sDS[qc][key of the stage][query], the lane's 4 queries
-      // 8 g + 4 hl .. + 3 of its key in one 8-byte write
+      if (dh == 0) {
+        // dS through LDS (sDS[qc][key][query]) and its row sums over this
+        // wavefront's 32 keys
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        bf16x4 w;
+        for (int g = 0; g < 4; ++g) {
+          bf16x4 w;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) w[j] = (bf16)dp[4 * g + j];
-        *(bf16x4*)&sDS[qc][kst + n][8 * g + 4 * hl] = w;
-      }
-      // row sums of dS over this wavefront's 32 keys (fp32), one per query row
+          for (int j = 0; j < 4; ++j) w[j] = (bf16)ds[4 * g + j];
+          *(bf16x4*)&sDS[qc][kst + n][8 * g + 4 * hl] = w;
+        }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dp[r] = half32_sum(dp[r]);
-      if (n == 0) {
+        for (int r = 0; r < 16; ++r) ds[r] = half32_sum(ds[r]);
+        if (n == 0) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
+          for (int g = 0; g < 4; ++g)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) sDb[kh][qst + 8 * g + 4 * hl + j] = dp[4 * g + j];
+            for (int j = 0; j < 4; ++j) sDb[kh][qst + 8 * g + 4 * hl + j] = ds[4 * g + j];
+        }
       }
       lds_barrier();
-      // dQ^T = K^T dS^T over the 64 keys: wavefront kh takes dims 64 kh .. 64 kh + 63
-      floatx16 acc_q[2];
+      // dQ^T tile dtq = K^T dS^T over the stage's 64 keys for the chunk's 32 queries
+      floatx16 acc_q;
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc_q[u][r] = 0.f;
-      // B operand of dS^T (query n, keys 16 ks + 4 hl + e and + 8) by transposing
-      // reads: in each 16-lane group (queries 16 (g % 2) .., half g / 2) lane 4 j + m
-      // reads keys row kb + j, queries 4 m .. + 3 of the group.  The reads are one asm
-      // block with its own LDS wait: issued by the builtin they would also wait for
-      // the next step's row loads (vmcnt), which are in flight.
+      for (int r = 0; r < 16; ++r) acc_q[r] = 0.f;
       const int tg = lane >> 4;
       const uint32_t dsa = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) bf16*)
           &sDS[qc][4 * (tg >> 1) + ((lane & 15) >> 2)][16 * (tg & 1) + 4 * (lane & 3)];
-      bf16x4 dst[8];                       // [2 ks + half]: keys 16 ks + 8 half + 4 hl ..
+      bf16x4 dst[8];
       asm volatile(
           "ds_read_b64_tr_b16 %0, %8\n"
           "ds_read_b64_tr_b16 %1, %8 offset:576\n"
@@ -547,20 +591,13 @@ __global__ __launch_bounds__(256, 1) void bwd_kv_kernel(BwdArgs a) {
         bf16x8 dsb;
 #pragma unroll
         for (int e = 0; e < 4; ++e) { dsb[e] = dst[2 * ks][e]; dsb[e + 4] = dst[2 * ks + 1][e]; }
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-          acc_q[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag_at(sK, tk, ks, 2 * kh + u), dsb,
-                                                             acc_q[u], 0, 0, 0);
+        acc_q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag_at(sK, tk, ks, dtq), dsb, acc_q, 0, 0, 0);
       }
-      // the partials of the pair of query column n, stored at the start of the next
-      // step (see store_pending): dims 64 kh + 32 u + 8 g + 4 hl + j
-      float* st = sSt[wv];
+      // staged for the next step: dims 32 dtq + 8 g + 4 hl + j of query n
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-          *(float4*)(st + n * 64 + (((8 * u + 2 * g + hl) ^ (n & 15)) << 2)) =
-              make_float4(acc_q[u][4 * g], acc_q[u][4 * g + 1], acc_q[u][4 * g + 2], acc_q[u][4 * g + 3]);
+      for (int g = 0; g < 4; ++g)
+        *(float4*)(xs + n * 32 + (((2 * g + hl) ^ (n & 7)) << 2)) =
+            make_float4(acc_q[4 * g], acc_q[4 * g + 1], acc_q[4 * g + 2], acc_q[4 * g + 3]);
       const int pos = M.pos[qst + n];
       pend_pi = pos >= 0 ? ((int64_t)h * p.ppos + pos) * a.nsub + sub : -1;
       pend_db = sDb[0][qst + n] + sDb[1][qst + n];
@@ -569,7 +606,7 @@ __global__ __launch_bounds__(256, 1) void bwd_kv_kernel(BwdArgs a) {
 
     if (wv == 0) {
       if (s + 1 < n_steps) meta_store(s + 1, ml, sM[P ^ 1]);
-      if (s + 2 < n_steps) sRow[P][tid & 15][tid >> 4] = row_of(s + 2, pid2);
+      if (s + 2 < n_steps) sRow[P][tid & 31][tid >> 5] = row_of(s + 2, pid2);
       pid_next = pid2;
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -583,16 +620,16 @@ __global__ __launch_bounds__(256, 1) void bwd_kv_kernel(BwdArgs a) {
   if (s < n_steps) step(s, std::integral_constant<int, 0>{});
   store_pending((n_steps - 1) & 1);
 
-  // ---- dK and dV: the two query groups' sums, written by wavefronts 0 and 1 ----
-  float* const redk = (float*)(kh ? sQ1 : sQ0);     // 16 KB each, no longer read
-  float* const redv = (float*)(kh ? sO1 : sO0);
+  // ---- dK and dV: the two query chunks' sums (16 KB per (kh, dh) pair) ----
+  const int ri = kh + 2 * dh;
+  float* const red = (float*)(ri == 0 ? sQ0 : ri == 1 ? sQ1 : ri == 2 ? sO0 : sO1);
   if (qc == 1) {
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        redk[(dt * 16 + r) * kWave + lane] = acc_dk[dt][r];
-        redv[(dt * 16 + r) * kWave + lane] = acc_dv[dt][r];
+        red[(t * 16 + r) * kWave + lane] = acc_dk[t][r];
+        red[((2 + t) * 16 + r) * kWave + lane] = acc_dv[t][r];
       }
   }
   __syncthreads();
@@ -600,18 +637,18 @@ __global__ __launch_bounds__(256, 1) void bwd_kv_kernel(BwdArgs a) {
     bf16* dkp = seq_base(a.dk, p.cu, b, a.dk_sb, a.dk_st) + (int64_t)h * a.dk_sh + (int64_t)key * a.dk_st;
     bf16* dvp = seq_base(a.dv, p.cu, b, a.dv_sb, a.dv_st) + (int64_t)h * a.dv_sh + (int64_t)key * a.dv_st;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         bf16x4 wk, wvv;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int r = 4 * g + j;
-          wk[j] = (bf16)((acc_dk[dt][r] + redk[(dt * 16 + r) * kWave + lane]) * a.scale);
-          wvv[j] = (bf16)(acc_dv[dt][r] + redv[(dt * 16 + r) * kWave + lane]);
+          wk[j] = (bf16)((acc_dk[t][r] + red[(t * 16 + r) * kWave + lane]) * a.scale);
+          wvv[j] = (bf16)(acc_dv[t][r] + red[((2 + t) * 16 + r) * kWave + lane]);
         }
-        *(bf16x4*)(dkp + 32 * dt + 8 * g + 4 * hl) = wk;
-        *(bf16x4*)(dvp + 32 * dt + 8 * g + 4 * hl) = wvv;
+        *(bf16x4*)(dkp + 64 * dh + 32 * t + 8 * g + 4 * hl) = wk;
+        *(bf16x4*)(dvp + 64 * dh + 32 * t + 8 * g + 4 * hl) = wvv;
       }
   }
 }
