@@ -28,6 +28,7 @@ struct DecodeArgs {
   float* lse; int64_t lse_sb, lse_sh;
   float* part;                   // [B*H*nsplit, D + 2]: o[D], m, l
   int S, H, bs, lw, nsplit;
+  int piece;                     // keys per window piece of the fused decode step
   float scale_log2e;
 };
 

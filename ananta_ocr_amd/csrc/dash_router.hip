@@ -1780,15 +1780,27 @@ __global__ __launch_bounds__(kDrThreads) void decode_route_kernel(DecodeRouteArg
 // sequence each (as decode_route_kernel), B .. 2B-1 refresh the tail block's
 // summary of one sequence each (beside its routing, which does not read it once
 // the window spans a block), the rest are 16 wavefronts of window
-// pieces, one 32-key piece of the window of one (sequence, head) per wavefront,
-// each writing an (o, m, l) partial (32 keys per round trip keep a wavefront
-// within the 128 registers a 1024-thread work-group allows).  A second launch
-// takes one wavefront per routed slot of (sequence, head), a third merges.
+// pieces, one piece of the window of one (sequence, head) per wavefront (32 or
+// 64 keys, see ds_piece_keys; 32 keys per round trip keep a wavefront within the
+// 128 registers a 1024-thread work-group allows), each writing an (o, m, l)
+// partial.  A second launch takes one wavefront per routed slot of (sequence,
+// head), a third merges.
 // ---------------------------------------------------------------------------
-constexpr int kDsPiece = 32;              // keys per window piece
+constexpr int kDsPieceMin = 32;           // keys per window piece: 32, or 64 (see ds_piece_keys)
+constexpr int64_t kDsWideTasks = 4096;
+
+// Keys per window piece: 64 (two round trips per wavefront) while the window part
+// is small enough that the router work-groups bound the first launch (fewer
+// partials then shorten the merge: 8 sequences x 10 heads at a 1,024-token window,
+// 43.2 -> 40.4 us per step), else 32 (more wavefronts; 32 sequences x 10 heads:
+// 1,666 us per 12-layer step against 1,716 with 64).
+inline int ds_piece_keys(int64_t B, int H, int local_window, int block_size) {
+  const int64_t tasks = B * H * ((local_window + block_size - 1 + kDsPieceMin - 1) / kDsPieceMin);
+  return tasks <= kDsWideTasks ? 2 * kDsPieceMin : kDsPieceMin;
+}
 
 __device__ __forceinline__ int ds_pieces(const DecodeArgs& da, const DcSpan& sp) {
-  return sp.n_win > 0 ? (sp.qp + 1 - sp.w0 * da.bs + kDsPiece - 1) / kDsPiece : 0;
+  return sp.n_win > 0 ? (sp.qp + 1 - sp.w0 * da.bs + da.piece - 1) / da.piece : 0;
 }
 
 // With nrw = 2 (split), ra routes without the refresh (refresh_tail 0, skip_tail 1)
@@ -1814,8 +1826,8 @@ __global__ __launch_bounds__(kDrThreads) void decode_route_window_kernel(DecodeR
   if (piece >= ds_pieces(da, sp)) return;
   DcState st;
   dc_init(st, da, b, h, lane);
-  const int j0 = sp.w0 * da.bs + piece * kDsPiece;
-  dc_keys<kDsPiece>(st, da, b, h, sp, j0, min(j0 + kDsPiece, sp.len), false, 0.f);
+  const int j0 = sp.w0 * da.bs + piece * da.piece;
+  dc_keys<32>(st, da, b, h, sp, j0, min(j0 + da.piece, sp.len), false, 0.f);
   dc_store_partial<128>(st, da.part + ((int64_t)bh * (npw + da.K) + piece) * (128 + 2), lane);
 }
 
@@ -1933,7 +1945,8 @@ extern "C" int dash_decode_step_workspace_size(int B, int H, int D, int block_si
                                                int local_window, int64_t* bytes) {
   using namespace dash;
   if (!bytes || B < 0 || H < 0 || D <= 0 || block_size <= 0 || local_window < 1) return kErrInvalid;
-  const int npw = (local_window + block_size - 1 + kDsPiece - 1) / kDsPiece;
+  // room for the partials of the smallest pieces (the most of them)
+  const int npw = (local_window + block_size - 1 + kDsPieceMin - 1) / kDsPieceMin;
   *bytes = (int64_t)B * H * (npw + kDcMaxK) * (D + 2) * (int64_t)sizeof(float);
   return kOk;
 }
@@ -1968,7 +1981,8 @@ extern "C" int dash_decode_step(
   if (block_size % 64 != 0 && block_size != 32) return kErrUnsupported;
   if (local_window < 1) return kErrInvalid;
   if (block_table && page_size % block_size != 0) return kErrUnsupported;
-  const int npw = (local_window + block_size - 1 + kDsPiece - 1) / kDsPiece;
+  const int piece = ds_piece_keys(B, H, local_window, block_size);
+  const int npw = (local_window + block_size - 1 + piece - 1) / piece;
   if (npw + Kout > kWave) return kErrUnsupported;     // partials of one merge wavefront
   if (B == 0) return kOk;
   const int64_t strides[] = {q_sb, q_sh, k_sb, k_sh, k_st, k_sp, v_sb, v_sh, v_st, v_sp};
@@ -1991,7 +2005,7 @@ extern "C" int dash_decode_step(
   a.out = out; a.out_bf16 = out_bf16; a.o_sb = o_sb; a.o_sh = o_sh;
   a.lse = lse; a.lse_sb = lse_sb; a.lse_sh = lse_sh;
   a.part = (float*)workspace;
-  a.S = S; a.H = H; a.bs = block_size; a.lw = local_window; a.nsplit = npw;
+  a.S = S; a.H = H; a.bs = block_size; a.lw = local_window; a.nsplit = npw; a.piece = piece;
   a.scale_log2e = scale * 1.4426950408889634f;
   const int64_t tasks = (int64_t)B * H * npw;
   // the tail refresh beside the routing when the tail block cannot be remote
