@@ -209,6 +209,18 @@ __device__ __forceinline__ int dc_routed(const DecodeArgs& a, int b, const DcSpa
 template <int D, typename PartAt>
 __device__ __forceinline__ void dc_merge(const DecodeArgs& a, int b, int h, int lane, int n,
                                          float ms, float lsum, float* sW, PartAt part_at) {
+  // every partial's o (n <= 64, in groups of eight, the last group's surplus
+  // loads repeating partial n - 1) is loaded before the weights are known, so
+  // the merge waits on memory once
+  float2 ov[kWave];
+  if (n > 0) {
+#pragma unroll
+    for (int g = 0; g < kWave / 8; ++g)
+      if (8 * g < n) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) ov[8 * g + u] = *(const float2*)(part_at(min(8 * g + u, n - 1)) + lane * 2);
+      }
+  }
   const float M = wave_max(ms);
   const float Mu = (M == -INFINITY) ? 0.f : M;
   const float w = lane < n ? fast_exp2(ms - Mu) : 0.f;
@@ -219,23 +231,16 @@ __device__ __forceinline__ void dc_merge(const DecodeArgs& a, int b, int h, int 
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const float inv = L > 0.f ? 1.f / L : 0.f;
   float acc0 = 0.f, acc1 = 0.f;
-  // eight partials' loads in flight at a time
-  int s = 0;
-  for (; s + 8 <= n; s += 8) {
-    float2 ov[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) ov[u] = *(const float2*)(part_at(s + u) + lane * 2);
+  for (int g = 0; g < kWave / 8; ++g)
+    if (8 * g < n) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      acc0 += ov[u].x * sW[s + u];
-      acc1 += ov[u].y * sW[s + u];
+      for (int u = 0; u < 8; ++u) {
+        const float wu = 8 * g + u < n ? sW[8 * g + u] : 0.f;
+        acc0 += ov[8 * g + u].x * wu;
+        acc1 += ov[8 * g + u].y * wu;
+      }
     }
-  }
-  for (; s < n; ++s) {
-    const float2 ov = *(const float2*)(part_at(s) + lane * 2);
-    acc0 += ov.x * sW[s];
-    acc1 += ov.y * sW[s];
-  }
   const int64_t off = (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + lane * 2;
   if (a.out_bf16) {
     bf16x2 r;
