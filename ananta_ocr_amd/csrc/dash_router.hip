@@ -1823,11 +1823,14 @@ __global__ __launch_bounds__(kDrThreads) void decode_route_window_kernel(DecodeR
   const int h = bh % da.H, b = bh / da.H;
   const int lane = wave_lane();
   const DcSpan sp = dc_span(da, b);
-  if (piece >= ds_pieces(da, sp)) return;
   DcState st;
   dc_init(st, da, b, h, lane);
-  const int j0 = sp.w0 * da.bs + piece * da.piece;
-  dc_keys<32>(st, da, b, h, sp, j0, min(j0 + da.piece, sp.len), false, 0.f);
+  // pieces past the window write an empty partial, so that the merge reads every
+  // slot without knowing the window's length
+  if (piece < ds_pieces(da, sp)) {
+    const int j0 = sp.w0 * da.bs + piece * da.piece;
+    dc_keys<32>(st, da, b, h, sp, j0, min(j0 + da.piece, sp.len), false, 0.f);
+  }
   dc_store_partial<128>(st, da.part + ((int64_t)bh * (npw + da.K) + piece) * (128 + 2), lane);
 }
 
@@ -1849,16 +1852,16 @@ __global__ __launch_bounds__(64) void decode_routed_kernel(DecodeArgs da, int np
                         lane);
 }
 
-// Merge of the fused step: the window pieces of (b, h) (slots below its piece count)
-// and its K routed slots (npw ..), one wavefront per (b, h).
+// Merge of the fused step: the npw window-piece slots of (b, h) and its K routed
+// slots (npw ..), one wavefront per (b, h).
 __global__ __launch_bounds__(64) void decode_step_merge_kernel(DecodeArgs da, int npw) {
   __shared__ float sW[kWave];
   const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  const DcSpan sp = dc_span(da, b);
-  const int nw = ds_pieces(da, sp);
-  const int n = nw + da.K;
+  // every slot holds a partial (empty ones past the window and the routed count),
+  // so the loads need nothing but the launch arguments
+  const int n = npw + da.K;
   const float* pb = da.part + (int64_t)(b * da.H + h) * (npw + da.K) * (128 + 2);
-  auto part_at = [&](int s) -> const float* { return pb + (s < nw ? s : npw + s - nw) * (128 + 2); };
+  auto part_at = [&](int s) -> const float* { return pb + s * (128 + 2); };
   float ms = -INFINITY, lsum = 0.f;
   if (lane < n) { ms = part_at(lane)[128]; lsum = part_at(lane)[129]; }
   dc_merge<128>(da, b, h, lane, n, ms, lsum, sW, part_at);
