@@ -74,6 +74,8 @@ def _case(seed, B, H, S, bs, lw, K, dup=True):
     (1, 2, 333, 128, 200, 4),           # window not a block multiple, 128-key blocks
     (1, 2, 1200, 32, 128, 64),          # the training schedule's first k
     (1, 2, 900, 64, 256, 20),           # two slot groups, the last one partial
+    (1, 2, 800, 96, 288, 8),            # 96-key blocks: key stages that span two blocks
+    (1, 2, 1100, 256, 512, 4),          # 256-key blocks: four key stages per block
 ])
 def test_backward_matches_torch_autograd(B, H, S, bs, lw, K):
     q, k, v, topi, bias, valid, dout = _case(10 + S + bs, B, H, S, bs, lw, K)
@@ -95,6 +97,34 @@ def test_backward_matches_torch_autograd(B, H, S, bs, lw, K):
     _close_grad(db, br.grad, "dbias")
     # slots that are not the first valid occurrence of their block get no gradient
     assert bool((db.cpu()[br.grad == 0] == 0).all())
+
+
+def test_backward_segment_starts():
+    """kmin (packed segments inside one sequence, packing_patch.py): keys before a
+    row's segment start are invisible to it, in the window and in routed blocks."""
+    B, H, S, bs, lw, K = 1, 2, 1000, 64, 256, 8
+    q, k, v, topi, bias, valid, dout = _case(77, B, H, S, bs, lw, K)
+    starts = torch.tensor([0, 130, 131, 420, 777])
+    kmin = torch.zeros(B, S, dtype=torch.int32)
+    for s0, s1 in zip(starts.tolist(), starts.tolist()[1:] + [S]):
+        kmin[:, s0:s1] = s0
+    scale = 1 / math.sqrt(128)
+    qr, kr, vr = (t.float().requires_grad_() for t in (q, k, v))
+    br = bias.clone().requires_grad_()
+    out_r = _ref(qr, kr, vr, topi, br, valid, bs, lw, scale, kmin=kmin)
+    out_r.backward(dout.float())
+    args = [t.to(DEV) for t in (q, k, v)]
+    km = kmin.to(DEV)
+    out, lse = ops.attn_prefill(*args, topi.to(DEV), bias.to(DEV), valid.to(DEV), bs, lw, scale,
+                                kmin=km, return_lse=True)
+    dq, dk, dv, db = ops.attn_prefill_backward(*args, out, lse, dout.to(DEV), topi.to(DEV),
+                                               bias.to(DEV), valid.to(DEV), bs, lw, scale, kmin=km)
+    torch.cuda.synchronize()
+    _close_grad(out, out_r.detach(), "out")
+    _close_grad(dq, qr.grad, "dq")
+    _close_grad(dk, kr.grad, "dk")
+    _close_grad(dv, vr.grad, "dv")
+    _close_grad(db, br.grad, "dbias")
 
 
 def test_backward_without_routing_is_sliding_window():
