@@ -932,7 +932,14 @@ __device__ __forceinline__ float train_tau(const float (&x)[NPL], float xmax) {
 #pragma unroll
   for (int i = 0; i < NPL; ++i) X[i] = __fdiv_rn(__fsub_rn(x[i], xmax), 2.0f);   // -inf stays
   double lo = -1.0, hi = 0.0;               // f(-1) >= 1 (the maximum contributes 1), f(0) = 0
+  // The root stays in [lo, hi).  Once no entry lies in (lo, hi], every point of the
+  // bracket has the support {X > lo}, the one the 48 steps would end on, and the
+  // closed form below gives the same threshold: the bisection stops there.
   for (int it = 0; it < 48; ++it) {
+    bool inside = false;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) inside |= ((double)X[i] > lo) & ((double)X[i] <= hi);
+    if (!__any(inside)) break;
     const double mid = 0.5 * (lo + hi);
     double f = 0.0;
 #pragma unroll
