@@ -16,10 +16,10 @@
 //     stage's K and V stay in LDS while 64 queries at a time stream through it --
 //     first the window band (every query whose window reaches the stage), then
 //     the routed pairs of the stage's blocks, gathered.  Per 32-query chunk and
-//     32-key half, two wavefronts (one per half of the head dims): S = Q K^T in
-//     one, dP = dO V^T in the other, on the matrix cores (lane = key), exchanged
-//     through LDS so that both hold P and dS; each adds its dims of dV^T += dO^T P
-//     and dK^T += Q^T dS, the transposed operands read by ds_read_tr16_b64.  dK
+//     32-key half, two wavefronts (one per half of the head dims), each computing
+//     S = Q K^T and dP = dO V^T on the matrix cores (lane = key), P and dS in
+//     registers, and its dims of dV^T += dO^T P and dK^T += Q^T dS, the transposed
+//     operands read by ds_read_tr16_b64.  dK
 //     and dV are complete when the work-group ends (no atomics).  For routed
 //     pairs it also writes dQ^T = K^T dS^T (dS through LDS, read transposed) and
 //     the row sums of dS as fp32 partials per (head, pair).  The steps are
@@ -240,9 +240,9 @@ __device__ __forceinline__ void stage_rows8r(bf16* sX, int wv, int lane, const b
 // Key-major kernel, eight wavefronts: wavefront (kh, qc, dh) = (wv % 2, wv / 2 % 2,
 // wv / 4) owns keys 32 kh .. + 31 of the stage, queries 32 qc .. + 31 of a step and
 // head dims 64 dh .. + 63 of dK and dV, so that two wavefronts fit on a SIMD.  Per
-// step the dh = 0 wavefront of a (kh, qc) pair computes S and P, the dh = 1 one dP;
-// they exchange P and dP (fp32) through LDS and both form dS; each then adds its
-// dims' share of dV^T += dO^T P and dK^T += Q^T dS.  Routed steps: dQ^T = K^T dS^T
+// step both wavefronts of a (kh, qc) pair compute S, P, dP and dS (the products are
+// cheap here; an exchange through LDS cost a barrier), and each adds its dims'
+// share of dV^T += dO^T P and dK^T += Q^T dS.  Routed steps: dQ^T = K^T dS^T
 // for the step's 64 queries x 128 dims, one 32 x 32 tile per wavefront (dims
 // 32 (2 dh + kh) ..), and the bias-gradient row sums.
 // Software pipeline over the steps: step s computes on the query rows in buffer
@@ -266,8 +266,7 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_kernel(BwdArgs a) {
   // row numbers of a step for the loads: query slot q at [q % 32][q / 32]
   __shared__ __attribute__((aligned(16))) int sRow[2][32][2];
   __shared__ float sDb[2][kBwIT];
-  // per wavefront 4 KB: the P / dP exchange inside a step, and the dQ^T staging of
-  // a routed step until the start of the next
+  // per wavefront 4 KB: the dQ^T staging of a routed step until the start of the next
   __shared__ __attribute__((aligned(16))) float sX[8][1024];
 
   const PrefillArgs& p = a.p;
@@ -367,8 +366,7 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_kernel(BwdArgs a) {
   const int key = j0 + 32 * kh + n;
   const int kst = 32 * kh, qst = 32 * qc;
   const int dtq = 2 * dh + kh;             // this wavefront's dQ dim tile
-  float* const xs = sX[wv];                // own exchange / staging area
-  const float* const xp = sX[wv ^ 4];      // the partner's (other dim half)
+  float* const xs = sX[wv];                // own staging area
 
   int pid_next = -1;
   if (n_steps > 0) {
@@ -435,86 +433,58 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_kernel(BwdArgs a) {
       if (s + 2 < n_steps && s + 2 >= n_win) pid2 = pair_of(s + 2);
     }
 
-    // S (dh = 0) or dP (dh = 1) of the (kh, qc) tile, lane = key, rows = queries
-    // 8 g + 4 hl + j of the chunk
-    floatx16 x;
+    // S and dP of the (kh, qc) tile, lane = key, rows = queries 8 g + 4 hl + j of the
+    // chunk.  Both wavefronts of a dim pair compute both (the matrix cores have room;
+    // no exchange and no barrier between them).  The next k-step's four operand reads
+    // are issued before the current k-step's two products, fenced by scheduling
+    // barriers (left to itself the scheduler reads just before each product).
+    floatx16 xs_, xd_;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) x[r] = 0.f;
-    // The operand reads of four products are issued together, fenced from the
-    // products by scheduling barriers, so that one LDS latency serves four products
-    // (left to itself the scheduler reads just before each product).
-    // (a branch per dim half, so that each names its LDS arrays statically: reads
-    // through a pointer chosen at run time would wait for the row loads in flight)
-    auto sdp = [&](const bf16* sA, const bf16* sB) {
-      bf16x8 fa[4], fb[4];
+    for (int r = 0; r < 16; ++r) { xs_[r] = 0.f; xd_[r] = 0.f; }
+    {
+      auto rd = [&](int kk, bf16x8 (&f)[4]) {
+        f[0] = k_frag_at(sQ, kl, qc, kk);
+        f[1] = k_frag_at(sK, kl, kh, kk);
+        f[2] = k_frag_at(sO, kl, qc, kk);
+        f[3] = k_frag_at(sV, kl, kh, kk);
+      };
+      bf16x8 f0[4], f1[4];
+      rd(0, f0);
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) { fa[kk] = k_frag_at(sA, kl, qc, kk); fb[kk] = k_frag_at(sB, kl, kh, kk); }
-      __builtin_amdgcn_sched_barrier(0);
-      bf16x8 ga[4], gb[4];
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        ga[kk] = k_frag_at(sA, kl, qc, kk + 4);
-        gb[kk] = k_frag_at(sB, kl, kh, kk + 4);
+      for (int kk = 0; kk < D / 16; kk += 2) {
+        rd(kk + 1, f1);
+        __builtin_amdgcn_sched_barrier(0);
+        xs_ = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0[0], f0[1], xs_, 0, 0, 0);
+        xd_ = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0[2], f0[3], xd_, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kk + 2 < D / 16) rd(kk + 2, f0);
+        __builtin_amdgcn_sched_barrier(0);
+        xs_ = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1[0], f1[1], xs_, 0, 0, 0);
+        xd_ = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1[2], f1[3], xd_, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) x = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk], fb[kk], x, 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) x = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ga[kk], gb[kk], x, 0, 0, 0);
-    };
-    if (dh == 0)
-      sdp(sQ, sK);
-    else
-      sdp(sO, sV);
+    }
     float pr[16], ds[16];
-    if (dh == 0) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int q0 = qst + 8 * g + 4 * hl;
-        const float4 l2 = *(const float4*)&M.l2[q0];
-        const float4 b2 = *(const float4*)&M.b2[q0];
-        const int4 lo = *(const int4*)&M.lo[q0];
-        const int4 hi = *(const int4*)&M.hi[q0];
-        const float l2a[4] = {l2.x, l2.y, l2.z, l2.w};
-        const float b2a[4] = {b2.x, b2.y, b2.z, b2.w};
-        const int loa[4] = {lo.x, lo.y, lo.z, lo.w};
-        const int hia[4] = {hi.x, hi.y, hi.z, hi.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float e = fast_exp2(fmaf(x[4 * g + j], c2, b2a[j] - l2a[j]));
-          const bool vis = (key >= loa[j]) & (key <= hia[j]);
-          pr[4 * g + j] = vis ? e : 0.f;
-        }
-      }
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4)
-        *(float4*)(xs + (r4 * 64 + lane) * 4) = make_float4(pr[4 * r4], pr[4 * r4 + 1], pr[4 * r4 + 2],
-                                                            pr[4 * r4 + 3]);
-    } else {
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4)
-        *(float4*)(xs + (r4 * 64 + lane) * 4) = make_float4(x[4 * r4], x[4 * r4 + 1], x[4 * r4 + 2],
-                                                            x[4 * r4 + 3]);
-    }
-    lds_barrier();
-    // the partner's half: dP for dh = 0, P for dh = 1; then dS = P (dP - delta)
-    float other[16];
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const float4 v = *(const float4*)(xp + (r4 * 64 + lane) * 4);
-      other[4 * r4] = v.x; other[4 * r4 + 1] = v.y; other[4 * r4 + 2] = v.z; other[4 * r4 + 3] = v.w;
-    }
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const float4 de = *(const float4*)&M.del[qst + 8 * g + 4 * hl];
+      const int q0 = qst + 8 * g + 4 * hl;
+      const float4 l2 = *(const float4*)&M.l2[q0];
+      const float4 b2 = *(const float4*)&M.b2[q0];
+      const float4 de = *(const float4*)&M.del[q0];
+      const int4 lo = *(const int4*)&M.lo[q0];
+      const int4 hi = *(const int4*)&M.hi[q0];
+      const float l2a[4] = {l2.x, l2.y, l2.z, l2.w};
+      const float b2a[4] = {b2.x, b2.y, b2.z, b2.w};
       const float dea[4] = {de.x, de.y, de.z, de.w};
+      const int loa[4] = {lo.x, lo.y, lo.z, lo.w};
+      const int hia[4] = {hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = 4 * g + j;
-        const float pv = dh == 0 ? pr[r] : other[r];
-        const float dpv = dh == 0 ? other[r] : x[r];
-        pr[r] = pv;
-        ds[r] = pv * (dpv - dea[j]);
+        const float e = fast_exp2(fmaf(xs_[r], c2, b2a[j] - l2a[j]));
+        const bool vis = (key >= loa[j]) & (key <= hia[j]);
+        pr[r] = vis ? e : 0.f;
+        ds[r] = pr[r] * (xd_[r] - dea[j]);
       }
     }
     // this wavefront's dims of dV^T += dO^T P and dK^T += Q^T dS (operand reads
