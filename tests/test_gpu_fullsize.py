@@ -1,7 +1,9 @@
 """GPU parity at the workloads' full sizes: the 27,300-token prefill (block 64,
 window 1,024, cap 16, 5 % offset key blocks), the 16-document packed prefill
-(78,078 tokens for seed 4, block-diagonal varlen) and one layer of the 32-sequence
-paged decode (lengths 2,730..27,300, pages of 64 tokens in a random physical order).
+(78,078 tokens for seed 4, block-diagonal varlen), the 32-sequence paged decode
+(lengths 2,730..27,300, pages of 64 tokens in a random physical order: every sequence
+of one layer, and all 12 layers run back to back with three sequences of each
+checked) and the 8 x 27,300 contiguous decode.
 
 Every stage is checked against the CPU oracle on the same inputs: the block
 summaries and scores within fp32 tolerance, the routing bit-exact on the GPU's own
@@ -120,34 +122,25 @@ def _gather_pages(x, table_row, L):
     return x[table_row[:npg].long()].reshape(-1, *x.shape[2:])[:L]
 
 
-def test_paged_decode_32_sequences_full_size():
-    cfg = W.PAGED_12L
-    lens, table = W.paged_layout(cfg)
-    d = W.make_paged_decode(cfg, DEV, 0, lens, table)
+def _check_paged_sequences(cfg, d, lens, table, out, ti, bi, va, seqs, what):
+    """Oracle check of the given sequences of one paged decode step: routing on the
+    oracle's own scores (only blocks tied with the last selected one to fp32 rounding
+    may differ), attention on the GPU's routing.  Pages are gathered on the GPU, so that
+    only the checked sequences travel to the host.  Returns the near-tie count."""
     lb = cfg.lw // cfg.bs
     hc = torch.zeros(128)
-    print(f"paged decode {cfg.name}: B={cfg.B}, tokens={int(lens.sum())}", flush=True)
-    st = pipeline.init_decode_state(d["idx_k"], hc.to(DEV), cfg.bs, table.shape[1],
-                                    seq_lens=d["seq_lens"], block_table=d["block_table"],
-                                    page_size=cfg.bs)
-    out, (ti, bi, va) = pipeline.decode_step(
-        st, d["q"], d["k"], d["v"], d["idx_q"], d["idx_k"], hc.to(DEV), cfg.bs, lb,
-        W.IDX_SCALE, W.FLOOR, W.SIGMA, cfg.cap, cfg.cap, SCALE, seq_lens=d["seq_lens"],
-        block_table=d["block_table"], page_size=cfg.bs, return_routing=True)
-    out = out.cpu()
+    out = out.float().cpu()
     ti, bi, va = ti.cpu().long(), bi.cpu(), va.cpu()
-    q, iq = d["q"].cpu(), d["idx_q"].cpu()
-    kp, vp, ikp = d["k"].cpu(), d["v"].cpu(), d["idx_k"].cpu()
-    del d, st
     ties = 0
-    for b in range(cfg.B):
+    for b in seqs:
         L = int(lens[b])
-        ik = _gather_pages(ikp, table[b], L)[None]                       # [1, L, d]
-        k = _gather_pages(kp, table[b], L).permute(1, 0, 2)[None]       # [1, H, L, D]
-        v = _gather_pages(vp, table[b], L).permute(1, 0, 2)[None]
+        row = table[b].to(d["k"].device)
+        ik = _gather_pages(d["idx_k"], row, L)[None].cpu()                   # [1, L, d]
+        k = _gather_pages(d["k"], row, L).permute(1, 0, 2)[None].cpu()      # [1, H, L, D]
+        v = _gather_pages(d["v"], row, L).permute(1, 0, 2)[None].cpu()
+        q, iq = d["q"][b:b + 1].cpu(), d["idx_q"][b:b + 1].cpu()
         kb_r, cv = O.kbar_headcls(ik, hc, cfg.bs)
-        z_r = O.block_scores_headcls(iq[b:b + 1], kb_r, cv, torch.tensor([[L - 1]]), cfg.bs,
-                                     lb)
+        z_r = O.block_scores_headcls(iq, kb_r, cv, torch.tensor([[L - 1]]), cfg.bs, lb)
         t_r, b_r, v_r = O.infer_route_select(z_r, None, W.IDX_SCALE, W.FLOOR, W.SIGMA,
                                              cfg.cap, cfg.cap)
         kp_ = t_r.shape[-1]
@@ -160,17 +153,65 @@ def test_paged_decode_32_sequences_full_size():
             edge = zz[t_r[0, 0, kp_ - 1]].item()
             for c in g_ids ^ r_ids:
                 assert abs(zz[c].item() - edge) <= 1e-5 * abs(edge) + 1e-6, \
-                    f"sequence {b}: block {c} routed on one side only"
+                    f"{what}, sequence {b}: block {c} routed on one side only"
             ties += 1
         else:
-            assert torch.equal(ti[b, 0, :kp_], t_r[0, 0]), f"sequence {b}: slot order"
+            assert torch.equal(ti[b, 0, :kp_], t_r[0, 0]), f"{what}, sequence {b}: slot order"
             torch.testing.assert_close(bi[b, 0, :kp_], b_r[0, 0], atol=1e-4, rtol=1e-4)
         # attention on the GPU's routing
-        ref = O.decode_attend(q[b:b + 1, :, None], k, v, ti[b:b + 1, :, :kp_],
+        ref = O.decode_attend(q[:, :, None], k, v, ti[b:b + 1, :, :kp_],
                               bi[b:b + 1, :, :kp_], va[b:b + 1, :, :kp_],
                               torch.tensor([[L - 1]]), cfg.bs, cfg.lw, SCALE)
-        _close(out[b:b + 1], ref[:, :, 0], f"decode sequence {b} ({L} tokens)")
+        _close(out[b:b + 1], ref[:, :, 0], f"{what}, sequence {b} ({L} tokens)")
+    return ties
+
+
+def _paged_step(cfg, d, st):
+    hc = torch.zeros(128, device=DEV)
+    return pipeline.decode_step(
+        st, d["q"], d["k"], d["v"], d["idx_q"], d["idx_k"], hc, cfg.bs, cfg.lw // cfg.bs,
+        W.IDX_SCALE, W.FLOOR, W.SIGMA, cfg.cap, cfg.cap, SCALE, seq_lens=d["seq_lens"],
+        block_table=d["block_table"], page_size=cfg.bs, return_routing=True)
+
+
+def _paged_state(cfg, d, table):
+    return pipeline.init_decode_state(d["idx_k"], torch.zeros(128, device=DEV), cfg.bs,
+                                      table.shape[1], seq_lens=d["seq_lens"],
+                                      block_table=d["block_table"], page_size=cfg.bs)
+
+
+def test_paged_decode_32_sequences_full_size():
+    cfg = W.PAGED_12L
+    lens, table = W.paged_layout(cfg)
+    d = W.make_paged_decode(cfg, DEV, 0, lens, table)
+    print(f"paged decode {cfg.name}: B={cfg.B}, tokens={int(lens.sum())}", flush=True)
+    st = _paged_state(cfg, d, table)
+    out, (ti, bi, va) = _paged_step(cfg, d, st)
+    ties = _check_paged_sequences(cfg, d, lens, table, out, ti, bi, va, range(cfg.B), "layer 0")
     assert ties <= 2, f"{ties} sequences with near-tied routing"
+
+
+def test_paged_decode_12_layers_stacked():
+    """The 12-layer paged decode as the benchmark runs it: every layer's cache and state
+    made first, then the 12 fused steps back to back on one stream, then each layer
+    checked against the oracle on three of its 32 sequences (layer l: sequences l,
+    l + 12 and l + 24 mod 32, so that every sequence is checked in some layer)."""
+    cfg = W.PAGED_12L
+    lens, table = W.paged_layout(cfg)
+    layers = []
+    for layer in range(cfg.layers):
+        d = W.make_paged_decode(cfg, DEV, layer, lens, table)
+        layers.append((d, _paged_state(cfg, d, table)))
+    print(f"paged decode {cfg.name}: {cfg.layers} layers made", flush=True)
+    results = [_paged_step(cfg, d, st) for d, st in layers]
+    torch.cuda.synchronize()
+    ties = 0
+    for layer, ((d, _), (out, (ti, bi, va))) in enumerate(zip(layers, results)):
+        seqs = sorted({(layer + 12 * j) % cfg.B for j in range(3)})
+        ties += _check_paged_sequences(cfg, d, lens, table, out, ti, bi, va, seqs,
+                                       f"layer {layer}")
+        print(f"layer {layer}: sequences {seqs} match", flush=True)
+    assert ties <= 3, f"{ties} sequences with near-tied routing"
 
 
 def test_decode_b8_27300_full_size():
