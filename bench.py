@@ -660,10 +660,11 @@ def _cpu_fields(value, unit, sample):
                 sample=sample, cpu_model=model, physical_cores=phys, logical_cpus=logical)
 
 
-def cpu_prefill_baseline(res, cfg, rows=8192, reps=3, docs=None):
+def cpu_prefill_baseline(res, cfg, rows=None, reps=3, docs=None):
     """The oracle (the reference's torch path restated in fp32) on this host: k_bar and
     scores for the whole sequence, routing and dense attention for the last `rows` query
-    rows; for packed inputs, whole documents (`docs` of them) on their own block grids."""
+    rows (None: every row, the whole workload); for packed inputs, whole documents
+    (`docs` of them) on their own block grids."""
     from oracle import dash_oracle as O
     d = res["data"]
     lb = cfg.lw // cfg.bs
@@ -691,7 +692,7 @@ def cpu_prefill_baseline(res, cfg, rows=8192, reps=3, docs=None):
                   f"after 1 warm-up; {t:.2f} s per sample")
         return _cpu_fields(4.0 * W.D * W.H * pairs / t / 1e12, "TFLOP/s", sample)
     S = d["S"]
-    r0 = max(0, S - rows)
+    r0 = 0 if rows is None else max(0, S - rows)
 
     def run():
         kb, cv = O.kbar_headcls(ik, torch.zeros(W.D), cfg.bs)
@@ -711,9 +712,10 @@ def cpu_prefill_baseline(res, cfg, rows=8192, reps=3, docs=None):
                           torch.cat([torch.zeros(r0, ti.shape[-1], dtype=torch.bool), va[0]]),
                           S, cfg.bs, cfg.lw)
     pairs -= sum(min(t_ + 1, cfg.lw) for t_ in range(r0))
-    sample = (f"oracle fp32 on the last {S - r0} of {S} query rows (full k_bar/scores over the "
-              f"sequence; dense masked SDPA as the reference's CPU path); median of {reps} after "
-              f"1 warm-up; {t:.2f} s per sample")
+    rows_txt = (f"all {S} query rows" if r0 == 0 else
+                f"the last {S - r0} of {S} query rows (full k_bar/scores over the sequence)")
+    sample = (f"oracle fp32 on {rows_txt}; dense masked SDPA as the reference's CPU path; "
+              f"median of {reps} after 1 warm-up; {t:.2f} s per sample")
     return _cpu_fields(4.0 * W.D * W.H * pairs / t / 1e12, "TFLOP/s", sample)
 
 
