@@ -1419,6 +1419,9 @@ extern "C" int dash_attn_prefill(
   const bool hybrid = dense_threshold > 0 && K > 0 && block_size <= 64;
   if (hybrid) {
     if (total_rows <= 0) return kErrInvalid;
+    // the plan's arrays hold total_rows rows: B * S without cu_seqlens (with them,
+    // cu_seqlens[B], which the host does not read, is the caller's to pass)
+    if (!cu_seqlens && total_rows != (int64_t)B * S) return kErrInvalid;
     const PlanLayout L = plan_layout(B, H, S, total_rows, K, D, nblk_cap, block_size);
     if (!workspace || workspace_bytes < L.total || (uintptr_t)workspace % 256 != 0)
       return kErrWorkspace;
@@ -1487,6 +1490,9 @@ extern "C" int dash_attn_prefill_backward(
   if (K < 0 || K > kPfMaxSlots) return kErrUnsupported;
   if (local_window < 1) return kErrInvalid;
   if (B == 0 || S == 0) return kOk;
+  // delta and the pair arrays hold total_rows rows: B * S without cu_seqlens (with them,
+  // cu_seqlens[B], which the host does not read, is the caller's to pass)
+  if (!cu_seqlens && total_rows != (int64_t)B * S) return kErrInvalid;
   const int nblk_cap = (S + block_size - 1) / block_size;
   if (nblk_cap > kPfMaxBlocks) return kErrUnsupported;
   const int64_t strides[] = {q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st,
