@@ -41,7 +41,7 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeArgs a) {
     const bool routed = u >= sp.n_win;
     const int cu = routed ? sRC[u - sp.n_win] : sp.w0 + u;
     const float blog = routed ? sRB[u - sp.n_win] : 0.f;
-    dc_block<32>(st, a, b, h, sp, cu, routed, blog);
+    dc_block<16>(st, a, b, h, sp, cu, routed, blog);
   }
   const int bh = b * a.H + h;
   dc_store_partial<D>(st, a.part + ((int64_t)bh * a.nsplit + split) * (D + 2), lane);
