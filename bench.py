@@ -972,8 +972,8 @@ def main():
         counter_probe(args.counter_probe)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this benchmark measures one GPU only (every GPU box here has one "
-              "GPU; no figure at several GPUs is produced); run with --gpus 1", file=sys.stderr)
+        print("bench.py: this benchmark measures one GPU only (no figure at several GPUs is "
+              "produced; the path's sharding is design only); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     torch.cuda.set_device(0)
     torch.backends.cuda.matmul.allow_tf32 = False
