@@ -1385,6 +1385,11 @@ extern "C" int dash_attn_prefill(
   if (D != 128) return kErrUnsupported;
   if (block_size <= 0 || block_size % 32 != 0 || block_size > 256) return kErrUnsupported;
   if (K < 0 || K > kPfMaxSlots) return kErrUnsupported;
+  // Routed blocks of more than 64 keys are refused (windows alone take any block size):
+  // a GPU memory fault followed a forward and backward pass with 128-key blocks in which
+  // the last block, routed, reaches 64 or more keys past the end of the sequence (43
+  // tokens, window 31, 4 slots), and its cause is not found.
+  if (K > 0 && block_size > kPfIT) return kErrUnsupported;
   // above 16 slots every routed pair goes through the block-major sparse kernel
   if (K > kPfMaxK) {
     if (block_size > kPfIT) return kErrUnsupported;
@@ -1488,6 +1493,8 @@ extern "C" int dash_attn_prefill_backward(
   if (D != 128) return kErrUnsupported;
   if (block_size <= 0 || block_size % 32 != 0 || block_size > 256) return kErrUnsupported;
   if (K < 0 || K > kPfMaxSlots) return kErrUnsupported;
+  // routed blocks of more than 64 keys are refused, as in the forward pass
+  if (K > 0 && block_size > kPfIT) return kErrUnsupported;
   if (local_window < 1) return kErrInvalid;
   if (B == 0 || S == 0) return kOk;
   // delta and the pair arrays hold total_rows rows: B * S without cu_seqlens (with them,
