@@ -480,10 +480,14 @@ __device__ __forceinline__ void rows_fetch(bf16* sX, const bf16* xb, int64_t x_s
                                        (__attribute__((address_space(3))) void*)(sX + (4 * u + wv) * 4 * D),
                                        16, 0, 0);
   } else {
+    // rows past the end read the last row; the item may start at or past the end (the
+    // second 64-key item of a routed block of more than 64 keys that the sequence ends
+    // inside), so the row is addressed from the sequence base with 64-bit arithmetic
+    // rather than as an unsigned offset from j0, which such a start would wrap
 #pragma unroll
     for (int u = 0; u < ROWS / 16; ++u) {
-      const int dr = min(j0 + 16 * u + r0, len - 1) - j0;     // >= 0: j0 < len
-      __builtin_amdgcn_global_load_lds((const void*)(xb0 + ((uint32_t)dr * row_b + cb)),
+      const int row = min(j0 + 16 * u + r0, len - 1);
+      __builtin_amdgcn_global_load_lds((const void*)((const char*)(xb + (int64_t)row * x_st) + cb),
                                        (__attribute__((address_space(3))) void*)(sX + (4 * u + wv) * 4 * D),
                                        16, 0, 0);
     }
@@ -1385,11 +1389,6 @@ extern "C" int dash_attn_prefill(
   if (D != 128) return kErrUnsupported;
   if (block_size <= 0 || block_size % 32 != 0 || block_size > 256) return kErrUnsupported;
   if (K < 0 || K > kPfMaxSlots) return kErrUnsupported;
-  // Routed blocks of more than 64 keys are refused (windows alone take any block size):
-  // a GPU memory fault followed a forward and backward pass with 128-key blocks in which
-  // the last block, routed, reaches 64 or more keys past the end of the sequence (43
-  // tokens, window 31, 4 slots), and its cause is not found.
-  if (K > 0 && block_size > kPfIT) return kErrUnsupported;
   // above 16 slots every routed pair goes through the block-major sparse kernel
   if (K > kPfMaxK) {
     if (block_size > kPfIT) return kErrUnsupported;
@@ -1493,8 +1492,6 @@ extern "C" int dash_attn_prefill_backward(
   if (D != 128) return kErrUnsupported;
   if (block_size <= 0 || block_size % 32 != 0 || block_size > 256) return kErrUnsupported;
   if (K < 0 || K > kPfMaxSlots) return kErrUnsupported;
-  // routed blocks of more than 64 keys are refused, as in the forward pass
-  if (K > 0 && block_size > kPfIT) return kErrUnsupported;
   if (local_window < 1) return kErrInvalid;
   if (B == 0 || S == 0) return kOk;
   // delta and the pair arrays hold total_rows rows: B * S without cu_seqlens (with them,

@@ -187,8 +187,7 @@ int dash_train_route_backward(const float* z, int64_t z_stride, int rows, int nb
  * packing segment start, triton_gather_attention (sparse_gather_triton.py:29-104,
  * :343-392).  q/k/v/o [B, H, S, D] by strides (or varlen via cu_seqlens, S = the longest
  * sequence); lse (optional) fp32 at lse[token_row*lse_row + h*lse_sh].  D == 128,
- * block_size in {32, 64, ..., 256}, K <= 64; with routed slots (K > 0) block_size <= 64
- * (larger routed blocks return -2; the backward has the same rule).  K > 16 needs a
+ * block_size in {32, 64, ..., 256}, K <= 64.  K > 16 needs block_size <= 64 and a
  * workspace (dense_threshold > 0): every routed pair then takes the sparse path.
  * dense_threshold > 0 (block_size <= 64): routed blocks selected by fewer than
  * dense_threshold of the 128 queries of a tile go through the block-major sparse path,

@@ -9,7 +9,6 @@ import pytest
 from ananta_ocr_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-ERR_UNSUPPORTED = -2             # kErrUnsupported, a shape the library does not implement
 ERR_INVALID = -3                 # kErrInvalid, inconsistent arguments
 
 
@@ -95,15 +94,10 @@ def test_argument_checks_return_before_any_device_call():
     fwd = dict(common, **strides_o, lse_row=10, lse_sh=1, dense_threshold=32,
                workspace_bytes=1 << 40, stream=None)
     assert _call("dash_attn_prefill", **fwd, total_rows=1999) == ERR_INVALID
-    # routed blocks of more than 64 keys are refused (windows alone take any size)
-    assert _call("dash_attn_prefill", **dict(fwd, block_size=128), total_rows=2000) == \
-        ERR_UNSUPPORTED
     bwd = dict(common, **strides_o, lse_row=10, lse_sh=1, do_sb=0, do_sh=0, do_st=128,
                dq_sb=0, dq_sh=0, dq_st=128, dk_sb=0, dk_sh=0, dk_st=128, dv_sb=0, dv_sh=0,
                dv_st=128, workspace_bytes=1 << 40, stream=None)
     assert _call("dash_attn_prefill_backward", **bwd, total_rows=1999) == ERR_INVALID
-    assert _call("dash_attn_prefill_backward", **dict(bwd, block_size=96), total_rows=2000) == \
-        ERR_UNSUPPORTED
     dec = dict(iq_sb=128, ik_sb=0, ik_st=128, ik_sp=0, block_table=None, table_stride=0,
                page_size=0, seq_lens=None, q_pos=None, head_cls=1, refresh_tail=1, kb_sb=0,
                kb_table=None, kb_ts=0, bounds=None, cand=None, cand_stride=0, B=2, d=128,

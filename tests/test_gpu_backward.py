@@ -22,7 +22,6 @@ from oracle import dash_oracle as O
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-BIG_BLOCKS = ("routed blocks of more than 64 keys are refused by the prefill entry points (a GPU memory fault with 128-key blocks whose routed last block reaches 64 or more keys past the sequence end; cause not found)")
 
 
 def _ref(q, k, v, topi, bias, valid, bs, lw, scale, kmin=None):
@@ -72,14 +71,12 @@ def _case(seed, B, H, S, bs, lw, K, dup=True):
     (1, 2, 700, 64, 256, 6),
     (2, 2, 1000, 32, 128, 12),          # the shipped checkpoint's block 32, window 128, K 12
     (1, 3, 1300, 64, 512, 16),
-    pytest.param(1, 2, 333, 128, 200, 4,       # window not a block multiple, 128-key blocks
-                 marks=pytest.mark.skip(reason=BIG_BLOCKS)),
+    (1, 2, 333, 128, 200, 4),           # window not a block multiple, 128-key blocks
     (1, 2, 1200, 32, 128, 64),          # the training schedule's first k
     (1, 2, 900, 64, 256, 20),           # two slot groups, the last one partial
-    pytest.param(1, 2, 800, 96, 288, 8,        # 96-key blocks: key stages spanning two blocks
-                 marks=pytest.mark.skip(reason=BIG_BLOCKS)),
-    pytest.param(1, 2, 1100, 256, 512, 4,      # 256-key blocks: four key stages per block
-                 marks=pytest.mark.skip(reason=BIG_BLOCKS)),
+    (1, 2, 800, 96, 288, 8),            # 96-key blocks: key stages that span two blocks
+    (1, 2, 1100, 256, 512, 4),          # 256-key blocks: four key stages per block
+    (1, 1, 43, 128, 31, 4),             # routed last block whose second key stage is past the end
 ])
 def test_backward_matches_torch_autograd(B, H, S, bs, lw, K):
     q, k, v, topi, bias, valid, dout = _case(10 + S + bs, B, H, S, bs, lw, K)

@@ -17,7 +17,6 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 # output tolerance of the path (bf16 output, fp32 accumulation)
 ATOL, RTOL = 2e-2, 1e-2
-BIG_BLOCKS = ("routed blocks of more than 64 keys are refused by the prefill entry points (a GPU memory fault with 128-key blocks whose routed last block reaches 64 or more keys past the sequence end; cause not found)")
 
 
 def _gen(seed):
@@ -199,8 +198,10 @@ def _attn_inputs(seed, B, H, S, bs, lw, K, qscale=1.0, dup=False):
     (1, 2, 300, 64, 128, 4, 3.0),
     (2, 3, 700, 64, 512, 8, 1.0),
     (1, 2, 513, 32, 100, 6, 3.0),     # window not a block multiple, bs 32
-    pytest.param(1, 1, 1100, 128, 256, 3, 2.0,   # bs 128 (tile path only)
-                 marks=pytest.mark.skip(reason=BIG_BLOCKS)),
+    (1, 1, 1100, 128, 256, 3, 2.0),   # bs 128 (tile path only)
+    # 128-key blocks, window 31: the last block is routed and its second 64-key item lies
+    # wholly past the end of the 43 tokens (its rows were once addressed out of bounds)
+    (1, 1, 43, 128, 31, 4, 2.0),
     (1, 2, 64, 64, 512, 4, 1.0),      # window covers everything
     (1, 2, 3000, 64, 256, 16, 2.0),   # many remote blocks per tile
 ])
