@@ -46,6 +46,9 @@ constexpr int kPfCH = 256;        // pairs per sparse chunk (work-group)
 // header and pair ids in one round trip.
 constexpr int kRecHead = 4;
 constexpr int kRec = kRecHead + kPfCH;
+// Largest K/V token stride (elements) whose 64-row byte offsets within a stage fit 32 bits:
+// 64 rows x 2 B x stride + 256 B of chunk offset < 2^32.
+constexpr int64_t kMaxKeyRowStride = (int64_t(1) << 25) - 64;
 
 struct PrefillArgs {
   const bf16* q; const bf16* k; const bf16* v;
@@ -1406,6 +1409,8 @@ extern "C" int dash_attn_prefill(
   const void* ptrs[] = {q, k, v, o};
   for (const void* p : ptrs)
     if ((uintptr_t)p % 16 != 0) return kErrUnsupported;
+  // the K/V stage loads form a row's byte offset inside a 64-key item in 32 bits
+  if (k_st > kMaxKeyRowStride || v_st > kMaxKeyRowStride) return kErrUnsupported;
   PrefillArgs a = {};
   a.q = (const bf16*)q; a.k = (const bf16*)k; a.v = (const bf16*)v;
   a.q_sb = q_sb; a.q_sh = q_sh; a.q_st = q_st;
@@ -1506,6 +1511,8 @@ extern "C" int dash_attn_prefill_backward(
     if (s % 8 != 0) return kErrUnsupported;
   // the key-major kernel forms the row offsets of Q and dO as 32 x 32-bit products
   if (q_st < 0 || q_st > INT32_MAX || do_st < 0 || do_st > INT32_MAX) return kErrUnsupported;
+  // K/V stage loads as in the forward
+  if (k_st > kMaxKeyRowStride || v_st > kMaxKeyRowStride) return kErrUnsupported;
   const void* ptrs[] = {q, k, v, o, dout, dq, dk, dv};
   for (const void* ptr : ptrs)
     if ((uintptr_t)ptr % 16 != 0) return kErrUnsupported;

@@ -19,6 +19,7 @@ topm} exactly as configure_dash_inference sets them (modeling_deepseekv2.py:299-
 An additive attention_mask is not supported (NotImplementedError); GPU tensors only.
 """
 
+import copy
 import math
 import os
 
@@ -108,6 +109,17 @@ class KSchedule:
 
 K_SCHEDULE = KSchedule()
 
+# sparse_attention_config as the checkpoint gave it, taken before the first router writes
+# its parameters into it (the role of modeling_deepseekv2.py:63-64): id of the live dict ->
+# (the live dict, its copy).  The live dict is held so that its id is never reused.
+CKPT_SP = {}
+
+
+def checkpoint_sparse_config(live):
+    """The copy of ``live`` taken before any router wrote into it, else ``live``."""
+    ent = CKPT_SP.get(id(live))
+    return ent[1] if ent is not None and ent[0] is live else live
+
 
 class GemmaRMSNorm(nn.Module):
     """RMSNorm with scale (1 + weight), fp32 math and the router's finiteness
@@ -163,14 +175,38 @@ class DashAttention(nn.Module):
         self.k_proj = nn.Linear(config.hidden_size, self.index_dim, bias=False)
         self.q_norm = GemmaRMSNorm(self.index_dim, eps=eps)
         self.k_norm = GemmaRMSNorm(self.index_dim, eps=eps)
-        self.stage0 = str(os.environ.get("DASH_STAGE0") or sp.get("dash_stage0", "indexer")).lower()
+        # training stage 0 comes from the environment only (dash_attention.py:748);
+        # the checkpoint's dash_stage0 is read by configure_dash_inference
+        self.stage0 = os.environ.get("DASH_STAGE0", "indexer").lower()
         self.head_cls = nn.Parameter(torch.zeros(self.index_dim))
         self._scale = 1.0 / math.sqrt(self.head_dim)
         self._idx_scale = self.scaling_factor / math.sqrt(self.index_dim)
         budget = sp.get("dash_topk_blocks") or sp.get("dash_image_fallback_remote") or 12
         self._infer_params = dict(idx_scale=self._idx_scale, floor=self._prior_floor,
                                   sigma=self.sigma, K=int(budget), topm=16)
+        if isinstance(sp, dict) and id(sp) not in CKPT_SP:
+            CKPT_SP[id(sp)] = (sp, copy.deepcopy(sp))
         self._ks_id = K_SCHEDULE.register()
+        self._sp = sp if isinstance(sp, dict) else None
+        self._persist_router_cfg()
+
+    def _persist_router_cfg(self):
+        """Write the router's live parameters into the config's sparse_attention_config
+        so that save_pretrained stores them (dash_attention.py:761-774); the first
+        registered layer only.  With the per-layer temperature loop off (its default,
+        and the only mode here) every layer's scale and floor are the config's."""
+        if self._sp is None or self._ks_id != K_SCHEDULE.leader:
+            return
+        n = K_SCHEDULE.registered
+        self._sp["dash_stage0"] = self.stage0
+        self._sp["dash_router"] = "entmax_topk_perlayer"
+        self._sp["dash_sigma"] = float(self.sigma)
+        self._sp["dash_topk_blocks"] = int(K_SCHEDULE.k)
+        self._sp["dash_scaling_factor"] = float(
+            self.scaling_factor / math.sqrt(self.index_dim) * math.sqrt(self.index_dim))
+        self._sp["dash_prior_floor"] = float(self._prior_floor)
+        self._sp["dash_scale_per_layer"] = [float(self.scaling_factor)] * n
+        self._sp["dash_floor_per_layer"] = [float(self._prior_floor)] * n
 
     # ---------------------------------------------------------------- router
     # fewest token rows for the fused front end: its work-groups own 64 rows and run
@@ -392,6 +428,7 @@ class DashAttention(nn.Module):
         if position_ids is None:
             position_ids = torch.arange(S, device=q.device)[None].expand(B, -1)
         K_SCHEDULE.advance(self._ks_id, self.training)
+        self._persist_router_cfg()
 
         iq, ik = self._index_qk_train(hidden_states, position_embeddings)
         if self.stage0 == "head_cls":

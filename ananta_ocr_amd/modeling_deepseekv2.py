@@ -24,11 +24,12 @@ fused decode launch, ops.decode_step_fused).
 """
 
 import math
+import os
 
 import torch
 
 from . import ops, pages
-from .dash_attention import DashAttention, apply_rotary
+from .dash_attention import DashAttention, apply_rotary, checkpoint_sparse_config
 
 _INFER = {"on": False}
 
@@ -36,8 +37,10 @@ _INFER = {"on": False}
 def configure_dash_inference(decoder, on, topm=16, page_scope_prefill=True, state=None):
     """Switch inference routing on/off for every DashAttention in ``decoder``
     (modeling_deepseekv2.py:269-306): sets ``_infer_params`` = {idx_scale, floor,
-    sigma, K, topm} per router from the config's per-layer scale/floor arrays
-    (indexed by the router's slot among the sparse layers, :256-266)."""
+    sigma, K, topm} per router from the checkpoint's sparse_attention_config (the copy
+    taken before the routers wrote into it) and its per-layer scale/floor arrays,
+    indexed by the layer's slot among the sparse layers (:256-266).  Stage 0 is
+    DASH_STAGE0 if set, else the checkpoint's dash_stage0, else "indexer"."""
     if not on:
         if state is not None:
             pages.PAGE_SCOPE["prefill"] = state["page_scope_prefill"]
@@ -47,13 +50,13 @@ def configure_dash_inference(decoder, on, topm=16, page_scope_prefill=True, stat
         return None
     state = {"stage0": [], "page_scope_prefill": pages.PAGE_SCOPE["prefill"]}
     cfg = getattr(decoder, "config", None)
-    sp = (getattr(cfg, "sparse_attention_config", None) or {}) if cfg is not None else {}
-    stage0 = str(sp.get("dash_stage0") or "indexer").lower()
+    live = (getattr(cfg, "sparse_attention_config", None) or {}) if cfg is not None else {}
+    sp = checkpoint_sparse_config(live)
+    stage0 = str(os.environ.get("DASH_STAGE0") or sp.get("dash_stage0") or "indexer").lower()
     budget = sp.get("dash_topk_blocks") or sp.get("dash_image_fallback_remote") or 12
-    routers = [m for m in decoder.modules() if isinstance(m, DashAttention)]
-    for li, router in enumerate(routers):
-        scale = _per_layer(sp, "dash_scale_per_layer", li)
-        floor = _per_layer(sp, "dash_floor_per_layer", li)
+    for slot, router in _dash_routers(decoder, sp):
+        scale = _per_layer(sp, "dash_scale_per_layer", slot)
+        floor = _per_layer(sp, "dash_floor_per_layer", slot)
         if scale is None:
             scale = float(sp.get("dash_scaling_factor", router.scaling_factor))
         if floor is None:
@@ -69,11 +72,37 @@ def configure_dash_inference(decoder, on, topm=16, page_scope_prefill=True, stat
     return state
 
 
-def _per_layer(sp, key, idx):
+def _sched_slot(sp, layer_idx):
+    """Index of a layer's entry in the per-layer arrays (modeling_deepseekv2.py:256-260):
+    its count among the sparse layers of sparse_attention_freq, else the layer index."""
+    freq = sp.get("sparse_attention_freq")
+    if not isinstance(freq, (list, tuple)) or layer_idx >= len(freq):
+        return int(layer_idx)
+    return sum(1 for f in freq[:layer_idx] if f)
+
+
+def _dash_routers(decoder, sp):
+    """(slot, router) of every DashAttention of ``decoder``: through decoder.layers[i]
+    .self_attn.dash_router with the layer's layer_idx, as the reference walks them;
+    a module tree without such layers gives its routers in order, slot = that order."""
+    layers = getattr(decoder, "layers", None)
+    if layers is not None:
+        out = []
+        for i, layer in enumerate(layers):
+            attn = getattr(layer, "self_attn", None)
+            router = getattr(attn, "dash_router", None)
+            if isinstance(router, DashAttention):
+                out.append((_sched_slot(sp, int(getattr(attn, "layer_idx", i))), router))
+        if out:
+            return out
+    return list(enumerate(m for m in decoder.modules() if isinstance(m, DashAttention)))
+
+
+def _per_layer(sp, key, slot):
     arr = sp.get(key)
     if not isinstance(arr, (list, tuple)) or not arr:
         return None
-    return float(arr[idx]) if 0 <= idx < len(arr) else None
+    return float(arr[slot]) if 0 <= slot < len(arr) else None
 
 
 @torch.no_grad()

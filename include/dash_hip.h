@@ -5,7 +5,10 @@
  * Conventions shared by every entry point
  *   - Every pointer argument is a device pointer unless stated otherwise; the
  *     caller owns every buffer (outputs and workspace included).  The library
- *     allocates nothing and keeps no state between calls.
+ *     allocates nothing.  It keeps no state between calls, except for the
+ *     allocation-free decode entry point (dash_decode_step_noalloc): a fixed 64 MiB
+ *     device array per GPU, held until the process ends, and that array's address per
+ *     device, looked up on the first call on each device.
  *   - Strides are in elements, not bytes.  The innermost (feature) axis must be
  *     contiguous; bf16 tensors need 16-byte aligned rows.
  *   - `stream` is a hipStream_t; all work is enqueued on it, nothing synchronises.

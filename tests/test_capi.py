@@ -9,6 +9,7 @@ import pytest
 from ananta_ocr_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ERR_UNSUPPORTED = -2             # kErrUnsupported, a shape or stride the kernels do not take
 ERR_INVALID = -3                 # kErrInvalid, inconsistent arguments
 
 
@@ -98,6 +99,12 @@ def test_argument_checks_return_before_any_device_call():
                dq_sb=0, dq_sh=0, dq_st=128, dk_sb=0, dk_sh=0, dk_st=128, dv_sb=0, dv_sh=0,
                dv_st=128, workspace_bytes=1 << 40, stream=None)
     assert _call("dash_attn_prefill_backward", **bwd, total_rows=1999) == ERR_INVALID
+    # a K/V token stride whose 64-row stage offsets would not fit 32 bits
+    big = (1 << 25) - 56
+    for kv in (dict(k_st=big), dict(v_st=big)):
+        assert _call("dash_attn_prefill", **dict(fwd, **kv), total_rows=2000) == ERR_UNSUPPORTED
+        assert _call("dash_attn_prefill_backward", **dict(bwd, **kv),
+                     total_rows=2000) == ERR_UNSUPPORTED
     dec = dict(iq_sb=128, ik_sb=0, ik_st=128, ik_sp=0, block_table=None, table_stride=0,
                page_size=0, seq_lens=None, q_pos=None, head_cls=1, refresh_tail=1, kb_sb=0,
                kb_table=None, kb_ts=0, bounds=None, cand=None, cand_stride=0, B=2, d=128,

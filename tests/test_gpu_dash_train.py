@@ -27,7 +27,7 @@ DEV = "cuda"
 def _config(H, bs, lb, stage0, scaling):
     sp = dict(sparse_block_size=bs, sparse_local_block=lb, dash_scaling_factor=scaling,
               dash_sigma=1.0, dash_prior_floor=1e-2, dash_image_only=False,
-              sparse_index_dim=128, dash_stage0=stage0)
+              sparse_index_dim=128)
     return SimpleNamespace(num_attention_heads=H, hidden_size=H * 128, rms_norm_eps=1e-6,
                            sparse_attention_config=sp)
 
@@ -55,6 +55,7 @@ def test_training_forward_and_gradients_match_oracle(stage0, H, S, bs, lb, K, mo
     # process): pin its k for this test
     monkeypatch.setattr(DA.K_SCHEDULE, "k", K)
     monkeypatch.setattr(DA.K_SCHEDULE, "advance", lambda sid, training: None)
+    monkeypatch.setenv("DASH_STAGE0", stage0)          # read by the constructor only
     g = torch.Generator().manual_seed(S + bs)
     cfg = _config(H, bs, lb, stage0, scaling=0.35)
     torch.manual_seed(S)

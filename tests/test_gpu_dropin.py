@@ -32,7 +32,8 @@ def _config(stage0, bs=64, lb=4, budget=6, scale=128.0, hidden=256, heads=2):
 
 
 @pytest.mark.parametrize("stage0", ["head_cls", "indexer"])
-def test_dash_attention_forward_matches_oracle(stage0):
+def test_dash_attention_forward_matches_oracle(stage0, monkeypatch):
+    monkeypatch.setenv("DASH_STAGE0", stage0)
     torch.manual_seed(0)
     cfg = _config(stage0)
     mod = DashAttention(cfg).eval()

@@ -16,6 +16,29 @@ IMG, PG, TXT, BOS = 5, 9, 7, 1
 PROMPT = [BOS, PG, IMG, IMG, IMG, PG, IMG, IMG, PG, IMG, IMG, IMG, TXT, TXT, PG, TXT, PG, TXT]
 
 
+def test_flat_image_token_mask_known_answer():
+    """The flat (any page) image-token mask of _build_flat_image_token_mask
+    (_sparse_base_impl.py:2363-2380): ids == image id over key_length tokens, the ids
+    cut or padded with -1, None without an image token or for ids that are not 2-D;
+    and the product's torch function (pages.build_flat_image_token_mask) equals it."""
+    from ananta_ocr_amd import pages as P
+    ids = torch.tensor([PROMPT, [TXT] * len(PROMPT)])
+    want = [[x == IMG for x in PROMPT], [False] * len(PROMPT)]
+    for L in (len(PROMPT), 10, len(PROMPT) + 5):
+        m = O.flat_image_token_mask(ids, IMG, L)
+        exp = [r[:L] + [False] * max(0, L - len(r)) for r in want]
+        assert m.tolist() == exp, L
+        assert torch.equal(P.build_flat_image_token_mask(ids, IMG, L), m), L
+    # the ids are padded with -1 before the comparison, so an image id of -1 matches the
+    # padding, as in the reference
+    assert O.flat_image_token_mask(torch.tensor([[TXT, TXT]]), -1, 4).tolist() == \
+        [[False, False, True, True]]
+    assert O.flat_image_token_mask(torch.tensor([[TXT, TXT]]), IMG, 2) is None
+    assert O.flat_image_token_mask(torch.tensor([IMG, IMG]), IMG, 2) is None
+    assert O.flat_image_token_mask(None, IMG, 2) is None
+    assert P.build_flat_image_token_mask(torch.tensor([[TXT, TXT]]), IMG, 2) is None
+
+
 def test_page_ids_marker_mode_known_answer():
     ids = torch.tensor([PROMPT])
     itm, ipi, qpi = O.page_aware_ids(ids, IMG, PG, len(PROMPT), per_page=3)

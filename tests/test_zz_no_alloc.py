@@ -55,6 +55,9 @@ def test_noalloc_decode_step_matches_workspace_entry_point():
 def test_noalloc_refuses_sizes_beyond_its_scratch():
     """Refused on the host before any device call: the workspace these sizes need
     exceeds the fixed array."""
+    if torch.cuda.is_available():
+        # the placeholder pointers must never reach a launch on a real device
+        pytest.skip("argument checks are exercised where no device is present")
     lib = _lib.load()
     cap = lib.dash_decode_step_scratch_bytes()
     assert cap == 64 << 20
