@@ -16,7 +16,7 @@ attention in ``libdash_hip.so`` with gradients to q, k, v and the bias
 The inference form (modeling_deepseekv2.py:309-333: top-M by score, entmax over
 the M, first K) is ``route``; ``_infer_params`` holds {idx_scale, floor, sigma, K,
 topm} exactly as configure_dash_inference sets them (modeling_deepseekv2.py:299-301).
-An additive attention_mask is not supported (NotImplementedError); GPU tensors only.
+An additive attention_mask (padding) is taken as per-row key starts; GPU tensors only.
 """
 
 import copy
@@ -147,6 +147,75 @@ def apply_rotary(q, k, cos, sin):
     cos = cos.unsqueeze(1)
     sin = sin.unsqueeze(1)
     return q * cos + _rotate_half(q) * sin, k * cos + _rotate_half(k) * sin
+
+
+MASK_NEG = -1.0e9
+# additive-mask entries at or below this exclude a key from a row that keeps another key
+# (exp(-1e4) is 0 in fp32 next to the row's own window keys)
+MASK_EXCLUDE = -1.0e4
+# a row whose every causal key is excluded attends uniformly to all S keys in the
+# reference (every logit clamps to -1e9): that needs entries that clamp exactly,
+# whatever block bias they add to
+MASK_EXCLUDE_ALL = -2.0e9
+
+
+@torch.no_grad()
+def mask_key_starts(attention_mask, B, S, q_chunk=2048):
+    """The additive attention mask of _forward_dense (dash_attention.py:1001-1003: added
+    to the DASH mask, clamped at -1e9) as per-row key starts.
+
+    attention_mask [B or 1, 1 or H, >= S, >= S]; its [:, :, :S, :S] part is used, as in
+    the reference.  Each entry must be 0 (allowed) or <= -1e4 (excluded), equal over
+    heads; each row t's allowed keys j <= t must be a suffix [kmin_t, t] (left padding,
+    block-diagonal documents), or empty with every causal entry <= -2e9 (a padding row,
+    which the reference attends uniformly over all S keys).  Returns (kmin [B, S]
+    int32, empty [B, S] bool); empty rows get kmin 0.  Other masks raise
+    NotImplementedError (one host synchronisation)."""
+    am = attention_mask
+    if am.dim() != 4 or am.shape[-2] < S or am.shape[-1] < S:
+        raise NotImplementedError(f"attention_mask of shape {tuple(am.shape)}")
+    am = am[:, :, :S, :S]
+    ok = torch.ones((), dtype=torch.bool, device=am.device)
+    if am.shape[1] != 1:
+        ok = ok & (am == am[:, :1]).all()
+    am = am[:, 0]
+    kidx = torch.arange(S, device=am.device)
+    kmin = torch.empty(B, S, dtype=torch.int32, device=am.device)
+    empty = torch.empty(B, S, dtype=torch.bool, device=am.device)
+    for q0 in range(0, S, q_chunk):
+        q1 = min(q0 + q_chunk, S)
+        a = am[:, q0:q1].float().expand(B, q1 - q0, S)
+        qidx = torch.arange(q0, q1, device=am.device)
+        causal = kidx[None, None, :] <= qidx[None, :, None]
+        zero = a == 0
+        allowed = zero & causal
+        cnt = allowed.sum(-1)
+        first = torch.where(cnt > 0, allowed.to(torch.int8).argmax(-1), qidx[None] + 1)
+        e = cnt == 0
+        ok = ok & (zero | (a <= MASK_EXCLUDE)).all()
+        ok = ok & (cnt == qidx[None] - first + 1).all()
+        ok = ok & (~e | ((a <= MASK_EXCLUDE_ALL) | ~causal).all(-1)).all()
+        kmin[:, q0:q1] = torch.where(e, torch.zeros_like(first), first).to(torch.int32)
+        empty[:, q0:q1] = e
+    if not bool(ok):
+        raise NotImplementedError(
+            "attention_mask rows must allow a suffix [kmin, t] of their causal keys (entries "
+            "0 / <= -1e4, equal over heads), or no causal key with entries <= -2e9")
+    return kmin, empty
+
+
+def _fill_empty_rows(out, v, empty):
+    """Rows whose causal keys are all masked: the reference's logits there are
+    q.k*scale - 1e9 for every one of the S keys, which round to -1e9, so its softmax is
+    uniform and the row is the mean of v over all S keys (per head).  The gradient is
+    that mean's (to v only).  The reference's own backward of such a row depends on how
+    its attention backend rounds -1e9 + s (a backward that recomputes exp(s - lse) with
+    both rounded to -1e9 takes every weight as 1), so it has no single value; these are
+    padding rows, whose upstream gradient is zero in a padded batch."""
+    if empty is None:
+        return out
+    vm = v.float().mean(2, keepdim=True).to(out.dtype)
+    return torch.where(empty[:, None, :, None], vm, out)
 
 
 class DashAttention(nn.Module):
@@ -314,20 +383,23 @@ class DashAttention(nn.Module):
     def _forward_dense(self, q, k, v, topi, blk_bias, valid, S, nblk, attention_mask):
         """The same attention over token positions 0..S-1 (dash_attention.py:980-1006:
         window keys with bias 0, keys of valid routed blocks below the window with the
-        block's bias).  An additive attention_mask is not supported by the kernels and
-        raises NotImplementedError (there is no second code path)."""
-        if attention_mask is not None:
-            raise NotImplementedError("additive attention_mask is not supported by the HIP path")
+        block's bias).  An additive attention_mask (padding) becomes per-row key starts
+        (``mask_key_starts``); a row it masks completely is the mean of v, as the
+        reference's clamped softmax gives; a mask of another form raises
+        NotImplementedError (there is no second code path)."""
         if k.shape[2] != S or q.shape[2] != S:
             raise NotImplementedError("query and key lengths must both be S")
+        kmin = empty = None
+        if attention_mask is not None:
+            kmin, empty = mask_key_starts(attention_mask, q.shape[0], S)
         if k.shape[1] != q.shape[1]:
             rep = q.shape[1] // k.shape[1]
             k = k.repeat_interleave(rep, dim=1)
             v = v.repeat_interleave(rep, dim=1)
         out = ops.attn_prefill(q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16),
                                topi, blk_bias, valid, self.block_size, self.local_window,
-                               self._scale)
-        return out.to(q.dtype)
+                               self._scale, kmin=kmin)
+        return _fill_empty_rows(out, v, empty).to(q.dtype)
 
     # ---------------------------------------------------------------- training stage 0
     def _index_qk_train(self, hidden_states, position_embeddings):
@@ -421,10 +493,12 @@ class DashAttention(nn.Module):
         dash_image_only); page_ids are diagnostics in the reference and are ignored.
         The reference's per-layer temperature loop (DASH_SPARSITY_SCHED, off by
         default) is not implemented: idx_scale and the prior floor are the config's."""
-        if attention_mask is not None:
-            raise NotImplementedError("additive attention_mask is not supported by the HIP path")
         B, H, S, D = q.shape
         nblk = (S + self.block_size - 1) // self.block_size
+        kmin = empty = None
+        if attention_mask is not None:
+            # the reference's dense fallback with the mask (dash_attention.py:1064-1071)
+            kmin, empty = mask_key_starts(attention_mask, B, S)
         if position_ids is None:
             position_ids = torch.arange(S, device=q.device)[None].expand(B, -1)
         K_SCHEDULE.advance(self._ks_id, self.training)
@@ -449,5 +523,6 @@ class DashAttention(nn.Module):
             v = v.repeat_interleave(rep, dim=1)
         bf = torch.bfloat16
         out = ops.attn_prefill_autograd(q.to(bf), k.to(bf), v.to(bf), topi, blk_bias, valid,
-                                        self.block_size, self.local_window, self._scale)
-        return out.to(q.dtype)
+                                        self.block_size, self.local_window, self._scale,
+                                        kmin=kmin)
+        return _fill_empty_rows(out, v, empty).to(q.dtype)

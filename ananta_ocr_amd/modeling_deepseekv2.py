@@ -260,15 +260,17 @@ def _infer_prefill_attend(self, router, hidden_states, q, k, v, idx_pe, pos_ids,
 
 @torch.no_grad()
 def _decode_attend(q, k_all, v_all, topi, bias, valid, q_pos, block_size, local_window, scale):
-    """Decode attention for Lq == 1 queries at q_pos [B,1] (modeling_deepseekv2.py:424-451).
-    q [B,H,1,D]; k_all/v_all [B,Hkv,S,D]; returns fp32 [B,H,1,D]."""
+    """Decode attention for queries at q_pos [B,Lq] (modeling_deepseekv2.py:424-451).
+    q [B,H,Lq,D]; k_all/v_all [B,Hkv,S,D]; topi/bias/valid [B,Lq,K]; row (b, l) attends
+    the keys j <= q_pos[b, l] of sequence b.  Returns fp32 [B,H,Lq,D]."""
     B, H, Lq, D = q.shape
-    if Lq != 1:
-        raise NotImplementedError("one decode query per sequence")
     if k_all.shape[1] != H:
         rep = H // k_all.shape[1]
         k_all = k_all.repeat_interleave(rep, dim=1)
         v_all = v_all.repeat_interleave(rep, dim=1)
+    if Lq != 1:
+        return ops.attn_decode_rows(q, k_all, v_all, topi, bias, valid,
+                                    q_pos.reshape(B, Lq), block_size, local_window, scale)
     qp = q_pos.reshape(B).to(torch.int32)
     lens = (qp + 1).clamp(max=k_all.shape[2]).to(torch.int32)
     return ops.attn_decode(q[:, :, 0].to(torch.bfloat16), k_all, v_all, topi[:, 0].to(torch.int32),
@@ -293,14 +295,13 @@ def _dash_indexer_rope(self, idx, router, x, pos_ids, coords, main_pe):
 def _dash_decode_attend(self, router, hidden_states, q, k_all, v_all, idx_pe, position_ids,
                         past_kv):
     """The DASH part of one decode step (modeling_deepseekv2.py:480-498) after the cache
-    update: router projections of the new token, its index key appended to the layer's
-    decode state, block scores, routing (with the layer's page-aware ``_dash_dec_allow``
-    candidates when ``router.image_only``) and attention.  q [B,H,1,D] (RoPE'd),
-    k_all/v_all [B,Hkv,S,D] the updated cache, position_ids [B,1].  Returns fp32
-    [B,H,1,D]."""
+    update: router projections of the new tokens, their index keys appended to the
+    layer's decode state, block scores, routing (with the layer's page-aware
+    ``_dash_dec_allow`` candidates when ``router.image_only``) and attention.  q
+    [B,H,Lq,D] (RoPE'd), k_all/v_all [B,Hkv,S,D] the updated cache, position_ids [B,Lq].
+    One row per sequence runs as one fused step; several rows per sequence each route
+    and attend at their own position.  Returns fp32 [B,H,Lq,D]."""
     B, H, Lq, D = q.shape
-    if Lq != 1:
-        raise NotImplementedError("one decode query per sequence")
     p = router._infer_params
     caches = _decode_caches(past_kv)
     dc = caches.get(self.layer_idx)
@@ -326,6 +327,9 @@ def _dash_decode_attend(self, router, hidden_states, q, k_all, v_all, idx_pe, po
         if allow.shape[-1] < nblk:
             allow = torch.nn.functional.pad(allow, (0, nblk - allow.shape[-1]), value=False)
         cand = allow[:, :nblk]
+    if Lq != 1:
+        return _dash_decode_rows(router, dc, q, k_all, v_all, idx_q, cand,
+                                 position_ids.reshape(B, Lq), p)
     qpos = position_ids.reshape(B, -1)[:, -1]
     if dc.kbar is not None:
         # fused step: tail summary refresh + scores + routing + attention
@@ -340,6 +344,31 @@ def _dash_decode_attend(self, router, hidden_states, q, k_all, v_all, idx_pe, po
     topi, bias, valid = _infer_route_select(sc, None if cand is None else cand[:, None], p)
     return _decode_attend(q, k_all, v_all, topi, bias, valid, qpos[:, None], router.block_size,
                           router.local_window, router._scale)
+
+
+@torch.no_grad()
+def _dash_decode_rows(router, dc, q, k_all, v_all, idx_q, cand, q_pos, p):
+    """Lq > 1 decode rows of one step (modeling_deepseekv2.py:480-498 with q_len rows at
+    position_ids [B, Lq]): the block summaries of every block the new tokens touched are
+    recomputed, then block scores of each row at its own position, routing, and the
+    attention of each row against the cache.  Returns fp32 [B,H,Lq,D]."""
+    B, Lq = q_pos.shape
+    S = dc.S
+    bs = router.block_size
+    nblk = (S + bs - 1) // bs
+    if dc.kbar is not None:
+        c0 = (S - Lq) // bs
+        ops.kbar(dc._buf[:, c0 * bs:S], dc.head_cls, bs, nblk_cap=nblk - c0,
+                 out=dc.kbar[:, c0:nblk])
+        sc = ops.block_scores(idx_q, dc.kbar[:, :nblk], bs, router.local_blocks,
+                              q_pos=q_pos.to(torch.int32), S=S)
+    else:
+        sc = _block_scores_infer(router, idx_q, dc.idx_k, q_pos, nblk)
+    if cand is not None:
+        cand = cand[:, None, :].expand(B, Lq, nblk)
+    topi, bias, valid = _infer_route_select(sc, cand, p)
+    return _decode_attend(q, k_all, v_all, topi, bias, valid, q_pos, bs, router.local_window,
+                          router._scale)
 
 
 def _dash_decode_forward(self, hidden_states, position_ids, past_kv):

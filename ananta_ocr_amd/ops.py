@@ -632,6 +632,63 @@ def attn_decode(q, k, v, idx, bias, valid, block_size, local_window, scale, seq_
     return (out, lse) if return_lse else out
 
 
+def attn_decode_rows(q, k, v, idx, bias, valid, q_pos, block_size, local_window, scale,
+                     seq_lens=None, block_table=None, page_size=None, out_dtype=torch.float32):
+    """Decode attention for Lq query rows per sequence, each at its own position.
+    q [B,H,Lq,D] bf16; idx/bias/valid [B,Lq,K]; q_pos [B,Lq].  Cache contiguous
+    [B,H,S,D] or paged [pages, page_size, H, D] with block_table [B,P] and seq_lens [B].
+    Row (b, l) attends keys j <= q_pos[b,l] (and j < the sequence's length) of sequence b.
+    Returns out [B,H,Lq,D] (out_dtype).
+
+    Each row runs as its own decode query of dash_attn_decode over a block table whose
+    row b * Lq + l addresses sequence b: for a contiguous cache, one page per sequence
+    that spans its whole length (page b at the sequence's batch offset), so no cache
+    data moves."""
+    _need_gpu(q, k, v, q_pos)
+    lib = _lib.load()
+    B, H, Lq, D = q.shape
+    R = B * Lq
+    qr = _rows(q.to(torch.bfloat16).permute(0, 2, 1, 3).reshape(R, H, D))
+    k = _rows(k.to(torch.bfloat16))
+    v = _rows(v.to(torch.bfloat16))
+    if block_table is not None:
+        table = _i32(block_table).repeat_interleave(Lq, 0)
+        page = int(page_size)
+        S = table.shape[1] * page
+        k_sp, k_st, k_sh = k.stride(0), k.stride(1), k.stride(2)
+        v_sp, v_st, v_sh = v.stride(0), v.stride(1), v.stride(2)
+        lens = None if seq_lens is None else _i32(seq_lens).repeat_interleave(Lq, 0)
+    else:
+        S = k.shape[2]
+        page = max(block_size, (S + block_size - 1) // block_size * block_size)
+        table = torch.arange(B, dtype=torch.int32, device=q.device).repeat_interleave(Lq)[:, None]
+        k_sp, k_st, k_sh = k.stride(0), k.stride(2), k.stride(1)
+        v_sp, v_st, v_sh = v.stride(0), v.stride(2), v.stride(1)
+        lens = torch.full((R,), S, dtype=torch.int32, device=q.device) if seq_lens is None \
+            else _i32(seq_lens).repeat_interleave(Lq, 0)
+    K = 0 if idx is None else idx.shape[-1]
+    idx_c = None if idx is None else _i32(idx.reshape(R, K))
+    bias_c = None if bias is None else bias.reshape(R, K).float().contiguous()
+    valid_c = None if valid is None else _u8(valid.reshape(R, K))
+    qp = _i32(q_pos.reshape(R))
+    nsplit = default_nsplit((local_window + block_size - 1) // block_size + 1 + K)
+    ws_bytes = ctypes.c_int64(0)
+    _lib.check(lib.dash_attn_decode_workspace_size(R, H, D, nsplit, ws_bytes), "workspace")
+    ws = torch.empty((ws_bytes.value + 3) // 4, dtype=torch.float32, device=q.device)
+    out = torch.empty(B, Lq, H, D, dtype=out_dtype, device=q.device)
+    o2 = out.view(R, H, D)
+    st_ = lib.dash_attn_decode(
+        _ptr(qr), qr.stride(0), qr.stride(1),
+        _ptr(k), 0, k_sh, k_st, k_sp, _ptr(v), 0, v_sh, v_st, v_sp,
+        _ptr(table), table.stride(0), page, _ptr(lens), _ptr(qp),
+        _ptr(idx_c), _ptr(valid_c), _ptr(bias_c), K,
+        _ptr(o2), int(out_dtype == torch.bfloat16), o2.stride(0), o2.stride(1),
+        None, 0, 0, R, H, S, D, int(block_size), int(local_window), float(scale), int(nsplit),
+        _ptr(ws), ws.numel() * 4, _stream())
+    _lib.check(st_, "dash_attn_decode")
+    return out.permute(0, 2, 1, 3)
+
+
 def _kbar_layout(kbar_cache, kbar_table, bounds):
     """(nblk_cap, kb_sb, table int32 or None, kb_ts, bounds int32 or None) of a k_bar
     cache: per sequence [B, nblk_cap, d], or a page pool [pages, d] addressed through

@@ -76,12 +76,12 @@ def gather_attention(query_states, key_states, value_states, block_indices, posi
     if Hkv != HQ:
         key_states = key_states.repeat_interleave(HQ // Hkv, dim=1)
         value_states = value_states.repeat_interleave(HQ // Hkv, dim=1)
+    # every row's segment start (sparse_gather_triton.py:374), 0 on unpacked rows; the
+    # kernels read it per token row b * T + t, so packed rows of any batch size work
     ar = torch.arange(T, device=position_ids.device)
-    seg = (ar[None, :] - position_ids).to(torch.int32)
-    if B != 1 and bool((seg != 0).any()):
-        raise NotImplementedError("packed rows are supported with batch 1")
+    seg = (ar[None, :] - position_ids).to(torch.int32).expand(B, T)
     lw = block_size if local_window is None else max(1, int(local_window))
-    kmin = None if not bool((seg != 0).any()) else seg.reshape(-1)
+    kmin = seg.reshape(-1)
     grad = torch.is_grad_enabled() and any(t.requires_grad for t in
                                            (query_states, key_states, value_states))
     # query head h reads index head h // (HQ / HI) (sparse_gather_triton.py:47)

@@ -342,13 +342,15 @@ def dense_block_bias(topi, bias, valid, nblk):
 
 
 def dense_attend(q, k, v, topi, bias, valid, block_size, local_window, scale,
-                 q_chunk=2048, kmin=None, rows=None):
+                 q_chunk=2048, kmin=None, rows=None, attention_mask=None):
     """Prefill DASH attention, fp32: dash_attention.py:980-1006.
 
     Key j is kept for query t when it is causal and either in the token-level
     window ``(t - LW, t]`` (bias 0) or in a routed block (bias of that block);
     the window wins on overlap.  ``kmin`` [B,S] (optional) adds ``j >= kmin[t]``
     (the packing segment start of sparse_gather_triton.py:42,63,73).
+    ``attention_mask`` (optional, additive, [B or 1, 1 or H, >= S, >= S]) is added to
+    the mask before the clamp at -1e9, as dash_attention.py:1001-1003 does.
     q, k, v: [B,H,S,D]; topi/bias/valid: [B,S,K].  Returns [B,H,S,D] fp32.
     """
     q = q.float(); k = k.float(); v = v.float()
@@ -372,6 +374,8 @@ def dense_attend(q, k, v, topi, bias, valid, block_size, local_window, scale,
             keep = keep & (kidx[None, None, None, :] >= kmin[:, None, qs:qe, None].long())
         mask = torch.where(local, torch.zeros_like(base), base)
         mask = mask.masked_fill(~keep, MASK_NEG)
+        if attention_mask is not None:
+            mask = mask + attention_mask[:, :, qs:qe, :S].to(mask.dtype)
         mask = mask.clamp_min(MASK_NEG)
         out_chunks.append(F.scaled_dot_product_attention(
             q[:, :, qs:qe], k, v, attn_mask=mask, is_causal=False, scale=scale))

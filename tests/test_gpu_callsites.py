@@ -182,11 +182,15 @@ def test_forward_triton_and_dense_match_reference_semantics():
         _close(o2, ref, "_forward_dense")
         # non-arange positions: the fused entry point declines, as the reference's does
         assert router._forward_triton(*a, S, nblk, (pos + 1).to(DEV)) is None
+        # an all-open additive mask: the same attention; a mask with a hole is refused
+        o3 = router._forward_dense(*a, S, nblk, torch.zeros(1, 1, S, S, device=DEV))
+        _close(o3, ref, "_forward_dense, open mask")
+        hole = torch.zeros(1, 1, S, S, device=DEV)
+        hole[..., 5] = -1e30
         with pytest.raises(NotImplementedError):
-            router._forward_dense(*a, S, nblk, torch.zeros(1, 1, S, S, device=DEV))
+            router._forward_dense(*a, S, nblk, hole)
         with pytest.raises(NotImplementedError):
-            router(torch.zeros(B, S, 256, device=DEV), *a[:3],
-                   attention_mask=torch.zeros(1, 1, S, S, device=DEV))
+            router(torch.zeros(B, S, 256, device=DEV), *a[:3], attention_mask=hole)
 
 
 def test_decode_position_before_cache_end():

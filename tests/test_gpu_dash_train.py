@@ -123,9 +123,12 @@ def test_training_forward_and_gradients_match_oracle(stage0, H, S, bs, lb, K, mo
         _grad_close(got[n], ref_p[n], n, 5e-2)
 
 
-def test_training_forward_rejects_attention_mask():
+def test_training_forward_rejects_unsupported_attention_mask():
+    """A right-padded mask (pad query rows keep keys [0, len), not a suffix of their
+    causal range) is refused before any kernel runs."""
     mod = DA.DashAttention(_config(2, 64, 2, "indexer", 1.0)).to(DEV)
     q = torch.zeros(1, 2, 128, 128, dtype=torch.bfloat16, device=DEV)
+    i = torch.arange(128, device=DEV)
+    right = torch.where((i[None, :] <= i[:, None]) & (i[None, :] < 100), 0.0, -1e30)
     with pytest.raises(NotImplementedError):
-        mod(torch.zeros(1, 128, 256, device=DEV), q, q, q,
-            attention_mask=torch.zeros(1, 1, 128, 128, device=DEV))
+        mod(torch.zeros(1, 128, 256, device=DEV), q, q, q, attention_mask=right[None, None])

@@ -96,11 +96,18 @@ def test_dash_attention_candidate_mask_and_errors():
                                          p["sigma"], p["K"], p["topm"])
     ref = O.dense_attend(q.cpu(), k.cpu(), v.cpu(), t_r, b_r, v_r, 64, 256, 1 / math.sqrt(128))
     _close(out, ref, "DashAttention block_cand")
+    # an all-open additive mask is the plain path; a right-padded one (pad query rows
+    # keep keys that are not a suffix of their causal range) is refused
+    out_m = MD._infer_prefill_attend(layer, mod, hs, q, k, v, None, pos, cand,
+                                     torch.zeros(1, 1, S, S, device=DEV), None)
+    _close(out_m, ref, "DashAttention block_cand, open mask")
+    i = torch.arange(S, device=DEV)
+    right = torch.where((i[None, :] <= i[:, None]) & (i[None, :] < 600), 0.0, -1e30)
     with pytest.raises(NotImplementedError):
         MD._infer_prefill_attend(layer, mod, hs, q, k, v, None, pos, None,
-                                 torch.zeros(1, 1, S, S, device=DEV), None)
-    with pytest.raises(NotImplementedError):          # no additive mask in the training forward
-        mod(hs, q, k, v, attention_mask=torch.zeros(1, 1, S, S, device=DEV))
+                                 right[None, None], None)
+    with pytest.raises(NotImplementedError):
+        mod(hs, q, k, v, attention_mask=right[None, None])
 
 
 def test_gather_attention_e2e_matches_oracle_and_returns_none():

@@ -416,6 +416,63 @@ def test_decode_attend_equals_prefill_last_row_and_brute_force():
         torch.testing.assert_close(dec[:, :, 0], full[:, :, t], atol=1e-5, rtol=1e-5)
 
 
+def _left_pad_mask(B, S, pads, fill):
+    """HF-style 4-D additive mask: causal, and keys before the row's left padding end
+    excluded, with ``fill`` for excluded entries."""
+    i = torch.arange(S)
+    m = torch.zeros(B, 1, S, S)
+    for b, p in enumerate(pads):
+        bad = (i[None, :] > i[:, None]) | (i[None, :] < p)
+        m[b, 0] = torch.where(bad, torch.full((), fill), torch.zeros(()))
+    return m
+
+
+def test_dense_attend_attention_mask_left_padding():
+    """The additive mask term (dash_attention.py:1001-1003): an all-zero mask changes
+    nothing; with left padding, a row past the padding attends the key-set enumeration
+    with segment start = the padding length; a row whose causal keys are all padding
+    gets every logit clamped to -1e9, so the mean of v over all S keys."""
+    B, S = 2, 60
+    q, k, v, topi, bias, valid, bs, lw = _attn_case(33, B=B, S=S)
+    scale = 0.3
+    plain = O.dense_attend(q, k, v, topi, bias, valid, bs, lw, scale)
+    zero = O.dense_attend(q, k, v, topi, bias, valid, bs, lw, scale,
+                          attention_mask=torch.zeros(1, 1, S, S))
+    assert torch.equal(plain, zero)
+    pads = [0, 23]
+    am = _left_pad_mask(B, S, pads, torch.finfo(torch.float32).min)
+    out = O.dense_attend(q, k, v, topi, bias, valid, bs, lw, scale, q_chunk=19,
+                         attention_mask=am)
+    kmin = torch.tensor(pads)[:, None].expand(B, S)
+    ref = bf.attend_brute(q.double().numpy(), k.double().numpy(), v.double().numpy(),
+                          topi.numpy(), bias.numpy(), valid.numpy(), bs, lw, scale,
+                          kmin=kmin.numpy())
+    for (b, h, t), o in ref.items():
+        if t >= pads[b]:
+            np.testing.assert_allclose(out[b, h, t].double().numpy(), o, atol=2e-5)
+    vm = v[1].mean(1)                                   # [H, D]
+    for t in range(pads[1]):
+        torch.testing.assert_close(out[1, :, t], vm, atol=1e-5, rtol=1e-5)
+    # -1e4 excludes a key as well as the dtype minimum on rows that keep a key
+    out2 = O.dense_attend(q, k, v, topi, bias, valid, bs, lw, scale,
+                          attention_mask=_left_pad_mask(B, S, pads, -1e4))
+    torch.testing.assert_close(out2[1, :, pads[1]:], out[1, :, pads[1]:], atol=1e-6, rtol=0)
+
+
+def test_decode_attend_several_rows_per_sequence():
+    """Lq > 1 decode rows (modeling_deepseekv2.py:424-451 with q_pos [B, Lq]): each row
+    equals the prefill row at its position."""
+    q, k, v, topi, bias, valid, bs, lw = _attn_case(34, B=2, S=90, K=4)
+    scale = 0.3
+    full = O.dense_attend(q, k, v, topi, bias, valid, bs, lw, scale)
+    pos = torch.tensor([[89, 40, 41], [7, 88, 60]])
+    qs = torch.stack([q[b][:, pos[b]] for b in range(2)])
+    sel = [torch.stack([x[b][pos[b]] for b in range(2)]) for x in (topi, bias, valid)]
+    dec = O.decode_attend(qs, k, v, *sel, pos, bs, lw, scale)
+    for b in range(2):
+        torch.testing.assert_close(dec[b], full[b][:, pos[b]], atol=1e-5, rtol=1e-5)
+
+
 def test_varlen_documents_are_isolated():
     g = _rng(40)
     H, D, d = 2, 16, 8

@@ -19,6 +19,7 @@ import os
 from types import SimpleNamespace
 
 import pytest
+import torch
 import torch.nn as nn
 
 from ananta_ocr_amd import dash_attention as DA
@@ -158,3 +159,58 @@ def test_persist_router_cfg_writes_leader_parameters(monkeypatch, fresh_schedule
     # a config that is not a dict is left alone
     cfg3 = SimpleNamespace(num_attention_heads=2, hidden_size=256, rms_norm_eps=1e-6)
     DA.DashAttention(cfg3)
+
+
+def _mask(rows, S, fill):
+    """[B, 1, S, S] additive mask: 0 where rows[b](t, j) allows key j, else fill."""
+    i = torch.arange(S)
+    m = torch.zeros(len(rows), 1, S, S)
+    for b, allow in enumerate(rows):
+        ok = allow(i[:, None], i[None, :])
+        m[b, 0] = torch.where(ok, torch.zeros(()), torch.full((), fill))
+    return m
+
+
+def test_mask_key_starts_left_padding_and_documents():
+    S = 40
+    causal = lambda t, j: j <= t
+    mn = torch.finfo(torch.float32).min
+    m = _mask([causal, lambda t, j: (j <= t) & (j >= 11),
+               lambda t, j: (j <= t) & (j >= torch.where(t >= 25, 25, 0))], S, mn)
+    kmin, empty = DA.mask_key_starts(m, 3, S)
+    t = torch.arange(S)
+    assert kmin[0].tolist() == [0] * S and not empty[0].any()
+    # rows before the padding end have no causal key: empty, kmin 0
+    assert empty[1].tolist() == (t < 11).tolist()
+    assert kmin[1].tolist() == torch.where(t < 11, 0, 11).tolist()
+    assert kmin[2].tolist() == torch.where(t >= 25, 25, 0).tolist() and not empty[2].any()
+    # a mask of batch 1 and larger than S broadcasts; the rows of _unmask_unattended
+    # (all zero) allow everything
+    big = torch.zeros(1, 1, S + 5, S + 7)
+    kmin, empty = DA.mask_key_starts(big, 2, S)
+    assert not kmin.any() and not empty.any()
+    # identical heads are accepted
+    kmin, _ = DA.mask_key_starts(m[1:2].expand(1, 4, S, S), 1, S)
+    assert kmin[0].tolist() == torch.where(t < 11, 0, 11).tolist()
+
+
+@pytest.mark.parametrize("case", ["right_pad", "hole", "partial_value", "heads",
+                                  "fp16_min_empty_row", "shape"])
+def test_mask_key_starts_refuses_other_masks(case):
+    S = 32
+    if case == "right_pad":      # pad query rows keep keys [0, 20): not a suffix of [0, t]
+        m = _mask([lambda t, j: (j <= t) & (j < 20)], S, -1e30)
+    elif case == "hole":
+        m = _mask([lambda t, j: (j <= t) & (j != 5)], S, -1e30)
+    elif case == "partial_value":
+        m = _mask([lambda t, j: j <= t], S, -1e30)
+        m[0, 0, 10, 3] = -3.0
+    elif case == "heads":
+        m = _mask([lambda t, j: j <= t], S, -1e30).expand(1, 2, S, S).clone()
+        m[0, 1, 20, 20] = -1e30
+    elif case == "fp16_min_empty_row":   # a fully masked row whose entries do not clamp
+        m = _mask([lambda t, j: (j <= t) & (j >= 8)], S, -65504.0)
+    else:
+        m = torch.zeros(1, S, S)
+    with pytest.raises(NotImplementedError):
+        DA.mask_key_starts(m, 1, S)
