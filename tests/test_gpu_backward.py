@@ -43,7 +43,7 @@ def _ref(q, k, v, topi, bias, valid, bs, lw, scale, kmin=None):
     return torch.matmul(torch.softmax(s, dim=-1), v)
 
 
-def _close_grad(got, ref, what, frac=3e-2):
+def _close_grad(got, ref, what, frac=1.5e-2):
     got, ref = got.float().cpu(), ref.float().cpu()
     scale = ref.abs().max().item()
     err = (got - ref).abs()

@@ -184,7 +184,7 @@ def test_gather_attention_index_heads_packed_with_gradients():
     for got, want, what in ((qg.grad, qr.grad, "dq"), (kg.grad, kr.grad, "dk"),
                             (vg.grad, vr.grad, "dv")):
         err = (got.float().cpu() - want).abs().max().item()
-        assert err <= 3e-2 * want.abs().max().item() + 1e-6, f"{what}: {err:.3e}"
+        assert err <= 1.5e-2 * want.abs().max().item() + 1e-6, f"{what}: {err:.3e}"
 
 
 def test_decode_attend_helper_matches_oracle():

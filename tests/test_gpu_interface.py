@@ -159,7 +159,7 @@ def test_training_forward_with_padding_mask(monkeypatch):
     for gg, rr, what in ((qg.grad, qr.grad, "dq"), (kg.grad, kr.grad, "dk"),
                          (vg.grad, vr.grad, "dv")):
         err = (gg.float().cpu() - rr).abs().max().item()
-        assert err <= 3e-2 * rr.abs().max().item() + 1e-6, f"{what}: {err:.3e}"
+        assert err <= 1.5e-2 * rr.abs().max().item() + 1e-6, f"{what}: {err:.3e}"
     ref_p = {n: p.grad for n, p in mc.named_parameters() if p.grad is not None}
     for n in ["q_proj.weight", "k_proj.weight"]:
         err = (got[n] - ref_p[n]).abs().max().item()
@@ -329,4 +329,4 @@ def test_gather_attention_packed_rows_batch_two():
     for got, want, what in ((qg.grad, qr.grad, "dq"), (kg.grad, kr.grad, "dk"),
                             (vg.grad, vr.grad, "dv")):
         err = (got.float().cpu() - want).abs().max().item()
-        assert err <= 3e-2 * want.abs().max().item() + 1e-6, f"{what}: {err:.3e}"
+        assert err <= 1.5e-2 * want.abs().max().item() + 1e-6, f"{what}: {err:.3e}"
