@@ -77,6 +77,11 @@ SIGNATURES = {
     "dash_decode_page_state": (_i, [_p, _l, _i, _i, _l, _l, _i, _i, _i, _p, _p, _p, _p, _p, _l,
                                     _p]),
     "dash_decode_allow": (_i, [_p, _l, _i, _l, _p, _p, _i, _p, _p, _i, _p, _l, _p]),
+    "dash_page_rope_workspace_size": (_i, [_i, _i, ctypes.POINTER(_l)]),
+    "dash_page_rope_pos": (_i, [_p, _l, _i, _i, _l, _l, _i, _p, _p, _p, _l, _p, _p, _l, _p]),
+    "dash_rope2d_cos_sin": (_i, [_p, _p, _l, _i, _i, _p, _i, _p, _i, _i, _p, _p, _i, _l, _l,
+                                 _p]),
+    "dash_page_rope_advance": (_i, [_p, _l, _i, _l, _p, _p, _p, _l, _p, _p, _p, _p]),
 }
 
 _LIB = None

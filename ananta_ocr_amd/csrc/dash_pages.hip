@@ -456,6 +456,194 @@ __global__ __launch_bounds__(256) void win_bounds_kernel(const uint8_t* __restri
   }
 }
 
+
+// ---------------------------------------------------------------------------------
+// Page2D RoPE coordinates (_build_page_rope_pos / _page_rope_offsets,
+// _sparse_base_impl.py:2269-2362).  Per prompt row, with cum[t] = <PAGE> markers at
+// positions <= t, last = the last image-token position and n = cum[last] (the prompt's
+// pages):
+//   page[t] = t <= last ? cum[t] : cum[t] - n       (page 0 = the text before the first
+//                                                    marker and after the last image)
+//   tok[t]  = (tokens at positions <= t with the same page) - 1
+// Up to `last` the page never decreases and page p spans [m_p, m_{p+1}) (m_p = the p-th
+// marker, m_0 = 0); after `last` page p spans the p-th to (p+1)-th marker after it (from
+// last + 1 for page 0), and its count continues from the prefill count
+//   pf[p] = min(m_{p+1}, last + 1) - m_p   (p <= n; 0 for later pages).
+// So a token's count is its distance from the start of its run plus, after `last`, pf of
+// its page, which needs only the marker positions: the page kernel writes page ids and
+// every marker's position (mpos[cum - 1] = t), the count kernel the counts, pf and the
+// optional span scaling, the meta kernel the batch's page count and whether every row
+// has a marker at or before its last image token (else the reference falls back to 1-D).
+
+__device__ __forceinline__ int64_t rope_pf(const int32_t* mpos, int n, int last, int64_t p) {
+  if (p < 0 || p > n) return 0;
+  const int64_t end = p < n ? (int64_t)mpos[p] : (int64_t)last + 1;
+  const int64_t start = p == 0 ? 0 : (int64_t)mpos[p - 1];
+  return end - start;
+}
+
+__global__ __launch_bounds__(kPgThreads) void rope_page_kernel(
+    const int64_t* __restrict__ ids, int64_t ids_sb, int L, int64_t img_id, int64_t page_id,
+    int chunk, int nchunks, const int32_t* __restrict__ summ, int64_t* __restrict__ page,
+    int32_t* __restrict__ mpos) {
+  __shared__ uint64_t sWave[kPgThreads / kWave];
+  __shared__ ChunkPrefix sPre;
+  const int k = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const ChunkPrefix pre = chunk_prefix(summ, b, k, nchunks, &sPre);
+  const int t = k * chunk + tid;
+  const bool live = tid < chunk && t < L;
+  const int64_t id = live ? ids[(int64_t)b * ids_sb + t] : -1;
+  const bool mk = live && id == page_id;
+  uint64_t tot;
+  const uint64_t inc = block_incl_scan((uint64_t)mk, sWave, tot);
+  const int cum = pre.mk + (int)inc;
+  if (live) {
+    const int n = pre.last >= 0 ? pre.prompt_pages : 0;
+    page[(int64_t)b * L + t] = t <= pre.last ? cum : cum - n;
+    if (mk) mpos[(int64_t)b * L + cum - 1] = t;
+  }
+}
+
+__global__ __launch_bounds__(kPgThreads) void rope_tok_kernel(
+    int L, int chunk, int nchunks, const int32_t* __restrict__ summ,
+    const int64_t* __restrict__ page, const int32_t* __restrict__ mpos, int span,
+    int64_t* __restrict__ tok, int64_t* __restrict__ pf_cnt, int64_t pf_stride) {
+  __shared__ ChunkPrefix sPre;
+  const int k = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const ChunkPrefix pre = chunk_prefix(summ, b, k, nchunks, &sPre);
+  const int last = pre.last;
+  const int n = last >= 0 ? pre.prompt_pages : 0;
+  const int32_t* mp = mpos + (int64_t)b * L;
+  const int t = k * chunk + tid;
+  if (tid < chunk && t < L) {
+    const int64_t pg = page[(int64_t)b * L + t];
+    const bool in_pre = t <= last;
+    const int64_t cum = in_pre ? pg : pg + n;
+    const int lastmk = cum > 0 ? mp[cum - 1] : -1;
+    const int seg0 = in_pre ? max(lastmk, 0) : max(lastmk, last + 1);
+    const int64_t run = (int64_t)(t - seg0);
+    const int64_t pfk = rope_pf(mp, n, last, pg);
+    int64_t tk = in_pre ? run : pfk + run;
+    if (span > 0 && pg > 0) {
+      if (in_pre) {
+        // round(tok * span / max(pf, 1)) in fp32, half to even, as torch.round
+        const float x = __fdiv_rn(__fmul_rn((float)tk, (float)span), (float)max(pfk, (int64_t)1));
+        tk = (int64_t)rintf(x);
+      } else {
+        tk = (int64_t)span + (tk - pfk);
+      }
+    }
+    tok[(int64_t)b * L + t] = tk;
+  }
+  // the prefill count of every page id 0 .. L (the row's pages are at most L + 1)
+  for (int64_t p = (int64_t)k * chunk + tid; p <= L; p += (int64_t)chunk * nchunks)
+    if (tid < chunk) pf_cnt[(int64_t)b * pf_stride + p] = rope_pf(mp, n, last, p);
+}
+
+// meta[0] = 1 + the largest page id of any row; meta[1] = 1 if every row has a marker at
+// or before its last image token (then it also has an image token and a marker).
+__global__ __launch_bounds__(kWave) void rope_meta_kernel(int B, int nchunks,
+                                                          const int32_t* __restrict__ summ,
+                                                          int64_t* __restrict__ meta) {
+  const int lane = threadIdx.x;
+  int maxpg = 0, ok = 1;
+  for (int b = 0; b < B; ++b) {
+    const int32_t* row = summ + (int64_t)b * nchunks * kSumWords;
+    int total = 0, last = -1, kl = -1;
+    for (int j = lane; j < nchunks; j += kWave) {
+      total += row[j * kSumWords];
+      const int lj = row[j * kSumWords + 2];
+      if (lj > last) { last = lj; kl = j; }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      total += __shfl_xor(total, m, kWave);
+      const int ol = __shfl_xor(last, m, kWave), ok2 = __shfl_xor(kl, m, kWave);
+      if (ol > last) { last = ol; kl = ok2; }
+    }
+    int pre = 0;
+    for (int j = lane; j < kl; j += kWave) pre += row[j * kSumWords];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) pre += __shfl_xor(pre, m, kWave);
+    const int n = kl >= 0 ? pre + row[kl * kSumWords + 3] : 0;
+    maxpg = max(maxpg, max(n, total - n));
+    if (n <= 0) ok = 0;
+  }
+  if (lane == 0) {
+    meta[0] = (int64_t)maxpg + 1;
+    meta[1] = ok;
+  }
+}
+
+// cos / sin of the two-axis RoPE (DeepseekV2IndexerRotary2D.forward,
+// _sparse_base_impl.py:1876-1891): frequency pair j < n_tok turns with the token
+// coordinate, pair n_tok + i with the page coordinate (mod page_mod when > 0); both
+// halves of the row repeat the pairs (cat(ang, ang)).  Angles and cos/sin in fp32, then
+// the output dtype.  One thread per (token, pair).
+__global__ __launch_bounds__(256) void rope2d_cos_sin_kernel(
+    const int64_t* __restrict__ tok, const int64_t* __restrict__ page, int64_t pos_sb, int S,
+    int64_t rows, const float* __restrict__ inv_tok, int n_tok, const float* __restrict__ inv_page,
+    int half, int page_mod, void* __restrict__ cos_out, void* __restrict__ sin_out, int out_bf16,
+    int64_t cs_sb, int64_t cs_st) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * half) return;
+  const int64_t r = i / half;
+  const int j = (int)(i - r * half);
+  const int64_t b = r / S, t = r - b * S;
+  float ang;
+  if (j < n_tok) {
+    ang = __fmul_rn((float)tok[b * pos_sb + t], inv_tok[j]);
+  } else {
+    int64_t p = page[b * pos_sb + t];
+    if (page_mod > 0) {
+      p %= page_mod;
+      if (p < 0) p += page_mod;
+    }
+    ang = __fmul_rn((float)p, inv_page[j - n_tok]);
+  }
+  float sv, cv;
+  sincosf(ang, &sv, &cv);
+  const int64_t o = b * cs_sb + t * cs_st;
+  if (out_bf16) {
+    bf16* c = (bf16*)cos_out + o;
+    bf16* s = (bf16*)sin_out + o;
+    c[j] = (bf16)cv; c[j + half] = (bf16)cv;
+    s[j] = (bf16)sv; s[j + half] = (bf16)sv;
+  } else {
+    float* c = (float*)cos_out + o;
+    float* s = (float*)sin_out + o;
+    c[j] = cv; c[j + half] = cv;
+    s[j] = sv; s[j + half] = sv;
+  }
+}
+
+// One decode token per row advances the page coordinates (_main_rope_coords decode branch,
+// _sparse_base_impl.py:1384-1390): a <PAGE> token moves to the next page (at most the last
+// page id of the prompt, meta[0] - 1) and restarts at that page's prefill count; any
+// other token counts one further.  state page/tok [B] are updated; the new coordinates are
+// also written to out_tok / out_page [B].
+__global__ __launch_bounds__(256) void rope_advance_kernel(
+    const int64_t* __restrict__ new_ids, int64_t new_stride, int B, int64_t page_id,
+    int64_t* __restrict__ page, int64_t* __restrict__ tok, const int64_t* __restrict__ pf_cnt,
+    int64_t pf_stride, const int64_t* __restrict__ meta, int64_t* __restrict__ out_tok,
+    int64_t* __restrict__ out_page) {
+  const int b = blockIdx.x * 256 + threadIdx.x;
+  if (b >= B) return;
+  const bool is_pg = new_ids[(int64_t)b * new_stride] == page_id;
+  int64_t pg = page[b];
+  int64_t tk = tok[b];
+  if (is_pg) {
+    pg = min(pg + 1, meta[0] - 1);
+    tk = pf_cnt[(int64_t)b * pf_stride + max(pg, (int64_t)0)];
+  } else {
+    tk = tk + 1;
+  }
+  page[b] = pg;
+  tok[b] = tk;
+  if (out_tok) out_tok[b] = tk;
+  if (out_page) out_page[b] = pg;
+}
+
 }  // namespace dash
 
 namespace {
@@ -604,5 +792,86 @@ extern "C" int dash_decode_win_bounds(const uint8_t* allow, int64_t allow_sb, in
   hipLaunchKernelGGL(win_bounds_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream, allow, allow_sb,
                      allow_w, seq_lens, q_pos, S, nblk_cap, block_size, local_blocks, tile, bounds,
                      fit);
+  return pages_status();
+}
+
+extern "C" int dash_page_rope_workspace_size(int B, int L, int64_t* bytes) {
+  using namespace dash;
+  if (!bytes || B < 0 || L < 0) return kErrInvalid;
+  int64_t summ = 0;
+  dash_pages_workspace_size(B, L, &summ);
+  *bytes = (summ + 255) / 256 * 256 + (int64_t)B * L * (int64_t)sizeof(int32_t);
+  return kOk;
+}
+
+extern "C" int dash_page_rope_pos(const int64_t* ids, int64_t ids_sb, int B, int L,
+                                  int64_t image_token_id, int64_t page_token_id, int page_span,
+                                  int64_t* tok, int64_t* page, int64_t* pf_cnt, int64_t pf_stride,
+                                  int64_t* meta, void* workspace, int64_t workspace_bytes,
+                                  void* stream) {
+  using namespace dash;
+  if (B < 0 || L < 0 || page_span < 0) return kErrInvalid;
+  if (!meta) return kErrInvalid;
+  if (B == 0 || L == 0) {
+    if (B == 0) return kOk;
+    return kErrInvalid;
+  }
+  if (!ids || !tok || !page || !pf_cnt || pf_stride < (int64_t)L + 1) return kErrInvalid;
+  int64_t need = 0;
+  dash_page_rope_workspace_size(B, L, &need);
+  if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 256 != 0) return kErrWorkspace;
+  int64_t summ = 0;
+  dash_pages_workspace_size(B, L, &summ);
+  int32_t* mpos = (int32_t*)((char*)workspace + (summ + 255) / 256 * 256);
+  hipStream_t st = (hipStream_t)stream;
+  int nchunks = 0;
+  const int rs = page_summaries(ids, ids_sb, B, L, image_token_id, page_token_id, kPgThreads,
+                                workspace, workspace_bytes, nullptr, st, &nchunks);
+  if (rs != kOk) return rs;
+  hipLaunchKernelGGL(rope_page_kernel, dim3(nchunks, B), dim3(kPgThreads), 0, st, ids, ids_sb, L,
+                     image_token_id, page_token_id, kPgThreads, nchunks,
+                     (const int32_t*)workspace, page, mpos);
+  hipLaunchKernelGGL(rope_tok_kernel, dim3(nchunks, B), dim3(kPgThreads), 0, st, L, kPgThreads,
+                     nchunks, (const int32_t*)workspace, (const int64_t*)page,
+                     (const int32_t*)mpos, page_span, tok, pf_cnt, pf_stride);
+  hipLaunchKernelGGL(rope_meta_kernel, dim3(1), dim3(kWave), 0, st, B, nchunks,
+                     (const int32_t*)workspace, meta);
+  return pages_status();
+}
+
+extern "C" int dash_rope2d_cos_sin(const int64_t* tok, const int64_t* page, int64_t pos_sb, int B,
+                                   int S, const float* inv_tok, int n_tok, const float* inv_page,
+                                   int page_pairs, int page_mod, void* cos_out, void* sin_out,
+                                   int out_bf16, int64_t cs_sb, int64_t cs_st, void* stream) {
+  using namespace dash;
+  if (B < 0 || S < 0 || n_tok < 0 || page_pairs < 0 || page_mod < 0) return kErrInvalid;
+  if (n_tok + page_pairs <= 0) return kErrInvalid;
+  const int64_t rows = (int64_t)B * S;
+  if (rows == 0) return kOk;
+  if (!tok || !page || !cos_out || !sin_out || (n_tok > 0 && !inv_tok) ||
+      (page_pairs > 0 && !inv_page))
+    return kErrInvalid;
+  const int half = n_tok + page_pairs;
+  if (cs_st < 2 * half) return kErrInvalid;
+  const int64_t n = rows * half;
+  if ((n + 255) / 256 > INT32_MAX) return kErrUnsupported;
+  hipLaunchKernelGGL(rope2d_cos_sin_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, tok, page, pos_sb, S, rows, inv_tok, n_tok, inv_page,
+                     half, page_mod, cos_out, sin_out, out_bf16, cs_sb, cs_st);
+  return pages_status();
+}
+
+extern "C" int dash_page_rope_advance(const int64_t* new_ids, int64_t new_stride, int B,
+                                      int64_t page_token_id, int64_t* page, int64_t* tok,
+                                      const int64_t* pf_cnt, int64_t pf_stride,
+                                      const int64_t* meta, int64_t* out_tok, int64_t* out_page,
+                                      void* stream) {
+  using namespace dash;
+  if (B < 0) return kErrInvalid;
+  if (B == 0) return kOk;
+  if (!new_ids || !page || !tok || !pf_cnt || !meta || pf_stride < 1) return kErrInvalid;
+  hipLaunchKernelGGL(rope_advance_kernel, dim3((B + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                     new_ids, new_stride, B, page_token_id, page, tok, pf_cnt, pf_stride, meta,
+                     out_tok, out_page);
   return pages_status();
 }

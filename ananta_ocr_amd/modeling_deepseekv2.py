@@ -28,7 +28,7 @@ import os
 
 import torch
 
-from . import ops, pages
+from . import ops, page_rope, pages
 from .dash_attention import DashAttention, apply_rotary, checkpoint_sparse_config
 
 _INFER = {"on": False}
@@ -393,7 +393,8 @@ def _dash_decode_forward(self, hidden_states, position_ids, past_kv):
     coords = None
     if getattr(self, "main_rope_mode", None) == "page2d" and \
             getattr(self, "rotary_emb_2d_main", None) is not None:
-        coords = self._main_rope_coords(q_len, past_kv)
+        # the page coordinates advanced on the device (page_rope.main_rope_coords)
+        coords = page_rope.main_rope_coords(self, q_len, past_kv)
     if coords is not None:
         cos, sin = self.rotary_emb_2d_main(v, coords[0], coords[1])
     else:

@@ -444,6 +444,47 @@ int dash_decode_win_bounds(const uint8_t* allow, int64_t allow_sb, int allow_w,
                            int32_t* bounds, uint8_t* fit, void* stream);
 
 /*
+ * Page2D RoPE coordinates of prompt rows: tok[b, t] (running count of tokens of the same
+ * page up to t, minus 1, optionally scaled by page_span) and page[b, t] (<PAGE> markers up
+ * to t; after the last image token, minus the prompt's pages), int64 [B, L] row stride L;
+ * pf_cnt[b, p] (tokens of page p up to the last image token) for p = 0 .. L, int64 with row
+ * stride pf_stride >= L + 1; meta int64 [2] = (1 + the largest page id of the batch, 1 if
+ * every row has a <PAGE> marker at or before its last image token, else 0: then the
+ * reference falls back to 1-D RoPE).  Replaces _build_page_rope_pos and _page_rope_offsets
+ * (_sparse_base_impl.py:2269-2362) without host synchronisation (ids pre-padded / cut to L
+ * as the reference does).  workspace: dash_page_rope_workspace_size bytes, 256-byte aligned.
+ */
+int dash_page_rope_workspace_size(int B, int L, int64_t* bytes);
+int dash_page_rope_pos(const int64_t* ids, int64_t ids_sb, int B, int L, int64_t image_token_id,
+                       int64_t page_token_id, int page_span, int64_t* tok, int64_t* page,
+                       int64_t* pf_cnt, int64_t pf_stride, int64_t* meta, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
+/*
+ * cos / sin [B, S, 2 * (n_tok + page_pairs)] (bf16 or fp32, batch/token strides cs_sb,
+ * cs_st) of the two-axis RoPE at coordinates tok / page (int64, batch stride pos_sb):
+ * pair j < n_tok turns by tok * inv_tok[j], pair n_tok + i by (page mod page_mod, when
+ * page_mod > 0) * inv_page[i], and the second half of the row repeats the first.
+ * Replaces DeepseekV2IndexerRotary2D.forward (_sparse_base_impl.py:1876-1891).
+ */
+int dash_rope2d_cos_sin(const int64_t* tok, const int64_t* page, int64_t pos_sb, int B, int S,
+                        const float* inv_tok, int n_tok, const float* inv_page, int page_pairs,
+                        int page_mod, void* cos, void* sin, int out_bf16, int64_t cs_sb,
+                        int64_t cs_st, void* stream);
+
+/*
+ * One decode token per row advances the page coordinates in place: page[b] / tok[b] (int64
+ * [B]); a <PAGE> token moves to min(page + 1, meta[0] - 1) and restarts at pf_cnt[b, page],
+ * any other token increments tok.  The new (tok, page) are also written to out_tok /
+ * out_page when non-null.  Replaces the decode branch of _main_rope_coords
+ * (_sparse_base_impl.py:1384-1390); pf_cnt and meta as dash_page_rope_pos writes them.
+ */
+int dash_page_rope_advance(const int64_t* new_ids, int64_t new_stride, int B,
+                           int64_t page_token_id, int64_t* page, int64_t* tok,
+                           const int64_t* pf_cnt, int64_t pf_stride, const int64_t* meta,
+                           int64_t* out_tok, int64_t* out_page, void* stream);
+
+/*
  * Allocation-free decode step.  No counterpart in the reference: it is for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving loops).
  * Same arguments and results as dash_decode_step without the workspace: the window and

@@ -623,3 +623,93 @@ def decode_win_bounds(allow, seq_lens, max_block, block_size, local_blocks, tile
     lo_v = torch.where(any_r, lo, torch.zeros_like(lo))
     hi_v = torch.where(any_r, hi + 1, torch.where(no_remote, torch.zeros_like(hi), w_seq))
     return lo_v, hi_v, (hi_v - lo_v) <= tile
+
+
+# ----------------------------------------------------------------------------
+# page2d RoPE: the OCR prompt's two-axis (token, page) coordinates
+# ----------------------------------------------------------------------------
+
+def page_rope_pos(source_input_ids, img_id, page_id, key_length, page_span=0):
+    """(tok_pos, page_pos, pf_cnt, n_pg) or None: _build_page_rope_pos with
+    _page_rope_offsets (_sparse_base_impl.py:2269-2362; the one-shot diagnostic print left
+    out).  tok_pos / page_pos [B, key_length] int64, pf_cnt [B, n_pg] int64 (tokens of each
+    page up to the last image token), n_pg = 1 + the largest page id.  None where the
+    reference falls back to 1-D RoPE: no ids, no image token or no <PAGE> marker in the
+    batch, or a row without a marker at or before its last image token."""
+    if source_input_ids is None or getattr(source_input_ids, "ndim", 0) != 2:
+        return None
+    if img_id is None or page_id is None:
+        return None
+    ids = _pad_ids(source_input_ids, key_length)
+    B, S = ids.shape
+    ar = torch.arange(S)
+    img = ids == img_id
+    mk = ids == page_id
+    if not bool(img.any()) or not bool(mk.any()):
+        return None
+    cum = torch.cumsum(mk.long(), dim=-1)
+    last_img = (img.long() * (ar + 1)).max(dim=-1).values - 1
+    n_pages = cum.gather(1, last_img.clamp(min=0)[:, None])
+    n_pages = n_pages * (last_img >= 0)[:, None].long()
+    if not bool((n_pages > 0).all()):
+        return None
+    in_prefill = ar[None, :] <= last_img[:, None]
+    page = torch.where(in_prefill, cum, cum - n_pages).clamp(min=0)
+    n_pg = int(page.max().item()) + 1
+    onehot = F.one_hot(page, num_classes=n_pg).to(torch.int32)
+    run = onehot.cumsum(dim=1)
+    tok = run.gather(2, page[:, :, None].to(torch.int64)).squeeze(-1).to(torch.int64) - 1
+    pf_cnt = (onehot * in_prefill[:, :, None].to(torch.int32)).sum(dim=1)
+    pf_k = pf_cnt.gather(1, page.reshape(B, S).to(torch.int64)).to(torch.int64)
+    if page_span > 0:
+        s_span = float(page_span)
+        pre = torch.round(tok.float() * s_span / pf_k.clamp(min=1).float())
+        post = s_span + (tok - pf_k).float()
+        scaled = torch.where(in_prefill, pre, post).to(torch.int64)
+        tok = torch.where(page > 0, scaled, tok)
+    return tok, page, pf_cnt.to(torch.int64), n_pg
+
+
+def rotary2d_inv_freq(dim, base_tok, base_page, page_pairs, tok_freq_mode="resample"):
+    """(inv_tok [n_tok], inv_page [page_pairs]) fp32 of the two-axis RoPE:
+    DeepseekV2IndexerRotary2D.__init__ (_sparse_base_impl.py:1848-1873)."""
+    half = dim // 2
+    page_pairs = int(page_pairs)
+    if not (0 < page_pairs < half):
+        raise ValueError(f"page_pairs={page_pairs} must be in (0, {half})")
+    n_tok = half - page_pairs
+    ar = torch.arange(0, n_tok, dtype=torch.int64).float()
+    if str(tok_freq_mode).lower() == "truncate":
+        inv_tok = 1.0 / (base_tok ** (ar * 2 / dim))
+    else:
+        inv_tok = 1.0 / (base_tok ** (ar / n_tok))
+    inv_page = 1.0 / (base_page ** (torch.arange(0, page_pairs, dtype=torch.int64).float()
+                                    / page_pairs))
+    return inv_tok, inv_page
+
+
+def rotary2d_cos_sin(tok_pos, page_pos, inv_tok, inv_page, page_mod=0, dtype=torch.float32):
+    """cos / sin [B, S, dim] of the two-axis RoPE at (tok_pos, page_pos) [B, S]:
+    DeepseekV2IndexerRotary2D.forward (_sparse_base_impl.py:1876-1891)."""
+    t = tok_pos.float()[:, :, None]
+    p = page_pos
+    if page_mod > 0:
+        p = torch.remainder(p.to(torch.int64), page_mod)
+    p = p.float()[:, :, None]
+    a_tok = t * inv_tok.float()[None, None, :]
+    a_page = p * inv_page.float()[None, None, :]
+    ang = torch.cat((a_tok, a_page), dim=-1)
+    emb = torch.cat((ang, ang), dim=-1)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
+def page_rope_advance(page, tok, pf_cnt, n_pg, new_ids, page_id):
+    """The decode step of the page coordinates, one new token per row:
+    _main_rope_coords' decode branch (_sparse_base_impl.py:1384-1390).  page / tok [B]
+    int64 (the previous token's coordinates), pf_cnt [B, >= n_pg], new_ids [B].  Returns
+    the new (tok, page)."""
+    is_pg = new_ids == page_id
+    page = torch.where(is_pg, (page + 1).clamp(max=n_pg - 1), page)
+    pg_start = pf_cnt.gather(1, page[:, None].clamp(min=0)).squeeze(1)
+    tok = torch.where(is_pg, pg_start, tok + 1)
+    return tok, page

@@ -238,3 +238,25 @@ def win_bounds_row(allow, seq, max_block, bs, lb, tile):
     else:
         lo, hi = 0, min(max_block, max((seq + bs - 1) // bs, 1))
     return lo, hi, hi - lo <= tile
+
+
+def walk_page_rope(ids_row, img_id, page_id):
+    """Two-axis coordinates of one prompt row from the definition, token by token:
+    page = markers so far (up to the last image token), else markers after it; tok = how
+    many earlier tokens share the page.  Returns (tok list, page list, prefill count per
+    page dict, prompt pages)."""
+    last = max((i for i, x in enumerate(ids_row) if x == img_id), default=-1)
+    n = sum(1 for x in ids_row[:last + 1] if x == page_id)
+    seen, pf = {}, {}
+    toks, pages = [], []
+    marks = 0
+    for i, x in enumerate(ids_row):
+        if x == page_id:
+            marks += 1
+        p = marks if i <= last else marks - n
+        toks.append(seen.get(p, 0))
+        seen[p] = seen.get(p, 0) + 1
+        pages.append(p)
+        if i <= last:
+            pf[p] = pf.get(p, 0) + 1
+    return toks, pages, pf, n

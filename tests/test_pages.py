@@ -180,3 +180,125 @@ def test_win_bounds_match_definition(seed):
     for b in range(B):
         assert (int(lo[b]), int(hi[b]), bool(fit[b])) == \
             BF.win_bounds_row(allow[b].tolist(), int(seq[b]), W, bs, lb, 6), b
+
+
+# ---------------------------------------------------------------- page2d RoPE coordinates
+
+def test_page_rope_pos_known_answer():
+    """_build_page_rope_pos / _page_rope_offsets on a hand-worked prompt: page = markers so
+    far up to the last image, markers after it afterwards (page 0 = the text before the first
+    marker and the instruction after the last image); tok = running count in the page; the
+    span scaling rounds half to even."""
+    ids = torch.tensor([PROMPT])
+    tok, page, pf, n_pg = O.page_rope_pos(ids, IMG, PG, len(PROMPT))
+    assert page[0].tolist() == [0, 1, 1, 1, 1, 2, 2, 2, 3, 3, 3, 3, 0, 0, 1, 1, 2, 2]
+    assert tok[0].tolist() == [0, 0, 1, 2, 3, 0, 1, 2, 0, 1, 2, 3, 1, 2, 4, 5, 3, 4]
+    assert pf[0].tolist() == [1, 4, 3, 4] and n_pg == 4
+    tok, page, _, _ = O.page_rope_pos(ids, IMG, PG, len(PROMPT), page_span=10)
+    assert tok[0].tolist() == [0, 0, 2, 5, 8, 0, 3, 7, 0, 2, 5, 8, 1, 2, 10, 11, 10, 11]
+    # padded to a longer key length with -1: the padding continues the last page
+    tok, page, _, _ = O.page_rope_pos(ids, IMG, PG, len(PROMPT) + 2)
+    assert page[0].tolist()[-3:] == [2, 2, 2] and tok[0].tolist()[-3:] == [4, 5, 6]
+
+
+def test_page_rope_pos_falls_back_where_the_reference_does():
+    assert O.page_rope_pos(torch.tensor([[TXT, PG, TXT]]), IMG, PG, 3) is None     # no image
+    assert O.page_rope_pos(torch.tensor([[TXT, IMG, IMG]]), IMG, PG, 3) is None    # no marker
+    # a marker only after the last image token: not marker mode
+    assert O.page_rope_pos(torch.tensor([[IMG, IMG, PG, TXT]]), IMG, PG, 4) is None
+    # one row of the batch without a prompt page: the whole batch falls back
+    two = torch.tensor([[PG, IMG, TXT], [IMG, PG, TXT]])
+    assert O.page_rope_pos(two, IMG, PG, 3) is None
+    assert O.page_rope_pos(None, IMG, PG, 3) is None
+    assert O.page_rope_pos(torch.tensor([PG, IMG]), IMG, PG, 2) is None
+
+
+def _random_ocr_prompt(rng, pages, resp_pages, per_page=(2, 9), prefix=3):
+    ids = [BOS] + [TXT] * rng.randint(0, prefix)
+    for _ in range(pages):
+        ids += [PG] + [IMG] * rng.randint(*per_page)
+    ids += [TXT] * rng.randint(0, 4)
+    for _ in range(resp_pages):
+        ids += [PG] + [TXT] * rng.randint(0, 6)
+    return ids
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_page_rope_pos_matches_token_walk(seed):
+    rng = random.Random(seed)
+    B = 3
+    rows = [_random_ocr_prompt(rng, rng.randint(1, 6), rng.randint(0, 5)) for _ in range(B)]
+    L = max(len(r) for r in rows) + rng.randint(0, 3)
+    ids = torch.full((B, L), -1, dtype=torch.long)
+    for b, r in enumerate(rows):
+        ids[b, :len(r)] = torch.tensor(r)
+    tok, page, pf, n_pg = O.page_rope_pos(ids, IMG, PG, L)
+    maxp = 0
+    for b in range(B):
+        wt, wp, wpf, n = BF.walk_page_rope(ids[b].tolist(), IMG, PG)
+        assert tok[b].tolist() == wt and page[b].tolist() == wp
+        maxp = max(maxp, max(wp))
+        for p in range(n_pg):
+            assert int(pf[b, p]) == wpf.get(p, 0)
+    assert n_pg == maxp + 1
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_page_rope_decode_advance_equals_recompute(seed):
+    """Stepping the coordinates one generated token at a time equals recomputing them on
+    the longer prompt while the page stays within the prompt's pages; a further <PAGE>
+    stays on the last page and restarts at its prefill count (the reference's clamp)."""
+    rng = random.Random(100 + seed)
+    prompt = _random_ocr_prompt(rng, rng.randint(3, 6), 0)
+    tok, page, pf, n_pg = O.page_rope_pos(torch.tensor([prompt]), IMG, PG, len(prompt))
+    t, p = tok[:, -1], page[:, -1]
+    seq = list(prompt)
+    for step in range(30):
+        x = PG if rng.random() < 0.25 else TXT
+        seq.append(x)
+        t, p = O.page_rope_advance(p, t, pf, n_pg, torch.tensor([x]), PG)
+        if int(p) < n_pg - 1 or x != PG:
+            ref = O.page_rope_pos(torch.tensor([seq]), IMG, PG, len(seq))
+            if ref[3] == n_pg:
+                assert int(t) == int(ref[0][0, -1]) and int(p) == int(ref[1][0, -1]), step
+    # the clamp, by hand: at the last page a <PAGE> keeps the page and restarts the count
+    last = torch.tensor([n_pg - 1])
+    t2, p2 = O.page_rope_advance(last, torch.tensor([50]), pf, n_pg, torch.tensor([PG]), PG)
+    assert int(p2) == n_pg - 1 and int(t2) == int(pf[0, n_pg - 1])
+
+
+def test_rotary2d_frequencies_and_angles():
+    """DeepseekV2IndexerRotary2D: inverse frequencies base ** -(j / n) (resample) or
+    base ** -(2 j / dim) (truncate) for the token pairs and base_page ** -(i / pairs) for
+    the page pairs; cos/sin [.., dim] with the first n_tok pairs turned by tok only, the
+    rest by page (mod page_mod), both halves equal; against float64 closed forms."""
+    dim, bt, bp = 128, 10000.0, 256.0
+    for mode in ("resample", "truncate"):
+        it, ip = O.rotary2d_inv_freq(dim, bt, bp, 1, mode)
+        n = dim // 2 - 1
+        j = torch.arange(n, dtype=torch.float64)
+        exp = bt ** (-(j / n) if mode == "resample" else -(2 * j / dim))
+        torch.testing.assert_close(it.double(), exp, atol=0, rtol=1e-6)
+        assert ip.tolist() == [1.0]
+    it, ip = O.rotary2d_inv_freq(dim, bt, bp, 4)
+    torch.testing.assert_close(ip.double(), bp ** -(torch.arange(4).double() / 4), rtol=1e-6,
+                               atol=0)
+    with pytest.raises(ValueError):
+        O.rotary2d_inv_freq(dim, bt, bp, 64)
+    tok = torch.tensor([[0, 1, 7, 2730]])
+    page = torch.tensor([[0, 3, 4, 5]])
+    c, s = O.rotary2d_cos_sin(tok, page, it, ip, page_mod=2)
+    assert c.shape == (1, 4, dim)
+    torch.testing.assert_close(c[..., :64], c[..., 64:], atol=0, rtol=0)
+    # the angles are fp32 products (an angle of ~800 rad carries a 6e-5 rounding step);
+    # cos / sin of those fp32 angles in float64
+    ang_t = (tok.float()[..., None] * it[None, None]).double()
+    ang_p = ((page % 2).float()[..., None] * ip[None, None]).double()
+    ang = torch.cat([ang_t, ang_p], -1)
+    torch.testing.assert_close(c[..., :64].double(), ang.cos(), atol=2e-6, rtol=0)
+    torch.testing.assert_close(s[..., :64].double(), ang.sin(), atol=2e-6, rtol=0)
+    assert c[0, 0].eq(1).all() and s[0, 0].eq(0).all()
+    # page 3 and 5 fold to the same parity: equal page part, different token part
+    torch.testing.assert_close(c[0, 1, 60:64], c[0, 3, 60:64], atol=0, rtol=0)
+    c0, _ = O.rotary2d_cos_sin(tok, page, it, ip, page_mod=0)
+    assert not torch.equal(c0[0, 1, 60:64], c0[0, 3, 60:64])
