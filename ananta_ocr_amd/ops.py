@@ -103,9 +103,11 @@ def kbar(idx_k, head_cls, block_size, cu_seqlens=None, seq_lens=None, nblk_cap=N
 
 
 def block_scores(idx_q, kb, block_size, local_blocks, q_pos=None, cu_seqlens=None,
-                 seq_lens=None, S=None, max_seqlen=None):
+                 seq_lens=None, S=None, max_seqlen=None, key_lens=None):
     """Block scores z for query rows idx_q fp32 [B,Lq,d] (or [1,T,d] + cu_seqlens)
-    against k_bar [B,nblk,d].  Returns [B,Lq,nblk] (or [T,nblk]) fp32."""
+    against k_bar [B,nblk,d].  Returns [B,Lq,nblk] (or [T,nblk]) fp32.  Key lengths
+    per sequence: key_lens [B] when given, else the cu_seqlens documents (or seq_lens,
+    else S)."""
     _need_gpu(idx_q, kb)
     lib = _lib.load()
     idx_q = idx_q.float()
@@ -130,9 +132,10 @@ def block_scores(idx_q, kb, block_size, local_blocks, q_pos=None, cu_seqlens=Non
         sb, st = idx_q.stride(0), idx_q.stride(1)
         Sk = Lq if S is None else S
     qp = _i32(q_pos)
-    lens = _i32(seq_lens)
+    lens = _i32(seq_lens if key_lens is None else key_lens)
+    cu_k = cu if key_lens is None else None
     st_ = lib.dash_block_scores(_ptr(idx_q), sb, st, _ptr(cu), Lq, _ptr(qp), _ptr(kb),
-                                kb.stride(0), nblk, _ptr(cu), _ptr(lens), Sk, B, d, block_size,
+                                kb.stride(0), nblk, _ptr(cu_k), _ptr(lens), Sk, B, d, block_size,
                                 local_blocks, _ptr(z), zs, _stream())
     _lib.check(st_, "dash_block_scores")
     return z
@@ -632,40 +635,40 @@ def attn_decode(q, k, v, idx, bias, valid, block_size, local_window, scale, seq_
     return (out, lse) if return_lse else out
 
 
-def attn_decode_rows(q, k, v, idx, bias, valid, q_pos, block_size, local_window, scale,
-                     seq_lens=None, block_table=None, page_size=None, out_dtype=torch.float32):
-    """Decode attention for Lq query rows per sequence, each at its own position.
-    q [B,H,Lq,D] bf16; idx/bias/valid [B,Lq,K]; q_pos [B,Lq].  Cache contiguous
-    [B,H,S,D] or paged [pages, page_size, H, D] with block_table [B,P] and seq_lens [B].
-    Row (b, l) attends keys j <= q_pos[b,l] (and j < the sequence's length) of sequence b.
-    Returns out [B,H,Lq,D] (out_dtype).
+def attn_rows(q, k, v, idx, bias, valid, q_pos, row_seq, block_size, local_window, scale,
+              seq_lens=None, block_table=None, page_size=None, out_dtype=torch.float32):
+    """Attention of R query rows, each of its own sequence and position: q [R,H,D] bf16,
+    row r of sequence row_seq[r] at position q_pos[r] attends that sequence's window
+    (q_pos - LW, q_pos] and the keys below the window of its routed blocks idx[r] (with
+    bias[r]).  Cache contiguous [B,H,S,D] or paged [pages, page_size, H, D] with
+    block_table [B,P]; seq_lens [B] (default S).  Returns out [R,H,D] (out_dtype).
 
-    Each row runs as its own decode query of dash_attn_decode over a block table whose
-    row b * Lq + l addresses sequence b: for a contiguous cache, one page per sequence
-    that spans its whole length (page b at the sequence's batch offset), so no cache
-    data moves."""
-    _need_gpu(q, k, v, q_pos)
+    Each row runs as one query of dash_attn_decode over a block table whose row r
+    addresses sequence row_seq[r]: for a contiguous cache one page per sequence that spans
+    its whole length (page b at the sequence's batch offset), so no cache data moves."""
+    _need_gpu(q, k, v, q_pos, row_seq)
     lib = _lib.load()
-    B, H, Lq, D = q.shape
-    R = B * Lq
-    qr = _rows(q.to(torch.bfloat16).permute(0, 2, 1, 3).reshape(R, H, D))
+    R, H, D = q.shape
+    qr = _rows(q.to(torch.bfloat16))
     k = _rows(k.to(torch.bfloat16))
     v = _rows(v.to(torch.bfloat16))
+    rs = row_seq.to(torch.int64)
     if block_table is not None:
-        table = _i32(block_table).repeat_interleave(Lq, 0)
+        table = _i32(block_table).index_select(0, rs)
         page = int(page_size)
         S = table.shape[1] * page
         k_sp, k_st, k_sh = k.stride(0), k.stride(1), k.stride(2)
         v_sp, v_st, v_sh = v.stride(0), v.stride(1), v.stride(2)
-        lens = None if seq_lens is None else _i32(seq_lens).repeat_interleave(Lq, 0)
     else:
         S = k.shape[2]
         page = max(block_size, (S + block_size - 1) // block_size * block_size)
-        table = torch.arange(B, dtype=torch.int32, device=q.device).repeat_interleave(Lq)[:, None]
+        table = row_seq.to(torch.int32).reshape(R, 1).contiguous()
         k_sp, k_st, k_sh = k.stride(0), k.stride(2), k.stride(1)
         v_sp, v_st, v_sh = v.stride(0), v.stride(2), v.stride(1)
-        lens = torch.full((R,), S, dtype=torch.int32, device=q.device) if seq_lens is None \
-            else _i32(seq_lens).repeat_interleave(Lq, 0)
+    if seq_lens is None:
+        lens = torch.full((R,), S, dtype=torch.int32, device=q.device)
+    else:
+        lens = _i32(seq_lens).index_select(0, rs)
     K = 0 if idx is None else idx.shape[-1]
     idx_c = None if idx is None else _i32(idx.reshape(R, K))
     bias_c = None if bias is None else bias.reshape(R, K).float().contiguous()
@@ -675,18 +678,39 @@ def attn_decode_rows(q, k, v, idx, bias, valid, q_pos, block_size, local_window,
     ws_bytes = ctypes.c_int64(0)
     _lib.check(lib.dash_attn_decode_workspace_size(R, H, D, nsplit, ws_bytes), "workspace")
     ws = torch.empty((ws_bytes.value + 3) // 4, dtype=torch.float32, device=q.device)
-    out = torch.empty(B, Lq, H, D, dtype=out_dtype, device=q.device)
-    o2 = out.view(R, H, D)
+    out = torch.empty(R, H, D, dtype=out_dtype, device=q.device)
+    if R == 0:
+        return out
     st_ = lib.dash_attn_decode(
         _ptr(qr), qr.stride(0), qr.stride(1),
         _ptr(k), 0, k_sh, k_st, k_sp, _ptr(v), 0, v_sh, v_st, v_sp,
         _ptr(table), table.stride(0), page, _ptr(lens), _ptr(qp),
         _ptr(idx_c), _ptr(valid_c), _ptr(bias_c), K,
-        _ptr(o2), int(out_dtype == torch.bfloat16), o2.stride(0), o2.stride(1),
+        _ptr(out), int(out_dtype == torch.bfloat16), out.stride(0), out.stride(1),
         None, 0, 0, R, H, S, D, int(block_size), int(local_window), float(scale), int(nsplit),
         _ptr(ws), ws.numel() * 4, _stream())
     _lib.check(st_, "dash_attn_decode")
-    return out.permute(0, 2, 1, 3)
+    return out
+
+
+def attn_decode_rows(q, k, v, idx, bias, valid, q_pos, block_size, local_window, scale,
+                     seq_lens=None, block_table=None, page_size=None, out_dtype=torch.float32):
+    """Decode attention for Lq query rows per sequence, each at its own position.
+    q [B,H,Lq,D] bf16; idx/bias/valid [B,Lq,K]; q_pos [B,Lq].  Cache contiguous
+    [B,H,S,D] or paged [pages, page_size, H, D] with block_table [B,P] and seq_lens [B].
+    Row (b, l) attends keys j <= q_pos[b,l] (and j < the sequence's length) of sequence b.
+    Returns out [B,H,Lq,D] (out_dtype)."""
+    B, H, Lq, D = q.shape
+    qr = q.permute(0, 2, 1, 3).reshape(B * Lq, H, D)
+    row_seq = torch.arange(B, device=q.device).repeat_interleave(Lq)
+    K = 0 if idx is None else idx.shape[-1]
+    out = attn_rows(qr, k, v, None if idx is None else idx.reshape(B * Lq, K),
+                    None if bias is None else bias.reshape(B * Lq, K),
+                    None if valid is None else valid.reshape(B * Lq, K),
+                    q_pos.reshape(B * Lq), row_seq, block_size, local_window, scale,
+                    seq_lens=seq_lens, block_table=block_table, page_size=page_size,
+                    out_dtype=out_dtype)
+    return out.view(B, Lq, H, D).permute(0, 2, 1, 3)
 
 
 def _kbar_layout(kbar_cache, kbar_table, bounds):

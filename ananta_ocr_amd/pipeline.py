@@ -62,7 +62,10 @@ class KBarPageCache:
     paged = True
 
     def __init__(self, num_pages, dim, device):
-        self.kbar = torch.zeros(num_pages, dim, dtype=torch.float32, device=device)
+        # one spare row past the pool takes the writes of table entries that are not
+        # refreshed (refresh_from), so that every write of a step is one index_copy_
+        self._buf = torch.zeros(num_pages + 1, dim, dtype=torch.float32, device=device)
+        self.kbar = self._buf[:num_pages]
 
     def put(self, pages, k_bar):
         """Write the summaries k_bar [n, d] of the given physical pages [n]."""
@@ -89,6 +92,78 @@ class KBarPageCache:
         c = torch.arange(nblk, device=kb.device)[None, :]
         sel = (c < nb[:, None]) & (c >= nb[:, None] - int(tail_pages))
         self.kbar[block_table.to(torch.int64)[sel]] = kb[sel]
+
+
+    def refresh_from(self, idx_k, head_cls, block_size, block_table, seq_lens, first_block):
+        """Recompute the summaries of blocks first_block[b] .. of every sequence (an extend
+        step's boundary page and new pages, kbar_all_plan of route_triton.py:576-601),
+        without a host synchronisation."""
+        nblk = block_table.shape[1]
+        kb = ops.kbar(idx_k, head_cls, block_size, seq_lens=seq_lens, nblk_cap=nblk,
+                      block_table=block_table, page_size=block_size)
+        nb = (seq_lens.to(torch.int64) + block_size - 1) // block_size
+        c = torch.arange(nblk, device=kb.device)[None, :]
+        sel = (c < nb[:, None]) & (c >= first_block.to(torch.int64)[:, None])
+        dump = self._buf.shape[0] - 1
+        tgt = torch.where(sel, block_table.to(torch.int64), torch.full_like(c, dump))
+        self._buf.index_copy_(0, tgt.reshape(-1), kb.reshape(-1, kb.shape[-1]))
+
+
+def extend_prefill(state, q, k_cache, v_cache, idx_q, idx_k, head_cls, block_size,
+                   local_blocks, idx_scale, floor, sigma, K, topm, block_table, seq_lens,
+                   context_lens, cu_seqlens_q, max_query_len=None, scale=None,
+                   block_cand=None, out_dtype=torch.bfloat16, return_routing=False):
+    """Extend (chunked or prefix-cached) prefill over a paged cache: the query rows of
+    request b are the tokens at positions context_lens[b] .. seq_lens[b] - 1 (rows
+    cu_seqlens_q[b] .. cu_seqlens_q[b + 1] - 1 of q), attending the request's whole
+    cached sequence, as the serving backend's extend path does
+    (whl:sglang/srt/layers/attention/unlimited_ocr_v2_backend.py:1302-1335, :1454-1463;
+    route_prefill_triton, route_triton.py:529-678) with the routing of
+    _infer_route_select (modeling_deepseekv2.py:309-333) per request:
+
+    * the k_bar page pool (state, a KBarPageCache) is refreshed from each request's
+      boundary page (context_lens // block_size) on;
+    * block scores of each query row at q_pos = context_len + row against the request's
+      summaries (remote: c <= q_pos // block_size - local_blocks, c < its block count);
+    * routing (top-M, 1.5-entmax, first K, centred log-prior bias) per row;
+    * attention of each row over the window (q_pos - LW, q_pos] and its routed blocks.
+
+    q [T,H,D] bf16, k_cache / v_cache [pages, block_size, H, D] bf16 (the new tokens
+    already written), idx_q [T,d] fp32, idx_k the paged index keys [pages, block_size, d]
+    (new ones written), block_table [B,P] int32 (pages of block_size tokens), seq_lens /
+    context_lens [B], cu_seqlens_q [B+1].  max_query_len (the longest request chunk) keeps
+    the pass free of host synchronisations.  Returns out [T,H,D] (out_dtype)."""
+    if not getattr(state, "paged", False):
+        raise NotImplementedError("extend_prefill takes a k_bar page pool (KBarPageCache)")
+    T, H, D = q.shape
+    B = block_table.shape[0]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    dev = q.device
+    seq = seq_lens.to(device=dev, dtype=torch.int64)
+    ctx = context_lens.to(device=dev, dtype=torch.int64)
+    cu = cu_seqlens_q.to(device=dev, dtype=torch.int64)
+    state.refresh_from(idx_k, head_cls, block_size, block_table, seq, ctx // block_size)
+    P = block_table.shape[1]
+    pages = block_table.to(torch.int64).clamp(0, state.kbar.shape[0] - 1)
+    kb_seq = state.kbar.index_select(0, pages.reshape(-1)).view(B, P, -1)
+    q_lens = cu[1:] - cu[:-1]
+    row_seq = torch.repeat_interleave(torch.arange(B, device=dev), q_lens, output_size=T)
+    rows = torch.arange(T, device=dev)
+    q_pos = (ctx.index_select(0, row_seq) + rows - cu.index_select(0, row_seq)).to(torch.int32)
+    z = ops.block_scores(idx_q.reshape(1, T, -1), kb_seq, block_size, local_blocks,
+                         q_pos=q_pos, cu_seqlens=cu, max_seqlen=max_query_len, key_lens=seq,
+                         S=P * block_size)
+    nblk_b = (seq + block_size - 1) // block_size
+    width = max(1, min(int(K), int(topm))) if int(topm) > 0 else max(1, int(K))
+    idx, bias, valid = ops.route(z, block_cand, idx_scale, floor, sigma, K, topm,
+                                 row_nblk=nblk_b.index_select(0, row_seq), width=width)
+    out = ops.attn_rows(q, k_cache, v_cache, idx, bias, valid, q_pos, row_seq, block_size,
+                        local_blocks * block_size, scale, seq_lens=seq, block_table=block_table,
+                        page_size=block_size, out_dtype=out_dtype)
+    if return_routing:
+        return out, (idx, bias, valid.bool()), q_pos
+    return out
 
 
 def init_decode_state(idx_k, head_cls, block_size, nblk_cap, seq_lens=None, block_table=None,
