@@ -60,6 +60,9 @@ struct PrefillArgs {
   const int32_t* idx; const uint8_t* valid; const float* bias; int K;   // [rows, K]
   const int32_t* cu;                   // varlen: [B+1]
   const int32_t* kmin;                 // per token row, or null
+  // K % 4 == 0 with 16-byte aligned ids and biases and 4-byte aligned validity: the
+  // slots of a row are read and written four at a time
+  int slots_vec;
   int S, H, bs, lw, nblk_cap;
   int ntiles;                          // 128-query tiles per sequence (of S)
   float scale_log2e;
@@ -138,23 +141,36 @@ __device__ __forceinline__ bool slot_usable(const PrefillArgs& a, int c, int64_t
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4v lds_short4;
 
-// Load the routed slots g0 .. g0+15 of one row (K <= 64): ids and validity, with
-// vector loads where the slots are 16-byte aligned; slots past K get id -1.
+// Load the routed slots g0 .. g0+15 of one row (K <= 64): ids and validity, four
+// slots per load where slots_vec allows (ng is then a multiple of 4); slots past K get
+// id -1.
 __device__ __forceinline__ void load_row_slots(const PrefillArgs& a, int64_t row, int g0,
                                                int32_t (&c)[kPfMaxK], uint32_t& vmask) {
   const int64_t p0 = row * a.K + g0;
   const int ng = min(kPfMaxK, a.K - g0);
-  if (a.K % kPfMaxK == 0) {
+  if (a.slots_vec) {
     const int4* ip = (const int4*)(a.idx + p0);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int4 v = ip[q];
+      const int4 v = 4 * q < ng ? ip[q] : make_int4(-1, -1, -1, -1);
       c[4 * q] = v.x; c[4 * q + 1] = v.y; c[4 * q + 2] = v.z; c[4 * q + 3] = v.w;
     }
-  } else {
+    vmask = 0;
+    if (a.valid) {
 #pragma unroll
-    for (int s = 0; s < kPfMaxK; ++s) c[s] = s < ng ? a.idx[p0 + s] : -1;
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t w = 4 * q < ng ? *(const uint32_t*)(a.valid + p0 + 4 * q) : 0u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if ((w >> (8 * e)) & 0xffu) vmask |= 1u << (4 * q + e);
+      }
+    } else {
+      vmask = (1u << ng) - 1u;
+    }
+    return;
   }
+#pragma unroll
+  for (int s = 0; s < kPfMaxK; ++s) c[s] = s < ng ? a.idx[p0 + s] : -1;
   vmask = 0;
   if (a.valid) {
 #pragma unroll
@@ -228,6 +244,13 @@ __global__ __launch_bounds__(kPfTQ) void prefill_plan_kernel(PrefillArgs a) {
 #pragma unroll
         for (int s = 0; s < kPfMaxK; ++s) w[s >> 2] |= kind_of(g0 + s) << (8 * (s & 3));
         *(uint4*)(a.kind + row * a.K + g0) = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    } else if (a.K % 4 == 0) {              // 4 kinds per 4-byte store
+      for (int s0 = 0; s0 < a.K; s0 += 4) {
+        uint32_t w = 0u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w |= kind_of(s0 + e) << (8 * e);
+        *(uint32_t*)(a.kind + row * a.K + s0) = w;
       }
     } else {
       for (int s = 0; s < a.K; ++s) a.kind[row * a.K + s] = (uint8_t)kind_of(s);
@@ -361,11 +384,19 @@ __global__ __launch_bounds__(kPfTQ) void prefill_scatter_kernel(PrefillArgs a) {
     const int ng = min(kPfMaxK, a.K - g0);
     int pos[kPfMaxK];
     bool sp[kPfMaxK];
+    if (a.slots_vec) {
+      uint32_t kw[4];
 #pragma unroll
-    for (int s = 0; s < kPfMaxK; ++s) {
-      sp[s] = s < ng && a.kind[row * a.K + g0 + s] == 2;
-      pos[s] = sp[s] ? atomicAdd(&sFill[c[s]], 1) : 0;
+      for (int q = 0; q < 4; ++q)
+        kw[q] = 4 * q < ng ? *(const uint32_t*)(a.kind + row * a.K + g0 + 4 * q) : 0u;
+#pragma unroll
+      for (int s = 0; s < kPfMaxK; ++s) sp[s] = ((kw[s >> 2] >> (8 * (s & 3))) & 0xffu) == 2;
+    } else {
+#pragma unroll
+      for (int s = 0; s < kPfMaxK; ++s) sp[s] = s < ng && a.kind[row * a.K + g0 + s] == 2;
     }
+#pragma unroll
+    for (int s = 0; s < kPfMaxK; ++s) pos[s] = sp[s] ? atomicAdd(&sFill[c[s]], 1) : 0;
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s)
       if (sp[s]) {
@@ -650,24 +681,26 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
       ++cnt;
       atomicOr(&sBits[c >> 5], 1u << (c & 31));
     };
-    if (t < len && a.kind && a.K == kPfMaxK) {
-      // Planned rows of 16 slots (kinds, ids and biases read with 16-byte loads;
-      // the plan has already dropped duplicate and unusable slots).  The dense
-      // slots are sorted by block id with a bitonic network on the keys
-      // id << 5 | slot in registers (ids < 2048; other slots take id 2048 and
-      // sort last); the biases, stored in slot order, are then gathered by slot.
-      const int64_t p0 = (r0 + t) * kPfMaxK;
-      const uint4 kv = *(const uint4*)(a.kind + p0);
+    if (t < len && a.kind && a.slots_vec && a.K <= kPfMaxK) {
+      // Planned rows of up to 16 slots, K a multiple of 4 (kinds, ids and biases read
+      // four slots per load; the plan has already dropped duplicate and unusable
+      // slots).  The dense slots are sorted by block id with a bitonic network on the
+      // keys id << 5 | slot in registers (ids < 2048; other slots, and slots past K,
+      // take id 2048 and sort last); the biases, stored in slot order, are then
+      // gathered by slot.
+      const int64_t p0 = (r0 + t) * a.K;
+      uint32_t kw[4];
       int4 iv[4];
       float4 bv4[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        iv[q] = ((const int4*)(a.idx + p0))[q];
-        bv4[q] = ((const float4*)(a.bias + p0))[q];
+        const bool in = 4 * q < a.K;
+        kw[q] = in ? *(const uint32_t*)(a.kind + p0 + 4 * q) : 0u;
+        iv[q] = in ? ((const int4*)(a.idx + p0))[q] : make_int4(0, 0, 0, 0);
+        bv4[q] = in ? ((const float4*)(a.bias + p0))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) ((float4*)&sBias[tid][0])[q] = bv4[q];
-      const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
       uint32_t key[kPfMaxK];
 #pragma unroll
       for (int s = 0; s < kPfMaxK; ++s) {
@@ -977,14 +1010,15 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
     float l2[kPfMaxK];
     int32_t sp[kPfMaxK];                   // positions (read for sparse slots only)
     uint32_t smask = 0;
-    if (pa.K % kPfMaxK == 0) {
-      const uint4 kv = *(const uint4*)(pa.kind + p0);
+    if (pa.slots_vec) {                    // ng is a multiple of 4
+      uint32_t kw[4];
 #pragma unroll
       for (int g = 0; g < kPfMaxK / 4; ++g) {
-        const int4 pv = *(const int4*)(pa.spos + p0 + 4 * g);
+        const bool in = 4 * g < ng;
+        kw[g] = in ? *(const uint32_t*)(pa.kind + p0 + 4 * g) : 0u;
+        const int4 pv = in ? *(const int4*)(pa.spos + p0 + 4 * g) : make_int4(0, 0, 0, 0);
         sp[4 * g] = pv.x; sp[4 * g + 1] = pv.y; sp[4 * g + 2] = pv.z; sp[4 * g + 3] = pv.w;
       }
-      const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
       for (int s = 0; s < kPfMaxK; ++s)
         if (qvalid && ((kw[s >> 2] >> (8 * (s & 3))) & 0xffu) == 2) smask |= 1u << s;
@@ -1283,6 +1317,16 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
 }
 
 // Workspace layout of the hybrid plan (byte offsets, 256-byte aligned pieces).
+// Slots of a row read and written four at a time: K a multiple of 4, ids and biases
+// 16-byte aligned, validity 4-byte aligned (a row starts at row * K).
+inline int slots_vectorizable(int K, const int32_t* idx, const uint8_t* valid,
+                              const float* bias) {
+  if (K <= 0 || K % 4 != 0) return 0;
+  if ((uintptr_t)idx % 16 != 0 || (uintptr_t)bias % 16 != 0) return 0;
+  if (valid && (uintptr_t)valid % 4 != 0) return 0;
+  return 1;
+}
+
 struct PlanLayout {
   int64_t count, done, err, tbase, bch, nchunks, cpref, rec, kind, spos, plse, po, total;
   int64_t ppos;
@@ -1420,6 +1464,7 @@ extern "C" int dash_attn_prefill(
   a.lse = lse; a.lse_row = lse_row; a.lse_sh = lse_sh;
   a.idx = idx; a.valid = valid; a.bias = bias; a.K = K;
   a.cu = cu_seqlens; a.kmin = kmin;
+  a.slots_vec = slots_vectorizable(K, idx, valid, bias);
   a.S = S; a.H = H; a.bs = block_size; a.lw = local_window; a.nblk_cap = nblk_cap;
   a.scale_log2e = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
@@ -1528,6 +1573,7 @@ extern "C" int dash_attn_prefill_backward(
   p.v_sb = v_sb; p.v_sh = v_sh; p.v_st = v_st;
   p.idx = idx; p.valid = valid; p.bias = bias; p.K = K;
   p.cu = cu_seqlens; p.kmin = kmin;
+  p.slots_vec = slots_vectorizable(K, idx, valid, bias);
   p.S = S; p.H = H; p.bs = block_size; p.lw = local_window; p.nblk_cap = nblk_cap;
   p.scale_log2e = scale * 1.4426950408889634f;
   p.ntiles = (S + kPfTQ - 1) / kPfTQ;
