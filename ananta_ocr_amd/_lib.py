@@ -38,6 +38,7 @@ SIGNATURES = {
                                _p, _l, _l, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _f,
                                _i, _l, _p, _l, _p]),
     "dash_attn_prefill_workspace_size": (_i, [_i, _i, _i, _l, _i, _i, _i, ctypes.POINTER(_l)]),
+    "dash_attn_prefill_split_workspace_size": (_i, [_i, _i, _i, _i, ctypes.POINTER(_l)]),
     "dash_attn_prefill_backward_workspace_size": (_i, [_i, _i, _i, _l, _i, _i, _i,
                                                        ctypes.POINTER(_l)]),
     "dash_attn_prefill_backward": (_i, [_p, _l, _l, _l, _p, _l, _l, _l, _p, _l, _l, _l,

@@ -23,7 +23,9 @@
 //     that each lane owns one query's softmax state; base-2 online softmax;
 //     O^T += V^T P^T; finally the query's sparse partials are merged in.
 // With no plan (dense_threshold <= 0) the tile kernel processes every routed
-// block of the tile as a dense block.
+// block of the tile as a dense block; when its grid alone cannot fill the chip,
+// the items of each tile are divided among nsplit work-groups, each writing a
+// normalised bf16 partial per row, and a merge kernel combines them.
 
 #include "dash_common.h"
 
@@ -78,6 +80,13 @@ struct PrefillArgs {
   int32_t* done;                       // arrival counter of the scan (follows blk_count)
   int32_t* err;                        // nonzero: a plan count exceeded its capacity (follows done)
   int B;
+  // packed documents (cu): the tile grid runs over the documents' real tiles in one
+  // order, head-major, so that the XCDs get equal shares (the scan kernel writes these):
+  // tile_pref [B+1] the first tile of each document, tile_doc [ntv] the document of
+  // each tile; ntv bounds the number of tiles
+  int32_t* tile_pref;
+  int32_t* tile_doc;
+  int ntv;
   int32_t* chunk_rec;                  // [B, chunk_cap, kRec] chunk records
   int chunk_cap;
   // sparse partials, one per (head, pair position) (see part_row): a pair's
@@ -87,6 +96,12 @@ struct PrefillArgs {
   float* part_lse;                     // [H, ppos]  base-2 log-sum-exp
   bf16* part_o;                        // [H, ppos, D]  normalised partial output, dims
                                        // in MFMA lane order (see part_index)
+  // split tiles (no plan; nsplit > 1): work-group part p of tile tl (the logical
+  // (sequence, head, tile) id) takes an equal share of the tile's items and writes
+  // its rows' normalised output and base-2 log-sum-exp
+  int nsplit;
+  bf16* split_o;                       // [tiles, nsplit, kPfTQ, D] bf16, dims in order
+  float* split_lse;                    // [tiles, nsplit, kPfTQ]
 };
 
 __device__ __forceinline__ int seq_len(const PrefillArgs& a, int b) {
@@ -299,6 +314,27 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(PrefillArgs a) {
   const int xc = bc + ic - sc;                       // exclusive prefix of this thread
   if (e0 < kPfMaxBlocks) { sC[e0] = v0; sCh[e0] = xc; }
   if (e1 < kPfMaxBlocks) { sC[e1] = v1; sCh[e1] = xc + c0; }
+  if (a.tile_doc) {
+    // this sequence's first tile in the one order of all sequences' tiles
+    int pre = 0;
+    for (int bb = tid; bb < b; bb += 1024) pre += (seq_len(a, bb) + kPfTQ - 1) / kPfTQ;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) pre += __shfl_xor(pre, m, kWave);
+    __syncthreads();
+    if (lane == 0) sWave[0][wv] = pre;
+    __syncthreads();
+    int first = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) first += sWave[0][w];
+    const int nt = (len + kPfTQ - 1) / kPfTQ;
+    if (tid == 0) {
+      a.tile_pref[b] = first;
+      if (b == (int)gridDim.x - 1) a.tile_pref[b + 1] = first + nt;
+    }
+    for (int i = tid; i < nt; i += 1024)
+      if (first + i < a.ntv) a.tile_doc[first + i] = b;
+    __syncthreads();
+  }
   __shared__ int sLast;
   if (tid == 1023) {
     // the sparse grid covers no chunk past the sequence's records
@@ -636,6 +672,24 @@ __device__ __forceinline__ int next_union(const uint32_t* sBits, int nwords, int
   return __builtin_amdgcn_readfirstlane((((b0 >> 5) + f) << 5) + (int)__builtin_ctz(fb));
 }
 
+// The j-th (from 0) dense block of the tile's bitmap (nwords <= 64 words, one per
+// lane); j is below the number of set bits.
+__device__ __forceinline__ int nth_union(const uint32_t* sBits, int nwords, int j, int lane) {
+  const uint32_t bits = lane < nwords ? sBits[lane] : 0u;
+  const int cnt = __popc(bits);
+  int x = cnt;                             // inclusive prefix of the counts over lanes
+#pragma unroll
+  for (int s = 1; s < kWave; s <<= 1) {
+    const int y = __shfl_up(x, s, kWave);
+    if (lane >= s) x += y;
+  }
+  const int f = __builtin_ctzll(__ballot(x > j));   // the word holding it
+  const int before = __builtin_amdgcn_readlane(x - cnt, f);
+  uint32_t w = __builtin_amdgcn_readlane(bits, f);
+  for (int i = before; i < j; ++i) w &= w - 1u;      // drop the lower set bits
+  return __builtin_amdgcn_readfirstlane((f << 5) + (int)__builtin_ctz(w));
+}
+
 template <int D, int IT, int OCC>
 __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
   static_assert(D == 128, "head_dim 128");
@@ -647,10 +701,29 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) float sBias[kPfTQ][kPfMaxK];
   __shared__ uint32_t sBits[kPfMaxBlocks / 32];
 
-  // logical order (sequence, head, tile), tile fastest, contiguous per XCD
-  const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
-  const int tile = lid % a.ntiles, bh = lid / a.ntiles;
-  const int h = bh % a.H, b = bh / a.H;
+  // logical order (sequence, head, tile), tile fastest, contiguous per XCD; packed
+  // documents in the order (head, tile of all documents), so that every logical id
+  // below the tile count is a real tile and the XCDs get equal shares
+  // (split tiles: the nsplit parts of a tile are consecutive logical ids)
+  int lid = xcd_logical_id(blockIdx.x, gridDim.x);
+  int part = 0;
+  if (a.nsplit > 1) {
+    part = lid % a.nsplit;
+    lid /= a.nsplit;
+  }
+  int tile, h, b;
+  if (a.tile_doc) {
+    const int g = lid % a.ntv;
+    h = lid / a.ntv;
+    if (g >= a.tile_pref[a.B]) return;
+    b = a.tile_doc[g];
+    tile = g - a.tile_pref[b];
+  } else {
+    tile = lid % a.ntiles;
+    const int bh = lid / a.ntiles;
+    h = bh % a.H;
+    b = bh / a.H;
+  }
   const int len = seq_len(a, b);
   const int t0 = tile * kPfTQ;
   if (t0 >= len) return;
@@ -807,6 +880,19 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
     nu = __builtin_amdgcn_readfirstlane(nu);
   }
   const int n_items = n_win + nu * ipb;
+  // this work-group's items [i0, i1): all of them, or with split tiles an equal
+  // share cut at routed-block boundaries
+  int i0 = 0, i1 = n_items;
+  if (a.nsplit > 1) {
+    auto cut = [&](int p) {
+      const int x = (int)((int64_t)p * n_items / a.nsplit);
+      return x <= n_win ? x : n_win + (x - n_win) / ipb * ipb;
+    };
+    i0 = cut(part);
+    i1 = cut(part + 1);
+  }
+  // first dense block of the share (0 when it starts in the window band)
+  const int c_first = (i0 > n_win && i0 < i1) ? nth_union(sBits, nwords, (i0 - n_win) / ipb, lane) : 0;
   // fetch byte offsets: row r0 of a 16-row group and its swizzled chunk
   const int fr0 = wv * 4 + (lane >> 4);
   const uint32_t fkc = (uint32_t)(k_slot(fr0, lane & 15) * 16), fvc = (uint32_t)(v_slot(fr0, lane & 15) * 16);
@@ -817,7 +903,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
   const float csc = a.scale_log2e;
 
   // Fetch iterator: block and sub-item of the last item whose K rows were fetched.
-  int pf_c = -1, pf_sub = ipb - 1;
+  int pf_c = c_first - 1, pf_sub = ipb - 1;
   int jk = 0, ck = -1, subk = 0;           // that item's first key, block, sub-item
   auto advance = [&](int it) {
     if (it >= n_win && ++pf_sub >= ipb) { pf_sub = 0; pf_c = next_union(sBits, nwords, pf_c, lane); }
@@ -825,14 +911,15 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
     ck = pf_c;
     subk = pf_sub;
   };
-  if (n_items > 0) {
-    advance(0);
+  if (i1 > i0) {
+    advance(i0);
     rows_fetch<D, IT>(sK0, kb, a.k_st, fk0, fkc, fr0, jk, len, wv);
   }
   // Cursor into this query's ascending dense-block list (ended by id 2048): the
   // next candidate block is read one match ahead.
   int ptr = 0;
-  int cand_c = sIdx[myrow][0];
+  while (c_first > 0 && ptr < kPfMaxK && sIdx[myrow][ptr] < c_first) ++ptr;
+  int cand_c = ptr < kPfMaxK ? sIdx[myrow][ptr] : kPfMaxBlocks;
   float cur_b = -INFINITY;                 // bias (base 2) of the current routed block
 
   // Software pipeline over the items: step i computes S^T of item i, its row
@@ -895,7 +982,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
     float bl = -INFINITY;
     int kq = 0;
     uint32_t span = 0;
-    if (it < n_items) {
+    if (it < i1) {
       rows_fetch<D, IT>(sVc, vb, a.v_st, fv, fvc, fr0, jk, len, wv);
       // item it: visible keys and bias of this query
       int lo, hi;
@@ -920,7 +1007,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
       full = __all(!live || (lo <= j0 && j0 + IT - 1 <= hi));
       span = lo <= hi ? (uint32_t)(hi - lo) : 0u;
       kq = j0 + 4 * hl - (lo <= hi ? lo : 0x40000000);
-      if (it + 1 < n_items) {
+      if (it + 1 < i1) {
         advance(it + 1);
         rows_fetch<D, IT>(sKn, kb, a.k_st, fk, fkc, fr0, jk, len, wv);
       }
@@ -985,9 +1072,9 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
         }
     __builtin_amdgcn_s_setprio(0);
   };
-  for (int it = 0; it <= n_items; it += 2) {
+  for (int it = i0; it <= i1; it += 2) {
     step(it, std::integral_constant<int, 0>{});
-    if (it + 1 <= n_items) step(it + 1, std::integral_constant<int, 1>{});
+    if (it + 1 <= i1) step(it + 1, std::integral_constant<int, 1>{});
   }
 
   // Arguments used only from here on are read again through an opaque copy of
@@ -1083,6 +1170,25 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
 
   // ---- epilogue: normalise and store ----
   const float l_tot = xor32_sum(l_run);
+  if (pa.nsplit > 1) {
+    // the share's partials: slot tile id x nsplit + part, which is the logical id
+    const int64_t slot = xcd_logical_id(blockIdx.x, gridDim.x);
+    if (qvalid) {
+      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+      bf16* so = pa.split_o + (slot * kPfTQ + myrow) * D;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          bf16x4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = (bf16)(acc_o[dt][g * 4 + e] * inv);
+          *(bf16x4*)(so + dt * 32 + 8 * g + 4 * hl) = w;
+        }
+      if (hl == 0) pa.split_lse[slot * kPfTQ + myrow] = l_tot > 0.f ? m_run + log2f(l_tot) : -INFINITY;
+    }
+    return;
+  }
   if (qvalid) {
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     bf16* ob = (pa.cu ? pa.o + (int64_t)pa.cu[b] * pa.o_st : pa.o + (int64_t)b * pa.o_sb) +
@@ -1101,6 +1207,52 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
       pa.lse[(r0 + tq) * pa.lse_row + (int64_t)h * pa.lse_sh] = lse;
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Merge of split tiles: each (row, head) row's nsplit partials, weighted by
+// 2^(lse_p - max) in fp32; 16 lanes of 8 dims per row, 16 rows per work-group.
+// Rows no share saw a key of give 0 (log-sum-exp -inf), as an unsplit tile does.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void prefill_split_merge_kernel(PrefillArgs a) {
+  constexpr int D = 128;
+  const int64_t item = (int64_t)blockIdx.x * 16 + threadIdx.x / 16;   // (tile id, row)
+  const int sub = threadIdx.x & 15;
+  if (item >= (int64_t)a.ntiles * a.H * a.B * kPfTQ) return;
+  const int64_t tl = item / kPfTQ;
+  const int r = (int)(item % kPfTQ);
+  const int tile = (int)(tl % a.ntiles);
+  const int bh = (int)(tl / a.ntiles);
+  const int h = bh % a.H, b = bh / a.H;
+  const int t = tile * kPfTQ + r;
+  if (t >= seq_len(a, b)) return;
+  const int P = a.nsplit;
+  const float* ls = a.split_lse + tl * P * kPfTQ + r;
+  float mx = -INFINITY;
+  for (int p = 0; p < P; ++p) mx = fmaxf(mx, ls[p * kPfTQ]);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float wsum = 0.f;
+  if (mx != -INFINITY) {
+    for (int p = 0; p < P; ++p) {
+      const float l = ls[p * kPfTQ];
+      if (l == -INFINITY) continue;
+      const float w = exp2f(l - mx);
+      wsum += w;
+      const bf16x8 x = *(const bf16x8*)(a.split_o + ((tl * P + p) * kPfTQ + r) * D + sub * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += w * bf2f(x[e]);
+    }
+  }
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  bf16x8 y;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = (bf16)(acc[e] * inv);
+  bf16* ob = (a.cu ? a.o + (int64_t)a.cu[b] * a.o_st : a.o + (int64_t)b * a.o_sb) +
+             (int64_t)h * a.o_sh + (int64_t)t * a.o_st;
+  *(bf16x8*)(ob + sub * 8) = y;
+  if (a.lse && sub == 0)
+    a.lse[(row0(a, b) + t) * a.lse_row + (int64_t)h * a.lse_sh] =
+        wsum > 0.f ? (mx + log2f(wsum)) * 0.6931471805599453f : -INFINITY;
 }
 
 // ---------------------------------------------------------------------------
@@ -1328,12 +1480,32 @@ inline int slots_vectorizable(int K, const int32_t* idx, const uint8_t* valid,
 }
 
 struct PlanLayout {
-  int64_t count, done, err, tbase, bch, nchunks, cpref, rec, kind, spos, plse, po, total;
+  int64_t count, done, err, tbase, bch, nchunks, cpref, rec, kind, spos, plse, po, tpref,
+      tdoc, total;
   int64_t ppos;
-  int chunk_cap, ntiles_cap;
+  int chunk_cap, ntiles_cap, ntv;
 };
 
 inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+// Split tiles (no plan): work-groups per tile (tiles = tiles per sequence x heads x
+// sequences), as many as one round of two work-groups on each of the 256 CUs holds,
+// at most 8.  Measured on the 2,730-token prefill (220 tiles, no plan): 2 parts
+// 64.6 us, 3 72.7, 5 82.2, 8 106.7 against 82.2 unsplit (each part repeats the
+// tile's prologue, and a second round of work-groups costs more than it shares).
+constexpr int64_t kSplitSlots = 512;
+constexpr int kSplitMax = 8;
+inline int tile_splits(int64_t tiles) {
+  if (tiles <= 0) return 1;
+  return (int)std::min<int64_t>(kSplitMax, std::max<int64_t>(1, kSplitSlots / tiles));
+}
+// Workspace of the split partials: bf16 rows, then the base-2 log-sum-exps.
+inline int64_t split_o_bytes(int64_t tiles, int ns, int D) {
+  return align256(tiles * ns * kPfTQ * D * 2);
+}
+inline int64_t split_bytes(int64_t tiles, int ns, int D) {
+  return ns > 1 ? split_o_bytes(tiles, ns, D) + align256(tiles * ns * kPfTQ * 4) : 0;
+}
 
 inline PlanLayout plan_layout(int B, int H, int S_max, int64_t rows, int K, int D,
                               int nblk_cap, int bs) {
@@ -1357,6 +1529,10 @@ inline PlanLayout plan_layout(int B, int H, int S_max, int64_t rows, int K, int 
   L.ppos = (rows * K / kPfCH + rows / bs + B + 2) * kPfCH;
   L.plse = o; o = align256(o + L.ppos * H * 4);
   L.po = o; o = align256(o + L.ppos * H * D * 2);
+  // tiles of all sequences in one order: sum ceil(len / kPfTQ) <= (rows + (kPfTQ - 1) B) / kPfTQ
+  L.ntv = (int)((rows + (int64_t)(kPfTQ - 1) * B) / kPfTQ) + 1;
+  L.tpref = o; o = align256(o + (int64_t)(B + 1) * 4);
+  L.tdoc = o; o = align256(o + (int64_t)L.ntv * 4);
   L.total = o;
   return L;
 }
@@ -1415,7 +1591,18 @@ extern "C" int dash_attn_prefill_workspace_size(int B, int H, int S_max, int64_t
   if (!bytes || B < 0 || H <= 0 || S_max < 0 || total_rows < 0 || K < 0 || block_size <= 0)
     return kErrInvalid;
   const int nblk_cap = (S_max + block_size - 1) / block_size;
-  *bytes = plan_layout(B, H, S_max, total_rows, K, D, nblk_cap, block_size).total;
+  const int64_t tiles = (int64_t)((S_max + kPfTQ - 1) / kPfTQ) * H * B;
+  *bytes = std::max(plan_layout(B, H, S_max, total_rows, K, D, nblk_cap, block_size).total,
+                    split_bytes(tiles, tile_splits(tiles), D));
+  return kOk;
+}
+
+extern "C" int dash_attn_prefill_split_workspace_size(int B, int H, int S_max, int D,
+                                                      int64_t* bytes) {
+  using namespace dash;
+  if (!bytes || B < 0 || H <= 0 || S_max < 0 || D <= 0) return kErrInvalid;
+  const int64_t tiles = (int64_t)((S_max + kPfTQ - 1) / kPfTQ) * H * B;
+  *bytes = split_bytes(tiles, tile_splits(tiles), D);
   return kOk;
 }
 
@@ -1466,6 +1653,7 @@ extern "C" int dash_attn_prefill(
   a.cu = cu_seqlens; a.kmin = kmin;
   a.slots_vec = slots_vectorizable(K, idx, valid, bias);
   a.S = S; a.H = H; a.bs = block_size; a.lw = local_window; a.nblk_cap = nblk_cap;
+  a.B = B;
   a.scale_log2e = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
   const int ntiles = (S + kPfTQ - 1) / kPfTQ;
@@ -1490,13 +1678,17 @@ extern "C" int dash_attn_prefill(
     a.chunk_pref = (int32_t*)(w + L.cpref);
     a.done = (int32_t*)(w + L.done);
     a.err = (int32_t*)(w + L.err);
-    a.B = B;
     a.chunk_rec = (int32_t*)(w + L.rec);
     a.chunk_cap = L.chunk_cap;
     a.spos = (int32_t*)(w + L.spos);
     a.ppos = L.ppos;
     a.part_lse = (float*)(w + L.plse);
     a.part_o = (bf16*)(w + L.po);
+    if (cu_seqlens) {
+      a.tile_pref = (int32_t*)(w + L.tpref);
+      a.tile_doc = (int32_t*)(w + L.tdoc);
+      a.ntv = L.ntv;
+    }
     const int ncount = (int)((L.err - L.count) / 4) + 1;  // block counters, arrival, error
     hipLaunchKernelGGL(prefill_clear_kernel, dim3((ncount + 255) / 256), dim3(256), 0, st,
                        a.blk_count, ncount);
@@ -1505,7 +1697,25 @@ extern "C" int dash_attn_prefill(
     hipLaunchKernelGGL(prefill_scatter_kernel, dim3(ntiles, B), dim3(kPfTQ), 0, st, a);
     hipLaunchKernelGGL(prefill_sparse_kernel<128>, dim3(L.chunk_cap * H * B), dim3(256), 0, st, a);
   }
-  hipLaunchKernelGGL((prefill_tile_kernel<128, kTileIT, kTileOcc>), dim3(ntiles * H * B), dim3(256), 0, st, a);
+  const int64_t tiles = (int64_t)ntiles * H * B;
+  if (!hybrid && K <= kPfMaxK) {
+    // no plan: split the tiles of a grid too small to fill the chip (with a
+    // workspace to hold the partials; without one every tile is one work-group)
+    const int ns = tile_splits(tiles);
+    if (ns > 1 && workspace && workspace_bytes >= split_bytes(tiles, ns, D) &&
+        (uintptr_t)workspace % 256 == 0) {
+      a.nsplit = ns;
+      a.split_o = (bf16*)workspace;
+      a.split_lse = (float*)((char*)workspace + split_o_bytes(tiles, ns, D));
+    }
+  }
+  const int64_t tile_grid = a.tile_doc ? (int64_t)a.ntv * H : tiles * std::max(a.nsplit, 1);
+  if (tile_grid > INT32_MAX) return kErrUnsupported;
+  hipLaunchKernelGGL((prefill_tile_kernel<128, kTileIT, kTileOcc>), dim3((unsigned)tile_grid), dim3(256),
+                     0, st, a);
+  if (a.nsplit > 1)
+    hipLaunchKernelGGL(prefill_split_merge_kernel, dim3((unsigned)((tiles * kPfTQ + 15) / 16)), dim3(256),
+                       0, st, a);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? kOk : (int)e;
 }

@@ -195,9 +195,12 @@ int dash_train_route_backward(const float* z, int64_t z_stride, int rows, int nb
  * dense_threshold > 0 (block_size <= 64): routed blocks selected by fewer than
  * dense_threshold of the 128 queries of a tile go through the block-major sparse path,
  * which needs `workspace` (dash_attn_prefill_workspace_size bytes, 256-byte aligned, any
- * contents: the call clears its counters first) and total_rows (B*S, or cu_seqlens[B]).  dense_threshold <= 0: no workspace,
- * every routed block of a tile is processed with the tile.  Calls sharing a workspace
- * must not overlap.
+ * contents: the call clears its counters first) and total_rows (B*S, or cu_seqlens[B]).
+ * dense_threshold <= 0: every routed block of a tile is processed with the tile; when
+ * the grid of tiles (ceil(S / 128) x H x B) is too small to fill the chip and a workspace
+ * of dash_attn_prefill_split_workspace_size bytes is given, each tile's items are divided
+ * among several work-groups whose partials a second launch merges (no workspace: one
+ * work-group per tile).  Calls sharing a workspace must not overlap.
  */
 int dash_attn_prefill(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                       const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
@@ -210,9 +213,14 @@ int dash_attn_prefill(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                       float scale, int dense_threshold, int64_t total_rows,
                       void* workspace, int64_t workspace_bytes, void* stream);
 
-/* Workspace bytes of the sparse path of dash_attn_prefill. */
+/* Workspace bytes of dash_attn_prefill (the sparse path's plan, or split tiles). */
 int dash_attn_prefill_workspace_size(int B, int H, int S_max, int64_t total_rows, int K, int D,
                                      int block_size, int64_t* bytes);
+
+/* Workspace bytes of dash_attn_prefill's split tiles (dense_threshold <= 0); 0 when the
+ * grid of tiles needs no split.  No counterpart in the reference (whose Triton kernel
+ * launches one program per query tile): a property of this library's decomposition. */
+int dash_attn_prefill_split_workspace_size(int B, int H, int S_max, int D, int64_t* bytes);
 
 /* Workspace bytes of dash_attn_prefill_backward. */
 int dash_attn_prefill_backward_workspace_size(int B, int H, int S_max, int64_t total_rows, int K,

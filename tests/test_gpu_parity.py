@@ -346,6 +346,37 @@ def test_prefill_empty_documents_single_tokens_no_routing(thr, K):
         _close(out[:, :, s0:s1], ref, f"document {b}")
 
 
+@pytest.mark.parametrize("B,H,S,bs,lw,K,qs,km", [
+    (1, 2, 300, 64, 128, 4, 3.0, False),     # 6 tiles: 8 parts each, most of them empty
+    (2, 3, 700, 64, 512, 8, 1.0, True),      # 36 tiles, segment starts
+    (1, 1, 1100, 128, 256, 3, 2.0, False),   # 128-key blocks: parts cut at block boundaries
+    (1, 10, 2730, 64, 512, 8, 1.0, False),   # 220 tiles: 2 parts
+])
+def test_prefill_split_tiles(B, H, S, bs, lw, K, qs, km):
+    """Every routed block with its tile, the tiles of a small grid split over several
+    work-groups (their partials merged by a second launch) and unsplit: both against
+    the oracle, and their log-sum-exps against each other."""
+    q, k, v, idx, bias, valid = _attn_inputs(360 + S, B, H, S, bs, lw, K, qscale=qs)
+    kmin = None
+    if km:
+        kmin = torch.zeros(B, S, dtype=torch.long)
+        kmin[:, 250:] = 250
+        kmin[1:, 480:] = 480
+    scale = 1 / math.sqrt(128)
+    ref = O.dense_attend(q, k, v, idx, bias, valid, bs, lw, scale, kmin=kmin)
+    args = (q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), bias.to(DEV), valid.to(DEV), bs, lw,
+            scale)
+    kw = dict(return_lse=True, dense_threshold=0,
+              kmin=None if kmin is None else kmin.to(DEV))
+    o_split, l_split = ops.attn_prefill(*args, **kw)
+    o_one, l_one = ops.attn_prefill(*args, split_tiles=False, **kw)
+    _close(o_split, ref, "split tiles")
+    _close(o_one, ref, "one work-group per tile")
+    # each side sums bf16-rounded probabilities (relative error <= 2^-9 per term, so
+    # <= 2^-9 in the sum and in the log-sum-exp) against its own running maxima
+    torch.testing.assert_close(l_split.cpu(), l_one.cpu(), atol=2 * 2.0 ** -9, rtol=0)
+
+
 def test_prefill_workspace_any_contents():
     """The sparse path's workspace may hold anything, as a cached buffer last used by a
     call of another shape does: the call clears its own counters first."""
