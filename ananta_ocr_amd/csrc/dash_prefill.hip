@@ -24,8 +24,9 @@
 //     O^T += V^T P^T; finally the query's sparse partials are merged in.
 // With no plan (dense_threshold <= 0) the tile kernel processes every routed
 // block of the tile as a dense block; when its grid alone cannot fill the chip,
-// the items of each tile are divided among nsplit work-groups, each writing a
-// normalised bf16 partial per row, and a merge kernel combines them.
+// the items of each tile are divided among work-groups (more for the tiles with
+// more remote blocks), each writing a normalised bf16 partial per row, and a merge
+// kernel combines them.
 
 #include "dash_common.h"
 
@@ -42,6 +43,7 @@ constexpr int kPfMaxBlocks = 2048;
 // CU that the stage size and the register budget allow.
 constexpr int kTileIT = 64;
 constexpr int kTileOcc = 2;
+constexpr int kSplitMax = 8;      // work-groups (parts) per split tile
 constexpr int kPfCH = 256;        // pairs per sparse chunk (work-group)
 // A chunk record: block id, pair count, 2 unused words, then up to kPfCH pair ids
 // (token * K + slot within the sequence), so that a work-group reads its chunk's
@@ -96,13 +98,34 @@ struct PrefillArgs {
   float* part_lse;                     // [H, ppos]  base-2 log-sum-exp
   bf16* part_o;                        // [H, ppos, D]  normalised partial output, dims
                                        // in MFMA lane order (see part_index)
-  // split tiles (no plan; nsplit > 1): work-group part p of tile tl (the logical
-  // (sequence, head, tile) id) takes an equal share of the tile's items and writes
-  // its rows' normalised output and base-2 log-sum-exp
-  int nsplit;
-  bf16* split_o;                       // [tiles, nsplit, kPfTQ, D] bf16, dims in order
-  float* split_lse;                    // [tiles, nsplit, kPfTQ]
+  // split tiles (no plan; split_items > 0): tile t of every sequence is cut into
+  // tile_parts(t) parts of split_items items (the last part takes the rest); part p
+  // of tile tl (the logical (sequence, head, tile) id) writes its rows' normalised
+  // output and base-2 log-sum-exp to slot tl * kSplitMax + p
+  int split_items;
+  int split_parts;                     // parts per (sequence, head): the sum over tiles
+  bf16* split_o;                       // [tiles, kSplitMax, kPfTQ, D] bf16, dims in order
+  float* split_lse;                    // [tiles, kSplitMax, kPfTQ]
 };
+
+// Upper bound of the items of tile t (no plan) of a sequence of S tokens: its
+// window items, and the items of every block a routed slot of its rows may name
+// (blocks with a key before the window of its last row; at most K per row).
+__host__ __device__ inline int tile_item_bound(int t, int S, int lw, int bs, int K) {
+  const int t0 = t * kPfTQ;
+  const int t_last = (t0 + kPfTQ - 1 < S - 1) ? t0 + kPfTQ - 1 : S - 1;
+  const int jw0 = (t0 - lw + 1 > 0 ? t0 - lw + 1 : 0) / kTileIT * kTileIT;
+  const int n_win = (t_last - jw0) / kTileIT + 1;
+  const int ipb = (bs + kTileIT - 1) / kTileIT;
+  const int far = t_last - lw;
+  const int n_rem = far >= 0 ? far / bs + 1 : 0;
+  return n_win + ipb * (n_rem < kPfTQ * K ? n_rem : kPfTQ * K);
+}
+// Parts of tile t at `items` items per part (1 .. kSplitMax).
+__host__ __device__ inline int tile_parts(int t, int S, int lw, int bs, int K, int items) {
+  const int n = (tile_item_bound(t, S, lw, bs, K) + items - 1) / items;
+  return n < 1 ? 1 : (n > kSplitMax ? kSplitMax : n);
+}
 
 __device__ __forceinline__ int seq_len(const PrefillArgs& a, int b) {
   return a.cu ? a.cu[b + 1] - a.cu[b] : a.S;
@@ -704,13 +727,25 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
   // logical order (sequence, head, tile), tile fastest, contiguous per XCD; packed
   // documents in the order (head, tile of all documents), so that every logical id
   // below the tile count is a real tile and the XCDs get equal shares
-  // (split tiles: the nsplit parts of a tile are consecutive logical ids)
+  // (split tiles: (sequence, head, part of all tiles), the parts of a tile
+  // consecutive)
   int lid = xcd_logical_id(blockIdx.x, gridDim.x);
-  int part = 0;
-  if (a.nsplit > 1) {
-    part = lid % a.nsplit;
-    lid /= a.nsplit;
+  int part = 0, nparts = 1;
+  if (a.split_items > 0) {
+    const int j = lid % a.split_parts;
+    const int bh = lid / a.split_parts;
+    int t = 0, pre = 0;
+    for (; t < a.ntiles; ++t) {
+      nparts = tile_parts(t, a.S, a.lw, a.bs, a.K, a.split_items);
+      if (j < pre + nparts) break;
+      pre += nparts;
+    }
+    if (t >= a.ntiles) return;             // never: the grid holds split_parts per (b, h)
+    part = j - pre;
+    lid = bh * a.ntiles + t;
   }
+  // partial slot of a split tile
+  const int split_slot = lid * kSplitMax + part;
   int tile, h, b;
   if (a.tile_doc) {
     const int g = lid % a.ntv;
@@ -754,34 +789,78 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
       ++cnt;
       atomicOr(&sBits[c >> 5], 1u << (c & 31));
     };
-    if (t < len && a.kind && a.slots_vec && a.K <= kPfMaxK) {
-      // Planned rows of up to 16 slots, K a multiple of 4 (kinds, ids and biases read
-      // four slots per load; the plan has already dropped duplicate and unusable
-      // slots).  The dense slots are sorted by block id with a bitonic network on the
-      // keys id << 5 | slot in registers (ids < 2048; other slots, and slots past K,
-      // take id 2048 and sort last); the biases, stored in slot order, are then
-      // gathered by slot.
+    if (t < len && a.K <= kPfMaxK && (!a.kind || a.slots_vec)) {
+      // Rows of up to 16 slots, every load issued before any is used (four slots per
+      // load where slots_vec allows).  Dense slots: with a plan, its kind-1 slots
+      // (the plan has already dropped duplicate and unusable slots); without one,
+      // every usable slot whose block no earlier usable slot names.  They are sorted
+      // by block id with a bitonic network on the keys id << 5 | slot in registers
+      // (ids < 2048; other slots, and slots past K, take id 2048 and sort last); the
+      // biases, stored in slot order, are then gathered by slot.
       const int64_t p0 = (r0 + t) * a.K;
-      uint32_t kw[4];
-      int4 iv[4];
-      float4 bv4[4];
+      int32_t cs[kPfMaxK];
+      float bs4[kPfMaxK];
+      uint32_t dmask = 0;                  // slots whose block goes with the tile
+      if (a.slots_vec) {
+        uint32_t kw[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const bool in = 4 * q < a.K;
-        kw[q] = in ? *(const uint32_t*)(a.kind + p0 + 4 * q) : 0u;
-        iv[q] = in ? ((const int4*)(a.idx + p0))[q] : make_int4(0, 0, 0, 0);
-        bv4[q] = in ? ((const float4*)(a.bias + p0))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int q = 0; q < 4; ++q) {
+          const bool in = 4 * q < a.K;
+          kw[q] = (in && a.kind) ? *(const uint32_t*)(a.kind + p0 + 4 * q) : 0u;
+          const int4 iv = in ? ((const int4*)(a.idx + p0))[q] : make_int4(-1, -1, -1, -1);
+          const float4 bv = in ? ((const float4*)(a.bias + p0))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+          cs[4 * q] = iv.x; cs[4 * q + 1] = iv.y; cs[4 * q + 2] = iv.z; cs[4 * q + 3] = iv.w;
+          bs4[4 * q] = bv.x; bs4[4 * q + 1] = bv.y; bs4[4 * q + 2] = bv.z; bs4[4 * q + 3] = bv.w;
+        }
+        if (a.kind) {
+#pragma unroll
+          for (int s = 0; s < kPfMaxK; ++s)
+            if (((kw[s >> 2] >> (8 * (s & 3))) & 0xffu) == 1) dmask |= 1u << s;
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < kPfMaxK; ++s) {
+          cs[s] = s < a.K ? a.idx[p0 + s] : -1;
+          bs4[s] = s < a.K ? a.bias[p0 + s] : 0.f;
+        }
+      }
+      if (!a.kind) {
+        uint32_t vmask;
+        if (a.slots_vec && a.valid) {
+          vmask = 0;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t w = 4 * q < a.K ? *(const uint32_t*)(a.valid + p0 + 4 * q) : 0u;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if ((w >> (8 * e)) & 0xffu) vmask |= 1u << (4 * q + e);
+          }
+        } else if (a.valid) {
+          vmask = 0;
+#pragma unroll
+          for (int s = 0; s < kPfMaxK; ++s)
+            if (s < a.K && a.valid[p0 + s]) vmask |= 1u << s;
+        } else {
+          vmask = a.K >= 32 ? ~0u : (1u << a.K) - 1u;
+        }
+        const int km = a.kmin ? a.kmin[r0 + t] : 0;
+        const int ls = t - a.lw + 1;
+#pragma unroll
+        for (int s = 0; s < kPfMaxK; ++s) {
+          const int c = cs[s];
+          bool keep = ((vmask >> s) & 1u) && c >= 0 && c < nblk && c * a.bs < ls && (c + 1) * a.bs > km;
+#pragma unroll
+          for (int u = 0; u < s; ++u) keep = keep && !(((dmask >> u) & 1u) && cs[u] == c);
+          if (keep) dmask |= 1u << s;
+        }
       }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) ((float4*)&sBias[tid][0])[q] = bv4[q];
+      for (int q = 0; q < 4; ++q)
+        ((float4*)&sBias[tid][0])[q] = make_float4(bs4[4 * q], bs4[4 * q + 1], bs4[4 * q + 2], bs4[4 * q + 3]);
       uint32_t key[kPfMaxK];
 #pragma unroll
-      for (int s = 0; s < kPfMaxK; ++s) {
-        const uint32_t kd = (kw[s >> 2] >> (8 * (s & 3))) & 0xffu;
-        const int q = s >> 2, e = s & 3;
-        const int c = e == 0 ? iv[q].x : e == 1 ? iv[q].y : e == 2 ? iv[q].z : iv[q].w;
-        key[s] = ((kd == 1 ? (uint32_t)c : (uint32_t)kPfMaxBlocks) << 5) | (uint32_t)s;
-      }
+      for (int s = 0; s < kPfMaxK; ++s)
+        key[s] = ((((dmask >> s) & 1u) ? (uint32_t)cs[s] : (uint32_t)kPfMaxBlocks) << 5) | (uint32_t)s;
 #pragma unroll
       for (int k = 2; k <= kPfMaxK; k <<= 1)
 #pragma unroll
@@ -880,16 +959,16 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
     nu = __builtin_amdgcn_readfirstlane(nu);
   }
   const int n_items = n_win + nu * ipb;
-  // this work-group's items [i0, i1): all of them, or with split tiles an equal
-  // share cut at routed-block boundaries
+  // this work-group's items [i0, i1): all of them, or with split tiles the part's
+  // split_items (the last part: the rest), cut at routed-block boundaries
   int i0 = 0, i1 = n_items;
-  if (a.nsplit > 1) {
-    auto cut = [&](int p) {
-      const int x = (int)((int64_t)p * n_items / a.nsplit);
+  if (a.split_items > 0) {
+    auto cut = [&](int x) {
+      x = min(x, n_items);
       return x <= n_win ? x : n_win + (x - n_win) / ipb * ipb;
     };
-    i0 = cut(part);
-    i1 = cut(part + 1);
+    i0 = cut(part * a.split_items);
+    i1 = part == nparts - 1 ? n_items : cut((part + 1) * a.split_items);
   }
   // first dense block of the share (0 when it starts in the window band)
   const int c_first = (i0 > n_win && i0 < i1) ? nth_union(sBits, nwords, (i0 - n_win) / ipb, lane) : 0;
@@ -1170,9 +1249,8 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
 
   // ---- epilogue: normalise and store ----
   const float l_tot = xor32_sum(l_run);
-  if (pa.nsplit > 1) {
-    // the share's partials: slot tile id x nsplit + part, which is the logical id
-    const int64_t slot = xcd_logical_id(blockIdx.x, gridDim.x);
+  if (pa.split_items > 0) {
+    const int64_t slot = split_slot;
     if (qvalid) {
       const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
       bf16* so = pa.split_o + (slot * kPfTQ + myrow) * D;
@@ -1210,7 +1288,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Merge of split tiles: each (row, head) row's nsplit partials, weighted by
+// Merge of split tiles: each (row, head) row's partials, weighted by
 // 2^(lse_p - max) in fp32; 16 lanes of 8 dims per row, 16 rows per work-group.
 // Rows no share saw a key of give 0 (log-sum-exp -inf), as an unsplit tile does.
 // ---------------------------------------------------------------------------
@@ -1226,8 +1304,8 @@ __global__ __launch_bounds__(256) void prefill_split_merge_kernel(PrefillArgs a)
   const int h = bh % a.H, b = bh / a.H;
   const int t = tile * kPfTQ + r;
   if (t >= seq_len(a, b)) return;
-  const int P = a.nsplit;
-  const float* ls = a.split_lse + tl * P * kPfTQ + r;
+  const int P = tile_parts(tile, a.S, a.lw, a.bs, a.K, a.split_items);
+  const float* ls = a.split_lse + tl * kSplitMax * kPfTQ + r;
   float mx = -INFINITY;
   for (int p = 0; p < P; ++p) mx = fmaxf(mx, ls[p * kPfTQ]);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -1238,7 +1316,7 @@ __global__ __launch_bounds__(256) void prefill_split_merge_kernel(PrefillArgs a)
       if (l == -INFINITY) continue;
       const float w = exp2f(l - mx);
       wsum += w;
-      const bf16x8 x = *(const bf16x8*)(a.split_o + ((tl * P + p) * kPfTQ + r) * D + sub * 8);
+      const bf16x8 x = *(const bf16x8*)(a.split_o + ((tl * kSplitMax + p) * kPfTQ + r) * D + sub * 8);
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] += w * bf2f(x[e]);
     }
@@ -1488,23 +1566,46 @@ struct PlanLayout {
 
 inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
-// Split tiles (no plan): work-groups per tile (tiles = tiles per sequence x heads x
-// sequences), as many as one round of two work-groups on each of the 256 CUs holds,
-// at most 8.  Measured on the 2,730-token prefill (220 tiles, no plan): 2 parts
-// 64.6 us, 3 72.7, 5 82.2, 8 106.7 against 82.2 unsplit (each part repeats the
-// tile's prologue, and a second round of work-groups costs more than it shares).
+// Split tiles (no plan) when the grid of tiles (tiles per sequence x heads x
+// sequences) is below kSplitSlots, one round of two work-groups on each of the 256
+// CUs: the items per part are the fewest (from kSplitMinItems) whose parts over all
+// tiles fit that round, so that the tiles with many remote blocks get more parts.
+// Each part repeats the tile's prologue (its rows' routed lists, ~6 us), so parts
+// stay above a few items.
 constexpr int64_t kSplitSlots = 512;
-constexpr int kSplitMax = 8;
-inline int tile_splits(int64_t tiles) {
-  if (tiles <= 0) return 1;
-  return (int)std::min<int64_t>(kSplitMax, std::max<int64_t>(1, kSplitSlots / tiles));
+constexpr int kSplitMinItems = 6;
+inline int64_t seq_split_parts(int ntiles, int S, int lw, int bs, int K, int items) {
+  int64_t n = 0;
+  for (int t = 0; t < ntiles; ++t) n += tile_parts(t, S, lw, bs, K, items);
+  return n;
 }
-// Workspace of the split partials: bf16 rows, then the base-2 log-sum-exps.
-inline int64_t split_o_bytes(int64_t tiles, int ns, int D) {
-  return align256(tiles * ns * kPfTQ * D * 2);
+// Items per part (0: no split) and the parts per (sequence, head).
+inline int split_items_for(int ntiles, int64_t seqheads, int S, int lw, int bs, int K,
+                           int64_t* parts) {
+  *parts = ntiles;
+  if (ntiles <= 0 || (int64_t)ntiles * seqheads >= kSplitSlots) return 0;
+  int hi = 1;
+  for (int t = 0; t < ntiles; ++t) hi = std::max(hi, tile_item_bound(t, S, lw, bs, K));
+  if (hi <= kSplitMinItems) return 0;
+  // parts decrease as the items per part grow: the smallest items in
+  // [kSplitMinItems, hi] whose parts fit, else hi (kSplitMax parts at most per tile)
+  int lo = kSplitMinItems, up = hi;
+  while (lo < up) {
+    const int mid = (lo + up) / 2;
+    if (seq_split_parts(ntiles, S, lw, bs, K, mid) * seqheads <= kSplitSlots) up = mid; else lo = mid + 1;
+  }
+  const int64_t n = seq_split_parts(ntiles, S, lw, bs, K, lo);
+  if (n <= ntiles) return 0;                 // one part per tile: no split
+  *parts = n;
+  return lo;
 }
-inline int64_t split_bytes(int64_t tiles, int ns, int D) {
-  return ns > 1 ? split_o_bytes(tiles, ns, D) + align256(tiles * ns * kPfTQ * 4) : 0;
+// Workspace of the split partials: bf16 rows, then the base-2 log-sum-exps, kSplitMax
+// slots per tile.
+inline int64_t split_o_bytes(int64_t tiles, int D) {
+  return align256(tiles * kSplitMax * kPfTQ * D * 2);
+}
+inline int64_t split_bytes(int64_t tiles, int D) {
+  return tiles < kSplitSlots ? split_o_bytes(tiles, D) + align256(tiles * kSplitMax * kPfTQ * 4) : 0;
 }
 
 inline PlanLayout plan_layout(int B, int H, int S_max, int64_t rows, int K, int D,
@@ -1593,7 +1694,7 @@ extern "C" int dash_attn_prefill_workspace_size(int B, int H, int S_max, int64_t
   const int nblk_cap = (S_max + block_size - 1) / block_size;
   const int64_t tiles = (int64_t)((S_max + kPfTQ - 1) / kPfTQ) * H * B;
   *bytes = std::max(plan_layout(B, H, S_max, total_rows, K, D, nblk_cap, block_size).total,
-                    split_bytes(tiles, tile_splits(tiles), D));
+                    split_bytes(tiles, D));
   return kOk;
 }
 
@@ -1602,7 +1703,7 @@ extern "C" int dash_attn_prefill_split_workspace_size(int B, int H, int S_max, i
   using namespace dash;
   if (!bytes || B < 0 || H <= 0 || S_max < 0 || D <= 0) return kErrInvalid;
   const int64_t tiles = (int64_t)((S_max + kPfTQ - 1) / kPfTQ) * H * B;
-  *bytes = split_bytes(tiles, tile_splits(tiles), D);
+  *bytes = split_bytes(tiles, D);
   return kOk;
 }
 
@@ -1698,22 +1799,25 @@ extern "C" int dash_attn_prefill(
     hipLaunchKernelGGL(prefill_sparse_kernel<128>, dim3(L.chunk_cap * H * B), dim3(256), 0, st, a);
   }
   const int64_t tiles = (int64_t)ntiles * H * B;
-  if (!hybrid && K <= kPfMaxK) {
+  int64_t tile_grid = a.tile_doc ? (int64_t)a.ntv * H : tiles;
+  if (!hybrid && K <= kPfMaxK && workspace && (uintptr_t)workspace % 256 == 0 &&
+      workspace_bytes >= split_bytes(tiles, D)) {
     // no plan: split the tiles of a grid too small to fill the chip (with a
     // workspace to hold the partials; without one every tile is one work-group)
-    const int ns = tile_splits(tiles);
-    if (ns > 1 && workspace && workspace_bytes >= split_bytes(tiles, ns, D) &&
-        (uintptr_t)workspace % 256 == 0) {
-      a.nsplit = ns;
+    int64_t parts = 0;
+    const int items = split_items_for(ntiles, (int64_t)H * B, S, local_window, block_size, K, &parts);
+    if (items > 0) {
+      a.split_items = items;
+      a.split_parts = (int)parts;
       a.split_o = (bf16*)workspace;
-      a.split_lse = (float*)((char*)workspace + split_o_bytes(tiles, ns, D));
+      a.split_lse = (float*)((char*)workspace + split_o_bytes(tiles, D));
+      tile_grid = parts * H * B;
     }
   }
-  const int64_t tile_grid = a.tile_doc ? (int64_t)a.ntv * H : tiles * std::max(a.nsplit, 1);
   if (tile_grid > INT32_MAX) return kErrUnsupported;
   hipLaunchKernelGGL((prefill_tile_kernel<128, kTileIT, kTileOcc>), dim3((unsigned)tile_grid), dim3(256),
                      0, st, a);
-  if (a.nsplit > 1)
+  if (a.split_items > 0)
     hipLaunchKernelGGL(prefill_split_merge_kernel, dim3((unsigned)((tiles * kPfTQ + 15) / 16)), dim3(256),
                        0, st, a);
   const hipError_t e = hipGetLastError();
