@@ -1571,9 +1571,12 @@ inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 // CUs: the items per part are the fewest (from kSplitMinItems) whose parts over all
 // tiles fit that round, so that the tiles with many remote blocks get more parts.
 // Each part repeats the tile's prologue (its rows' routed lists, ~6 us), so parts
-// stay above a few items.
+// stay above a few items.  A work-group finds its tile by walking the parts of the
+// sequence's tiles (two divisions each), so sequences of more than kSplitMaxTiles
+// tiles are not split.
 constexpr int64_t kSplitSlots = 512;
 constexpr int kSplitMinItems = 6;
+constexpr int kSplitMaxTiles = 64;
 inline int64_t seq_split_parts(int ntiles, int S, int lw, int bs, int K, int items) {
   int64_t n = 0;
   for (int t = 0; t < ntiles; ++t) n += tile_parts(t, S, lw, bs, K, items);
@@ -1583,7 +1586,7 @@ inline int64_t seq_split_parts(int ntiles, int S, int lw, int bs, int K, int ite
 inline int split_items_for(int ntiles, int64_t seqheads, int S, int lw, int bs, int K,
                            int64_t* parts) {
   *parts = ntiles;
-  if (ntiles <= 0 || (int64_t)ntiles * seqheads >= kSplitSlots) return 0;
+  if (ntiles <= 0 || ntiles > kSplitMaxTiles || (int64_t)ntiles * seqheads >= kSplitSlots) return 0;
   int hi = 1;
   for (int t = 0; t < ntiles; ++t) hi = std::max(hi, tile_item_bound(t, S, lw, bs, K));
   if (hi <= kSplitMinItems) return 0;
@@ -1604,8 +1607,9 @@ inline int split_items_for(int ntiles, int64_t seqheads, int S, int lw, int bs, 
 inline int64_t split_o_bytes(int64_t tiles, int D) {
   return align256(tiles * kSplitMax * kPfTQ * D * 2);
 }
-inline int64_t split_bytes(int64_t tiles, int D) {
-  return tiles < kSplitSlots ? split_o_bytes(tiles, D) + align256(tiles * kSplitMax * kPfTQ * 4) : 0;
+inline int64_t split_bytes(int64_t tiles, int ntiles, int D) {
+  return tiles < kSplitSlots && ntiles <= kSplitMaxTiles
+             ? split_o_bytes(tiles, D) + align256(tiles * kSplitMax * kPfTQ * 4) : 0;
 }
 
 inline PlanLayout plan_layout(int B, int H, int S_max, int64_t rows, int K, int D,
@@ -1692,9 +1696,10 @@ extern "C" int dash_attn_prefill_workspace_size(int B, int H, int S_max, int64_t
   if (!bytes || B < 0 || H <= 0 || S_max < 0 || total_rows < 0 || K < 0 || block_size <= 0)
     return kErrInvalid;
   const int nblk_cap = (S_max + block_size - 1) / block_size;
-  const int64_t tiles = (int64_t)((S_max + kPfTQ - 1) / kPfTQ) * H * B;
+  const int ntiles = (S_max + kPfTQ - 1) / kPfTQ;
+  const int64_t tiles = (int64_t)ntiles * H * B;
   *bytes = std::max(plan_layout(B, H, S_max, total_rows, K, D, nblk_cap, block_size).total,
-                    split_bytes(tiles, D));
+                    split_bytes(tiles, ntiles, D));
   return kOk;
 }
 
@@ -1702,8 +1707,9 @@ extern "C" int dash_attn_prefill_split_workspace_size(int B, int H, int S_max, i
                                                       int64_t* bytes) {
   using namespace dash;
   if (!bytes || B < 0 || H <= 0 || S_max < 0 || D <= 0) return kErrInvalid;
-  const int64_t tiles = (int64_t)((S_max + kPfTQ - 1) / kPfTQ) * H * B;
-  *bytes = split_bytes(tiles, D);
+  const int ntiles = (S_max + kPfTQ - 1) / kPfTQ;
+  const int64_t tiles = (int64_t)ntiles * H * B;
+  *bytes = split_bytes(tiles, ntiles, D);
   return kOk;
 }
 
@@ -1801,7 +1807,7 @@ extern "C" int dash_attn_prefill(
   const int64_t tiles = (int64_t)ntiles * H * B;
   int64_t tile_grid = a.tile_doc ? (int64_t)a.ntv * H : tiles;
   if (!hybrid && K <= kPfMaxK && workspace && (uintptr_t)workspace % 256 == 0 &&
-      workspace_bytes >= split_bytes(tiles, D)) {
+      workspace_bytes >= split_bytes(tiles, ntiles, D)) {
     // no plan: split the tiles of a grid too small to fill the chip (with a
     // workspace to hold the partials; without one every tile is one work-group)
     int64_t parts = 0;

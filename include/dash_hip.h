@@ -218,7 +218,7 @@ int dash_attn_prefill_workspace_size(int B, int H, int S_max, int64_t total_rows
                                      int block_size, int64_t* bytes);
 
 /* Workspace bytes of dash_attn_prefill's split tiles (dense_threshold <= 0); 0 when the
- * grid of tiles needs no split.  No counterpart in the reference (whose Triton kernel
+ * grid of tiles needs no split (512 tiles or more, or sequences of more than 64 tiles).  No counterpart in the reference (whose Triton kernel
  * launches one program per query tile): a property of this library's decomposition. */
 int dash_attn_prefill_split_workspace_size(int B, int H, int S_max, int D, int64_t* bytes);
 

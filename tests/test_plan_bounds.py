@@ -8,6 +8,7 @@ returns before a launch).
 * The workspace holds every chunk that consistent counts can produce: for any split
   of a sequence's routed pairs over its blocks, sum ceil(count / 256) fits.
 * The decode router refuses a k_bar cache with fewer than ceil(S / block_size) rows.
+* Split tiles ask for a workspace only where the library splits them.
 """
 
 import ctypes
@@ -128,3 +129,27 @@ def test_decode_router_refuses_undersized_kbar_cache():
     assert _decode_route_status(lib, 1000, 15) == -3
     assert _decode_route_status(lib, 1025, 16) == -3
     assert _decode_route_status(lib, -1, 16) == -3
+
+
+def _split_bytes(lib, B, H, S, D=128):
+    n = ctypes.c_int64(-1)
+    assert lib.dash_attn_prefill_split_workspace_size(B, H, S, D, n) == 0
+    return n.value
+
+
+def test_split_tile_workspace():
+    """Split tiles (every routed block with its tile) need a workspace only for a grid
+    of fewer than 512 tiles over sequences of at most 64 tiles: 8 partial slots per
+    tile, each 128 rows of bf16 output and an fp32 log-sum-exp."""
+    lib = _lib_or_skip()
+    tiles = 22 * 10                                   # 2,730 tokens, 10 heads
+    assert _split_bytes(lib, 1, 10, 2730) >= tiles * 8 * 128 * (128 * 2 + 4)
+    assert _split_bytes(lib, 1, 10, 27300) == 0       # 2,140 tiles fill the chip
+    assert _split_bytes(lib, 1, 1, 60000) == 0        # 469 tiles, but 469 in one sequence
+    assert _split_bytes(lib, 3, 2, 8192) > 0          # 64 tiles per sequence, 384 in all
+    assert _split_bytes(lib, 3, 2, 8193) == 0         # 65 tiles per sequence
+    assert _split_bytes(lib, 0, 2, 100) == 0
+    # the prefill workspace covers either use
+    full = ctypes.c_int64(0)
+    assert lib.dash_attn_prefill_workspace_size(1, 10, 2730, 2730, 8, 128, 64, full) == 0
+    assert full.value >= _split_bytes(lib, 1, 10, 2730)
