@@ -769,6 +769,18 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
   const int n = lane & 31;          // query column within the wave
   const int64_t r0 = row0(a, b);
 
+  // ---- this lane's query and its Q^T operand (8 k-steps of 16 dims), loaded
+  // first so that the loads overlap the routed slots' loads below ----
+  const int tq = t0 + wv * 32 + n;
+  const bool qvalid = tq < len;
+  const int tqc = min(tq, len - 1);
+  const int64_t qrow = r0 + tqc;
+  const bf16* qb = seq_ptr(a.q, a.cu, b, a.q_sb, a.q_st) + (int64_t)h * a.q_sh;
+  bf16x8 qop[D / 16];
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk)
+    qop[kk] = *(const bf16x8*)(qb + (int64_t)tqc * a.q_st + kk * 16 + hl * 8);
+
   for (int i = tid; i < kPfMaxBlocks / 32; i += 256) sBits[i] = 0u;
   __syncthreads();
 
@@ -921,16 +933,6 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
     for (int u = cnt; u < kPfMaxK; ++u) sIdx[tid][u] = (int16_t)kPfMaxBlocks;
   }
 
-  // ---- this lane's query and its Q^T operand (8 k-steps of 16 dims) ----
-  const int tq = t0 + wv * 32 + n;
-  const bool qvalid = tq < len;
-  const int tqc = min(tq, len - 1);
-  const int64_t qrow = r0 + tqc;
-  const bf16* qb = seq_ptr(a.q, a.cu, b, a.q_sb, a.q_st) + (int64_t)h * a.q_sh;
-  bf16x8 qop[D / 16];
-#pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk)
-    qop[kk] = *(const bf16x8*)(qb + (int64_t)tqc * a.q_st + kk * 16 + hl * 8);
   const int q_ls = tq - a.lw + 1;
   const int q_km = a.kmin ? a.kmin[qrow] : 0;
   const int q_lo = max(max(q_ls, q_km), 0);       // first window key
@@ -1306,19 +1308,27 @@ __global__ __launch_bounds__(256) void prefill_split_merge_kernel(PrefillArgs a)
   if (t >= seq_len(a, b)) return;
   const int P = tile_parts(tile, a.S, a.lw, a.bs, a.K, a.split_items);
   const float* ls = a.split_lse + tl * kSplitMax * kPfTQ + r;
+  // every part's log-sum-exp and row piece loaded before any is used (one round trip)
+  float l[kSplitMax];
+  bf16x8 x[kSplitMax];
+#pragma unroll
+  for (int p = 0; p < kSplitMax; ++p) {
+    l[p] = p < P ? ls[p * kPfTQ] : -INFINITY;
+    if (p < P) x[p] = *(const bf16x8*)(a.split_o + ((tl * kSplitMax + p) * kPfTQ + r) * D + sub * 8);
+  }
   float mx = -INFINITY;
-  for (int p = 0; p < P; ++p) mx = fmaxf(mx, ls[p * kPfTQ]);
+#pragma unroll
+  for (int p = 0; p < kSplitMax; ++p) mx = fmaxf(mx, l[p]);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float wsum = 0.f;
   if (mx != -INFINITY) {
-    for (int p = 0; p < P; ++p) {
-      const float l = ls[p * kPfTQ];
-      if (l == -INFINITY) continue;
-      const float w = exp2f(l - mx);
-      wsum += w;
-      const bf16x8 x = *(const bf16x8*)(a.split_o + ((tl * kSplitMax + p) * kPfTQ + r) * D + sub * 8);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += w * bf2f(x[e]);
+    for (int p = 0; p < kSplitMax; ++p) {
+      if (l[p] == -INFINITY) continue;
+      const float w = exp2f(l[p] - mx);
+      wsum += w;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += w * bf2f(x[p][e]);
     }
   }
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
