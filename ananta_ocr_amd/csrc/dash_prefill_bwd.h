@@ -628,8 +628,12 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   constexpr int D = 128;
-  __shared__ __attribute__((aligned(16))) bf16 sK[kBwIT * D];
-  __shared__ __attribute__((aligned(16))) bf16 sV[kBwIT * D];
+  // double-buffered window stages (distinct arrays, so that reads of one never wait
+  // for the loads into the other)
+  __shared__ __attribute__((aligned(16))) bf16 sK0[kBwIT * D];
+  __shared__ __attribute__((aligned(16))) bf16 sV0[kBwIT * D];
+  __shared__ __attribute__((aligned(16))) bf16 sK1[kBwIT * D];
+  __shared__ __attribute__((aligned(16))) bf16 sV1[kBwIT * D];
   const PrefillArgs& p = a.p;
   const int lid = xcd_logical_id(blockIdx.x, gridDim.x);
   const int tile = lid % p.ntiles, bh = lid / p.ntiles;
@@ -666,17 +670,26 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc_q[dt][r] = 0.f;
 
-  // window keys of the tile: [max(t0 - LW + 1, 0), min(t0 + 127, len - 1)] in 64-key items
+  // window keys of the tile: [max(t0 - LW + 1, 0), min(t0 + 127, len - 1)] in 64-key
+  // items; item i + 1 loads into the other stage while item i computes
   const int k_lo = max(t0 - p.lw + 1, 0) / kBwIT * kBwIT;
   const int k_hi = min(t0 + kPfTQ - 1, len - 1);
-  for (int j0 = k_lo; j0 <= k_hi; j0 += kBwIT) {
-    __syncthreads();
-    stage_rows(sK, wv, lane, [&](int r) { return kb + (int64_t)min(j0 + r, len - 1) * p.k_st; });
-    stage_rows(sV, wv, lane, [&](int r) { return vb + (int64_t)min(j0 + r, len - 1) * p.v_st; });
+  const int nit = k_hi >= k_lo ? (k_hi - k_lo) / kBwIT + 1 : 0;
+  auto stage = [&](bf16* sKx, bf16* sVx, int j0) {
+    stage_rows(sKx, wv, lane, [&](int r) { return kb + (int64_t)min(j0 + r, len - 1) * p.k_st; });
+    stage_rows(sVx, wv, lane, [&](int r) { return vb + (int64_t)min(j0 + r, len - 1) * p.v_st; });
+  };
+  if (nit > 0) stage(sK0, sV0, k_lo);
+  auto item = [&](int it, auto par_tag) {
+    constexpr int P = decltype(par_tag)::value;
+    const bf16* const sK = P == 0 ? sK0 : sK1;
+    const bf16* const sV = P == 0 ? sV0 : sV1;
+    const int j0 = k_lo + it * kBwIT;
     __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    __syncthreads();                       // item it landed; item it - 1 is done
+    if (it + 1 < nit) stage(P == 0 ? sK1 : sK0, P == 0 ? sV1 : sV0, j0 + kBwIT);
     const bool need = __any(qvalid && lo <= j0 + kBwIT - 1 && hi >= j0);
-    if (!need) continue;
+    if (!need) return;
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       floatx16 s, dp;
@@ -704,22 +717,70 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
                                                               acc_q[dt], 0, 0, 0);
       }
     }
+  };
+  for (int it = 0; it < nit; it += 2) {
+    item(it, std::integral_constant<int, 0>{});
+    if (it + 1 < nit) item(it + 1, std::integral_constant<int, 1>{});
   }
   if (!qvalid) return;
-  // the routed partials of this query (every kept routed slot is block-major)
-  for (int s = 0; s < (p.kind ? p.K : 0); ++s) {
-    if (p.kind[qrow * p.K + s] != 2) continue;
-    const int pos = p.spos[qrow * p.K + s];
-    if (pos < 0) continue;
-    for (int u = 0; u < a.nsub; ++u) {
-      const float* pd = a.part_dq + (((int64_t)h * p.ppos + pos) * a.nsub + u) * D;
+  // The routed partials of this query (every kept routed slot is block-major), in
+  // slot order and, within a slot, sub-block order.  Slots in groups of 16: the
+  // group's kinds and pair positions are loaded before any is used, then the
+  // partial rows two at a time (both rows' loads in flight before either is added).
+  for (int g0 = 0; p.kind && g0 < p.K; g0 += kPfMaxK) {
+    const int ng = min(kPfMaxK, p.K - g0);
+    const int64_t q0 = qrow * p.K + g0;
+    int32_t pos[kPfMaxK];
+    uint32_t live = 0;
+    if (p.slots_vec) {                     // ng is a multiple of 4
+      uint32_t kw[4];
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
+      for (int q = 0; q < 4; ++q) {
+        const bool in = 4 * q < ng;
+        kw[q] = in ? *(const uint32_t*)(p.kind + q0 + 4 * q) : 0u;
+        const int4 pv = in ? *(const int4*)(p.spos + q0 + 4 * q) : make_int4(-1, -1, -1, -1);
+        pos[4 * q] = pv.x; pos[4 * q + 1] = pv.y; pos[4 * q + 2] = pv.z; pos[4 * q + 3] = pv.w;
+      }
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const float4 v4 = *(const float4*)(pd + 32 * dt + 8 * g + 4 * hl);
-          acc_q[dt][4 * g] += v4.x; acc_q[dt][4 * g + 1] += v4.y;
-          acc_q[dt][4 * g + 2] += v4.z; acc_q[dt][4 * g + 3] += v4.w;
+      for (int s = 0; s < kPfMaxK; ++s)
+        if (((kw[s >> 2] >> (8 * (s & 3))) & 0xffu) == 2 && pos[s] >= 0) live |= 1u << s;
+    } else {
+      uint8_t kd[kPfMaxK];
+#pragma unroll
+      for (int s = 0; s < kPfMaxK; ++s) {
+        kd[s] = s < ng ? p.kind[q0 + s] : 0;
+        pos[s] = s < ng ? p.spos[q0 + s] : -1;
+      }
+#pragma unroll
+      for (int s = 0; s < kPfMaxK; ++s)
+        if (kd[s] == 2 && pos[s] >= 0) live |= 1u << s;
+    }
+    if (!__any(live != 0u)) continue;
+    const int ne = ng * a.nsub;            // (slot, sub-block) rows of the group
+    for (int e0 = 0; e0 < ne; e0 += 2) {
+      float4 buf[2][16];
+      bool in[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int e = e0 + q, s = e / a.nsub, u = e - s * a.nsub;
+        in[q] = e < ne && ((live >> s) & 1u);
+        if (in[q]) {
+          const float* pd = a.part_dq + (((int64_t)h * p.ppos + pos[s]) * a.nsub + u) * D + 4 * hl;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) buf[q][i] = *(const float4*)(pd + 8 * i);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        if (in[q]) {
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const float4 v4 = buf[q][4 * dt + g];
+              acc_q[dt][4 * g] += v4.x; acc_q[dt][4 * g + 1] += v4.y;
+              acc_q[dt][4 * g + 2] += v4.z; acc_q[dt][4 * g + 3] += v4.w;
+            }
         }
     }
   }
