@@ -87,7 +87,16 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(BwdArgs a, int64_t rows)
   if (live && sub == 0) a.delta[item] = acc;
 }
 
-// A operand of X^T (rows = dims 32 dt + lane % 32, k = 8 rows of a k_slot-swizzled
+// Row swizzle of the backward kernels' stages: 16-byte chunk c of row r sits in
+// slot c ^ bw_swz(r % 16), bw_swz(r) = (r % 4) << 2 | (r / 4) % 4.  A bijection of
+// the 16 rows, so that the row reads (16 consecutive rows, one chunk each) fall on
+// 16 distinct slots, and with (r % 4) in the top two bits, so that the transposing
+// reads (4 consecutive rows, 4 chunks of one 64-byte group each) fall on the 4
+// different 64-byte groups: every read covers all 64 banks once.  (Chunk c ^ (r %
+// 16) puts the transposing reads of 4 rows on one 64-byte group: 4-way conflicts.)
+__device__ __forceinline__ int bw_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+// A operand of X^T (rows = dims 32 dt + lane % 32, k = 8 rows of a bw_swz-swizzled
 // 128-dim stage in the order kbase + 8 (e / 4) + 4 (lane / 32) + e % 4), by two
 // transposing reads: the row order of the B operands built from accumulators.
 __device__ __forceinline__ bf16x8 tr_frag_k(const bf16* sX, int kbase, int dt, int lane) {
@@ -97,9 +106,10 @@ __device__ __forceinline__ bf16x8 tr_frag_k(const bf16* sX, int kbase, int dt, i
   const int within = 4 * (lane & 1);
   const int c = dt * 4 + cq;
   const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_short4*)(__attribute__((address_space(3))) void*)(sX + row * 128 + k_slot(row, c) * 8 + within));
+      (lds_short4*)(__attribute__((address_space(3))) void*)(sX + row * 128 + (c ^ bw_swz(row & 15)) * 8 + within));
   const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_short4*)(__attribute__((address_space(3))) void*)(sX + (row + 8) * 128 + k_slot(row + 8, c) * 8 + within));
+      (lds_short4*)(__attribute__((address_space(3))) void*)(sX + (row + 8) * 128 + (c ^ bw_swz((row + 8) & 15)) * 8 +
+                                                             within));
   bf16x8 r;
   const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo);
   const bf16x4 h4 = __builtin_bit_cast(bf16x4, hi);
@@ -144,35 +154,29 @@ __device__ __forceinline__ bf16x8 acc_bop(const floatx16& x, int s) {
   return r;
 }
 
-// Loads rows of a 64-row, k_slot-swizzled stage from global memory: wavefront wv,
+// Loads rows of a 64-row, bw_swz-swizzled stage from global memory: wavefront wv,
 // lane l fills slot l % 16 of rows 16 u + 4 wv + l / 16 (u < 4) from the row
-// pointer rowp(r) (chunk (l % 16) ^ (r % 16) of it).
+// pointer rowp(r) (chunk (l % 16) ^ bw_swz(r % 16) of it).
 template <typename RowPtr>
 __device__ __forceinline__ void stage_rows(bf16* sX, int wv, int lane, RowPtr rowp) {
   const int r0 = 4 * wv + (lane >> 4), slot = lane & 15;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int r = 16 * u + r0;
-    const bf16* src = rowp(r) + (slot ^ (r0 & 15)) * 8;
+    const bf16* src = rowp(r) + (slot ^ bw_swz(r0 & 15)) * 8;
     __builtin_amdgcn_global_load_lds((const void*)src,
                                      (__attribute__((address_space(3))) void*)(sX + (4 * u + wv) * 4 * 128),
                                      16, 0, 0);
   }
 }
 
-// Lane byte offsets of tr_frag_k's reads for row base qbase (a multiple of 16): the
+// Lane byte offsets of the transposing reads of a stage (see bw_tr_lane_off): the
 // reads of k-step ks (rows qbase + 16 ks ..), dim tile dt are at 4096 ks + (lo ^ 64 dt)
 // and 4096 ks + (hi ^ 64 dt) of the stage (the row's swizzle is the same for every
 // k-step, and the dim tile only flips address bits 6-7).
 struct TrOff {
   uint32_t lo, hi;
 };
-__device__ __forceinline__ TrOff tr_lane_off(int qbase, int lane) {
-  const int hl = lane >> 5, rr = (lane & 15) >> 2;
-  const int cq = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-  const uint32_t lo = (uint32_t)((qbase + 4 * hl + rr) * 256 + 64 * hl + 16 * (cq ^ rr) + 8 * (lane & 1));
-  return {lo, (lo ^ 128u) + 2048u};
-}
 __device__ __forceinline__ bf16x8 tr_frag_at(const bf16* sX, const TrOff& t, int ks, int dt) {
   const char* p = (const char*)sX + 4096 * ks;
   const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -209,7 +213,32 @@ struct KvMetaLoad {
   int km;
 };
 
-// Loads rows of a 64-row, k_slot-swizzled stage by 8 wavefronts: wavefront wv,
+// Row read of a bw_swz stage: keys krow (lane % 32 of a 32-row half), dims
+// 16 kk + 8 (lane / 32) .. +7.
+__device__ __forceinline__ bf16x8 bw_k_frag(const bf16* sX, int krow, int kk, int hl) {
+  return *(const bf16x8*)(sX + krow * 128 + ((2 * kk + hl) ^ bw_swz(krow & 15)) * 8);
+}
+
+// Lane part of the row reads (k_frag_at) of a bw_swz stage: row n, chunk
+// (2 kk + hl) ^ bw_swz(n % 16).
+__device__ __forceinline__ uint32_t bw_k_lane_off(int n, int hl) {
+  return (uint32_t)(n * 256) | (uint32_t)((hl << 4) ^ (bw_swz(n & 15) << 4));
+}
+
+// Lane offsets of the transposing reads (tr_frag_at) of a bw_swz stage for row base
+// qbase (a multiple of 16): row qbase + 4 hl + rr (and + 8), chunk 4 dt + cq, whose
+// slot is (4 dt + cq) ^ bw_swz(4 hl + rr) = 4 (dt ^ rr) + (cq ^ hl) (rows + 8:
+// cq ^ (hl | 2)); the dim tile dt only flips address bits 6-7.
+__device__ __forceinline__ TrOff bw_tr_lane_off(int qbase, int lane) {
+  const int hl = lane >> 5, rr = (lane & 15) >> 2;
+  const int cq = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+  const uint32_t in = (uint32_t)(64 * rr + 8 * (lane & 1));
+  const uint32_t lo = (uint32_t)((qbase + 4 * hl + rr) * 256 + 16 * (cq ^ hl)) + in;
+  const uint32_t hi = (uint32_t)((qbase + 4 * hl + rr + 8) * 256 + 16 * (cq ^ (hl | 2))) + in;
+  return {lo, hi};
+}
+
+// Loads rows of a 64-row, bw_swz-swizzled stage by 8 wavefronts: wavefront wv,
 // lane l fills slot l % 16 of rows 32 u + r0 (r0 = 4 wv + l / 16, u < 2) from the
 // row pointer rowp(r).
 template <typename RowPtr>
@@ -218,7 +247,7 @@ __device__ __forceinline__ void stage_rows8(bf16* sX, int wv, int lane, RowPtr r
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     const int r = 32 * u + r0;
-    __builtin_amdgcn_global_load_lds((const void*)(rowp(r) + (slot ^ (r0 & 15)) * 8),
+    __builtin_amdgcn_global_load_lds((const void*)(rowp(r) + (slot ^ bw_swz(r0 & 15)) * 8),
                                      (__attribute__((address_space(3))) void*)(sX + (32 * u + 4 * wv) * 128),
                                      16, 0, 0);
   }
@@ -232,7 +261,7 @@ __device__ __forceinline__ void stage_rows8r(bf16* sX, int wv, int lane, const b
 #pragma unroll
   for (int u = 0; u < 2; ++u)
     __builtin_amdgcn_global_load_lds((const void*)(xb + (uint64_t)(uint32_t)rr[u] * (uint32_t)x_st +
-                                                   (slot ^ (r0 & 15)) * 8),
+                                                   (slot ^ bw_swz(r0 & 15)) * 8),
                                      (__attribute__((address_space(3))) void*)(sX + (32 * u + 4 * wv) * 128),
                                      16, 0, 0);
 }
@@ -366,8 +395,8 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_kernel(BwdArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) { acc_dk[t][r] = 0.f; acc_dv[t][r] = 0.f; }
 
-  const uint32_t kl0 = k_lane_off(n, hl);
-  const TrOff tq0 = tr_lane_off(32 * qc, lane), tk0 = tr_lane_off(0, lane);
+  const uint32_t kl0 = bw_k_lane_off(n, hl);
+  const TrOff tq0 = bw_tr_lane_off(32 * qc, lane), tk0 = bw_tr_lane_off(0, lane);
   const int key = j0 + 32 * kh + n;
   const int kst = 32 * kh, qst = 32 * qc;
   const int dtq = 2 * dh + kh;             // this wavefront's dQ dim tile
@@ -702,8 +731,8 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
       for (int r = 0; r < 16; ++r) { s[r] = 0.f; dp[r] = 0.f; }
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) {
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(sK, 32 * hf + n, kk, hl), qop[kk], s, 0, 0, 0);
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(sV, 32 * hf + n, kk, hl), oop[kk], dp, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw_k_frag(sK, 32 * hf + n, kk, hl), qop[kk], s, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw_k_frag(sV, 32 * hf + n, kk, hl), oop[kk], dp, 0, 0, 0);
       }
       // lane = query, rows = keys j0 + 32 hf + 8 g + 4 hl + j
 #pragma unroll
