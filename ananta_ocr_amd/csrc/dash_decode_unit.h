@@ -32,13 +32,36 @@ struct DecodeArgs {
   float scale_log2e;
 };
 
-__device__ __forceinline__ int64_t dc_row(const DecodeArgs& a, int b, int j, int64_t sb,
-                                          int64_t st, int64_t sp) {
+// Where the rows of one round trip (keys jb .. jl, jl - jb < ROWS <= 32) live: row j
+// is at element offset (j - rb < page ? o0 : o1) + (j - rb) * st.  With a block table
+// the entries of the at most two pages those keys touch (every page holds at least
+// 32 keys: block sizes are 32 or multiples of 64 and pages hold whole blocks) are read
+// once, as scalar loads, before any row load is issued; a table read per row made
+// each row load wait for its own table read, and so for every row load before it.
+struct DcRows {
+  int rb;
+  int64_t k0, k1, v0, v1;
+};
+
+__device__ __forceinline__ DcRows dc_rows(const DecodeArgs& a, int b, int jb, int jl) {
+  DcRows r;
   if (a.table) {
-    const int p = a.table[(int64_t)b * a.table_stride + j / a.page];
-    return (int64_t)p * sp + (int64_t)(j % a.page) * st;
+    const int bu = __builtin_amdgcn_readfirstlane(b);
+    const int pg = __builtin_amdgcn_readfirstlane(jb) / a.page;
+    r.rb = pg * a.page;
+    const int32_t* tr = a.table + (int64_t)bu * a.table_stride + pg;
+    const int p0 = tr[0];
+    const int p1 = __builtin_amdgcn_readfirstlane(jl) >= r.rb + a.page ? tr[1] : p0;
+    r.k0 = (int64_t)p0 * a.k_sp;
+    r.v0 = (int64_t)p0 * a.v_sp;
+    r.k1 = (int64_t)p1 * a.k_sp - (int64_t)a.page * a.k_st;
+    r.v1 = (int64_t)p1 * a.v_sp - (int64_t)a.page * a.v_st;
+  } else {
+    r.rb = 0;                            // one base: the page test picks either
+    r.k0 = r.k1 = (int64_t)b * a.k_sb;
+    r.v0 = r.v1 = (int64_t)b * a.v_sb;
   }
-  return (int64_t)b * sb + (int64_t)j * st;
+  return r;
 }
 
 // Sum over the 16 lanes of a DPP row; every lane of the row gets the sum.
@@ -94,18 +117,23 @@ __device__ __forceinline__ void dc_keys(DcState& st, const DecodeArgs& a, int b,
   constexpr int NT = ROWS / 4;
   const bf16* kh = a.k + (int64_t)h * a.k_sh;
   const bf16* vh = a.v + (int64_t)h * a.v_sh;
+  static_assert(ROWS <= 32, "the rows of a round trip touch at most two table pages");
   for (int jb = j0; jb < j1; jb += ROWS) {
+    const int jl = min(jb + ROWS, j1) - 1;   // last key; later rows repeat it
+    const DcRows rw = dc_rows(a, b, jb, jl);
     bf16x8 kr[NT], vr[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int j = min(jb + 4 * t + st.g, j1 - 1);
-      kr[t] = *(const bf16x8*)(kh + dc_row(a, b, j, a.k_sb, a.k_st, a.k_sp) + st.dl);
+      const int r = min(jb + 4 * t + st.g, jl) - rw.rb;
+      kr[t] = *(const bf16x8*)(kh + (r < a.page ? rw.k0 : rw.k1) + (int64_t)r * a.k_st + st.dl);
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int j = min(jb + 4 * t + st.g, j1 - 1);
-      vr[t] = *(const bf16x8*)(vh + dc_row(a, b, j, a.v_sb, a.v_st, a.v_sp) + st.dl);
+      const int r = min(jb + 4 * t + st.g, jl) - rw.rb;
+      vr[t] = *(const bf16x8*)(vh + (r < a.page ? rw.v0 : rw.v1) + (int64_t)r * a.v_st + st.dl);
     }
+    // every load of the round trip is issued before the first use
+    __builtin_amdgcn_sched_barrier(0);
     float s[NT];
     float mloc = -INFINITY;
 #pragma unroll

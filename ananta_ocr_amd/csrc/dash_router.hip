@@ -1824,7 +1824,9 @@ __global__ __launch_bounds__(kDrThreads) void decode_route_window_kernel(DecodeR
     decode_route_body<kTailOnly>(rt, (int)blockIdx.x - B);
     return;
   }
-  const int task = ((int)blockIdx.x - nrw * B) * (kDrThreads / kWave) + (int)threadIdx.x / kWave;
+  // one piece per wavefront (the index is made uniform, so that its loads are scalar)
+  const int task = __builtin_amdgcn_readfirstlane(((int)blockIdx.x - nrw * B) * (kDrThreads / kWave) +
+                                                 (int)threadIdx.x / kWave);
   if (task >= B * da.H * npw) return;
   const int piece = task % npw, bh = task / npw;
   const int h = bh % da.H, b = bh / da.H;
