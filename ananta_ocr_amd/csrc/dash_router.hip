@@ -1843,7 +1843,7 @@ __global__ __launch_bounds__(kDrThreads) void decode_route_window_kernel(DecodeR
   dc_store_partial<128>(st, da.part + ((int64_t)bh * (npw + da.K) + piece) * (128 + 2), lane);
 }
 
-// Routed blocks of the fused step: one wavefront per routed slot of (b, h), 64 keys
+// Routed blocks of the fused step: one wavefront per routed slot of (b, h), 32 keys
 // per round trip; slot npw + r of the partials (an empty partial past the routed
 // count).
 __global__ __launch_bounds__(64) void decode_routed_kernel(DecodeArgs da, int npw) {
@@ -1856,7 +1856,7 @@ __global__ __launch_bounds__(64) void decode_routed_kernel(DecodeArgs da, int np
   const int n_r = dc_routed(da, b, sp, lane, sTmp, sRC, sRB, [] { __syncthreads(); });
   DcState st;
   dc_init(st, da, b, h, lane);
-  if (r < n_r) dc_block<16>(st, da, b, h, sp, sRC[r], true, sRB[r]);
+  if (r < n_r) dc_block<32>(st, da, b, h, sp, sRC[r], true, sRB[r]);
   dc_store_partial<128>(st, da.part + ((int64_t)(b * da.H + h) * (npw + da.K) + npw + r) * (128 + 2),
                         lane);
 }
