@@ -734,13 +734,20 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
         s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw_k_frag(sK, 32 * hf + n, kk, hl), qop[kk], s, 0, 0, 0);
         dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw_k_frag(sV, 32 * hf + n, kk, hl), oop[kk], dp, 0, 0, 0);
       }
-      // lane = query, rows = keys j0 + 32 hf + 8 g + 4 hl + j
+      // lane = query, rows = keys j0 + 32 hf + 8 g + 4 hl + j; the visibility test
+      // only where some query of the wavefront does not see all 32 keys
+      const int k0 = j0 + 32 * hf;
+      if (__all(!qvalid || (lo <= k0 && hi >= k0 + 31))) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = j0 + 32 * hf + 8 * (r >> 2) + 4 * hl + (r & 3);
-        const bool vis = key >= lo && key <= hi;
-        const float pr = vis ? fast_exp2(fmaf(s[r], c2, -l2)) : 0.f;
-        dp[r] = pr * (dp[r] - del);
+        for (int r = 0; r < 16; ++r) dp[r] = fast_exp2(fmaf(s[r], c2, -l2)) * (dp[r] - del);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + 8 * (r >> 2) + 4 * hl + (r & 3);
+          const bool vis = key >= lo && key <= hi;
+          const float pr = vis ? fast_exp2(fmaf(s[r], c2, -l2)) : 0.f;
+          dp[r] = pr * (dp[r] - del);
+        }
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
