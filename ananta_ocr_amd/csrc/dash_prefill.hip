@@ -264,12 +264,24 @@ __global__ __launch_bounds__(kPfTQ) void prefill_plan_kernel(PrefillArgs a) {
   }
   __syncthreads();
   // one global atomic per sparse block of this tile: reserves the tile's range
-  // in the block's pair list (its base is kept for the scatter kernel)
+  // in the block's pair list (its base is kept for the scatter kernel).  A thread's
+  // atomics are all issued before any base is stored: stored one by one, each
+  // atomic waited for the store before it (the counters and the bases may alias
+  // for all the compiler knows), one round trip per block.
   int32_t* tb = a.tile_base + ((int64_t)b * a.ntiles_cap + blockIdx.x) * a.nblk_cap;
-  for (int cc = tid; cc < nblk; cc += kPfTQ) {
-    const int n = sCnt[cc];
-    if (n > 0 && n < a.dense_threshold)
-      tb[cc] = atomicAdd(&a.blk_count[(int64_t)b * a.nblk_cap + cc], n);
+  {
+    constexpr int kPer = kPfMaxBlocks / kPfTQ;   // blocks per thread at most
+    int base[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int cc = tid + k * kPfTQ;
+      const int n = cc < nblk ? sCnt[cc] : 0;
+      base[k] = (n > 0 && n < a.dense_threshold)
+                    ? atomicAdd(&a.blk_count[(int64_t)b * a.nblk_cap + cc], n) : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k)
+      if (base[k] >= 0) tb[tid + k * kPfTQ] = base[k];
   }
   if (t < len) {
     auto kind_of = [&](int s) -> uint32_t {
@@ -456,13 +468,22 @@ __global__ __launch_bounds__(kPfTQ) void prefill_scatter_kernel(PrefillArgs a) {
     }
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s) pos[s] = sp[s] ? atomicAdd(&sFill[c[s]], 1) : 0;
+    // the slots' tile bases and first chunks are all loaded before the first record is
+    // stored (the records may alias them for all the compiler knows, which made every
+    // slot wait for the stores of the slot before it)
+    int qs[kPfMaxK], ch[kPfMaxK];
+#pragma unroll
+    for (int s = 0; s < kPfMaxK; ++s) {
+      qs[s] = sp[s] ? tb[c[s]] + pos[s] : 0;        // position in the block's pair list
+      ch[s] = sp[s] ? bch[c[s]] : 0;
+    }
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s)
       if (sp[s]) {
         const int64_t slot = row * a.K + g0 + s;
-        const int q = tb[c[s]] + pos[s];               // position in the block's pair list
+        const int q = qs[s];
         int64_t rc, pp;
-        if (scatter_target(a.chunk_cap, a.ppos, pos0, bch[c[s]], q, &rc, &pp)) {
+        if (scatter_target(a.chunk_cap, a.ppos, pos0, ch[s], q, &rc, &pp)) {
           rec[rc * kRec + kRecHead + q % kPfCH] = (int32_t)(slot - base);
           a.spos[slot] = (int32_t)pp;
         } else {                                       // never with consistent counts
