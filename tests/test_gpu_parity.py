@@ -514,6 +514,69 @@ def test_decode_paged_matches_contiguous_oracle():
     _close(out, ref, "decode paged")
 
 
+def _pages_of(k, v, lens, page, seed):
+    """k/v [B,H,S,D] -> pages [n, page, H, D] in a random order, and the block table."""
+    B = k.shape[0]
+    g = _gen(seed)
+    npg = [(int(L) + page - 1) // page for L in lens]
+    perm = torch.randperm(sum(npg), generator=g)
+    table = torch.zeros(B, max(npg), dtype=torch.int32)
+    kp = torch.zeros(sum(npg), page, k.shape[1], 128, dtype=torch.bfloat16)
+    vp = torch.zeros_like(kp)
+    o = 0
+    for b in range(B):
+        for p_ in range(npg[b]):
+            phys = int(perm[o + p_])
+            table[b, p_] = phys
+            seg = slice(p_ * page, min((p_ + 1) * page, int(lens[b])))
+            n = seg.stop - seg.start
+            kp[phys, :n] = k[b, :, seg].transpose(0, 1)
+            vp[phys, :n] = v[b, :, seg].transpose(0, 1)
+        o += npg[b]
+    return kp, vp, table
+
+
+@pytest.mark.parametrize("bs,mult", [(64, 2), (64, 4), (32, 3)])
+def test_decode_pages_of_several_blocks_equal_contiguous(bs, mult):
+    """Pages holding several key blocks (page = mult * block): the split-K decode and the
+    fused decode step give the contiguous cache's results bit for bit.  A round trip's
+    block-table entry is read once and its rows are addressed from the page's first key,
+    so every row offset inside a page goes through that arithmetic."""
+    B, H, lw, K = 3, 2, 256, 4
+    lens = torch.tensor([1500, 333, 900], dtype=torch.int32)
+    S = int(lens.max())
+    q, k, v, idx, bias, valid, lens = _decode_inputs(430 + mult + bs, B, H, S, bs, lw, K, lens)
+    page = mult * bs
+    kp, vp, table = _pages_of(k, v, lens, page, 440 + mult)
+    scale = 1 / math.sqrt(128)
+    args = (idx.to(DEV), bias.to(DEV), valid.to(DEV), bs, lw, scale)
+    cont = ops.attn_decode(q.to(DEV), k.to(DEV), v.to(DEV), *args, seq_lens=lens.to(DEV)).cpu()
+    paged = ops.attn_decode(q.to(DEV), kp.to(DEV), vp.to(DEV), *args, seq_lens=lens.to(DEV),
+                            block_table=table.to(DEV), page_size=page).cpu()
+    assert torch.equal(cont, paged)
+    _close(paged, _decode_ref(q, k, v, idx, bias, valid, lens, bs, lw, scale), "decode, pages of blocks")
+    # the fused step (routing beside the window part) over the same two layouts
+    g = _gen(450 + mult)
+    iq = torch.randn(B, 1, 128, generator=g)
+    ik = torch.randn(B, S, 128, generator=g)
+    ik_pages = torch.zeros(kp.shape[0], page, 128)
+    for b in range(B):
+        for p_ in range((int(lens[b]) + page - 1) // page):
+            seg = slice(p_ * page, min((p_ + 1) * page, int(lens[b])))
+            ik_pages[int(table[b, p_]), :seg.stop - seg.start] = ik[b, seg]
+    hc = torch.zeros(128, device=DEV)
+    nblk_cap = table.shape[1] * page // bs          # the summaries cover the table's pages
+    outs = []
+    for kk, vv, ikk, kw in ((k, v, ik, {}), (kp, vp, ik_pages,
+                                             dict(block_table=table.to(DEV), page_size=page))):
+        kb = ops.kbar(ikk.to(DEV), hc, bs, seq_lens=lens.to(DEV), nblk_cap=nblk_cap, **kw)
+        o, _ = ops.decode_step_fused(q.to(DEV), kk.to(DEV), vv.to(DEV), iq.to(DEV), ikk.to(DEV), hc,
+                                     kb, bs, lw // bs, W.IDX_SCALE, W.FLOOR, W.SIGMA, K, K, scale,
+                                     seq_lens=lens.to(DEV), **kw)
+        outs.append(o.cpu())
+    assert torch.equal(outs[0], outs[1])
+
+
 def test_decode_equals_prefill_last_row():
     B, H, S, bs, lw, K = 1, 2, 900, 64, 256, 4
     q, k, v, idx, bias, valid = _attn_inputs(420, B, H, S, bs, lw, K, qscale=2.0)
