@@ -1679,10 +1679,11 @@ inline PlanLayout plan_layout(int B, int H, int S_max, int64_t rows, int K, int 
 
 namespace dash {
 // Workspace of the backward: the plan (as the forward's, every routed pair
-// block-major), fp32 bias-gradient and dQ partials per (head, pair position), delta.
+// block-major), per (head, pair position) the fp32 bias-gradient partials and the
+// scaled fp16 dQ partials with their scales (four 32-dim pieces a row), delta.
 struct BwdLayout {
   PlanLayout P;
-  int64_t pdb, pdq, delta, total;
+  int64_t pdb, pdq, pdqs, delta, total;
 };
 
 inline BwdLayout bwd_layout(int B, int H, int S_max, int64_t rows, int K, int D, int nblk_cap,
@@ -1692,7 +1693,8 @@ inline BwdLayout bwd_layout(int B, int H, int S_max, int64_t rows, int K, int D,
   int64_t o = L.P.plse;                    // the forward's partials are not needed
   const int64_t nsub = (bs + 63) / 64;     // 64-key stages per block
   L.pdb = o; o = align256(o + L.P.ppos * H * nsub * 4);
-  L.pdq = o; o = align256(o + L.P.ppos * H * nsub * (int64_t)D * 4);
+  L.pdq = o; o = align256(o + L.P.ppos * H * nsub * (int64_t)D * 2);
+  L.pdqs = o; o = align256(o + L.P.ppos * H * nsub * 4 * 4);
   L.delta = o; o = align256(o + rows * H * 4);
   L.total = o;
   return L;
@@ -1941,7 +1943,8 @@ extern "C" int dash_attn_prefill_backward(
   a.nstage = (int)(((int64_t)nblk_cap * block_size + kBwIT - 1) / kBwIT);
   a.delta = (float*)(w + L.delta);
   a.part_db = (float*)(w + L.pdb);
-  a.part_dq = (float*)(w + L.pdq);
+  a.part_dq = (_Float16*)(w + L.pdq);
+  a.part_dqs = (float*)(w + L.pdqs);
   hipStream_t st = (hipStream_t)stream;
   const int64_t nitems = total_rows * H;
   if (nitems > 0)

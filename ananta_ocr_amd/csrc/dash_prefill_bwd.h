@@ -46,7 +46,13 @@ struct BwdArgs {
   bf16* dk; int64_t dk_sb, dk_sh, dk_st;
   bf16* dv; int64_t dv_sb, dv_sh, dv_st;
   float* dbias;                           // [rows, K] (null: not wanted)
-  float* part_dq;                         // [H, ppos, nsub, 128] fp32, dims in MFMA lane order
+  // dQ partials of the routed pairs: [H, ppos, nsub, 128] fp16, dims in MFMA lane order;
+  // each 32-dim piece is stored as its values times 2^-e, e the binary exponent of the
+  // piece's largest magnitude (so every stored value lies in (-1, 1) and its rounding
+  // error is at most 2^-11 of that magnitude), and part_dqs [H, ppos, nsub, 4] holds
+  // the pieces' scales 2^e
+  _Float16* part_dq;
+  float* part_dqs;
   float* part_db;                         // [H, ppos, nsub] fp32
   float scale;                            // natural softmax scale
   int nstage;                             // 64-key stages per sequence (of nblk_cap blocks)
@@ -420,22 +426,24 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_kernel(BwdArgs a) {
   __syncthreads();
 
   // dQ^T partials of a routed step wait in the wavefront's area (query row r at 32
-  // floats, 16-byte chunk c in slot c ^ (r % 8)) and are stored at the start of the
-  // next step, 8 lanes per 128-byte row piece.
+  // halves, 8-byte chunk c in slot c ^ (r % 8), the row's scale at float 512 + r) and
+  // are stored at the start of the next step, 8 lanes per 64-byte row piece.
   bool pend = false;
   int64_t pend_pi = -1;
   float pend_db = 0.f;
   auto store_pending = [&](int par) {
     if (pend) {
       const int c = lane & 7;
+      const _Float16* const xh = (const _Float16*)xs;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 8 * i + (lane >> 3);
         const int pos = sM[par].pos[qst + r];
-        const float4 v = *(const float4*)(xs + r * 32 + ((c ^ (r & 7)) << 2));
+        const f16x4 v = *(const f16x4*)(xh + r * 32 + ((c ^ (r & 7)) << 2));
         if (pos >= 0) {
           const int64_t pi = ((int64_t)h * p.ppos + pos) * a.nsub + sub;
-          *(float4*)(a.part_dq + pi * D + 32 * dtq + 4 * c) = v;
+          *(f16x4*)(a.part_dq + pi * D + 32 * dtq + 4 * c) = v;
+          if (c == 0) a.part_dqs[pi * 4 + dtq] = xs[512 + r];
         }
       }
       if (kh == 0 && dh == 0 && hl == 0 && pend_pi >= 0) a.part_db[pend_pi] = pend_db;
@@ -597,11 +605,23 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_kernel(BwdArgs a) {
         for (int e = 0; e < 4; ++e) { dsb[e] = dst[2 * ks][e]; dsb[e + 4] = dst[2 * ks + 1][e]; }
         acc_q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag_at(sK, tk, ks, dtq), dsb, acc_q, 0, 0, 0);
       }
-      // staged for the next step: dims 32 dtq + 8 g + 4 hl + j of query n
+      // staged for the next step: dims 32 dtq + 8 g + 4 hl + j of query n, in fp16 after
+      // scaling by 2^-e (lanes n and n + 32 hold the two halves of the piece); the
+      // scale 2^e at xs[512 + n]
+      float mx = 0.f;
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *(float4*)(xs + n * 32 + (((2 * g + hl) ^ (n & 7)) << 2)) =
-            make_float4(acc_q[4 * g], acc_q[4 * g + 1], acc_q[4 * g + 2], acc_q[4 * g + 3]);
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fabsf(acc_q[r]));
+      mx = xor32_max(mx);
+      const int ex = min(__builtin_amdgcn_frexp_expf(mx), 127);
+      _Float16* const xh = (_Float16*)xs;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f16x4 hv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hv[j] = (_Float16)ldexpf(acc_q[4 * g + j], -ex);
+        *(f16x4*)(xh + n * 32 + (((2 * g + hl) ^ (n & 7)) << 2)) = hv;
+      }
+      if (hl == 0) xs[512 + n] = ldexpf(1.f, ex);
       const int pos = M.pos[qst + n];
       pend_pi = pos >= 0 ? ((int64_t)h * p.ppos + pos) * a.nsub + sub : -1;
       pend_db = sDb[0][qst + n] + sDb[1][qst + n];
@@ -799,28 +819,32 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
     if (!__any(live != 0u)) continue;
     const int ne = ng * a.nsub;            // (slot, sub-block) rows of the group
     for (int e0 = 0; e0 < ne; e0 += 2) {
-      float4 buf[2][16];
+      f16x4 buf[2][16];
+      float4 sc[2];                        // the scales of the row's four 32-dim pieces
       bool in[2];
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int e = e0 + q, s = e / a.nsub, u = e - s * a.nsub;
         in[q] = e < ne && ((live >> s) & 1u);
         if (in[q]) {
-          const float* pd = a.part_dq + (((int64_t)h * p.ppos + pos[s]) * a.nsub + u) * D + 4 * hl;
+          const int64_t pr = ((int64_t)h * p.ppos + pos[s]) * a.nsub + u;
+          const _Float16* pd = a.part_dq + pr * D + 4 * hl;
 #pragma unroll
-          for (int i = 0; i < 16; ++i) buf[q][i] = *(const float4*)(pd + 8 * i);
+          for (int i = 0; i < 16; ++i) buf[q][i] = *(const f16x4*)(pd + 8 * i);
+          sc[q] = *(const float4*)(a.part_dqs + pr * 4);
         }
       }
 #pragma unroll
       for (int q = 0; q < 2; ++q)
         if (in[q]) {
+          const float sca[4] = {sc[q].x, sc[q].y, sc[q].z, sc[q].w};
 #pragma unroll
           for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-              const float4 v4 = buf[q][4 * dt + g];
-              acc_q[dt][4 * g] += v4.x; acc_q[dt][4 * g + 1] += v4.y;
-              acc_q[dt][4 * g + 2] += v4.z; acc_q[dt][4 * g + 3] += v4.w;
+              const f16x4 v4 = buf[q][4 * dt + g];
+#pragma unroll
+              for (int j = 0; j < 4; ++j) acc_q[dt][4 * g + j] = fmaf((float)v4[j], sca[dt], acc_q[dt][4 * g + j]);
             }
         }
     }
