@@ -100,6 +100,31 @@ def test_backward_matches_torch_autograd(B, H, S, bs, lw, K):
     assert bool((db.cpu()[br.grad == 0] == 0).all())
 
 
+@pytest.mark.parametrize("gscale", [1e6, 1e-6])
+def test_backward_gradient_magnitudes(gscale):
+    """Output gradients far from 1: the routed pairs' dQ partials pass through fp16 with a
+    power-of-two scale per 32-dim piece, which must neither overflow (partials far above
+    fp16's 65,504 at the large scale) nor lose the small ones to fp16's subnormal range."""
+    B, H, S, bs, lw, K = 1, 2, 700, 64, 128, 8
+    q, k, v, topi, bias, valid, dout = _case(91, B, H, S, bs, lw, K)
+    dout = (dout.float() * gscale).bfloat16()
+    scale = 1 / math.sqrt(128)
+    qr, kr, vr = (t.float().requires_grad_() for t in (q, k, v))
+    br = bias.clone().requires_grad_()
+    out_r = _ref(qr, kr, vr, topi, br, valid, bs, lw, scale)
+    out_r.backward(dout.float())
+    args = [t.to(DEV) for t in (q, k, v)]
+    out, lse = ops.attn_prefill(*args, topi.to(DEV), bias.to(DEV), valid.to(DEV), bs, lw, scale,
+                                return_lse=True)
+    dq, dk, dv, db = ops.attn_prefill_backward(*args, out, lse, dout.to(DEV), topi.to(DEV),
+                                               bias.to(DEV), valid.to(DEV), bs, lw, scale)
+    torch.cuda.synchronize()
+    for got, ref, what in ((dq, qr.grad, "dq"), (dk, kr.grad, "dk"), (dv, vr.grad, "dv"),
+                           (db, br.grad, "dbias")):
+        assert torch.isfinite(got.float()).all(), what
+        _close_grad(got, ref, what)
+
+
 def test_backward_segment_starts():
     """kmin (packed segments inside one sequence, packing_patch.py): keys before a
     row's segment start are invisible to it, in the window and in routed blocks."""
