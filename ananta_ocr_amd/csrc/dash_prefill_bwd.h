@@ -124,18 +124,6 @@ __device__ __forceinline__ bf16x8 tr_frag_k(const bf16* sX, int kbase, int dt, i
   return r;
 }
 
-// Sum over the 32 lanes of a half-wavefront (lanes 0-31 and 32-63 separately),
-// every lane of the half gets it: rotations by 8 and 4 and the quad exchanges
-// within each 16-lane row (DPP), then the other row of the half (permlane16 swap).
-__device__ __forceinline__ float half32_sum(float v) {
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 // Barrier for LDS data written by ds_write: the wavefront's LDS accesses
 // complete (lgkmcnt 0) and nothing else is waited for, so that its outstanding
 // global loads, among them the next step's direct-to-LDS row loads, stay in
@@ -566,14 +554,27 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_kernel(BwdArgs a) {
           for (int j = 0; j < 4; ++j) w[j] = (bf16)ds[4 * g + j];
           *(bf16x4*)&sDS[qc][kst + n][8 * g + 4 * hl] = w;
         }
+        // the row sums in fp32: ds through the wavefront's staging area (free between the
+        // previous step's partial stores and this step's staging) as [key][query], in the
+        // staging's swizzle, then lanes q and q + 32 add 16 keys each (16 shuffle-sums of
+        // 32 lanes cost more)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ds[r] = half32_sum(ds[r]);
-        if (n == 0) {
+        for (int g = 0; g < 4; ++g)
+          *(float4*)(xs + n * 32 + (((2 * g + hl) ^ (n & 7)) << 2)) =
+              make_float4(ds[4 * g], ds[4 * g + 1], ds[4 * g + 2], ds[4 * g + 3]);
+        wave_lds_sync();
+        {
+          const int q = lane & 31;
+          float sum = 0.f;
 #pragma unroll
-          for (int g = 0; g < 4; ++g)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) sDb[kh][qst + 8 * g + 4 * hl + j] = ds[4 * g + j];
+          for (int i = 0; i < 16; ++i) {
+            const int key = 16 * hl + i;
+            sum += xs[key * 32 + (((q >> 2) ^ (key & 7)) << 2) + (q & 3)];
+          }
+          sum += __shfl_xor(sum, 32, kWave);
+          if (hl == 0) sDb[kh][qst + q] = sum;
         }
+        wave_lds_sync();
       }
       lds_barrier();
       // dQ^T tile dtq = K^T dS^T over the stage's 64 keys for the chunk's 32 queries
