@@ -46,7 +46,8 @@ struct BwdArgs {
   bf16* dk; int64_t dk_sb, dk_sh, dk_st;
   bf16* dv; int64_t dv_sb, dv_sh, dv_st;
   float* dbias;                           // [rows, K] (null: not wanted)
-  // dQ partials of the routed pairs: [H, ppos, nsub, 128] fp16, dims in MFMA lane order;
+  // dQ partials of the routed pairs: [H, ppos, nsub, 128] fp16, the 64 dims a lane of the
+  // query-major kernel adds contiguous (dim 32 dt + 8 g + 4 h + j at 64 h + 16 dt + 4 g + j);
   // each 32-dim piece is stored as its values times 2^-e, e the binary exponent of the
   // piece's largest magnitude (so every stored value lies in (-1, 1) and its rounding
   // error is at most 2^-11 of that magnitude), and part_dqs [H, ppos, nsub, 4] holds
@@ -430,7 +431,7 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_kernel(BwdArgs a) {
         const f16x4 v = *(const f16x4*)(xh + r * 32 + ((c ^ (r & 7)) << 2));
         if (pos >= 0) {
           const int64_t pi = ((int64_t)h * p.ppos + pos) * a.nsub + sub;
-          *(f16x4*)(a.part_dq + pi * D + 32 * dtq + 4 * c) = v;
+          *(f16x4*)(a.part_dq + pi * D + (c & 1) * 64 + 16 * dtq + 4 * (c >> 1)) = v;
           if (c == 0) a.part_dqs[pi * 4 + dtq] = xs[512 + r];
         }
       }
@@ -829,9 +830,13 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
         in[q] = e < ne && ((live >> s) & 1u);
         if (in[q]) {
           const int64_t pr = ((int64_t)h * p.ppos + pos[s]) * a.nsub + u;
-          const _Float16* pd = a.part_dq + pr * D + 4 * hl;
+          const _Float16* pd = a.part_dq + pr * D + 64 * hl;
 #pragma unroll
-          for (int i = 0; i < 16; ++i) buf[q][i] = *(const f16x4*)(pd + 8 * i);
+          for (int k = 0; k < 8; ++k) {
+            const f16x8 w = *(const f16x8*)(pd + 8 * k);
+            buf[q][2 * k] = f16x4{w[0], w[1], w[2], w[3]};
+            buf[q][2 * k + 1] = f16x4{w[4], w[5], w[6], w[7]};
+          }
           sc[q] = *(const float4*)(a.part_dqs + pr * 4);
         }
       }
