@@ -95,9 +95,12 @@ struct PrefillArgs {
   // position is its place in the chunk records, chunk-major over all sequences
   int32_t* spos;                       // [rows, K] position of each sparse pair
   int64_t ppos;                        // positions per head
-  float* part_lse;                     // [H, ppos]  base-2 log-sum-exp
-  bf16* part_o;                        // [H, ppos, D]  normalised partial output, dims
-                                       // in MFMA lane order (see part_index)
+  // the normalised partial output of a pair as bytes, dims in MFMA lane order (see
+  // part_index): dim value = (byte - 128) * scale, scale = (the row's largest
+  // magnitude) / 127, so that a stored value is off by at most half a step, 1/254
+  // of that magnitude
+  float2* part_ls;                     // [H, ppos]  (base-2 log-sum-exp, scale)
+  uint8_t* part_q;                     // [H, ppos, D]
   // split tiles (no plan; split_items > 0): tile t of every sequence is cut into
   // tile_parts(t) parts of split_items items (the last part takes the rest); part p
   // of tile tl (the logical (sequence, head, tile) id) writes its rows' normalised
@@ -1193,6 +1196,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
   // reference moves once to their maximum; partial rows are lane-contiguous and
   // read with 16-byte loads.
   // Slots are merged in groups of 16.
+  float qbias = 0.f;                       // -128 x the bytes' weights, added to every dim
   for (int g0 = 0; pa.kind && g0 < pa.K; g0 += kPfMaxK) {
     const int64_t p0 = (r0 + tqc) * pa.K + g0;
     const int ng = min(kPfMaxK, pa.K - g0);
@@ -1220,9 +1224,14 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
           sp[s] = pa.spos[p0 + s];
         }
     }
+    float qs[kPfMaxK];                     // the partial rows' byte scales
 #pragma unroll
-    for (int s = 0; s < kPfMaxK; ++s)
-      l2[s] = (((smask >> s) & 1u) && sp[s] >= 0) ? pa.part_lse[part_row(pa, sp[s], h)] : -INFINITY;
+    for (int s = 0; s < kPfMaxK; ++s) {
+      const float2 ls = (((smask >> s) & 1u) && sp[s] >= 0) ? pa.part_ls[part_row(pa, sp[s], h)]
+                                                           : make_float2(-INFINITY, 0.f);
+      l2[s] = ls.x;
+      qs[s] = ls.y;
+    }
     float mx = m_run;
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s) mx = fmaxf(mx, l2[s]);
@@ -1233,6 +1242,7 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
       for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
+      qbias *= alpha;
       m_run = mx;
     }
     // Slots in 4 batches of 4: a batch's loads (the lanes' live slots only) are
@@ -1242,33 +1252,40 @@ __global__ __launch_bounds__(256, OCC) void prefill_tile_kernel(PrefillArgs a) {
 #pragma unroll
     for (int s = 0; s < kPfMaxK; ++s)
       if (l2[s] != -INFINITY) live |= 1u << s;
-    const bf16* po = pa.part_o + part_row(pa, 0, h) * D + part_index(hl, 0, 0, 0);
+    const uint8_t* po = pa.part_q + part_row(pa, 0, h) * D + part_index(hl, 0, 0, 0);
 #pragma unroll
     for (int sb = 0; sb < kPfMaxK; sb += 4) {
       const uint32_t gm = (live >> sb) & 15u;
       if (!__any(gm != 0u)) continue;
-      bf16x8 buf[4][8];
+      uint4 buf[4][4];
 #pragma unroll
       for (int u = 0; u < 4; ++u)
         if ((gm >> u) & 1u) {
 #pragma unroll
-          for (int q = 0; q < 8; ++q) buf[u][q] = *(const bf16x8*)(po + (int64_t)sp[sb + u] * D + q * 8);
+          for (int q = 0; q < 4; ++q) buf[u][q] = *(const uint4*)(po + (int64_t)sp[sb + u] * D + q * 16);
         }
 #pragma unroll
       for (int u = 0; u < 4; ++u)
         if ((gm >> u) & 1u) {
           const float w = fast_exp2(l2[sb + u] - m_run);
           if (hl == 0) l_run += w;
+          // value = (byte - 128) * scale: the bytes times w * scale here, the -128 in qbias
+          const float c = w * qs[sb + u];
+          qbias = fmaf(-128.f, c, qbias);
 #pragma unroll
-          for (int dt = 0; dt < D / 32; ++dt)
+          for (int dt = 0; dt < D / 32; ++dt) {
+            const uint32_t wd[4] = {buf[u][dt].x, buf[u][dt].y, buf[u][dt].z, buf[u][dt].w};
 #pragma unroll
-            for (int g = 0; g < 4; g += 2)
-#pragma unroll
-              for (int e = 0; e < 8; ++e)
-                acc_o[dt][g * 4 + e] += w * bf2f(buf[u][dt * 2 + g / 2][e]);
+            for (int r = 0; r < 16; ++r)
+              acc_o[dt][r] = fmaf(c, (float)((wd[r >> 2] >> (8 * (r & 3))) & 0xffu), acc_o[dt][r]);
+          }
         }
     }
   }
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_o[dt][r] += qbias;
 
   // ---- epilogue: normalise and store ----
   const float l_tot = xor32_sum(l_run);
@@ -1539,39 +1556,55 @@ __global__ __launch_bounds__(256, 3) void prefill_sparse_kernel(PrefillArgs a) {
     }
     const float l_tot = xor32_sum(psum);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    // The row as bytes: the normalised values times 127 / (their largest magnitude),
+    // rounded, plus 128 (lanes n and n + 32 hold the two halves of row n).
+    float amax = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) amax = fmaxf(amax, fabsf(acc_o[dt][r]));
+    amax = xor32_max(amax) * inv;
+    const float qk = amax > 0.f ? inv * (127.f / amax) : 0.f;
+    const float qscale = amax * (1.f / 127.f);
     // The wavefront's 32 partial rows (consecutive positions) leave through LDS in
     // two pieces of 16 rows, so that every store instruction writes 1 KB
     // contiguously (whole 128-byte lines) instead of 16 bytes of 64 different
     // rows.  Rows of lanes past the chunk's pair count are written too: their
     // positions belong to this chunk and are never read.  In LDS, 16-byte chunk c
-    // of row r sits at slot c ^ r: the 16 rows a write instruction covers (one
-    // chunk each) then fall on distinct banks instead of all on the same four.
+    // of row r sits at slot c ^ (r % 8): the rows a write instruction covers then
+    // fall on distinct banks.
     const int64_t pw = part_row(a, (int64_t)(pb + ch) * kPfCH + wv * 32 + 128 * j, h);
+    uint8_t* const stq = (uint8_t*)st;
 #pragma unroll
     for (int piece = 0; piece < 2; ++piece) {
       if ((n >> 4) == piece) {
+        const int rr = n & 15;
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
+        for (int dt = 0; dt < D / 32; ++dt) {
+          uint32_t w4[4];
 #pragma unroll
-          for (int g = 0; g < 4; g += 2) {
-            bf16x8 w;
+          for (int q = 0; q < 4; ++q) {
+            uint32_t w = 0u;
 #pragma unroll
-            for (int e2 = 0; e2 < 8; ++e2) w[e2] = (bf16)(acc_o[dt][g * 4 + e2] * inv);
-            const int cidx = part_index(hl, dt, g, 0) / 8;
-            *(bf16x8*)(st + (n & 15) * D + ((cidx ^ (n & 15)) * 8)) = w;
+            for (int e = 0; e < 4; ++e)
+              w |= (uint32_t)fmaf(acc_o[dt][4 * q + e], qk, 128.5f) << (8 * e);
+            w4[q] = w;
           }
+          const int cidx = part_index(hl, dt, 0, 0) / 16;
+          *(uint4*)(stq + rr * D + ((cidx ^ (rr & 7)) * 16)) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
       }
       wave_lds_sync();                     // other lanes' rows are read below
-      char* const dst = (char*)(a.part_o + (pw + 16 * piece) * D);
+      char* const dst = (char*)(a.part_q + (pw + 16 * piece) * D);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int rr = 4 * k + (lane >> 4), cidx = lane & 15;
-        *(bf16x8*)(dst + k * 1024 + lane * 16) =
-            *(const bf16x8*)((const char*)st + rr * (D * 2) + ((cidx ^ rr) * 16));
+      for (int k = 0; k < 2; ++k) {
+        const int rr = 8 * k + (lane >> 3), cidx = lane & 7;
+        *(uint4*)(dst + k * 1024 + lane * 16) = *(const uint4*)(stq + rr * D + ((cidx ^ (rr & 7)) * 16));
       }
       wave_lds_sync();                     // and overwritten by the next piece
     }
-    if (active && hl == 0) a.part_lse[pw + n] = l_tot > 0.f ? mloc + log2f(l_tot) : -INFINITY;
+    if (active && hl == 0)
+      a.part_ls[pw + n] = make_float2(l_tot > 0.f ? mloc + log2f(l_tot) : -INFINITY, qscale);
   };
   if (nrounds > 0) round(0, inA);
   if (nrounds > 1) round(1, inB);
@@ -1663,8 +1696,8 @@ inline PlanLayout plan_layout(int B, int H, int S_max, int64_t rows, int K, int 
   // chunks over all sequences: at most (pairs / kPfCH) full ones plus one partly
   // filled chunk per block, and a sequence of len rows has ceil(len / bs) blocks
   L.ppos = (rows * K / kPfCH + rows / bs + B + 2) * kPfCH;
-  L.plse = o; o = align256(o + L.ppos * H * 4);
-  L.po = o; o = align256(o + L.ppos * H * D * 2);
+  L.plse = o; o = align256(o + L.ppos * H * 8);
+  L.po = o; o = align256(o + L.ppos * H * D);
   // tiles of all sequences in one order: sum ceil(len / kPfTQ) <= (rows + (kPfTQ - 1) B) / kPfTQ
   L.ntv = (int)((rows + (int64_t)(kPfTQ - 1) * B) / kPfTQ) + 1;
   L.tpref = o; o = align256(o + (int64_t)(B + 1) * 4);
@@ -1822,8 +1855,8 @@ extern "C" int dash_attn_prefill(
     a.chunk_cap = L.chunk_cap;
     a.spos = (int32_t*)(w + L.spos);
     a.ppos = L.ppos;
-    a.part_lse = (float*)(w + L.plse);
-    a.part_o = (bf16*)(w + L.po);
+    a.part_ls = (float2*)(w + L.plse);
+    a.part_q = (uint8_t*)(w + L.po);
     if (cu_seqlens) {
       a.tile_pref = (int32_t*)(w + L.tpref);
       a.tile_doc = (int32_t*)(w + L.tdoc);
