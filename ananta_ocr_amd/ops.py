@@ -395,7 +395,7 @@ def train_route(z, cand, idx_scale, floor, sigma, K, row_nblk=None):
     return _TrainRouteFn.apply(z, cand, idx_scale, floor, sigma, K, row_nblk)
 
 
-DENSE_THRESHOLD = 32   # of the 128 queries of a tile; below it a routed block goes sparse
+DENSE_THRESHOLD = 48   # of the 128 queries of a tile; below it a routed block goes sparse
 # Small prefills take every routed block with its tile (no plan, no sparse kernel):
 # a grid of at most SMALL_TILES 128-query tiles (which the library splits over
 # several work-groups each) over sequences of at most SMALL_BLOCKS blocks, so that
