@@ -72,6 +72,40 @@ __device__ __forceinline__ int xcd_logical_id(int L, int n) {
   return x * q + min(x, r) + k;
 }
 
+// Stream-local stage order over the XCDs: ns streams (e.g. (sequence, head) pairs)
+// of nst stages each, stage 0 the heaviest.  XCD x = L % 8 takes, stage by stage,
+// the whole streams x, x + 8, ... (q = ns / 8 of them) and, of the r = ns % 8 other
+// streams, stage s of stream 8 q + j whenever (s r + j) % 8 == x; its k-th work-group
+// (k = L / 8) takes the k-th of these items.  Every XCD thus runs its streams'
+// stages in order, neighbouring stages of one stream share its L2, and the heavy
+// stages of every stream start first.  Returns false for the ids past an XCD's
+// items (the grid is stream_stage_grid work-groups).
+__host__ __device__ inline int stream_stage_before(int s, int x, int q, int r) {
+  return q * s + (s * r - x + 7) / 8;    // items of XCD x at stages < s
+}
+__host__ __device__ inline bool stream_stage_item(int L, int ns, int nst, int& stream, int& stage) {
+  const int x = L & 7, k = L >> 3;
+  const int q = ns >> 3, r = ns & 7;
+  int s = (int)((int64_t)k * 8 / (8 * q + r));
+  if (s > nst) s = nst;
+  while (s > 0 && stream_stage_before(s, x, q, r) > k) --s;
+  while (s < nst && stream_stage_before(s + 1, x, q, r) <= k) ++s;
+  if (s >= nst) return false;
+  const int o = k - stream_stage_before(s, x, q, r);
+  if (o < q) {
+    stream = x + 8 * o;
+  } else {
+    const int j = (x - (s * r & 7)) & 7;
+    if (o > q || j >= r) return false;
+    stream = 8 * q + j;
+  }
+  stage = s;
+  return true;
+}
+__host__ __device__ inline int stream_stage_grid(int ns, int nst) {
+  return 8 * ((ns >> 3) * nst + (nst * (ns & 7) + 7) / 8);
+}
+
 // Where token t of sequence b lives, for the three layouts the path uses:
 //   contiguous  row = b*stride_b + t*stride_t
 //   varlen      row = (cu[b] + t)*stride_t          (packed documents)

@@ -2005,7 +2005,7 @@ extern "C" int dash_attn_prefill_backward(
     hipLaunchKernelGGL(prefill_scan_kernel, dim3(B), dim3(1024), 0, st, p);
     hipLaunchKernelGGL(prefill_scatter_kernel, dim3(p.ntiles, B), dim3(kPfTQ), 0, st, p);
   }
-  hipLaunchKernelGGL(bwd_kv_kernel, dim3(a.nstage * H * B), dim3(512), 0, st, a);
+  hipLaunchKernelGGL(bwd_kv_kernel, dim3(stream_stage_grid(B * H, a.nstage)), dim3(512), 0, st, a);
   hipLaunchKernelGGL(bwd_q_kernel, dim3(p.ntiles * H * B), dim3(256), 0, st, a);
   if (dbias && K > 0 && total_rows > 0)
     hipLaunchKernelGGL(bwd_dbias_kernel, dim3((unsigned)((total_rows * K + 255) / 256)), dim3(256), 0,

@@ -294,13 +294,15 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) float sX[8][1024];
 
   const PrefillArgs& p = a.p;
-  // Stage-major order, the work-groups dealt to the 8 XCDs in turn: an early stage
-  // takes the routed pairs of every later query (block 0 of 27,300 tokens ~6,000 of
-  // them, the last blocks almost none), so the heavy stages of every head start
-  // first and the light ones fill the end (numbered per (head, stage) and contiguous
-  // per XCD instead, the heavy stages of some heads started last: 2.61 -> 2.04 ms).
-  const int nbh = (int)(gridDim.x / a.nstage);
-  const int stage = (int)blockIdx.x / nbh, bh = (int)blockIdx.x % nbh;
+  // Stages in order per (sequence, head) stream, each stream's stages on one XCD
+  // (stream_stage_item): an early stage takes the routed pairs of every later query
+  // (block 0 of 27,300 tokens ~6,000 of them, the last blocks almost none), so the
+  // heavy stages start first and the light ones fill the end (numbered per (head,
+  // stage) and contiguous per XCD instead, the heavy stages of some heads started
+  // last: 2.61 -> 2.04 ms), while neighbouring stages, whose window bands overlap,
+  // share one L2.
+  int bh, stage;
+  if (!stream_stage_item((int)blockIdx.x, p.B * p.H, a.nstage, bh, stage)) return;
   const int h = bh % p.H, b = bh / p.H;
   const int len = seq_len(p, b);
   const int j0 = stage * kBwIT;
