@@ -628,6 +628,69 @@ __device__ __forceinline__ float ord_key_inv(uint32_t h) {
   return __uint_as_float((h & 0x80000000u) ? (h & 0x7fffffffu) : ~h);
 }
 
+// Phase 1 for one row held by one wavefront: entry c = lane + 64 i has value key
+// hi[i] (0: no entry) and candidate flag cb[i]; the M largest 64-bit keys
+// hi << 32 | (0xffff - c) << 1 | cb (value descending, block id ascending) are
+// written to sel[0 .. M) in no particular order.  s_cand: 64 entries of this
+// wavefront's LDS.  Every lane of the wavefront calls it.
+template <int NPL>
+__device__ __forceinline__ void route_row_topm(const uint32_t (&hi)[NPL], const uint8_t (&cb)[NPL],
+                                               int M, uint64_t* s_cand, uint64_t* sel) {
+  const int lane = wave_lane();
+  uint32_t cmx = 0;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) cmx = max(cmx, hi[i]);
+  // classes = lane quads (16 of them, all non-empty once the row has >= 61 entries):
+  // t0 = the smallest class maximum (0 if a class is empty), kmax = the row maximum
+  cmx = quad_max_u32(cmx);
+  const uint32_t t0 = wave_min_of_quads(cmx);
+  const uint32_t kmax = wave_max_of_quads(cmx);
+  int nc = 0;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const bool pass = hi[i] != 0u && hi[i] >= t0;
+    const uint64_t mask = __ballot(pass);
+    const int slot = nc + lane_prefix(mask);
+    const int c = lane + kWave * i;
+    if (pass && slot < kWave)
+      s_cand[slot] = ((uint64_t)hi[i] << 32) | ((uint32_t)(0xffff - c) << 1) | cb[i];
+    nc += __popcll(mask);
+  }
+  if (M == 0) {
+  } else if (nc <= kWave) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint64_t mine = lane < nc ? s_cand[lane] : 0ull;
+    const uint32_t h[1] = {(uint32_t)(mine >> 32)};
+    const uint32_t T = kth_key<1>(h, M, t0, kmax);
+    const int need_eq = M - __popcll(__ballot(h[0] > T));
+    const bool eq = h[0] == T && lane < nc;
+    const bool take = h[0] > T || (eq && lane_prefix(__ballot(eq)) < need_eq);
+    const uint64_t mt = __ballot(take);
+    if (take) sel[lane_prefix(mt)] = mine;
+  } else {
+    const uint32_t T = kth_key<NPL>(hi, M, t0, kmax);
+    int n_gt = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) n_gt += __popcll(__ballot(hi[i] > T));
+    const int need_eq = M - n_gt;
+    int taken = 0, eq_seen = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const bool eq = hi[i] == T;
+      const uint64_t meq = __ballot(eq);
+      const bool take = hi[i] > T || (eq && eq_seen + lane_prefix(meq) < need_eq);
+      const uint64_t mt = __ballot(take);
+      const int c = lane + kWave * i;
+      if (take)
+        sel[taken + lane_prefix(mt)] = ((uint64_t)hi[i] << 32) | ((uint32_t)(0xffff - c) << 1) | cb[i];
+      taken += __popcll(mt);
+      eq_seen += __popcll(meq);
+    }
+  }
+}
+
 // Phase 2 of the inference routing for one row per 16-lane group (lane m = entry
 // m): the row's M <= 16 selected keys sel[0..M) (any order; sorted in place) are
 // ranked, then 1.5-entmax with entry m on lane m (each lane forms its prefix sums
@@ -781,7 +844,6 @@ __global__ __launch_bounds__(kRtWaves * kWave) void route_kernel(
     // rows without any candidate fall back to every remote block
     const bool use_cand = cand_in && __any(any_cand);
     uint32_t hi[NPL];
-    uint32_t cmx = 0;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
       const int c = lane + kWave * i;
@@ -792,59 +854,9 @@ __global__ __launch_bounds__(kRtWaves * kWave) void route_kernel(
       // candidate flag in bit 0 of the key: only block ids break ties, never it
       hi[i] = c < nblk ? ord_key(x) : 0u;
       cb[i] = cd ? 1 : 0;
-      cmx = max(cmx, hi[i]);
     }
     const int M = nblk == 0 ? 0 : (topm > 0 ? max(1, min(topm, nblk)) : nblk);
-    // classes = lane quads (16 of them, all non-empty once nblk >= 61): t0 = the
-    // smallest class maximum (0 if a class is empty), kmax = the row maximum
-    cmx = quad_max_u32(cmx);
-    const uint32_t t0 = wave_min_of_quads(cmx);
-    const uint32_t kmax = wave_max_of_quads(cmx);
-    int nc = 0;
-#pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-      const bool pass = hi[i] != 0u && hi[i] >= t0;
-      const uint64_t mask = __ballot(pass);
-      const int slot = nc + lane_prefix(mask);
-      const int c = lane + kWave * i;
-      if (pass && slot < kWave)
-        s_cand[wv][slot] = ((uint64_t)hi[i] << 32) | ((uint32_t)(0xffff - c) << 1) | cb[i];
-      nc += __popcll(mask);
-    }
-    if (M == 0) {
-    } else if (nc <= kWave) {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const uint64_t mine = lane < nc ? s_cand[wv][lane] : 0ull;
-      const uint32_t h[1] = {(uint32_t)(mine >> 32)};
-      const uint32_t T = kth_key<1>(h, M, t0, kmax);
-      const int need_eq = M - __popcll(__ballot(h[0] > T));
-      const bool eq = h[0] == T && lane < nc;
-      const bool take = h[0] > T || (eq && lane_prefix(__ballot(eq)) < need_eq);
-      const uint64_t mt = __ballot(take);
-      if (take) s_sel[sr][lane_prefix(mt)] = mine;
-    } else {
-      const uint32_t T = kth_key<NPL>(hi, M, t0, kmax);
-      int n_gt = 0;
-#pragma unroll
-      for (int i = 0; i < NPL; ++i) n_gt += __popcll(__ballot(hi[i] > T));
-      const int need_eq = M - n_gt;
-      int taken = 0, eq_seen = 0;
-#pragma unroll
-      for (int i = 0; i < NPL; ++i) {
-        const bool eq = hi[i] == T;
-        const uint64_t meq = __ballot(eq);
-        const bool take = hi[i] > T || (eq && eq_seen + lane_prefix(meq) < need_eq);
-        const uint64_t mt = __ballot(take);
-        const int c = lane + kWave * i;
-        if (take)
-          s_sel[sr][taken + lane_prefix(mt)] =
-              ((uint64_t)hi[i] << 32) | ((uint32_t)(0xffff - c) << 1) | cb[i];
-        taken += __popcll(mt);
-        eq_seen += __popcll(meq);
-      }
-    }
+    route_row_topm<NPL>(hi, cb, M, s_cand[wv], s_sel[sr]);
     if (lane == 0) s_M[sr] = M;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -1514,6 +1526,8 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
   __shared__ uint8_t s_flag[kDrMaxBlocks];
   __shared__ float s_selv[kMaxM];
   __shared__ int s_selk[kMaxM];
+  __shared__ uint64_t s_wcand[kWave];
+  __shared__ uint64_t s_wsel[kMaxM];
 
   const int tid = threadIdx.x, lane = wave_lane(), wv = tid / kWave;
   const int len = a.lens ? min(max(a.lens[b], 0), a.S) : a.S;
@@ -1685,6 +1699,44 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
   }
   __syncthreads();
 
+  if (fast_scores) {
+    // rows of up to 512 blocks: the selection and the entmax in wavefront 0 alone
+    // (route_kernel's phase 1 and 2 on this row), no more work-group barriers
+    if (wv != 0) return;
+    uint8_t cb[8];
+    float zv[8];
+    bool any_cand = false;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = lane + kWave * i;
+      zv[i] = c < nblk ? s_x[c] : kScoreNeg;
+      cb[i] = (a.cand && c < nblk) ? a.cand[(int64_t)b * a.cand_stride + c] : 0;
+      any_cand |= c < nblk && zv[i] > kScoreNeg * 0.5f && cb[i] != 0;
+    }
+    // rows without any candidate fall back to every remote block
+    const bool use_cand = a.cand && __any(any_cand);
+    uint32_t hi[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = lane + kWave * i;
+      const bool remote = c < nblk && zv[i] > kScoreNeg * 0.5f;
+      const bool cd = use_cand ? (remote && cb[i] != 0) : remote;
+      float x = cd ? zv[i] * a.idx_scale : kEntmaxNeg;
+      if (!(fabsf(x) <= 3.402823466e38f)) x = kEntmaxNeg;
+      hi[i] = c < nblk ? ord_key(x) : 0u;
+      cb[i] = cd ? 1 : 0;
+    }
+    const int Mw = a.topm > 0 ? max(1, min(a.topm, nblk)) : nblk;
+    route_row_topm<8>(hi, cb, Mw, s_wcand, s_wsel);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const bool row_ok = lane < kMaxM;
+    route_finish(s_wsel, row_ok ? Mw : 0, row_ok, b, a.floor_p, a.inv_sigma, a.K, a.Kout, a.idx,
+                 a.bias, a.valid);
+    return;
+  }
+
   // candidates, with the fall-back to every remote block
   bool any = false;
   for (int c = tid; c < nblk; c += kDrThreads) {
@@ -1812,10 +1864,12 @@ __device__ __forceinline__ int ds_pieces(const DecodeArgs& da, const DcSpan& sp)
 
 // With nrw = 2 (split), ra routes without the refresh (refresh_tail 0, skip_tail 1)
 // and rt refreshes the tail blocks in work-groups B .. 2B-1.
+constexpr int kDsCUs = 256;               // compute units of an MI355X
+
 __global__ __launch_bounds__(kDrThreads) void decode_route_window_kernel(DecodeRouteArgs ra,
                                                                          DecodeRouteArgs rt,
                                                                          DecodeArgs da, int B,
-                                                                         int nrw, int npw) {
+                                                                         int nrw, int npw, int wpg) {
   if ((int)blockIdx.x < B) {
     decode_route_body<kRouteAll>(ra, blockIdx.x);
     return;
@@ -1824,9 +1878,11 @@ __global__ __launch_bounds__(kDrThreads) void decode_route_window_kernel(DecodeR
     decode_route_body<kTailOnly>(rt, (int)blockIdx.x - B);
     return;
   }
-  // one piece per wavefront (the index is made uniform, so that its loads are scalar)
-  const int task = __builtin_amdgcn_readfirstlane(((int)blockIdx.x - nrw * B) * (kDrThreads / kWave) +
-                                                 (int)threadIdx.x / kWave);
+  // one piece per wavefront, wpg wavefronts of each work-group (the others end at
+  // once); the index is made uniform, so that its loads are scalar
+  const int wv = (int)threadIdx.x / kWave;
+  if (wv >= wpg) return;
+  const int task = __builtin_amdgcn_readfirstlane(((int)blockIdx.x - nrw * B) * wpg + wv);
   if (task >= B * da.H * npw) return;
   const int piece = task % npw, bh = task / npw;
   const int h = bh % da.H, b = bh / da.H;
@@ -2024,10 +2080,17 @@ extern "C" int dash_decode_step(
   const int nrw = (refresh_tail && local_blocks >= 1) ? 2 : 1;
   const DecodeRouteArgs rt = ra;
   if (nrw == 2) { ra.refresh_tail = 0; ra.skip_tail = 1; }
-  const int64_t wgs = nrw * (int64_t)B + (tasks + kDrThreads / kWave - 1) / (kDrThreads / kWave);
+  // window pieces per work-group: at most one per wavefront, and as few as give each
+  // CU beside the routers' at most one work-group (a CU streams its pieces' rows at a
+  // bounded rate, so few pieces go faster spread over more CUs)
+  const int64_t free_cus = kDsCUs - nrw * (int64_t)B;
+  const int wpg = free_cus <= 0 ? kDrThreads / kWave
+                                : (int)std::min<int64_t>(kDrThreads / kWave,
+                                                         std::max<int64_t>(1, (tasks + free_cus - 1) / free_cus));
+  const int64_t wgs = nrw * (int64_t)B + (tasks + wpg - 1) / wpg;
   if (wgs > 0x7fffffff) return kErrUnsupported;
   hipLaunchKernelGGL(decode_route_window_kernel, dim3((unsigned)wgs), dim3(kDrThreads), 0,
-                     (hipStream_t)stream, ra, rt, a, B, nrw, npw);
+                     (hipStream_t)stream, ra, rt, a, B, nrw, npw, wpg);
   if (Kout > 0)
     hipLaunchKernelGGL(decode_routed_kernel, dim3(Kout, H, B), dim3(64), 0, (hipStream_t)stream, a,
                        npw);
