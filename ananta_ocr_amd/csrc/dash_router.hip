@@ -1654,8 +1654,7 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
       if (l16 == 0 && c < nblk) {
         float zz = kScoreNeg;
         if (c <= lim && c >= blo && c < bhi) zz = fminf(fmaxf(v * a.inv_sqrt_d, -kActClamp), kActClamp);
-        s_x[c] = zz;
-        a.z[(int64_t)b * a.z_stride + c] = zz;
+        s_x[c] = zz;                     // stored to z after the barrier below
       }
     }
   } else {
@@ -1701,8 +1700,13 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
 
   if (fast_scores) {
     // rows of up to 512 blocks: the selection and the entmax in wavefront 0 alone
-    // (route_kernel's phase 1 and 2 on this row), no more work-group barriers
-    if (wv != 0) return;
+    // (route_kernel's phase 1 and 2 on this row), no more work-group barriers; the
+    // other wavefronts store the scores (after the barrier, so that it does not wait
+    // for the stores)
+    if (wv != 0) {
+      for (int c = tid - kWave; c < nblk; c += kDrThreads - kWave) a.z[(int64_t)b * a.z_stride + c] = s_x[c];
+      return;
+    }
     uint8_t cb[8];
     float zv[8];
     bool any_cand = false;
