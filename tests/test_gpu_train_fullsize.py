@@ -126,7 +126,9 @@ def test_training_step_at_benchmark_size():
               f"scale), mean {err.mean().item() / want.abs().mean().item():.4f} of the mean",
               flush=True)
         assert err.max().item() <= GRAD_MAX * scale_ + 1e-6, what
-        assert err.mean().item() <= GRAD_MEAN * want.abs().mean().item() + 1e-7, what
+        # the absolute slack is far below the bar: the gradients' mean magnitudes here
+        # are ~1e-5 .. 1e-3, so a slack of 1e-7 would be ~1 % of them
+        assert err.mean().item() <= GRAD_MEAN * want.abs().mean().item() + 1e-10, what
 
     # ---- routing backward to the scores, on rows whose selected set both sides share ----
     dz = ops.train_route_backward(z, None, W.IDX_SCALE, W.FLOOR, W.SIGMA, idx, valid, topv, stat,
