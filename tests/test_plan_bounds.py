@@ -100,8 +100,9 @@ def test_workspace_holds_every_consistent_plan():
             assert ch <= chunk_cap, (L, K, bs, ch, chunk_cap)
             total_chunks += ch
         assert total_chunks * KPFCH <= ppos
-        # the library's layout is at least this large
-        assert _ws_bytes(lib, B, 10, S, rows, K, 128, bs) >= ppos * 10 * (128 * 2 + 4)
+        # the library's layout is at least this large: a partial row per (position,
+        # head) of 128 byte-coded dims and its (log-sum-exp, scale) pair
+        assert _ws_bytes(lib, B, 10, S, rows, K, 128, bs) >= ppos * 10 * (128 + 8)
 
 
 def test_error_word_inside_cleared_counters():
