@@ -697,11 +697,32 @@ __device__ __forceinline__ void route_row_topm(const uint32_t (&hi)[NPL], const 
 // in the serial order, so the result is the serial one bit for bit), first K,
 // centred log-prior bias; writes idx / bias / valid row `row` (Kout slots).  Every
 // lane of the wavefront calls it (wavefront barriers inside).
+// Routing slots published inside one launch.  The step counter (advanced by the
+// step's last launch) gives every step an odd epoch ep = 2 ctr + 1.  Slot s of the
+// routing is two 64-bit words whose upper halves hold ep: the block id + 1 (16
+// bits) and the valid flag (bit 16), and the bias bits.  They are stored and read
+// as relaxed atomics at agent scope, which every work-group of the device sees
+// coherently without a fence; a word holds the value it stamps, so no ordering
+// between words is needed.  Words of earlier steps carry other epochs, and so does
+// zeroed memory (even).
+__device__ __forceinline__ uint32_t step_epoch(const uint32_t* ctr) {
+  return 2u * __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+}
+__device__ __forceinline__ void publish_slot(uint64_t* pub, int64_t slot, uint32_t ep, int c,
+                                             bool valid, float bias) {
+  const uint64_t hi = (uint64_t)ep << 32;
+  __hip_atomic_store(pub + 2 * slot, hi | ((uint64_t)valid << 16) | (uint64_t)((uint32_t)(c + 1) & 0xffffu),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(pub + 2 * slot + 1, hi | (uint64_t)__float_as_uint(bias), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ void route_finish(uint64_t* sel, int M, bool row_ok, int64_t row,
                                              float floor_p, float inv_sigma, int K, int Kout,
                                              int32_t* __restrict__ idx_out,
                                              float* __restrict__ bias_out,
-                                             uint8_t* __restrict__ valid_out) {
+                                             uint8_t* __restrict__ valid_out,
+                                             uint64_t* pub = nullptr, uint32_t ep = 0u) {
 #pragma clang fp contract(off)
   const int lane = wave_lane();
   const int m = lane & 15, gbase = lane & ~15;
@@ -776,11 +797,14 @@ __device__ __forceinline__ void route_finish(uint64_t* sel, int M, bool row_ok, 
     io[m] = in ? sel_id : -1;
     bo[m] = va ? (logp - mu) * inv_sigma : 0.f;
     if (vo) vo[m] = va ? 1 : 0;
+    if (pub) publish_slot(pub, row * Kout + m, ep, in ? sel_id : -1, vo ? va : true,
+                          va ? (logp - mu) * inv_sigma : 0.f);
   }
   for (int mm = kMaxM + m; mm < Kout; mm += kMaxM) {
     io[mm] = -1;
     bo[mm] = 0.f;
     if (vo) vo[mm] = 0;
+    if (pub) publish_slot(pub, row * Kout + mm, ep, -1, false, 0.f);
   }
 }
 
@@ -1436,6 +1460,9 @@ struct DecodeRouteArgs {
   int K, topm, Kout;
   int32_t* idx; float* bias; uint8_t* valid;
   float* z; int64_t z_stride;
+  // fused decode step: the slots as published words [B * Kout, 2] for the routed-slot
+  // wavefronts of the same launch, stamped with the step counter's epoch (null: none)
+  uint64_t* pub; const uint32_t* step_ctr;
 };
 
 __device__ __forceinline__ float* kbar_row(const DecodeRouteArgs& a, int b, int c) {
@@ -1447,7 +1474,8 @@ __device__ __forceinline__ float* kbar_row(const DecodeRouteArgs& a, int b, int 
 // decode row, by one wavefront with lane m holding entry m (each lane forms its own
 // prefix sums serially), so the result is bit-for-bit the serial one.
 __device__ __forceinline__ void decode_route_finish(const DecodeRouteArgs& a, int b, int lane, int M,
-                                                    int Kp, const float* s_selv, const int* s_selk) {
+                                                    int Kp, const float* s_selv, const int* s_selk,
+                                                    uint32_t ep) {
 #pragma clang fp contract(off)
   const float xv = lane < M ? s_selv[lane] : 0.f;
   const int kv = lane < M ? s_selk[lane] : 0x3fffffff;
@@ -1494,9 +1522,12 @@ __device__ __forceinline__ void decode_route_finish(const DecodeRouteArgs& a, in
   const float mu = musum / (float)max(cnt, 1);
   for (int m = lane; m < a.Kout; m += kWave) {
     const bool kept = m < Kp;                   // m < Kp <= 16: lane m holds slot m
-    a.idx[(int64_t)b * a.Kout + m] = kept ? (kv & 0x3fffffff) : -1;
-    a.bias[(int64_t)b * a.Kout + m] = kept && va ? (logp - mu) * a.inv_sigma : 0.f;
+    const int c = kept ? (kv & 0x3fffffff) : -1;
+    const float bv = kept && va ? (logp - mu) * a.inv_sigma : 0.f;
+    a.idx[(int64_t)b * a.Kout + m] = c;
+    a.bias[(int64_t)b * a.Kout + m] = bv;
     if (a.valid) a.valid[(int64_t)b * a.Kout + m] = kept && va ? 1 : 0;
+    if (a.pub) publish_slot(a.pub, (int64_t)b * a.Kout + m, ep, c, a.valid ? kept && va : true, bv);
   }
 }
 
@@ -1538,11 +1569,13 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
   const int ct = nblk - 1;               // tail block
   constexpr bool own_refresh = mode == kRouteAll;   // and a.refresh_tail, at each use
   if (mode == kTailOnly && (!a.refresh_tail || nblk == 0)) return;
+  const uint32_t ep = (mode != kTailOnly && a.pub) ? step_epoch(a.step_ctr) : 0u;
   if (nblk == 0) {
     for (int m = tid; m < a.Kout; m += kDrThreads) {
       a.idx[(int64_t)b * a.Kout + m] = -1;
       a.bias[(int64_t)b * a.Kout + m] = 0.f;
       if (a.valid) a.valid[(int64_t)b * a.Kout + m] = 0;
+      if (a.pub) publish_slot(a.pub, (int64_t)b * a.Kout + m, ep, -1, false, 0.f);
     }
     return;
   }
@@ -1737,7 +1770,7 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const bool row_ok = lane < kMaxM;
     route_finish(s_wsel, row_ok ? Mw : 0, row_ok, b, a.floor_p, a.inv_sigma, a.K, a.Kout, a.idx,
-                 a.bias, a.valid);
+                 a.bias, a.valid, a.pub, ep);
     return;
   }
 
@@ -1824,7 +1857,7 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
   }
   __syncthreads();
   if (wv != 0) return;
-  decode_route_finish(a, b, lane, M, Kp, s_selv, s_selk);
+  decode_route_finish(a, b, lane, M, Kp, s_selv, s_selk, ep);
 }
 
 // Work-groups 0 .. B-1 route one sequence each; with nrw = 2, a routes without the
@@ -1846,8 +1879,10 @@ __global__ __launch_bounds__(kDrThreads) void decode_route_kernel(DecodeRouteArg
 // pieces, one piece of the window of one (sequence, head) per wavefront (32 or
 // 64 keys, see ds_piece_keys; 32 keys per round trip keep a wavefront within the
 // 128 registers a 1024-thread work-group allows), each writing an (o, m, l)
-// partial.  A second launch takes one wavefront per routed slot of (sequence,
-// head), a third merges.
+// partial.  The same wavefronts then take the routed slots of the (sequence, head)
+// pairs (one slot each) once the routers have published them (ds_routed_slot), so
+// the routed blocks load while other routers and pieces still run; a second launch
+// merges.
 // ---------------------------------------------------------------------------
 constexpr int kDsPieceMin = 32;           // keys per window piece: 32, or 64 (see ds_piece_keys)
 constexpr int64_t kDsWideTasks = 4096;
@@ -1870,10 +1905,74 @@ __device__ __forceinline__ int ds_pieces(const DecodeArgs& da, const DcSpan& sp)
 // and rt refreshes the tail blocks in work-groups B .. 2B-1.
 constexpr int kDsCUs = 256;               // compute units of an MI355X
 
+// Routed slot r of (b, h) in the fused step's first launch, once sequence b's router
+// (a work-group of the same launch) has published its slots: the slots are waited
+// for (bounded), filtered as dc_routed does (valid, remote, first occurrence, in slot
+// order), and the r-th kept block is streamed into slot npw + r of the partials (an
+// empty partial past the kept count).  The router work-groups have the lowest ids,
+// so they are dispatched before any wavefront that waits for them.
+constexpr int kPubSpinLimit = 1 << 16;    // polls (with a short sleep) before giving up
+
+__device__ __forceinline__ void ds_routed_slot(const DecodeRouteArgs& ra, const DecodeArgs& da,
+                                               int b, int h, int r, int npw, int lane) {
+  const uint32_t ep = step_epoch(ra.step_ctr);
+  const uint64_t* pw = ra.pub + 2 * ((int64_t)b * da.K + min(lane, da.K - 1));
+  // every lane watches the last slot's bias word (one request per poll; the router's
+  // wavefront stores all its slots together), then the slots are read
+  const uint64_t* pl = ra.pub + 2 * ((int64_t)b * da.K + da.K - 1) + 1;
+  for (int spin = 0; spin < kPubSpinLimit; ++spin) {
+    if ((uint32_t)(__hip_atomic_load(pl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 32) == ep) break;
+    __builtin_amdgcn_s_sleep(8);
+  }
+  uint64_t w0 = 0, w1 = 0;
+  bool ok = lane >= da.K;
+  for (int spin = 0;; ++spin) {
+    if (!ok) {
+      w0 = __hip_atomic_load(pw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      w1 = __hip_atomic_load(pw + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ok = (uint32_t)(w0 >> 32) == ep && (uint32_t)(w1 >> 32) == ep;
+    }
+    if (__all(ok) || spin >= kPubSpinLimit) break;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  const DcSpan sp = dc_span(da, b);
+  int c = -1;
+  float bl = 0.f;
+  bool keep = false;
+  if (lane < da.K && ok && sp.len > 0) {        // a slot never published counts as empty
+    c = (int)(uint32_t)(w0 & 0xffffu) - 1;
+    keep = ((w0 >> 16) & 1u) != 0 && c >= 0 && c < sp.nblk && c * da.bs < sp.ls;
+    bl = __uint_as_float((uint32_t)w1) * 1.4426950408889634f;
+  }
+  // first occurrence: no earlier lane that passed the filter names the same block
+  const int ck = keep ? c : -1;
+  bool dup = false;
+#pragma unroll
+  for (int j = 0; j < kDcMaxK; ++j) {
+    const int cj = __shfl(ck, j, kWave);
+    dup |= j < lane && cj == c;
+  }
+  keep = keep && !dup;
+  uint64_t mask = __ballot(keep);
+  const int n_r = __popcll(mask);
+  DcState st;
+  dc_init(st, da, b, h, lane);
+  if (r < n_r) {
+    for (int i = 0; i < r; ++i) mask &= mask - 1ull;
+    const int src = __builtin_ctzll(mask);
+    const int cr = __builtin_amdgcn_readlane(c, src);
+    const float br = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(bl), src));
+    dc_block<32>(st, da, b, h, sp, cr, true, br);
+  }
+  dc_store_partial<128>(st, da.part + ((int64_t)(b * da.H + h) * (npw + da.K) + npw + r) * (128 + 2),
+                        lane);
+}
+
 __global__ __launch_bounds__(kDrThreads) void decode_route_window_kernel(DecodeRouteArgs ra,
                                                                          DecodeRouteArgs rt,
                                                                          DecodeArgs da, int B,
-                                                                         int nrw, int npw, int wpg) {
+                                                                         int nrw, int npw, int wpg,
+                                                                         int ntask) {
   if ((int)blockIdx.x < B) {
     decode_route_body<kRouteAll>(ra, blockIdx.x);
     return;
@@ -1882,30 +1981,40 @@ __global__ __launch_bounds__(kDrThreads) void decode_route_window_kernel(DecodeR
     decode_route_body<kTailOnly>(rt, (int)blockIdx.x - B);
     return;
   }
-  // one piece per wavefront, wpg wavefronts of each work-group (the others end at
+  // one task per wavefront, wpg wavefronts of each work-group (the others end at
   // once); the index is made uniform, so that its loads are scalar
   const int wv = (int)threadIdx.x / kWave;
   if (wv >= wpg) return;
   const int task = __builtin_amdgcn_readfirstlane(((int)blockIdx.x - nrw * B) * wpg + wv);
-  if (task >= B * da.H * npw) return;
-  const int piece = task % npw, bh = task / npw;
-  const int h = bh % da.H, b = bh / da.H;
+  if (task >= ntask) return;
   const int lane = wave_lane();
-  const DcSpan sp = dc_span(da, b);
-  DcState st;
-  dc_init(st, da, b, h, lane);
-  // pieces past the window write an empty partial, so that the merge reads every
-  // slot without knowing the window's length
-  if (piece < ds_pieces(da, sp)) {
-    const int j0 = sp.w0 * da.bs + piece * da.piece;
-    dc_keys<32>(st, da, b, h, sp, j0, min(j0 + da.piece, sp.len), false, 0.f);
+  if (task < B * da.H * npw) {
+    const int piece = task % npw, bh = task / npw;
+    const int h = bh % da.H, b = bh / da.H;
+    const DcSpan sp = dc_span(da, b);
+    DcState st;
+    dc_init(st, da, b, h, lane);
+    // pieces past the window write an empty partial, so that the merge reads every
+    // slot without knowing the window's length
+    if (piece < ds_pieces(da, sp)) {
+      const int j0 = sp.w0 * da.bs + piece * da.piece;
+      dc_keys<32>(st, da, b, h, sp, j0, min(j0 + da.piece, sp.len), false, 0.f);
+    }
+    dc_store_partial<128>(st, da.part + ((int64_t)bh * (npw + da.K) + piece) * (128 + 2), lane);
   }
-  dc_store_partial<128>(st, da.part + ((int64_t)bh * (npw + da.K) + piece) * (128 + 2), lane);
+  // then routed slot ntask - 1 - task: the wavefronts dispatched last take the
+  // routed slots, so that their waits for the routers are the shortest
+  const int rtask = ntask - 1 - task;
+  if (ra.pub && rtask < B * da.H * da.K) {
+    const int r = rtask % da.K, bh = rtask / da.K;
+    ds_routed_slot(ra, da, bh / da.H, bh % da.H, r, npw, lane);
+  }
 }
 
-// Routed blocks of the fused step: one wavefront per routed slot of (b, h), 32 keys
-// per round trip; slot npw + r of the partials (an empty partial past the routed
-// count).
+// Routed blocks of the fused step in a launch of their own (grids of more than one
+// round of work-groups, where the slots taken by the first launch's last wavefronts
+// would lengthen its tail): one wavefront per routed slot of (b, h), 32 keys per
+// round trip; slot npw + r of the partials (an empty partial past the routed count).
 __global__ __launch_bounds__(64) void decode_routed_kernel(DecodeArgs da, int npw) {
   __shared__ int sTmp[kWave];
   __shared__ int sRC[kDcMaxK];
@@ -1923,9 +2032,14 @@ __global__ __launch_bounds__(64) void decode_routed_kernel(DecodeArgs da, int np
 
 // Merge of the fused step: the npw window-piece slots of (b, h) and its K routed
 // slots (npw ..), one wavefront per (b, h).
-__global__ __launch_bounds__(64) void decode_step_merge_kernel(DecodeArgs da, int npw) {
+__global__ __launch_bounds__(64) void decode_step_merge_kernel(DecodeArgs da, int npw,
+                                                              uint32_t* step_ctr) {
   __shared__ float sW[kWave];
   const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  // the step's last launch advances the counter, so that the next step's published
+  // slots carry another epoch
+  if (h == 0 && b == 0 && lane == 0)
+    __hip_atomic_fetch_add(step_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // every slot holds a partial (empty ones past the window and the routed count),
   // so the loads need nothing but the launch arguments
   const int n = npw + da.K;
@@ -1939,6 +2053,16 @@ __global__ __launch_bounds__(64) void decode_step_merge_kernel(DecodeArgs da, in
 }  // namespace dash
 
 namespace dash {
+// Workspace of the fused decode step: the (o, m, l) partials of the smallest window
+// pieces (the most of them) and the routed slots, then, 256-byte aligned, the step
+// counter (its own 256 bytes) and the published routing words [B, kDcMaxK, 2].
+inline int64_t step_sync_offset(int B, int H, int D, int block_size, int local_window) {
+  const int npw = (local_window + block_size - 1 + kDsPieceMin - 1) / kDsPieceMin;
+  const int64_t part = (int64_t)B * H * (npw + kDcMaxK) * (D + 2) * (int64_t)sizeof(float);
+  return (part + 255) / 256 * 256;
+}
+inline int64_t step_sync_bytes(int B) { return 256 + (int64_t)B * kDcMaxK * 2 * 8; }
+
 // Checks and packs the arguments of the decode router (shared by the router entry
 // and the fused decode step).
 static int decode_route_args(const float* idx_q, int64_t iq_sb, const float* idx_k,
@@ -1980,6 +2104,7 @@ static int decode_route_args(const float* idx_q, int64_t iq_sb, const float* idx
   a.K = K; a.topm = topm; a.Kout = Kout;
   a.idx = idx; a.bias = bias; a.valid = valid;
   a.z = z; a.z_stride = z_stride;
+  a.pub = nullptr; a.step_ctr = nullptr;
   return kOk;
 }
 }  // namespace dash
@@ -2017,9 +2142,7 @@ extern "C" int dash_decode_step_workspace_size(int B, int H, int D, int block_si
                                                int local_window, int64_t* bytes) {
   using namespace dash;
   if (!bytes || B < 0 || H < 0 || D <= 0 || block_size <= 0 || local_window < 1) return kErrInvalid;
-  // room for the partials of the smallest pieces (the most of them)
-  const int npw = (local_window + block_size - 1 + kDsPieceMin - 1) / kDsPieceMin;
-  *bytes = (int64_t)B * H * (npw + kDcMaxK) * (D + 2) * (int64_t)sizeof(float);
+  *bytes = step_sync_offset(B, H, D, block_size, local_window) + step_sync_bytes(B);
   return kOk;
 }
 
@@ -2079,27 +2202,44 @@ extern "C" int dash_decode_step(
   a.part = (float*)workspace;
   a.S = S; a.H = H; a.bs = block_size; a.lw = local_window; a.nsplit = npw; a.piece = piece;
   a.scale_log2e = scale * 1.4426950408889634f;
-  const int64_t tasks = (int64_t)B * H * npw;
   // the tail refresh beside the routing when the tail block cannot be remote
   const int nrw = (refresh_tail && local_blocks >= 1) ? 2 : 1;
-  const DecodeRouteArgs rt = ra;
-  if (nrw == 2) { ra.refresh_tail = 0; ra.skip_tail = 1; }
-  // window pieces per work-group: at most one per wavefront, and as few as give each
-  // CU beside the routers' at most one work-group (a CU streams its pieces' rows at a
+  // One wavefront per window piece; when the whole grid fits on the CUs at once
+  // (one round of work-groups), the same wavefronts then take the routed slots
+  // (extra wavefronts when there are more slots than pieces), else a second launch
+  // does.  The window-only grid is sized first, as the routed slots add no
+  // work-groups unless there are more slots than pieces.
+  const int64_t wtasks = (int64_t)B * H * npw;
+  // tasks per work-group: at most one per wavefront, and as few as give each CU
+  // beside the routers' at most one work-group (a CU streams its pieces' rows at a
   // bounded rate, so few pieces go faster spread over more CUs)
   const int64_t free_cus = kDsCUs - nrw * (int64_t)B;
-  const int wpg = free_cus <= 0 ? kDrThreads / kWave
-                                : (int)std::min<int64_t>(kDrThreads / kWave,
-                                                         std::max<int64_t>(1, (tasks + free_cus - 1) / free_cus));
+  auto wpg_for = [&](int64_t t) {
+    return free_cus <= 0 ? kDrThreads / kWave
+                         : (int)std::min<int64_t>(kDrThreads / kWave,
+                                                  std::max<int64_t>(1, (t + free_cus - 1) / free_cus));
+  };
+  const int64_t stasks = (int64_t)B * H * std::max(npw, Kout);
+  const int swpg = wpg_for(stasks);
+  const bool in_launch = Kout > 0 && nrw * (int64_t)B + (stasks + swpg - 1) / swpg <= kDsCUs;
+  const int64_t tasks = in_launch ? stasks : wtasks;
+  if (tasks > 0x7fffffff) return kErrUnsupported;
+  const DecodeRouteArgs rt = ra;
+  if (nrw == 2) { ra.refresh_tail = 0; ra.skip_tail = 1; }
+  char* sync = (char*)workspace + step_sync_offset(B, H, D, block_size, local_window);
+  uint32_t* step_ctr = (uint32_t*)sync;
+  ra.pub = in_launch ? (uint64_t*)(sync + 256) : nullptr;
+  ra.step_ctr = step_ctr;
+  const int wpg = wpg_for(tasks);
   const int64_t wgs = nrw * (int64_t)B + (tasks + wpg - 1) / wpg;
   if (wgs > 0x7fffffff) return kErrUnsupported;
   hipLaunchKernelGGL(decode_route_window_kernel, dim3((unsigned)wgs), dim3(kDrThreads), 0,
-                     (hipStream_t)stream, ra, rt, a, B, nrw, npw, wpg);
-  if (Kout > 0)
+                     (hipStream_t)stream, ra, rt, a, B, nrw, npw, wpg, (int)tasks);
+  if (Kout > 0 && !in_launch)
     hipLaunchKernelGGL(decode_routed_kernel, dim3(Kout, H, B), dim3(64), 0, (hipStream_t)stream, a,
                        npw);
   hipLaunchKernelGGL(decode_step_merge_kernel, dim3(H, B), dim3(64), 0, (hipStream_t)stream, a,
-                     npw);
+                     npw, step_ctr);
   return launch_status();
 }
 

@@ -8,7 +8,8 @@
  *     allocates nothing.  It keeps no state between calls, except for the
  *     allocation-free decode entry point (dash_decode_step_noalloc): a fixed 64 MiB
  *     device array per GPU, held until the process ends, and that array's address per
- *     device, looked up on the first call on each device.
+ *     device, looked up on the first call on each device.  The decode step's workspace
+ *     (caller-owned) carries a step counter from one call to the next.
  *   - Strides are in elements, not bytes.  The innermost (feature) axis must be
  *     contiguous; bf16 tensors need 16-byte aligned rows.
  *   - `stream` is a hipStream_t; all work is enqueued on it, nothing synchronises.
@@ -335,7 +336,8 @@ int dash_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
                      float scale, int nsplit, void* workspace, int64_t workspace_bytes,
                      void* stream);
 
-/* Workspace bytes dash_decode_step needs (the window partials). */
+/* Workspace bytes dash_decode_step needs (the window and routed partials, a step
+ * counter and the routing words the routers hand to the same launch). */
 int dash_decode_step_workspace_size(int B, int H, int D, int block_size, int local_window,
                                     int64_t* bytes);
 
@@ -345,10 +347,13 @@ int dash_decode_step_workspace_size(int B, int H, int D, int block_size, int loc
  * 454-500) chains _infer_route_select and _decode_attend.  The router arguments are
  * those of dash_decode_route (idx/bias/valid/z are its outputs, [B, Kout]); the
  * attention arguments those of dash_attn_decode with K = Kout.  The window part of the
- * attention runs in the router's launch (it does not depend on the routing), the routed
- * blocks and the merge in a second launch.  Kout <= 16; ceil((local_window + block_size
- * - 1) / 32) + Kout <= 64.  workspace: dash_decode_step_workspace_size bytes, 16-byte
- * aligned.
+ * attention runs in the router's launch (it does not depend on the routing).  When that
+ * launch fits on the GPU's CUs at once, its window wavefronts then take the routed blocks
+ * as each sequence's router publishes its slots; otherwise a second launch does.  The
+ * last launch merges.  Kout <= 16; ceil((local_window + block_size - 1) / 32) + Kout <=
+ * 64.  workspace: dash_decode_step_workspace_size bytes, 16-byte aligned, any contents.
+ * It keeps a step counter from call to call (the published slots carry its epoch).
+ * Calls that share a workspace must not overlap.
  */
 int dash_decode_step(const float* idx_q, int64_t iq_sb, const float* idx_k, int64_t ik_sb,
                      int64_t ik_st, int64_t ik_sp, const int32_t* block_table,
