@@ -691,12 +691,6 @@ __device__ __forceinline__ void route_row_topm(const uint32_t (&hi)[NPL], const 
   }
 }
 
-// Phase 2 of the inference routing for one row per 16-lane group (lane m = entry
-// m): the row's M <= 16 selected keys sel[0..M) (any order; sorted in place) are
-// ranked, then 1.5-entmax with entry m on lane m (each lane forms its prefix sums
-// in the serial order, so the result is the serial one bit for bit), first K,
-// centred log-prior bias; writes idx / bias / valid row `row` (Kout slots).  Every
-// lane of the wavefront calls it (wavefront barriers inside).
 // Routing slots published inside one launch.  The step counter (advanced by the
 // step's last launch) gives every step an odd epoch ep = 2 ctr + 1.  Slot s of the
 // routing is two 64-bit words whose upper halves hold ep: the block id + 1 (16
@@ -717,6 +711,13 @@ __device__ __forceinline__ void publish_slot(uint64_t* pub, int64_t slot, uint32
                      __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Phase 2 of the inference routing for one row per 16-lane group (lane m = entry
+// m): the row's M <= 16 selected keys sel[0..M) (any order; sorted in place) are
+// ranked, then 1.5-entmax with entry m on lane m (each lane forms its prefix sums
+// in the serial order, so the result is the serial one bit for bit), first K,
+// centred log-prior bias; writes idx / bias / valid row `row` (Kout slots), and with
+// pub also publishes them (publish_slot, epoch ep).  Every lane of the wavefront
+// calls it (wavefront barriers inside).
 __device__ __forceinline__ void route_finish(uint64_t* sel, int M, bool row_ok, int64_t row,
                                              float floor_p, float inv_sigma, int K, int Kout,
                                              int32_t* __restrict__ idx_out,
