@@ -691,23 +691,20 @@ __device__ __forceinline__ void route_row_topm(const uint32_t (&hi)[NPL], const 
   }
 }
 
-// Routing slots published inside one launch.  The step counter (advanced by the
-// step's last launch) gives every step an odd epoch ep = 2 ctr + 1.  Slot s of the
-// routing is two 64-bit words whose upper halves hold ep: the block id + 1 (16
-// bits) and the valid flag (bit 16), and the bias bits.  They are stored and read
-// as relaxed atomics at agent scope, which every work-group of the device sees
-// coherently without a fence; a word holds the value it stamps, so no ordering
-// between words is needed.  Words of earlier steps carry other epochs, and so does
-// zeroed memory (even).
-__device__ __forceinline__ uint32_t step_epoch(const uint32_t* ctr) {
-  return 2u * __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-}
-__device__ __forceinline__ void publish_slot(uint64_t* pub, int64_t slot, uint32_t ep, int c,
-                                             bool valid, float bias) {
-  const uint64_t hi = (uint64_t)ep << 32;
-  __hip_atomic_store(pub + 2 * slot, hi | ((uint64_t)valid << 16) | (uint64_t)((uint32_t)(c + 1) & 0xffffu),
+// Routing slots published inside one launch (the fused decode step).  Slot s of the
+// routing is two 64-bit words, each with its top bit set: the block id + 1 (16 bits)
+// and the valid flag (bit 16), and the bias bits.  They are stored and read as
+// relaxed atomics at agent scope, which every work-group of the device sees
+// coherently without a fence; a word holds the value it marks as published, so no
+// ordering between words is needed.  The words are zero between steps: zeroed
+// workspace before the first step, and the step's last launch zeroes the words it
+// published.
+constexpr uint64_t kPubBit = 1ull << 63;
+__device__ __forceinline__ void publish_slot(uint64_t* pub, int64_t slot, int c, bool valid,
+                                             float bias) {
+  __hip_atomic_store(pub + 2 * slot, kPubBit | ((uint64_t)valid << 16) | (uint64_t)((uint32_t)(c + 1) & 0xffffu),
                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(pub + 2 * slot + 1, hi | (uint64_t)__float_as_uint(bias), __ATOMIC_RELAXED,
+  __hip_atomic_store(pub + 2 * slot + 1, kPubBit | (uint64_t)__float_as_uint(bias), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -716,14 +713,14 @@ __device__ __forceinline__ void publish_slot(uint64_t* pub, int64_t slot, uint32
 // ranked, then 1.5-entmax with entry m on lane m (each lane forms its prefix sums
 // in the serial order, so the result is the serial one bit for bit), first K,
 // centred log-prior bias; writes idx / bias / valid row `row` (Kout slots), and with
-// pub also publishes them (publish_slot, epoch ep).  Every lane of the wavefront
+// pub also publishes them (publish_slot).  Every lane of the wavefront
 // calls it (wavefront barriers inside).
 __device__ __forceinline__ void route_finish(uint64_t* sel, int M, bool row_ok, int64_t row,
                                              float floor_p, float inv_sigma, int K, int Kout,
                                              int32_t* __restrict__ idx_out,
                                              float* __restrict__ bias_out,
                                              uint8_t* __restrict__ valid_out,
-                                             uint64_t* pub = nullptr, uint32_t ep = 0u) {
+                                             uint64_t* pub = nullptr) {
 #pragma clang fp contract(off)
   const int lane = wave_lane();
   const int m = lane & 15, gbase = lane & ~15;
@@ -798,14 +795,14 @@ __device__ __forceinline__ void route_finish(uint64_t* sel, int M, bool row_ok, 
     io[m] = in ? sel_id : -1;
     bo[m] = va ? (logp - mu) * inv_sigma : 0.f;
     if (vo) vo[m] = va ? 1 : 0;
-    if (pub) publish_slot(pub, row * Kout + m, ep, in ? sel_id : -1, vo ? va : true,
+    if (pub) publish_slot(pub, row * Kout + m, in ? sel_id : -1, vo ? va : true,
                           va ? (logp - mu) * inv_sigma : 0.f);
   }
   for (int mm = kMaxM + m; mm < Kout; mm += kMaxM) {
     io[mm] = -1;
     bo[mm] = 0.f;
     if (vo) vo[mm] = 0;
-    if (pub) publish_slot(pub, row * Kout + mm, ep, -1, false, 0.f);
+    if (pub) publish_slot(pub, row * Kout + mm, -1, false, 0.f);
   }
 }
 
@@ -1462,8 +1459,8 @@ struct DecodeRouteArgs {
   int32_t* idx; float* bias; uint8_t* valid;
   float* z; int64_t z_stride;
   // fused decode step: the slots as published words [B * Kout, 2] for the routed-slot
-  // wavefronts of the same launch, stamped with the step counter's epoch (null: none)
-  uint64_t* pub; const uint32_t* step_ctr;
+  // wavefronts of the same launch (null: none)
+  uint64_t* pub;
 };
 
 __device__ __forceinline__ float* kbar_row(const DecodeRouteArgs& a, int b, int c) {
@@ -1475,8 +1472,7 @@ __device__ __forceinline__ float* kbar_row(const DecodeRouteArgs& a, int b, int 
 // decode row, by one wavefront with lane m holding entry m (each lane forms its own
 // prefix sums serially), so the result is bit-for-bit the serial one.
 __device__ __forceinline__ void decode_route_finish(const DecodeRouteArgs& a, int b, int lane, int M,
-                                                    int Kp, const float* s_selv, const int* s_selk,
-                                                    uint32_t ep) {
+                                                    int Kp, const float* s_selv, const int* s_selk) {
 #pragma clang fp contract(off)
   const float xv = lane < M ? s_selv[lane] : 0.f;
   const int kv = lane < M ? s_selk[lane] : 0x3fffffff;
@@ -1528,7 +1524,7 @@ __device__ __forceinline__ void decode_route_finish(const DecodeRouteArgs& a, in
     a.idx[(int64_t)b * a.Kout + m] = c;
     a.bias[(int64_t)b * a.Kout + m] = bv;
     if (a.valid) a.valid[(int64_t)b * a.Kout + m] = kept && va ? 1 : 0;
-    if (a.pub) publish_slot(a.pub, (int64_t)b * a.Kout + m, ep, c, a.valid ? kept && va : true, bv);
+    if (a.pub) publish_slot(a.pub, (int64_t)b * a.Kout + m, c, a.valid ? kept && va : true, bv);
   }
 }
 
@@ -1570,13 +1566,12 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
   const int ct = nblk - 1;               // tail block
   constexpr bool own_refresh = mode == kRouteAll;   // and a.refresh_tail, at each use
   if (mode == kTailOnly && (!a.refresh_tail || nblk == 0)) return;
-  const uint32_t ep = (mode != kTailOnly && a.pub) ? step_epoch(a.step_ctr) : 0u;
   if (nblk == 0) {
     for (int m = tid; m < a.Kout; m += kDrThreads) {
       a.idx[(int64_t)b * a.Kout + m] = -1;
       a.bias[(int64_t)b * a.Kout + m] = 0.f;
       if (a.valid) a.valid[(int64_t)b * a.Kout + m] = 0;
-      if (a.pub) publish_slot(a.pub, (int64_t)b * a.Kout + m, ep, -1, false, 0.f);
+      if (a.pub) publish_slot(a.pub, (int64_t)b * a.Kout + m, -1, false, 0.f);
     }
     return;
   }
@@ -1771,7 +1766,7 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const bool row_ok = lane < kMaxM;
     route_finish(s_wsel, row_ok ? Mw : 0, row_ok, b, a.floor_p, a.inv_sigma, a.K, a.Kout, a.idx,
-                 a.bias, a.valid, a.pub, ep);
+                 a.bias, a.valid, a.pub);
     return;
   }
 
@@ -1858,7 +1853,7 @@ __device__ __forceinline__ void decode_route_body(const DecodeRouteArgs& a, int 
   }
   __syncthreads();
   if (wv != 0) return;
-  decode_route_finish(a, b, lane, M, Kp, s_selv, s_selk, ep);
+  decode_route_finish(a, b, lane, M, Kp, s_selv, s_selk);
 }
 
 // Work-groups 0 .. B-1 route one sequence each; with nrw = 2, a routes without the
@@ -1916,13 +1911,12 @@ constexpr int kPubSpinLimit = 1 << 16;    // polls (with a short sleep) before g
 
 __device__ __forceinline__ void ds_routed_slot(const DecodeRouteArgs& ra, const DecodeArgs& da,
                                                int b, int h, int r, int npw, int lane) {
-  const uint32_t ep = step_epoch(ra.step_ctr);
   const uint64_t* pw = ra.pub + 2 * ((int64_t)b * da.K + min(lane, da.K - 1));
   // every lane watches the last slot's bias word (one request per poll; the router's
   // wavefront stores all its slots together), then the slots are read
   const uint64_t* pl = ra.pub + 2 * ((int64_t)b * da.K + da.K - 1) + 1;
   for (int spin = 0; spin < kPubSpinLimit; ++spin) {
-    if ((uint32_t)(__hip_atomic_load(pl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 32) == ep) break;
+    if ((__hip_atomic_load(pl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kPubBit) != 0) break;
     __builtin_amdgcn_s_sleep(8);
   }
   uint64_t w0 = 0, w1 = 0;
@@ -1931,7 +1925,7 @@ __device__ __forceinline__ void ds_routed_slot(const DecodeRouteArgs& ra, const 
     if (!ok) {
       w0 = __hip_atomic_load(pw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       w1 = __hip_atomic_load(pw + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      ok = (uint32_t)(w0 >> 32) == ep && (uint32_t)(w1 >> 32) == ep;
+      ok = (w0 & kPubBit) != 0 && (w1 & kPubBit) != 0;
     }
     if (__all(ok) || spin >= kPubSpinLimit) break;
     __builtin_amdgcn_s_sleep(2);
@@ -2034,13 +2028,12 @@ __global__ __launch_bounds__(64) void decode_routed_kernel(DecodeArgs da, int np
 // Merge of the fused step: the npw window-piece slots of (b, h) and its K routed
 // slots (npw ..), one wavefront per (b, h).
 __global__ __launch_bounds__(64) void decode_step_merge_kernel(DecodeArgs da, int npw,
-                                                              uint32_t* step_ctr) {
+                                                              uint64_t* pub) {
   __shared__ float sW[kWave];
   const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  // the step's last launch advances the counter, so that the next step's published
-  // slots carry another epoch
-  if (h == 0 && b == 0 && lane == 0)
-    __hip_atomic_fetch_add(step_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // the step's last launch zeroes the slots sequence b's router published (every
+  // reader of them ran in the first launch), so the next step starts from zero
+  if (pub && h == 0 && lane < 2 * da.K) pub[2 * (int64_t)b * da.K + lane] = 0ull;
   // every slot holds a partial (empty ones past the window and the routed count),
   // so the loads need nothing but the launch arguments
   const int n = npw + da.K;
@@ -2055,14 +2048,20 @@ __global__ __launch_bounds__(64) void decode_step_merge_kernel(DecodeArgs da, in
 
 namespace dash {
 // Workspace of the fused decode step: the (o, m, l) partials of the smallest window
-// pieces (the most of them) and the routed slots, then, 256-byte aligned, the step
-// counter (its own 256 bytes) and the published routing words [B, kDcMaxK, 2].
+// pieces (the most of them) and the routed slots from its start; at its end, below
+// its last whole-256-byte boundary, the published routing words [B, kDcMaxK, 2],
+// which must be zero before the first step (each step zeroes them again).  Anchored
+// at the end, the words of a smaller batch lie inside those of a larger one on the
+// same buffer (as on the allocation-free entry's fixed array).
 inline int64_t step_sync_offset(int B, int H, int D, int block_size, int local_window) {
   const int npw = (local_window + block_size - 1 + kDsPieceMin - 1) / kDsPieceMin;
   const int64_t part = (int64_t)B * H * (npw + kDcMaxK) * (D + 2) * (int64_t)sizeof(float);
   return (part + 255) / 256 * 256;
 }
-inline int64_t step_sync_bytes(int B) { return 256 + (int64_t)B * kDcMaxK * 2 * 8; }
+inline int64_t step_sync_bytes(int B) { return (int64_t)B * kDcMaxK * 2 * 8; }
+inline int64_t step_pub_offset(int64_t workspace_bytes, int B) {
+  return workspace_bytes / 256 * 256 - step_sync_bytes(B);
+}
 
 // Checks and packs the arguments of the decode router (shared by the router entry
 // and the fused decode step).
@@ -2105,7 +2104,7 @@ static int decode_route_args(const float* idx_q, int64_t iq_sb, const float* idx
   a.K = K; a.topm = topm; a.Kout = Kout;
   a.idx = idx; a.bias = bias; a.valid = valid;
   a.z = z; a.z_stride = z_stride;
-  a.pub = nullptr; a.step_ctr = nullptr;
+  a.pub = nullptr;
   return kOk;
 }
 }  // namespace dash
@@ -2227,10 +2226,8 @@ extern "C" int dash_decode_step(
   if (tasks > 0x7fffffff) return kErrUnsupported;
   const DecodeRouteArgs rt = ra;
   if (nrw == 2) { ra.refresh_tail = 0; ra.skip_tail = 1; }
-  char* sync = (char*)workspace + step_sync_offset(B, H, D, block_size, local_window);
-  uint32_t* step_ctr = (uint32_t*)sync;
-  ra.pub = in_launch ? (uint64_t*)(sync + 256) : nullptr;
-  ra.step_ctr = step_ctr;
+  // the partials end at most at step_sync_offset, the words start at or above it
+  ra.pub = in_launch ? (uint64_t*)((char*)workspace + step_pub_offset(workspace_bytes, B)) : nullptr;
   const int wpg = wpg_for(tasks);
   const int64_t wgs = nrw * (int64_t)B + (tasks + wpg - 1) / wpg;
   if (wgs > 0x7fffffff) return kErrUnsupported;
@@ -2240,7 +2237,7 @@ extern "C" int dash_decode_step(
     hipLaunchKernelGGL(decode_routed_kernel, dim3(Kout, H, B), dim3(64), 0, (hipStream_t)stream, a,
                        npw);
   hipLaunchKernelGGL(decode_step_merge_kernel, dim3(H, B), dim3(64), 0, (hipStream_t)stream, a,
-                     npw, step_ctr);
+                     npw, ra.pub);
   return launch_status();
 }
 

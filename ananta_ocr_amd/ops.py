@@ -856,6 +856,9 @@ def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, l
     return_scores appends the block scores z [B, nblk_cap] the router computed.
     no_alloc: call dash_decode_step_noalloc, whose partials live in the library's fixed
     per-GPU scratch array (no workspace; the outputs are still allocated here).
+    workspace: a caller's buffer instead of the cached one; zero-filled before its first
+    step and passed whole on every step (the routing words at its end start at zero,
+    and each step leaves them zero).
     A wide entmax (topm <= 0 or > 16) routes through _decode_route_wide and attends
     with attn_decode (three launches instead of two)."""
     _need_gpu(q, k, v, idx_q, idx_k, kbar_cache)
@@ -940,7 +943,7 @@ def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, l
     _lib.check(lib.dash_decode_step_workspace_size(B, H, D, int(block_size), lw, ws_bytes),
                "workspace")
     if workspace is None:
-        ws = torch.empty((ws_bytes.value + 3) // 4, dtype=torch.float32, device=dev)
+        ws = _step_workspace(ws_bytes.value, dev)
     else:
         ws = workspace
         if ws.numel() * ws.element_size() < ws_bytes.value:
@@ -960,6 +963,26 @@ def decode_step_fused(q, k, v, idx_q, idx_k, head_cls, kbar_cache, block_size, l
         _stream())
     _lib.check(st_, "dash_decode_step")
     return _step_result(out, lse, idx, bias, valid, z, squeeze, return_lse, return_scores)
+
+
+_STEP_WORKSPACES = {}
+
+
+def _step_workspace(nbytes, device):
+    """The decode step's cached workspace on `device`: zeroed when it is allocated (the
+    routing words at its end must start at zero; every step leaves them zero), and
+    always passed whole, so those words stay in one place.  Calls that share it are
+    ordered on the current stream."""
+    k = str(device)
+    buf = _STEP_WORKSPACES.get(k)
+    if buf is None or buf.numel() * 4 < nbytes:
+        if buf is not None:
+            del _STEP_WORKSPACES[k]
+            del buf
+        buf = torch.zeros(((int(nbytes * 1.25) + 4095) // 4096) * 1024, dtype=torch.float32,
+                          device=device)
+        _STEP_WORKSPACES[k] = buf
+    return buf
 
 
 def _step_result(out, lse, idx, bias, valid, z, squeeze, return_lse, return_scores):

@@ -9,7 +9,7 @@
  *     allocation-free decode entry point (dash_decode_step_noalloc): a fixed 64 MiB
  *     device array per GPU, held until the process ends, and that array's address per
  *     device, looked up on the first call on each device.  The decode step's workspace
- *     (caller-owned) carries a step counter from one call to the next.
+ *     (caller-owned) keeps the zeros its routing words need from one call to the next.
  *   - Strides are in elements, not bytes.  The innermost (feature) axis must be
  *     contiguous; bf16 tensors need 16-byte aligned rows.
  *   - `stream` is a hipStream_t; all work is enqueued on it, nothing synchronises.
@@ -336,8 +336,8 @@ int dash_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
                      float scale, int nsplit, void* workspace, int64_t workspace_bytes,
                      void* stream);
 
-/* Workspace bytes dash_decode_step needs (the window and routed partials, a step
- * counter and the routing words the routers hand to the same launch). */
+/* Workspace bytes dash_decode_step needs (the window and routed partials and the
+ * routing words the routers hand to the same launch). */
 int dash_decode_step_workspace_size(int B, int H, int D, int block_size, int local_window,
                                     int64_t* bytes);
 
@@ -351,9 +351,12 @@ int dash_decode_step_workspace_size(int B, int H, int D, int block_size, int loc
  * launch fits on the GPU's CUs at once, its window wavefronts then take the routed blocks
  * as each sequence's router publishes its slots; otherwise a second launch does.  The
  * last launch merges.  Kout <= 16; ceil((local_window + block_size - 1) / 32) + Kout <=
- * 64.  workspace: dash_decode_step_workspace_size bytes, 16-byte aligned, any contents.
- * It keeps a step counter from call to call (the published slots carry its epoch).
- * Calls that share a workspace must not overlap.
+ * 64.  workspace: at least dash_decode_step_workspace_size bytes, 16-byte aligned.
+ * Its last B * 256 bytes below its last whole-256-byte boundary hold the routing words
+ * the routers hand to the same launch: they must be zero before the first call (a
+ * zero-filled buffer), and every call leaves them zero.  Pass a buffer with the same
+ * workspace_bytes on every call; a smaller batch may use a buffer sized for a larger
+ * one.  Calls that share a workspace must not overlap.
  */
 int dash_decode_step(const float* idx_q, int64_t iq_sb, const float* idx_k, int64_t ik_sb,
                      int64_t ik_st, int64_t ik_sp, const int32_t* block_table,

@@ -769,13 +769,14 @@ def test_decode_step_fused_matches_two_launch_path(paged, bs):
 
 
 @pytest.mark.parametrize("B", [5, 40])
-def test_decode_step_workspace_reuse_and_contents(B):
+def test_decode_step_workspace_reuse(B):
     """The fused step's routers hand their slots to the window wavefronts of the same
-    launch as words stamped with a step epoch that the workspace keeps.  Steps whose
-    routing changes, run on one reused workspace, on a zeroed one and on one of random
-    bytes, give identical results, and the results match decode_route + attn_decode.
-    B = 5 takes the routed slots in the first launch; B = 40 (a grid of several rounds)
-    takes them in a launch of their own."""
+    launch through words at the end of the workspace, which start at zero and which
+    every step zeroes again.  Steps whose routing changes, run on one reused buffer,
+    give the results of a freshly zeroed buffer bit for bit, and match decode_route +
+    attn_decode; so does a smaller batch on the same buffer.  B = 5 takes the routed
+    slots in the first launch; B = 40 (a grid of several rounds) in a launch of their
+    own."""
     import ctypes
     from ananta_ocr_amd import _lib, pipeline
     H, d, bs, lw, K = 10, 128, 64, 1024, 16
@@ -790,33 +791,41 @@ def test_decode_step_workspace_reuse_and_contents(B):
     st = pipeline.init_decode_state(ik, hc, bs, (S + bs - 1) // bs, seq_lens=L)
     need = ctypes.c_int64(0)
     assert _lib.load().dash_decode_step_workspace_size(B, H, 128, bs, lw, need) == 0
-    nf = (need.value + 3) // 4
-    reused = torch.empty(nf, dtype=torch.float32, device=DEV)
+    nf = (need.value + 3) // 4 + 1000            # not a multiple of 256 bytes
+    reused = torch.zeros(nf, dtype=torch.float32, device=DEV)
+    args = (hc, bs, lw // bs, W.IDX_SCALE * 50, W.FLOOR, W.SIGMA, K, K, 1 / math.sqrt(128))
     prev = None
     for step in range(3):
         q = (torch.randn(B, H, 128, generator=g) * 2).bfloat16().to(DEV)
         iq = torch.randn(B, d, generator=g).to(DEV)
-        args = (hc, bs, lw // bs, W.IDX_SCALE * 50, W.FLOOR, W.SIGMA, K, K, 1 / math.sqrt(128))
-        res = []
-        for ws in (reused, torch.zeros(nf, device=DEV),
-                   torch.randint(-2 ** 31, 2 ** 31 - 1, (nf,), dtype=torch.int32,
-                                 device=DEV).view(torch.float32)):
-            out, (ti, bi, va) = ops.decode_step_fused(q, k, v, iq, ik, hc, st.kbar, *args[1:],
-                                                      seq_lens=L, workspace=ws)
-            res.append((out, ti, bi, va))
-        for r in res[1:]:
-            for a_, b_ in zip(res[0], r):
-                assert torch.equal(a_, b_), step
+        res = [ops.decode_step_fused(q, k, v, iq, ik, hc, st.kbar, *args[1:], seq_lens=L,
+                                     workspace=ws)
+               for ws in (reused, torch.zeros(nf, device=DEV))]
+        for a_, b_ in zip(res[0][1], res[1][1]):
+            assert torch.equal(a_, b_), step
+        assert torch.equal(res[0][0], res[1][0]), step
         out_s, (ti_s, bi_s, va_s) = pipeline.decode_step(st, q, k, v, iq, ik, *args,
                                                          return_routing=True, fused=False,
                                                          seq_lens=L)
-        out, ti, bi, va = res[0]
+        out, (ti, bi, va) = res[0]
         assert torch.equal(ti[:, 0], ti_s[:, 0]) and torch.equal(bi[:, 0], bi_s[:, 0])
         assert bool(va.bool().any())
         torch.testing.assert_close(out, out_s, atol=2e-5, rtol=2e-5)
         if prev is not None:
             assert not torch.equal(ti, prev), step        # the routing changed
         prev = ti.clone()
+    # every step left the words zero
+    assert not bool(reused.view(torch.int64)[-(B * 32 + 64):].ne(0).any())
+    # a smaller batch on the same buffer
+    Bs = B // 2 + 1
+    sub = dict(seq_lens=L[:Bs])
+    st_s = pipeline.init_decode_state(ik[:Bs], hc, bs, (S + bs - 1) // bs, **sub)
+    res = [ops.decode_step_fused(q[:Bs], k[:Bs], v[:Bs], iq[:Bs], ik[:Bs], hc, st_s.kbar,
+                                 *args[1:], workspace=ws, **sub)
+           for ws in (reused, torch.zeros(nf, device=DEV))]
+    assert torch.equal(res[0][0], res[1][0])
+    for a_, b_ in zip(res[0][1], res[1][1]):
+        assert torch.equal(a_, b_)
 
 
 def test_decode_graph_replays_match_eager():
