@@ -163,8 +163,14 @@ def time_kernel(fn, reps):
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     # A spin kernel first keeps the GPU busy while the host enqueues every launch, so
     # that the event pair around the back-to-back launches brackets GPU work only (an
-    # event pair per launch would add its own gaps).
-    torch.cuda._sleep(int(2.4e9 * 2e-3 + reps * 2.4e9 * 100e-6))
+    # event pair per launch would add its own gaps).  The spin covers three times the
+    # host time of one untimed call per launch (at least 100 us each): a spin shorter
+    # than the enqueueing lets the GPU idle inside the bracket.
+    t0 = time.perf_counter()
+    fn(0)
+    host = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(2.4e9 * (2e-3 + reps * max(100e-6, 3.0 * host))))
     a.record(st)
     for i in range(reps):
         fn(i)
